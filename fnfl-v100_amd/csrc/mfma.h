@@ -1,0 +1,73 @@
+// CDNA4 building blocks shared by the attention kernels: operand types of v_mfma_f32_16x16x32_f16, the exact widening
+// of 8 stored (excess-128) codes to fp16, LDS direct loads and the vmcnt wait that orders them.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace fnkv {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// D = A B + C with A 16x32 (lane l: row l % 16, slots 8 (l / 16) .. + 7), B 32x16 (lane l: column l % 16, the same
+// slots), D 16x16 (lane l: rows 4 (l / 16) .. + 3 of column l % 16)
+__device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// two excess-128 code bytes u0, u1 of `w` (selected by `sel`) become fp16 1024 + u, then minus 1152: the codes
+// u - 128 exactly
+__device__ __forceinline__ uint32_t widen2(uint32_t w, uint32_t sel) {
+    const uint32_t biased = __builtin_amdgcn_perm(0x64646464u, w, sel);
+    half2v h = __builtin_bit_cast(half2v, biased);
+    h = h - half2v{static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// 8 codes (two dwords, byte i = slot i) as the fp16 operand
+__device__ __forceinline__ half8 widen8(uint32_t lo, uint32_t hi) {
+    u32x4 r;
+    r[0] = widen2(lo, 0x04010400u);
+    r[1] = widen2(lo, 0x04030402u);
+    r[2] = widen2(hi, 0x04010400u);
+    r[3] = widen2(hi, 0x04030402u);
+    return __builtin_bit_cast(half8, r);
+}
+
+// x (8 fp32 values) as hi + lo, both fp16: hi = x rounded toward zero, lo = the remainder rounded toward zero, so
+// hi + lo carries x to about 22 bits (the remainder of a truncation to fp16 is exact in fp32)
+__device__ __forceinline__ void split_hilo(const float (&x)[8], half8 & hi, half8 & lo) {
+    typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+    u32x4 h, l;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const fp16x2 hv = __builtin_amdgcn_cvt_pkrtz(x[2 * i], x[2 * i + 1]);
+        const float r0 = x[2 * i] - static_cast<float>(hv[0]);
+        const float r1 = x[2 * i + 1] - static_cast<float>(hv[1]);
+        const fp16x2 lv = __builtin_amdgcn_cvt_pkrtz(r0, r1);
+        h[i] = __builtin_bit_cast(uint32_t, hv);
+        l[i] = __builtin_bit_cast(uint32_t, lv);
+    }
+    hi = __builtin_bit_cast(half8, h);
+    lo = __builtin_bit_cast(half8, l);
+}
+
+// a wave's 64 x 16 B from global memory straight into LDS at lds_base + 16 lane (no registers)
+__device__ __forceinline__ void lds_load16(const void * gptr, void * lds_base) {
+    typedef __attribute__((address_space(3))) void lds_void;
+    __builtin_amdgcn_global_load_lds(gptr, (lds_void *)lds_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8)
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+} // namespace fnkv

@@ -1,0 +1,342 @@
+// Chunked-prefill attention on the matrix cores: `rows` query tokens of one sequence (the chunk just appended, at
+// positions ctx - rows .. ctx - 1) attend causally to the sequence's cells 0 .. ctx - 1 of one layer in the pool.
+//
+// What it computes (the reference's prompt attention, fn/kernels/qsa/qsa_prompt.h:50-58 and qsa_prompt_attn.cu:
+// 229-436, made dense and causal, on BASELINE's Q8_0 format): S = Q K^T * scale, online softmax, O = P V, fp16 out.
+// The reference rounds its K/V operand to fp16 once (q4_h4, qsa_prompt_attn.cu:195-207) and P to fp16, within a loose
+// 2e-2 bound; here K and V (code x scale, exact in fp32: 8 x 11 bits) and P go to the matrix cores as hi + lo fp16
+// pairs, so the products carry ~22 bits and the result meets 2e-3 against fp64 even when a few cells dominate.
+//
+// How (MI355X): matrix-core bound (4 d flops a visible (query, key) pair and head), so K/V tiles are dequantized once
+// a workgroup and shared by all its query rows.
+//   * A workgroup (4 waves) owns 128 query rows (128 / G query tokens x the G heads of one KV head); each wave owns
+//     two 16-row tiles. Its waves walk the key tiles (32 tokens) in order up to the block's last query position.
+//   * Each tile streams HBM -> LDS (17 direct 1 KiB loads split over the waves, double-buffered), is dequantized once
+//     into fp16 hi / lo MFMA operand planes in LDS (codes widened exactly, times the scale in fp32, split), and then
+//     every wave runs S^T = K Q^T (two v_mfma_f32_16x16x32_f16 a block a 16-token half: K hi, K lo) and
+//     O^T += V^T P^T (three a 16-value tile: Vhi Phi, Vlo Phi, Vhi Plo) on it.
+//   * The softmax (base 2) runs on the S^T registers exactly as in the decode kernel; P feeds the PV MFMA in place.
+#include "../../include/fnkv.h"
+#include "common.h"
+#include "layout.h"
+#include "mfma.h"
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+namespace fnkv {
+
+constexpr int32_t kPfWaves = 4;
+constexpr int32_t kPfNT = 2;                         // 16-row tiles a wave
+constexpr int32_t kPfRows = kPfWaves * kPfNT * 16;   // 128 rows a workgroup
+constexpr int32_t kPfStage = kTileBytes;             // one code tile
+constexpr int32_t kPfPlane = 16 * 1024;             // one fp16 operand plane of a tile (K or V, hi or lo)
+constexpr int32_t kPfLds = 2 * kPfStage + 4 * kPfPlane;
+constexpr float kPfNegInf = -__builtin_inff();
+
+struct pf_args {
+    pool_view pv;
+    const uint16_t * q; // fp16 [rows][hq][256]
+    uint16_t * out;     // fp16 [rows][hq][256]
+    float c2;           // scale * log2(e)
+    int64_t ctx;        // cells of the sequence (the chunk included)
+    int32_t rows, G, hq, layer, slot;
+};
+
+template <bool LAST>
+__device__ __forceinline__ void pf_issue(const uint8_t * tile, uint8_t * stage, int32_t wave, int32_t lane) {
+    // the tile's 17 chunks of 1 KiB: wave w issues chunks w, w + 4, ...
+#pragma unroll
+    for (int32_t c = 0; c < 5; ++c) {
+        const int32_t ch = wave + c * kPfWaves;
+        if (ch < 17) {
+            lds_load16(tile + ch * 1024 + lane * 16, stage + ch * 1024);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256, 1) void prefill_kernel(pf_args a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
+    const int32_t wave = static_cast<int32_t>(threadIdx.x) >> 6;
+    const int32_t j = lane & 15, qg = lane >> 4;
+    const int32_t kvh = static_cast<int32_t>(blockIdx.y);
+    const int32_t tok_per_wg = kPfRows / a.G;
+    const int32_t t_first = static_cast<int32_t>(blockIdx.x) * tok_per_wg;
+    const int64_t pos_first = a.ctx - a.rows; // position of query token 0
+    const int32_t t_last = min(a.rows, t_first + tok_per_wg) - 1;
+    const int64_t key_end = pos_first + t_last + 1; // keys the block's last query sees
+    const int32_t n_tiles = static_cast<int32_t>((key_end + kTileTokens - 1) / kTileTokens);
+
+    // Q operands (B of S^T = K Q^T) of this wave's two row tiles, and each row's causal limit
+    half8 qop[kPfNT][kBlocks];
+    int64_t lim[kPfNT];
+#pragma unroll
+    for (int nt = 0; nt < kPfNT; ++nt) {
+        const int32_t r = (wave * kPfNT + nt) * 16 + j;
+        const int32_t t = t_first + r / a.G;
+        const bool real = t < a.rows;
+        lim[nt] = real ? pos_first + t : pos_first + t_last;
+        const uint16_t * qrow = a.q + (int64_t(real ? t : t_last) * a.hq + int64_t(kvh) * a.G + r % a.G) * kHeadDim;
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) {
+            u32x4 v = {0, 0, 0, 0};
+            if (real) {
+                v = *reinterpret_cast<const u32x4 *>(qrow + b * kQK + 8 * qg);
+            }
+            qop[nt][b] = __builtin_bit_cast(half8, v);
+        }
+    }
+    floatx4 acc[kPfNT][16];
+    float m_run[kPfNT], l_run[kPfNT];
+#pragma unroll
+    for (int nt = 0; nt < kPfNT; ++nt) {
+        m_run[nt] = kPfNegInf;
+        l_run[nt] = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            acc[nt][m] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+
+    const pool_view & pv = a.pv;
+    const int32_t * table = pv.table + int64_t(a.slot) * pv.table_stride;
+    const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
+    auto tile_ptr = [&](int32_t ti) -> const uint8_t * {
+        const int64_t tok = int64_t(ti) * kTileTokens;
+        const int32_t phys = table[tok >> 8];
+        return layer_base + int64_t(phys) * pv.page_stride + int64_t((tok & 255) >> 5) * kTileBytes;
+    };
+    uint8_t * stage_base = smem;
+    uint8_t * planes = smem + 2 * kPfStage;
+
+    if (n_tiles > 0) {
+        pf_issue<false>(tile_ptr(0), stage_base, wave, lane);
+    }
+    for (int32_t ti = 0; ti < n_tiles; ++ti) {
+        uint8_t * st = stage_base + (ti & 1) * kPfStage;
+        uint8_t * pl = planes; // one set: the barriers above and below order its writers and readers
+        if (ti + 1 < n_tiles) {
+            pf_issue<false>(tile_ptr(ti + 1), stage_base + ((ti + 1) & 1) * kPfStage, wave, lane);
+            // this wave issued 4 or 5 chunks for the next tile; its chunks of this tile are older than those
+            if (wave == 0) {
+                wait_vmcnt<5>();
+            } else {
+                wait_vmcnt<4>();
+            }
+        } else {
+            wait_vmcnt<0>();
+        }
+        __syncthreads(); // every wave's chunks of tile ti have landed
+
+        // ---- dequantize: wave w converts K chunks (h, ld) = w and w + 4, V chunks ld = w and w + 4 ----
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int32_t kc = wave + 4 * c; // K chunk: h = kc / 4, ld = kc % 4
+            const int32_t h = kc >> 2, ld = kc & 3;
+            const u32x4 w = *reinterpret_cast<const u32x4 *>(st + kKCodes + kc * 1024 + lane * 16);
+            // this lane's row is token 16 h + j; blocks 2 ld and 2 ld + 1
+            const half2v s2 = *reinterpret_cast<const half2v *>(st + kKScales + (16 * h + j) * 16 + ld * 4);
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) {
+                const int32_t b = 2 * ld + bb;
+                const half8 code = widen8(w[2 * bb], w[2 * bb + 1]);
+                const float sc = static_cast<float>(s2[bb]);
+                float x[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    x[i] = static_cast<float>(code[i]) * sc;
+                }
+                half8 hi, lo;
+                split_hilo(x, hi, lo);
+                const int32_t off = ((h * kBlocks + b) * 64 + lane) * 16;
+                *reinterpret_cast<half8 *>(pl + off) = hi;
+                *reinterpret_cast<half8 *>(pl + kPfPlane + off) = lo;
+            }
+            const int32_t vc = wave + 4 * c; // V chunk ld = vc: MFMA tiles m = 2 vc, 2 vc + 1 of block vc
+            const u32x4 vw = *reinterpret_cast<const u32x4 *>(st + kVCodes + vc * 1024 + lane * 16);
+            const half8 vs = *reinterpret_cast<const half8 *>(st + kVScales + qg * 128 + vc * 16);
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm) {
+                const half8 code = widen8(vw[2 * mm], vw[2 * mm + 1]);
+                float x[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    x[i] = static_cast<float>(code[i]) * static_cast<float>(vs[i]);
+                }
+                half8 hi, lo;
+                split_hilo(x, hi, lo);
+                const int32_t off = ((2 * vc + mm) * 64 + lane) * 16;
+                *reinterpret_cast<half8 *>(pl + 2 * kPfPlane + off) = hi;
+                *reinterpret_cast<half8 *>(pl + 3 * kPfPlane + off) = lo;
+            }
+        }
+        __syncthreads(); // the operand planes are complete
+
+        const int64_t tok0 = int64_t(ti) * kTileTokens;
+        // ---- S^T = K Q^T ----
+        floatx4 sc[kPfNT][2];
+#pragma unroll
+        for (int nt = 0; nt < kPfNT; ++nt) {
+            sc[nt][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            sc[nt][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int32_t off = ((h * kBlocks + b) * 64 + lane) * 16;
+                const half8 khi = *reinterpret_cast<const half8 *>(pl + off);
+                const half8 klo = *reinterpret_cast<const half8 *>(pl + kPfPlane + off);
+#pragma unroll
+                for (int nt = 0; nt < kPfNT; ++nt) {
+                    sc[nt][h] = mfma16(khi, qop[nt][b], sc[nt][h]);
+                    sc[nt][h] = mfma16(klo, qop[nt][b], sc[nt][h]);
+                }
+            }
+        }
+        // ---- online softmax (base 2), P split hi + lo ----
+        half8 ph[kPfNT], plo[kPfNT];
+#pragma unroll
+        for (int nt = 0; nt < kPfNT; ++nt) {
+            float v[8];
+            float mx = kPfNegInf;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t pos = tok0 + 16 * h + 4 * qg + r;
+                    const float x = pos <= lim[nt] ? sc[nt][h][r] * a.c2 : kPfNegInf;
+                    v[4 * h + r] = x;
+                    mx = fmaxf(mx, x);
+                }
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float m_new = fmaxf(m_run[nt], mx);
+            const float m_use = m_new == kPfNegInf ? 0.0f : m_new;
+            const float alpha = __builtin_amdgcn_exp2f(m_run[nt] - m_use);
+            float lsum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                v[i] = __builtin_amdgcn_exp2f(v[i] - m_use);
+                lsum += v[i];
+            }
+            split_hilo(v, ph[nt], plo[nt]);
+            l_run[nt] = __builtin_fmaf(l_run[nt], alpha, lsum);
+            m_run[nt] = m_new;
+            if (__any(alpha != 1.0f)) {
+#pragma unroll
+                for (int m = 0; m < 16; ++m) {
+                    acc[nt][m] *= alpha;
+                }
+            }
+        }
+        // ---- O^T += V^T P^T ----
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            const int32_t off = (m * 64 + lane) * 16;
+            const half8 vhi = *reinterpret_cast<const half8 *>(pl + 2 * kPfPlane + off);
+            const half8 vlo = *reinterpret_cast<const half8 *>(pl + 3 * kPfPlane + off);
+#pragma unroll
+            for (int nt = 0; nt < kPfNT; ++nt) {
+                acc[nt][m] = mfma16(vhi, ph[nt], acc[nt][m]);
+                acc[nt][m] = mfma16(vlo, ph[nt], acc[nt][m]);
+                acc[nt][m] = mfma16(vhi, plo[nt], acc[nt][m]);
+            }
+        }
+    }
+
+    // ---- normalise and write ----
+#pragma unroll
+    for (int nt = 0; nt < kPfNT; ++nt) {
+        float l = l_run[nt];
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        const int32_t r = (wave * kPfNT + nt) * 16 + j;
+        const int32_t t = t_first + r / a.G;
+        if (t < a.rows) {
+            const float inv = 1.0f / l;
+            uint16_t * o = a.out + (int64_t(t) * a.hq + int64_t(kvh) * a.G + r % a.G) * kHeadDim + 4 * qg;
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                uint2 pk;
+                pk.x = uint32_t(__half_as_ushort(__float2half_rn(acc[nt][m][0] * inv))) |
+                       (uint32_t(__half_as_ushort(__float2half_rn(acc[nt][m][1] * inv))) << 16);
+                pk.y = uint32_t(__half_as_ushort(__float2half_rn(acc[nt][m][2] * inv))) |
+                       (uint32_t(__half_as_ushort(__float2half_rn(acc[nt][m][3] * inv))) << 16);
+                *reinterpret_cast<uint2 *>(o + 16 * m) = pk;
+            }
+        }
+    }
+}
+
+} // namespace fnkv
+
+using fnkv::set_error;
+
+extern "C" {
+
+int64_t fnkv_prefill_workspace_bytes(const fnkv_pool * pool, int64_t ctx, int32_t rows, int32_t hq) {
+    (void)ctx;
+    (void)rows;
+    (void)hq;
+    return pool == nullptr ? -1 : 0;
+}
+
+int fnkv_attn_prefill(const fnkv_pool * pool, int32_t slot, int32_t layer, int64_t ctx, int32_t rows, int32_t hq,
+                      float scale, const void * q, void * out, void * ws, int64_t ws_bytes, void * stream) {
+    (void)ws;
+    (void)ws_bytes;
+    const fnkv::kv_pool * p = fnkv::pool_of(pool);
+    if (p == nullptr || slot < 0 || slot >= p->pages().n_slots() || layer < 0 || layer >= p->layers() || rows <= 0 ||
+        ctx < rows || ctx > p->mapped_cells(slot) || hq <= 0 || hq % p->h_kv() != 0 || q == nullptr ||
+        out == nullptr || !(scale > 0.0f) || !std::isfinite(scale)) {
+        set_error("fnkv_attn_prefill: argument outside the contract");
+        return FNKV_ERR_ARG;
+    }
+    const int32_t G = hq / p->h_kv();
+    if (fnkv::kPfRows % G != 0) {
+        set_error("fnkv_attn_prefill: the GQA group must divide 128");
+        return FNKV_ERR_ARG;
+    }
+    if ((reinterpret_cast<uintptr_t>(q) & 15) != 0 || (reinterpret_cast<uintptr_t>(out) & 7) != 0) {
+        set_error("fnkv_attn_prefill: q must be 16-byte and out 8-byte aligned");
+        return FNKV_ERR_ARG;
+    }
+    fnkv::pf_args a;
+    a.pv = p->view();
+    a.q = static_cast<const uint16_t *>(q);
+    a.out = static_cast<uint16_t *>(out);
+    a.c2 = scale * 1.4426950408889634f;
+    a.ctx = ctx;
+    a.rows = rows;
+    a.G = G;
+    a.hq = hq;
+    a.layer = layer;
+    a.slot = slot;
+    const int32_t tok_per_wg = fnkv::kPfRows / G;
+    static bool attr_set[64] = {false};
+    const int32_t dev = p->device();
+    if (dev >= 0 && dev < 64 && !attr_set[dev]) {
+        int32_t cur = 0;
+        hipGetDevice(&cur);
+        hipSetDevice(dev);
+        hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::prefill_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::kPfLds);
+        hipGetLastError();
+        hipSetDevice(cur);
+        attr_set[dev] = true;
+    }
+    const dim3 grid(static_cast<uint32_t>((rows + tok_per_wg - 1) / tok_per_wg), static_cast<uint32_t>(p->h_kv()));
+    hipLaunchKernelGGL(fnkv::prefill_kernel, grid, dim3(256), fnkv::kPfLds, static_cast<hipStream_t>(stream), a);
+    if (hipGetLastError() != hipSuccess) {
+        set_error("fnkv_attn_prefill: launch failed");
+        return FNKV_ERR_HIP;
+    }
+    return FNKV_OK;
+}
+
+} // extern "C"

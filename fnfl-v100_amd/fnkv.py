@@ -1,0 +1,229 @@
+"""Python view of libfnkv.so (include/fnkv.h) through ctypes.
+
+This is plumbing for the tests and the bench: the product is the HIP library; device buffers are torch tensors on
+the GPU, passed by their data pointers, and streams are torch's current stream. Loading fails loudly when the
+library was not built; there is no CPU fallback.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfnkv.so")
+
+OK, ERR_ARG, ERR_CAPACITY, ERR_HIP = 0, 1, 2, 3
+F16, F32 = 0, 1
+PAGE_TOKENS = 256
+HEAD_DIM = 256
+EXPORTS = [
+    "fnkv_last_error", "fnkv_pages_for", "fnkv_reclaim_victim", "fnkv_pool_create", "fnkv_pool_destroy",
+    "fnkv_pool_ensure", "fnkv_pool_trim", "fnkv_pool_mapped_cells", "fnkv_pool_free_pages", "fnkv_pool_n_pages",
+    "fnkv_pool_mapped_pages", "fnkv_pool_physical", "fnkv_page_table", "fnkv_pool_ledger", "fnkv_pool_test_fail",
+    "fnkv_page_block_bytes", "fnkv_pool_device_base", "fnkv_pool_device_bytes", "fnkv_q8_append",
+    "fnkv_export_q8_0", "fnkv_decode_workspace_bytes", "fnkv_attn_decode", "fnkv_prefill_workspace_bytes",
+    "fnkv_attn_prefill",
+]
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+I64 = ctypes.c_int64
+
+_lib = None
+
+
+class SlotView(ctypes.Structure):
+    _fields_ = [("active", I32), ("pages", I32), ("released", ctypes.c_uint64)]
+
+
+class FnkvError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"fnkv error {code}: {msg}")
+        self.code = code
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build() first")
+        L = ctypes.CDLL(LIB_PATH)
+        L.fnkv_last_error.restype = ctypes.c_char_p
+        L.fnkv_pages_for.restype = I32
+        L.fnkv_pages_for.argtypes = [I64, I32, I32]
+        L.fnkv_reclaim_victim.restype = I32
+        L.fnkv_reclaim_victim.argtypes = [P, I32, I32]
+        L.fnkv_pool_create.restype = ctypes.c_int
+        L.fnkv_pool_create.argtypes = [I32, I32, I32, I32, I32, I64, I32, ctypes.POINTER(P)]
+        L.fnkv_pool_destroy.argtypes = [P]
+        L.fnkv_pool_ensure.restype = ctypes.c_int
+        L.fnkv_pool_ensure.argtypes = [P, I32, I64, ctypes.POINTER(I32)]
+        L.fnkv_pool_trim.restype = ctypes.c_int
+        L.fnkv_pool_trim.argtypes = [P, I32, I64]
+        L.fnkv_pool_mapped_cells.restype = I64
+        L.fnkv_pool_mapped_cells.argtypes = [P, I32]
+        for n in ("fnkv_pool_free_pages", "fnkv_pool_n_pages"):
+            getattr(L, n).restype = I32
+            getattr(L, n).argtypes = [P]
+        L.fnkv_pool_mapped_pages.restype = I32
+        L.fnkv_pool_mapped_pages.argtypes = [P, I32]
+        L.fnkv_pool_physical.restype = I32
+        L.fnkv_pool_physical.argtypes = [P, I32, I32]
+        L.fnkv_page_table.restype = I32
+        L.fnkv_page_table.argtypes = [P, I32, P, I32]
+        L.fnkv_pool_ledger.restype = I32
+        L.fnkv_pool_ledger.argtypes = [P, ctypes.c_char_p, I32]
+        L.fnkv_pool_test_fail.argtypes = [P, I32]
+        L.fnkv_page_block_bytes.restype = I64
+        L.fnkv_pool_device_base.restype = P
+        L.fnkv_pool_device_base.argtypes = [P]
+        L.fnkv_pool_device_bytes.restype = I64
+        L.fnkv_pool_device_bytes.argtypes = [P]
+        L.fnkv_q8_append.restype = ctypes.c_int
+        L.fnkv_q8_append.argtypes = [P, I32, I32, I64, I32, P, P, I32, P]
+        L.fnkv_export_q8_0.restype = ctypes.c_int
+        L.fnkv_export_q8_0.argtypes = [P, I32, I32, I32, I32, I64, I32, P, P]
+        L.fnkv_decode_workspace_bytes.restype = I64
+        L.fnkv_decode_workspace_bytes.argtypes = [P, I32, P, I32, I32]
+        L.fnkv_attn_decode.restype = ctypes.c_int
+        L.fnkv_attn_decode.argtypes = [P, I32, P, P, I32, I32, I32, ctypes.c_float, P, P, P, I64, P]
+        L.fnkv_prefill_workspace_bytes.restype = I64
+        L.fnkv_prefill_workspace_bytes.argtypes = [P, I64, I32, I32]
+        L.fnkv_attn_prefill.restype = ctypes.c_int
+        L.fnkv_attn_prefill.argtypes = [P, I32, I32, I64, I32, I32, ctypes.c_float, P, P, P, I64, P]
+        _lib = L
+    return _lib
+
+
+def last_error():
+    return lib().fnkv_last_error().decode()
+
+
+def check(code):
+    if code != OK:
+        raise FnkvError(code, last_error())
+    return code
+
+
+def pages_for(cells, page_cells, n_pages):
+    return lib().fnkv_pages_for(cells, page_cells, n_pages)
+
+
+def reclaim_victim(views, for_slot):
+    """views: list of (active, pages, released)"""
+    arr = (SlotView * max(1, len(views)))()
+    for i, (a, p, r) in enumerate(views):
+        arr[i].active, arr[i].pages, arr[i].released = int(bool(a)), p, r
+    return lib().fnkv_reclaim_victim(ctypes.cast(arr, P), len(views), for_slot)
+
+
+def _stream(stream):
+    if stream is not None:
+        return P(stream)
+    import torch
+    return P(torch.cuda.current_stream().cuda_stream)
+
+
+def _i32_array(xs):
+    a = (I32 * len(xs))(*[int(x) for x in xs])
+    return ctypes.cast(a, P), a
+
+
+def _i64_array(xs):
+    a = (I64 * len(xs))(*[int(x) for x in xs])
+    return ctypes.cast(a, P), a
+
+
+class Pool:
+    """The page pool (kv_pool.h:63-138) and the kernels that read and write it."""
+
+    def __init__(self, n_slots, n_pages, layers, h_kv, slot_tokens=0, device=0, page_tokens=PAGE_TOKENS):
+        h = P()
+        check(lib().fnkv_pool_create(n_slots, n_pages, page_tokens, layers, h_kv, slot_tokens, device,
+                                     ctypes.byref(h)))
+        self.h = h
+        self.n_slots, self.n_pages, self.layers, self.h_kv = n_slots, n_pages, layers, h_kv
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().fnkv_pool_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- book ----
+    def ensure(self, slot, cells):
+        cap = I32(0)
+        code = lib().fnkv_pool_ensure(self.h, slot, cells, ctypes.byref(cap))
+        return code, bool(cap.value)
+
+    def trim(self, slot, keep_cells):
+        return lib().fnkv_pool_trim(self.h, slot, keep_cells)
+
+    def mapped_cells(self, slot):
+        return lib().fnkv_pool_mapped_cells(self.h, slot)
+
+    def free_pages(self):
+        return lib().fnkv_pool_free_pages(self.h)
+
+    def mapped_pages(self, slot):
+        return lib().fnkv_pool_mapped_pages(self.h, slot)
+
+    def physical(self, slot, logical):
+        return lib().fnkv_pool_physical(self.h, slot, logical)
+
+    def table(self, slot):
+        n = lib().fnkv_page_table(self.h, slot, None, 0)
+        ptr, arr = _i32_array([0] * max(1, n))
+        lib().fnkv_page_table(self.h, slot, ptr, n)
+        return list(arr[:n])
+
+    def ledger(self):
+        buf = ctypes.create_string_buffer(4096)
+        lib().fnkv_pool_ledger(self.h, buf, 4096)
+        return buf.value.decode().splitlines()
+
+    def test_fail(self, after):
+        lib().fnkv_pool_test_fail(self.h, after)
+
+    def device_bytes(self):
+        return lib().fnkv_pool_device_bytes(self.h)
+
+    # ---- kernels (torch device tensors) ----
+    def append(self, slot, layer, pos0, k, v, stream=None):
+        """k, v: [rows][h_kv][256] fp16 or fp32 device tensors."""
+        import torch
+        assert k.shape == v.shape and k.dtype == v.dtype and k.is_contiguous() and v.is_contiguous()
+        dt = F32 if k.dtype == torch.float32 else F16
+        return check(lib().fnkv_q8_append(self.h, slot, layer, pos0, k.shape[0], P(k.data_ptr()),
+                                          P(v.data_ptr()), dt, _stream(stream)))
+
+    def export(self, slot, layer, head, kv, tok0, n_tok, out=None, stream=None):
+        """-> uint8 device tensor [n_tok][8][34] of ggml block_q8_0."""
+        import torch
+        if out is None:
+            out = torch.empty((n_tok, 8, 34), dtype=torch.uint8, device="cuda")
+        check(lib().fnkv_export_q8_0(self.h, slot, layer, head, kv, tok0, n_tok, P(out.data_ptr()),
+                                     _stream(stream)))
+        return out
+
+    def decode_ws_bytes(self, ctx, T, hq):
+        ptr, keep = _i64_array(ctx)
+        return lib().fnkv_decode_workspace_bytes(self.h, len(ctx), ptr, T, hq)
+
+    def decode(self, slots, ctx, T, layer, q, out, ws, scale=1.0 / 16.0, stream=None):
+        """q, out: fp16 [n_seq][T][hq][256]; ws: a device tensor of at least decode_ws_bytes bytes."""
+        sp, k1 = _i32_array(slots)
+        cp, k2 = _i64_array(ctx)
+        hq = q.shape[2]
+        return check(lib().fnkv_attn_decode(self.h, len(slots), sp, cp, T, layer, hq, scale, P(q.data_ptr()),
+                                            P(out.data_ptr()), P(ws.data_ptr()), ws.numel() * ws.element_size(),
+                                            _stream(stream)))
+
+    def prefill(self, slot, layer, ctx, q, out, scale=1.0 / 16.0, stream=None):
+        """q, out: fp16 [rows][hq][256]: the chunk's queries at positions ctx - rows .. ctx - 1."""
+        rows, hq = q.shape[0], q.shape[1]
+        return check(lib().fnkv_attn_prefill(self.h, slot, layer, ctx, rows, hq, scale, P(q.data_ptr()),
+                                             P(out.data_ptr()), None, 0, _stream(stream)))

@@ -1,0 +1,141 @@
+/*
+ * fnkv — MI355X (gfx950) 8-bit paged KV cache: the page pool, the Q8_0 append and the attention that reads it.
+ *
+ * The C-ABI drop-in for the reference's KV8 path. Plain pointers and sizes only; streams are hipStream_t passed as
+ * void *. Every call that enqueues work returns FNKV_OK or an error code with NOTHING enqueued when an argument is
+ * outside the contract (the reference's rule, fn/kernels/qsa/attend.h:139-141); fnkv_last_error() then holds the
+ * message (the reference's std::string & err, fn/model/kv_pool.h:80-86). Host calls are not thread-safe with respect
+ * to one pool (the reference's engine thread owns its pool, kv_pool.h:12-15).
+ *
+ * Geometry: pages of FNKV_PAGE_TOKENS tokens; head_dim 256; Q8_0 blocks of 32 values with an fp16 scale.
+ * Query heads hq = G * h_kv (GQA group G); one launch serves G * T <= 48 query rows per KV head.
+ */
+#ifndef FNKV_H
+#define FNKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FNKV_PAGE_TOKENS 256
+#define FNKV_HEAD_DIM 256
+#define FNKV_QK 32          /* values a Q8_0 block (ggml QK8_0, ggml-common.h:258) */
+#define FNKV_MAX_SEQS 16    /* sequences a decode launch */
+#define FNKV_MAX_ROWS 48    /* G * T a KV head */
+
+enum fnkv_status {
+    FNKV_OK = 0,
+    FNKV_ERR_ARG = 1,      /* an argument outside the contract; nothing enqueued */
+    FNKV_ERR_CAPACITY = 2, /* the pool's free pages do not suffice; nothing taken */
+    FNKV_ERR_HIP = 3,      /* a HIP call failed */
+};
+
+enum fnkv_dtype { FNKV_F16 = 0, FNKV_F32 = 1 };
+
+typedef struct fnkv_pool fnkv_pool;
+
+/* the message of the calling thread's last failed call ("" when none) */
+const char * fnkv_last_error(void);
+
+/* ---- the page book, host only (fn/model/kv_pool.h:31-62) ---- */
+
+/* kv_pages::pages_for (kv_pool.h:39, kv_pool.cpp:103-108): ceil(cells / page_cells), at most n_pages, 0 for none */
+int32_t fnkv_pages_for(int64_t cells, int32_t page_cells, int32_t n_pages);
+
+/* kv_slot_view (kv_pool.h:56-60) */
+typedef struct {
+    int32_t active;    /* a request or a read on the slot: never reclaimed */
+    int32_t pages;     /* pages it holds */
+    uint64_t released; /* release order (0: never used) */
+} fnkv_slot_view;
+
+/* kv_reclaim_victim (kv_pool.h:61, kv_pool.cpp:146-158): the least recently released idle slot holding pages, never
+ * for_slot; -1 when none */
+int32_t fnkv_reclaim_victim(const fnkv_slot_view * views, int32_t n, int32_t for_slot);
+
+/* ---- the pool (fn/model/kv_pool.h:63-138) ---- */
+
+/* kv_pool::init (kv_pool.h:73-75): n_pages physical pages of page_tokens tokens shared by n_slots slots, each slot's
+ * logical range slot_tokens (0: the whole pool); every page holds `layers` layers x h_kv heads of Q8_0 K and V.
+ * Device memory on `device`: n_pages * layers * h_kv * fnkv_page_block_bytes(). page_tokens must be 256. */
+int fnkv_pool_create(int32_t n_slots, int32_t n_pages, int32_t page_tokens, int32_t layers, int32_t h_kv,
+                     int64_t slot_tokens, int32_t device, fnkv_pool ** out);
+/* kv_pool::~kv_pool (kv_pool.cpp:162-205); null is a no-op */
+void fnkv_pool_destroy(fnkv_pool * pool);
+
+/* kv_pool::ensure (kv_pool.h:80-83, kv_pool.cpp:448-501): the slot's logical prefix of at least `cells` cells (capped
+ * at the slot range) backed by pages, the new pages zeroed, the device page table updated; synchronous. One
+ * transaction: on failure the slot's pages are unchanged; *capacity (optional) is 1 when the free pages did not
+ * suffice (FNKV_ERR_CAPACITY). */
+int fnkv_pool_ensure(fnkv_pool * pool, int32_t slot, int64_t cells, int32_t * capacity);
+/* kv_pool::trim (kv_pool.h:84-86, kv_pool.cpp:503-516): the slot's pages past pages_for(keep_cells) back to the free
+ * list (keep 0: all). The caller has drained every consumer of them. */
+int fnkv_pool_trim(fnkv_pool * pool, int32_t slot, int64_t keep_cells);
+/* kv_pool::mapped_cells (kv_pool.h:90) */
+int64_t fnkv_pool_mapped_cells(const fnkv_pool * pool, int32_t slot);
+/* kv_pages::free_pages / n_pages / mapped / physical (kv_pool.h:33-38) */
+int32_t fnkv_pool_free_pages(const fnkv_pool * pool);
+int32_t fnkv_pool_n_pages(const fnkv_pool * pool);
+int32_t fnkv_pool_mapped_pages(const fnkv_pool * pool, int32_t slot);
+int32_t fnkv_pool_physical(const fnkv_pool * pool, int32_t slot, int32_t logical);
+/* the slot's page table (physical page of each mapped logical page) into out[cap]; returns the count */
+int32_t fnkv_page_table(const fnkv_pool * pool, int32_t slot, int32_t * out, int32_t cap);
+/* kv_pool::ledger (kv_pool.h:96-97, kv_pool.cpp:544-570): the startup lines, '\n'-separated, into buf[cap] */
+int32_t fnkv_pool_ledger(const fnkv_pool * pool, char * buf, int32_t cap);
+/* kv_pool::test_fail_map (kv_pool.h:98-103): TEST ONLY — the next ensure fails after readying `after` of its new pages
+ * (a mid-transaction failure); -1: off */
+void fnkv_pool_test_fail(fnkv_pool * pool, int32_t after);
+/* bytes of one (page, layer, head) block: 256 tokens of K and V codes and scales */
+int64_t fnkv_page_block_bytes(void);
+/* the pool's device allocation and its size */
+void * fnkv_pool_device_base(const fnkv_pool * pool);
+int64_t fnkv_pool_device_bytes(const fnkv_pool * pool);
+
+/* ---- the append (fn/kernels/qsa/qsa_prompt.h:90-104 qsp_kv, attend.cu:218-260 prepare) ---- */
+
+/* Quantizes rows new K and V rows (k, v: [rows][h_kv][256] of dtype, device) into Q8_0 by ggml's
+ * quantize_row_q8_0_ref rule (ggml-quants.c:274-297) and writes them at the slot's positions pos0 .. pos0 + rows - 1
+ * of `layer` through the page table (cell pos: logical page pos / 256, offset pos % 256). The positions must be
+ * mapped (fnkv_pool_ensure). */
+int fnkv_q8_append(fnkv_pool * pool, int32_t slot, int32_t layer, int64_t pos0, int32_t rows, const void * k,
+                   const void * v, int32_t dtype, void * stream);
+
+/* Reads the slot's cells tok0 .. tok0 + n_tok - 1 of (layer, head, kv: 0 K, 1 V) back as ggml block_q8_0 (34 B a
+ * block, 8 blocks a cell) into out (device, n_tok * 272 bytes): the interchange form of the stored codes. */
+int fnkv_export_q8_0(const fnkv_pool * pool, int32_t slot, int32_t layer, int32_t head, int32_t kv, int64_t tok0,
+                     int32_t n_tok, void * out, void * stream);
+
+/* ---- decode / speculative verify attention (fn/kernels/qsa/attend.h:97-151 attend, attend_lanes) ---- */
+
+/* The workspace a decode launch over these sequences needs (bytes; device memory the caller allocates; no zeroing
+ * needed). ctx[n_seq] as for fnkv_attn_decode. */
+int64_t fnkv_decode_workspace_bytes(const fnkv_pool * pool, int32_t n_seq, const int64_t * ctx, int32_t T, int32_t hq);
+
+/* Dense causal attention of T query tokens of each of n_seq sequences over their pooled Q8_0 K/V of `layer`.
+ * slots[n_seq], ctx[n_seq] host arrays: sequence i lives in slot slots[i] and holds ctx[i] cells (its T new ones
+ * included, already appended); query t of it sits at position ctx[i] - T + t and sees cells 0 .. ctx[i] - T + t.
+ * q: fp16 [n_seq][T][hq][256], out: fp16 [n_seq][T][hq][256] (device). Scores q.k * scale (the reference: 1/16),
+ * softmax and accumulation in fp32, split-K over pages merged by log-sum-exp. hq = G * h_kv with G * T <= 48. */
+int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx, int32_t T,
+                     int32_t layer, int32_t hq, float scale, const void * q, void * out, void * ws, int64_t ws_bytes,
+                     void * stream);
+
+/* ---- chunked-prefill attention (fn/kernels/qsa/qsa_prompt.h:106-124 qsp_attend) ---- */
+
+int64_t fnkv_prefill_workspace_bytes(const fnkv_pool * pool, int64_t ctx, int32_t rows, int32_t hq);
+
+/* Causal attention of `rows` query tokens (positions ctx - rows .. ctx - 1 of the slot, already appended) over the
+ * slot's cells 0 .. ctx - 1 of `layer`, on the matrix cores: K and V dequantized to fp16 (code x scale, rounded once,
+ * as the reference's prompt attention does, qsa_prompt.h:55-58), QK^T and PV in fp16 with fp32 accumulation.
+ * q: fp16 [rows][hq][256], out: fp16 [rows][hq][256]. */
+int fnkv_attn_prefill(const fnkv_pool * pool, int32_t slot, int32_t layer, int64_t ctx, int32_t rows, int32_t hq,
+                      float scale, const void * q, void * out, void * ws, int64_t ws_bytes, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FNKV_H */

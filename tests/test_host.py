@@ -1,0 +1,50 @@
+"""Host-side checks of the C-ABI library, CPU only: it loads, exports every entry point include/fnkv.h declares,
+and its pure host logic (the page rounding and the reclaim choice) gives the reference's known answers
+(fn/runtime/slots_test.cpp:26-84). No GPU call is made here."""
+import os
+import re
+
+import fnkv
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    src = open(os.path.join(ROOT, "include", "fnkv.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(fnkv_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = fnkv.lib()
+    names = declared()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(L, n)]
+    assert missing == []
+    assert sorted(fnkv.EXPORTS) == names
+
+
+def test_pages_for_known_answers():
+    pc, n = 16384, 16
+    assert [fnkv.pages_for(c, pc, n) for c in (0, 1, pc, pc + 1, 262144, 262144 + 5)] == [0, 1, 1, 2, 16, 16]
+    assert fnkv.pages_for(32768 + 128 + 69, pc, n) == 3
+    assert fnkv.pages_for(131072 + 32 + 69, pc, n) == 9
+    assert fnkv.pages_for(-5, pc, n) == 0 and fnkv.pages_for(5, 0, n) == 0
+    assert fnkv.pages_for(262144, 256, 1 << 20) == 1024
+
+
+def test_reclaim_victim_known_answers():
+    v = [[False, 3, 7], [False, 2, 4], [True, 5, 1], [False, 0, 2]]
+    a = fnkv.reclaim_victim(v, 0)
+    b = fnkv.reclaim_victim(v, 1)
+    v[1][0] = True
+    c = fnkv.reclaim_victim(v, 0)
+    v[0][2] = 0
+    d = fnkv.reclaim_victim(v, 3)
+    assert (a, b, c, d) == (1, 0, -1, 0)
+    # ties on the release order go to the lower slot (strict <)
+    assert fnkv.reclaim_victim([[False, 1, 5], [False, 1, 5]], -1) == 0
+
+
+def test_page_block_bytes():
+    assert fnkv.lib().fnkv_page_block_bytes() == 8 * 17408

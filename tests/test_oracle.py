@@ -1,0 +1,199 @@
+"""The CPU oracle, pinned (CPU only).
+
+What pins each oracle function (oracle/fnkv_oracle.c):
+  or_f32_to_f16        the reference's ggml_compute_fp32_to_fp16 on 40,000 seeded bit patterns + edges (golden), and
+                       numpy's independent fp16 rounding on every non-NaN input
+  or_f16_to_f32        the reference's ggml_compute_fp16_to_fp32 on all 65,536 halves (golden), and numpy's widening
+  or_q8_0_quantize     quantize_row_q8_0_ref outputs (golden: stress rows, every finite fp16 value, exact ties, seeded
+                       BASELINE rows), plus closed forms (|code| <= 127, the amax element at +-127, a zero block)
+  or_q8_0_dequantize   dequantize_row_q8_0 outputs (golden)
+  or_kv8_quantize      FNFL's kv_q8_quantize outputs (golden)
+  or_pages_*           the reference's own known answers, fn/runtime/slots_test.cpp:26-84, 1:1
+  or_reclaim_victim    the same file's reclaim answers
+  or_attn_f64          closed forms (one visible key returns its V row; q = 0 returns the visible rows' mean; equal
+                       keys give the mean), brute force by numpy on tiny inputs, and key-order invariance
+  or_attn_ggml         the fp64 form within 2e-3 (fp32 Q) on a seeded BASELINE-shaped case
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+
+
+def test_f32_to_f16_matches_ggml(golden):
+    g = golden("f16_golden.npz")
+    got = O.f32_to_f16(g["f32"])
+    assert np.array_equal(got, g["f16"])
+    x = g["f32"]
+    ok = ~np.isnan(x)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(got[ok], x[ok].astype(np.float16).view(np.uint16))
+
+
+def test_f16_to_f32_matches_ggml(golden):
+    g = golden("f16_golden.npz")
+    h = np.arange(65536, dtype=np.uint16)
+    got = O.f16_to_f32(h).view(np.uint32)
+    assert np.array_equal(got, g["halves_f32_bits"])
+    w = h.view(np.float16).astype(np.float32)
+    ok = ~np.isnan(w)
+    assert np.array_equal(got[ok], w[ok].view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["stress", "allf16", "ties", "rows"])
+def test_q8_0_matches_reference(golden, name):
+    g = golden("q8_0_golden.npz")
+    x = g[f"{name}_x"]
+    qs, d = O.q8_0_quantize(x)
+    assert np.array_equal(qs, g[f"{name}_qs"])
+    assert np.array_equal(d, g[f"{name}_d"])
+    y = O.q8_0_dequantize(qs, d)
+    assert np.array_equal(y.view(np.uint32), g[f"{name}_y"].view(np.uint32))
+
+
+def test_q8_0_closed_forms():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((512, 32)) * rng.uniform(0.01, 100, (512, 1))).astype(np.float16).astype(np.float32)
+    x[5] = 0.0
+    qs, d = O.q8_0_quantize(x)
+    assert np.abs(qs.astype(np.int32)).max() <= 127
+    am = np.argmax(np.abs(x), axis=1)
+    peak = qs[np.arange(512), am]
+    nz = np.abs(x).max(axis=1) > 0
+    assert np.all(np.abs(peak[nz]) == 127)
+    assert np.all(np.sign(peak[nz]) == np.sign(x[np.arange(512), am][nz]))
+    assert np.all(qs[5] == 0) and d[5] == 0
+    # d is fp16(amax / 127)
+    amax = np.abs(x).max(axis=1)
+    assert np.array_equal(d.reshape(-1), O.f32_to_f16((amax / np.float32(127.0)).astype(np.float32)))
+
+
+def test_q8_0_ties_round_away_from_zero(golden):
+    g = golden("q8_0_golden.npz")
+    x, qs = g["ties_x"][:64], g["ties_qs"][:64]  # amax 127: d = 1, x = k + 0.5 exactly
+    want = (np.sign(x) * np.floor(np.abs(x) + 0.5)).astype(np.int8)
+    assert np.array_equal(qs, want)
+    assert np.array_equal(O.q8_0_quantize(x)[0], want)
+
+
+@pytest.mark.parametrize("name", ["stress", "rows"])
+def test_kv8_rule_matches_reference(golden, name):
+    g = golden("kv8_golden.npz")
+    c, s = O.kv8_quantize(g[f"{name}_x"])
+    assert np.array_equal(c, g[f"{name}_codes"])
+    assert np.array_equal(s, g[f"{name}_scales"])
+
+
+def test_pages_known_answers():
+    # fn/runtime/slots_test.cpp:26-84, with its page of 16,384 cells and 262,144 cells (16 pages)
+    pc, n = 16384, 16
+    pf = O.Pages.pages_for
+    assert pf(0, pc, n) == 0 and pf(1, pc, n) == 1 and pf(pc, pc, n) == 1 and pf(pc + 1, pc, n) == 2
+    assert pf(262144, pc, n) == 16 and pf(262144 + 5, pc, n) == 16
+    r5, r4 = pf(32768 + 128 + 69, pc, n), pf(131072 + 32 + 69, pc, n)
+    assert r5 == 3 and 4 * r5 <= n and r4 == 9 and 2 * r4 > n
+    p = O.Pages(4, n)
+    ok, t = p.take(0, 9)
+    assert ok and len(t) == 9 and t[0] == 0 and p.free_pages() == 7
+    ok, t = p.take(1, 9)
+    assert not ok and t == [] and p.mapped(1) == 0 and p.free_pages() == 7
+    ok, t = p.take(1, 7)
+    assert ok and t[0] == 9 and p.free_pages() == 0
+    ok, _ = p.take(2, 1)
+    assert not ok
+    out = p.give(0, 3)
+    assert len(out) == 6 and out[0] == 8 and p.mapped(0) == 3 and p.free_pages() == 6
+    ok, t = p.take(2, 2)
+    assert ok and t == [3, 4] and p.physical(2, 1) == 4
+    p.give(0, 0)
+    p.give(1, 0)
+    p.give(2, 0)
+    ok, _ = p.take(3, n)
+    assert ok and p.free_pages() == 0 and p.mapped(3) == n and p.physical(3, n - 1) == n - 1
+    ok, _ = p.take(3, n + 1)
+    assert not ok and p.mapped(3) == n
+
+
+def test_reclaim_known_answers():
+    v = [[False, 3, 7], [False, 2, 4], [True, 5, 1], [False, 0, 2]]
+    a = O.reclaim_victim(v, 0)
+    b = O.reclaim_victim(v, 1)
+    v[1][0] = True
+    c = O.reclaim_victim(v, 0)
+    v[0][2] = 0
+    d = O.reclaim_victim(v, 3)
+    assert (a, b, c, d) == (1, 0, -1, 0)
+
+
+def _rand_case(rng, n_ctx, T, hq=4, hkv=2, d=64):
+    q16 = (rng.standard_normal((T, hq, d))).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((n_ctx, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((n_ctx, hkv, d)).astype(np.float32)
+    return q16, k, v
+
+
+def test_attn_f64_closed_forms():
+    rng = np.random.default_rng(11)
+    q16, k, v = _rand_case(rng, 9, 1)
+    # one visible key: the query at position 0 of a 1-cell context returns that cell's V row
+    out = O.attn_f64(q16, k, v, 1)
+    for h in range(4):
+        assert np.array_equal(out[0, h], v[0, h // 2].astype(np.float64))
+    # q = 0: the mean of the visible V rows
+    z = np.zeros_like(q16)
+    out = O.attn_f64(z, k, v, 9)
+    for h in range(4):
+        assert np.allclose(out[0, h], v[:9, h // 2].astype(np.float64).mean(axis=0), rtol=0, atol=1e-12)
+    # equal keys: the mean whatever q is
+    ke = np.repeat(k[:1], 9, axis=0)
+    out = O.attn_f64(q16, ke, v, 9)
+    assert np.allclose(out[0, 0], v[:9, 0].astype(np.float64).mean(axis=0), atol=1e-12)
+
+
+def test_attn_f64_brute_force_and_causality():
+    rng = np.random.default_rng(12)
+    n, T, hq, hkv, d = 23, 3, 4, 2, 64
+    q16, k, v = _rand_case(rng, n, T, hq, hkv, d)
+    out = O.attn_f64(q16, k, v, n, scale=0.125)
+    q = q16.view(np.float16).astype(np.float64)
+    for t in range(T):
+        last = n - T + t
+        for h in range(hq):
+            s = (k[: last + 1, h // 2].astype(np.float64) @ q[t, h]) * 0.125
+            p = np.exp(s - s.max())
+            ref = (p[:, None] * v[: last + 1, h // 2]).sum(0) / p.sum()
+            assert np.allclose(out[t, h], ref, rtol=1e-12, atol=1e-12)
+    # rows subset gives the same rows
+    sub = O.attn_f64(q16, k, v, n, scale=0.125, rows=[2, 0])
+    assert np.array_equal(sub[0], out[2]) and np.array_equal(sub[1], out[0])
+
+
+def test_attn_f64_key_order_invariance():
+    rng = np.random.default_rng(13)
+    n = 40
+    q16, k, v = _rand_case(rng, n, 1)
+    perm = rng.permutation(n - 1)
+    kp = np.concatenate([k[perm], k[n - 1:]])
+    vp = np.concatenate([v[perm], v[n - 1:]])
+    a = O.attn_f64(q16, k, v, n)
+    b = O.attn_f64(q16, kp, vp, n)
+    assert np.allclose(a, b, rtol=1e-12, atol=1e-13)
+
+
+def test_attn_ggml_path_within_tolerance():
+    rng = np.random.default_rng(14)
+    n, T, hq, hkv, d = 700, 3, 16, 2, 256
+    x = rng.standard_normal((2, n, hkv, d)).astype(np.float32)
+    x[:, :, :, rng.choice(d, 4, replace=False)] *= 8
+    x = x.astype(np.float16).astype(np.float32)
+    kq, kd = O.q8_0_quantize(x[0])
+    vq, vd = O.q8_0_quantize(x[1])
+    kb = O.to_block_q8_0(kq, kd).reshape(n, hkv, 8, 34)
+    vb = O.to_block_q8_0(vq, vd).reshape(n, hkv, 8, 34)
+    q16 = rng.standard_normal((T, hq, d)).astype(np.float16).view(np.uint16)
+    ref = O.attn_f64(q16, O.q8_0_dequantize(kq, kd), O.q8_0_dequantize(vq, vd), n)
+    got = O.attn_ggml(q16, kb, vb, n, threads=4).view(np.float16).astype(np.float64)
+    assert np.abs(got - ref).max() <= 2e-3
+    got8 = O.attn_ggml(q16, kb, vb, n, q_as_q8=True, threads=4).view(np.float16).astype(np.float64)
+    # Q itself quantized to Q8_0 (ggml's vec_dot operand): a documented divergence of ~2.6e-2 here, bounded loosely
+    assert np.abs(got8 - ref).max() <= 5e-2
