@@ -1,37 +1,18 @@
 // The Q8_0 append (new K/V rows quantized into the pool) and the export back to ggml's block_q8_0.
 //
-// Quantization rule, bit for bit ggml's quantize_row_q8_0_ref (ggml/src/ggml-quants.c:274-297) on the fp32 value of
-// each input: per block of 32, amax = max |x|; d = amax / 127 (IEEE division); id = d != 0 ? 1 / d : 0 (IEEE
-// division); code = roundf(x * id) (IEEE product, ties away from zero); the stored scale is fp16(d), round to nearest
-// even (ggml-impl.h:414-438). The reference's device writers of its own KV8 format (fn/kernels/qsa/kv_q8.cuh:244-267,
-// qsa_prompt_attn.cu:90-122) use one warp a row; here one wave64 quantizes one 256-value row, 4 values a lane, the
-// 8 lanes of a block reducing amax with cross-lane max.
+// The quantization rule is q8_0.h's (ggml's quantize_row_q8_0_ref, bit for bit). The reference's device writers of its
+// own KV8 format (fn/kernels/qsa/kv_q8.cuh:244-267, qsa_prompt_attn.cu:90-122) use one warp a row; here one wave64
+// quantizes one 256-value row. This entry point serves chunked prefill and any caller appending outside a decode
+// launch; fnkv_attn_decode appends a step's new rows itself.
 #include "../../include/fnkv.h"
 #include "common.h"
 #include "layout.h"
+#include "q8_0.h"
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
 namespace fnkv {
-
-// The quantizer's arithmetic must round at every step as the reference's does (amax / 127, 1 / d, x * id, then
-// roundf): no contraction of x * id into the fraction test below. This file is also compiled with -ffp-contract=off.
-#pragma clang fp contract(off)
-
-// roundf: round half away from zero, exact (x - trunc(x) is exact in fp32)
-__device__ __forceinline__ float round_half_away(float x) {
-    const float t = __builtin_truncf(x);
-    const float f = x - t;
-    return __builtin_fabsf(f) >= 0.5f ? t + __builtin_copysignf(1.0f, x) : t;
-}
-
-__device__ __forceinline__ uint8_t * tile_of(const pool_view & pv, int32_t slot, int32_t layer, int32_t head,
-                                             int64_t pos) {
-    const int32_t phys = pv.table[int64_t(slot) * pv.table_stride + (pos >> 8)];
-    return pv.base + int64_t(layer) * pv.layer_stride + int64_t(phys) * pv.page_stride + int64_t(head) * kPageBlock +
-           int64_t((pos & 255) >> 5) * kTileBytes;
-}
 
 template <bool F32>
 __global__ __launch_bounds__(256) void append_kernel(pool_view pv, int32_t slot, int32_t layer, int64_t pos0,
@@ -46,58 +27,16 @@ __global__ __launch_bounds__(256) void append_kernel(pool_view pv, int32_t slot,
     if (row >= rows) {
         return;
     }
-    const int64_t src = (row * pv.h_kv + head) * kHeadDim + 4 * lane;
+    const int64_t src = (row * pv.h_kv + head) * kHeadDim;
     float x[4];
     if (F32) {
-        const float4 f = *reinterpret_cast<const float4 *>(static_cast<const float *>(kv ? vin : kin) + src);
-        x[0] = f.x;
-        x[1] = f.y;
-        x[2] = f.z;
-        x[3] = f.w;
+        load4<true>(static_cast<const float *>(kv ? vin : kin) + src, lane, x);
     } else {
-        const uint2 u = *reinterpret_cast<const uint2 *>(static_cast<const __half *>(kv ? vin : kin) + src);
-        x[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(u.x & 0xffffu)));
-        x[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(u.x >> 16)));
-        x[2] = __half2float(__ushort_as_half(static_cast<unsigned short>(u.y & 0xffffu)));
-        x[3] = __half2float(__ushort_as_half(static_cast<unsigned short>(u.y >> 16)));
-    }
-    float amax = fmaxf(fmaxf(__builtin_fabsf(x[0]), __builtin_fabsf(x[1])),
-                       fmaxf(__builtin_fabsf(x[2]), __builtin_fabsf(x[3])));
-    // the 8 lanes of a block: lanes 8 b .. 8 b + 7
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    amax = fmaxf(amax, __shfl_xor(amax, 4));
-    const float d = __fdiv_rn(amax, 127.0f);
-    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-    uint32_t packed = 0;
-    uint8_t bytes[4];
-#pragma unroll
-    for (int32_t e = 0; e < 4; ++e) {
-        const float r = round_half_away(__fmul_rn(x[e], id));
-        // an in-contract input gives |r| <= 127; outside it (an fp32 input whose d underflows to a subnormal, so id
-        // is inf) the reference's int8 store of roundf keeps the low byte of x86's 0x80000000 result: code 0
-        const int32_t c = __builtin_fabsf(r) < 2147483648.0f ? static_cast<int32_t>(r) : INT32_MIN;
-        bytes[e] = static_cast<uint8_t>((c & 0xff) ^ 0x80); // excess-128 storage
-        packed |= uint32_t(bytes[e]) << (8 * e);
+        load4<false>(static_cast<const uint16_t *>(kv ? vin : kin) + src, lane, x);
     }
     const int64_t pos = pos0 + row;
-    uint8_t * t = tile_of(pv, slot, layer, head, pos);
-    const int32_t tt = static_cast<int32_t>(pos & 31);
-    const int32_t d0 = 4 * lane, b = lane >> 3;
-    if (kv == 0) {
-        *reinterpret_cast<uint32_t *>(t + k_code_off(tt, d0)) = packed;
-        if ((lane & 7) == 0) {
-            *reinterpret_cast<uint16_t *>(t + k_scale_off(tt, b)) = __half_as_ushort(__float2half_rn(d));
-        }
-    } else {
-#pragma unroll
-        for (int32_t e = 0; e < 4; ++e) {
-            t[v_code_off(tt, d0 + e)] = bytes[e];
-        }
-        if ((lane & 7) == 0) {
-            *reinterpret_cast<uint16_t *>(t + v_scale_off(tt, b)) = __half_as_ushort(__float2half_rn(d));
-        }
-    }
+    uint8_t * t = tile_of(pv, pv.table + int64_t(slot) * pv.table_stride, layer, head, pos);
+    quantize_store(x, lane, t, static_cast<int32_t>(pos & 31), kv);
 }
 
 // one wave a cell: its 8 blocks of (layer, head, kv) as 8 x 34 bytes of block_q8_0
@@ -109,7 +48,7 @@ __global__ __launch_bounds__(256) void export_kernel(pool_view pv, int32_t slot,
         return;
     }
     const int64_t pos = tok0 + i;
-    const uint8_t * t = tile_of(pv, slot, layer, head, pos);
+    const uint8_t * t = tile_of(pv, pv.table + int64_t(slot) * pv.table_stride, layer, head, pos);
     const int32_t tt = static_cast<int32_t>(pos & 31);
     const int32_t d0 = 4 * lane, b = lane >> 3;
     uint8_t * o = out + i * (kBlocks * 34) + b * 34;

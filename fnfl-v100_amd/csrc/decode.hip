@@ -25,6 +25,7 @@
 #include "common.h"
 #include "layout.h"
 #include "mfma.h"
+#include "q8_0.h"
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -41,6 +42,9 @@ constexpr float kNegInf = -__builtin_inff();
 struct dec_args {
     pool_view pv;
     const uint16_t * q; // fp16 [n_seq][T][hq][256]
+    const void * k_new; // optional [n_seq][T][h_kv][256] fp16 / fp32: the step's new cells, appended by the launch
+    const void * v_new;
+    int32_t new_f32;
     float * po;         // [total_splits][h_kv][R][256] partial accumulators
     float * pml;        // [total_splits][h_kv][R][2] partial (m, l), base-2 domain
     float c2;           // scale * log2(e)
@@ -82,6 +86,33 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(dec_args a) {
     const int64_t end = ctx < begin + a.split_tokens ? ctx : begin + a.split_tokens;
     const int32_t n_tiles = static_cast<int32_t>((end - begin + kTileTokens - 1) / kTileTokens);
 
+    const pool_view & pv = a.pv;
+    const int32_t * table = pv.table + int64_t(a.slot[s]) * pv.table_stride;
+
+    // the step's new cells ctx - T .. ctx - 1 that fall in this split: quantized and written here (each position lies
+    // in exactly one split, so one workgroup writes it), then made visible to this workgroup's own reads
+    if (a.k_new != nullptr) {
+        const int64_t first_new = ctx - a.T;
+        const int64_t p0 = begin > first_new ? begin : first_new;
+        const int32_t nrow = static_cast<int32_t>(end - p0);
+        if (nrow > 0) {
+            for (int32_t job = wave; job < 2 * nrow; job += kWaves) {
+                const int64_t pos = p0 + (job >> 1);
+                const int32_t kv = job & 1;
+                const int64_t src = ((int64_t(s) * a.T + (pos - first_new)) * pv.h_kv + kvh) * kHeadDim;
+                float x[4];
+                if (a.new_f32) {
+                    load4<true>(static_cast<const float *>(kv ? a.v_new : a.k_new) + src, lane, x);
+                } else {
+                    load4<false>(static_cast<const uint16_t *>(kv ? a.v_new : a.k_new) + src, lane, x);
+                }
+                quantize_store(x, lane, tile_of(pv, table, a.layer, kvh, pos), static_cast<int32_t>(pos & 31), kv);
+            }
+            __threadfence();
+            __syncthreads();
+        }
+    }
+
     // this lane's query rows (one per row tile: row nt * 16 + j) and causal limits; the Q operands go to LDS once
     // (B operand layout: [nt][block][lane] 16 B) and are read back per use, keeping them out of the registers
     uint8_t * qlds = smem + kWaves * 2 * kTileBytes;
@@ -119,8 +150,6 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(dec_args a) {
     }
 
     uint8_t * wbuf = smem + wave * 2 * kTileBytes;
-    const pool_view & pv = a.pv;
-    const int32_t * table = pv.table + int64_t(a.slot[s]) * pv.table_stride;
     const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
     auto tile_ptr = [&](int32_t ti) -> const uint8_t * {
         const int64_t tok = begin + int64_t(ti) * kTileTokens;
@@ -459,12 +488,13 @@ int64_t fnkv_decode_workspace_bytes(const fnkv_pool * pool, int32_t n_seq, const
 }
 
 int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx, int32_t T,
-                     int32_t layer, int32_t hq, float scale, const void * q, void * out, void * ws, int64_t ws_bytes,
-                     void * stream) {
+                     int32_t layer, int32_t hq, float scale, const void * q, const void * k_new, const void * v_new,
+                     int32_t new_dtype, void * out, void * ws, int64_t ws_bytes, void * stream) {
     const fnkv::kv_pool * p = fnkv::pool_of(pool);
     if (p == nullptr || n_seq <= 0 || n_seq > FNKV_MAX_SEQS || slots == nullptr || ctx == nullptr || T <= 0 ||
         layer < 0 || layer >= p->layers() || hq <= 0 || hq % p->h_kv() != 0 || q == nullptr || out == nullptr ||
-        ws == nullptr || !(scale > 0.0f) || !std::isfinite(scale)) {
+        ws == nullptr || !(scale > 0.0f) || !std::isfinite(scale) || ((k_new == nullptr) != (v_new == nullptr)) ||
+        (new_dtype != FNKV_F16 && new_dtype != FNKV_F32)) {
         set_error("fnkv_attn_decode: argument outside the contract");
         return FNKV_ERR_ARG;
     }
@@ -494,6 +524,9 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
     fnkv::dec_args a;
     a.pv = p->view();
     a.q = static_cast<const uint16_t *>(q);
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.new_f32 = new_dtype == FNKV_F32 ? 1 : 0;
     a.po = static_cast<float *>(ws);
     a.pml = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + pl.po_bytes);
     a.c2 = scale * 1.4426950408889634f;

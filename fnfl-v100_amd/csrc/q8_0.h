@@ -1,0 +1,91 @@
+// The Q8_0 quantizer of one 256-value row by one wave64, shared by the append kernel and the decode kernel's fused
+// append. Rule, bit for bit ggml's quantize_row_q8_0_ref (ggml/src/ggml-quants.c:274-297) on the fp32 value of each
+// input: per block of 32, amax = max |x|; d = amax / 127 (IEEE division); id = d != 0 ? 1 / d : 0 (IEEE division);
+// code = roundf(x * id) (IEEE product, ties away from zero); the stored scale is fp16(d), round to nearest even
+// (ggml-impl.h:414-438). Lane l holds values 4 l .. 4 l + 3; the 8 lanes of a block reduce amax with cross-lane max.
+#pragma once
+
+#include "layout.h"
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace fnkv {
+
+// roundf: round half away from zero, exact (x - trunc(x) is exact in fp32)
+__device__ __forceinline__ float round_half_away(float x) {
+#pragma clang fp contract(off)
+    const float t = __builtin_truncf(x);
+    const float f = x - t;
+    return __builtin_fabsf(f) >= 0.5f ? t + __builtin_copysignf(1.0f, x) : t;
+}
+
+// the 32-token tile of pool position pos, for (layer, head), through the slot's page table row
+__device__ __forceinline__ uint8_t * tile_of(const pool_view & pv, const int32_t * table_row, int32_t layer,
+                                             int32_t head, int64_t pos) {
+    const int32_t phys = table_row[pos >> 8];
+    return pv.base + int64_t(layer) * pv.layer_stride + int64_t(phys) * pv.page_stride + int64_t(head) * kPageBlock +
+           int64_t((pos & 255) >> 5) * kTileBytes;
+}
+
+// load this lane's 4 values of a 256-value row (fp16 or fp32) as fp32
+template <bool F32> __device__ __forceinline__ void load4(const void * row, int32_t lane, float (&x)[4]) {
+    if (F32) {
+        const float4 f = *reinterpret_cast<const float4 *>(static_cast<const float *>(row) + 4 * lane);
+        x[0] = f.x;
+        x[1] = f.y;
+        x[2] = f.z;
+        x[3] = f.w;
+    } else {
+        const uint2 u = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(row) + 4 * lane);
+        x[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(u.x & 0xffffu)));
+        x[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(u.x >> 16)));
+        x[2] = __half2float(__ushort_as_half(static_cast<unsigned short>(u.y & 0xffffu)));
+        x[3] = __half2float(__ushort_as_half(static_cast<unsigned short>(u.y >> 16)));
+    }
+}
+
+// quantize this wave's row (x: the lane's 4 values) and store it as cell tt of `tile` (kv: 0 K, 1 V)
+__device__ __forceinline__ void quantize_store(const float (&x)[4], int32_t lane, uint8_t * tile, int32_t tt,
+                                               int32_t kv) {
+#pragma clang fp contract(off)
+    float amax = fmaxf(fmaxf(__builtin_fabsf(x[0]), __builtin_fabsf(x[1])),
+                       fmaxf(__builtin_fabsf(x[2]), __builtin_fabsf(x[3])));
+    // the 8 lanes of a block: lanes 8 b .. 8 b + 7
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    uint32_t packed = 0;
+    uint8_t bytes[4];
+#pragma unroll
+    for (int32_t e = 0; e < 4; ++e) {
+        const float r = round_half_away(x[e] * id);
+        // an in-contract input gives |r| <= 127; outside it (an fp32 input whose d underflows to a subnormal, so id
+        // is inf) the reference's int8 store of roundf keeps the low byte of x86's 0x80000000 result: code 0
+        const int32_t c = __builtin_fabsf(r) < 2147483648.0f ? static_cast<int32_t>(r) : INT32_MIN;
+        bytes[e] = static_cast<uint8_t>((c & 0xff) ^ 0x80); // excess-128 storage
+        packed |= uint32_t(bytes[e]) << (8 * e);
+    }
+    const int32_t d0 = 4 * lane, b = lane >> 3;
+    const uint16_t dh = __half_as_ushort(__float2half_rn(d));
+    if (kv == 0) {
+        *reinterpret_cast<uint32_t *>(tile + k_code_off(tt, d0)) = packed;
+        if ((lane & 7) == 0) {
+            *reinterpret_cast<uint16_t *>(tile + k_scale_off(tt, b)) = dh;
+        }
+    } else {
+#pragma unroll
+        for (int32_t e = 0; e < 4; ++e) {
+            tile[v_code_off(tt, d0 + e)] = bytes[e];
+        }
+        if ((lane & 7) == 0) {
+            *reinterpret_cast<uint16_t *>(tile + v_scale_off(tt, b)) = dh;
+        }
+    }
+}
+
+} // namespace fnkv

@@ -84,7 +84,7 @@ def lib():
         L.fnkv_decode_workspace_bytes.restype = I64
         L.fnkv_decode_workspace_bytes.argtypes = [P, I32, P, I32, I32]
         L.fnkv_attn_decode.restype = ctypes.c_int
-        L.fnkv_attn_decode.argtypes = [P, I32, P, P, I32, I32, I32, ctypes.c_float, P, P, P, I64, P]
+        L.fnkv_attn_decode.argtypes = [P, I32, P, P, I32, I32, I32, ctypes.c_float, P, P, P, I32, P, P, I64, P]
         L.fnkv_prefill_workspace_bytes.restype = I64
         L.fnkv_prefill_workspace_bytes.argtypes = [P, I64, I32, I32]
         L.fnkv_attn_prefill.restype = ctypes.c_int
@@ -213,13 +213,18 @@ class Pool:
         ptr, keep = _i64_array(ctx)
         return lib().fnkv_decode_workspace_bytes(self.h, len(ctx), ptr, T, hq)
 
-    def decode(self, slots, ctx, T, layer, q, out, ws, scale=1.0 / 16.0, stream=None):
-        """q, out: fp16 [n_seq][T][hq][256]; ws: a device tensor of at least decode_ws_bytes bytes."""
+    def decode(self, slots, ctx, T, layer, q, out, ws, scale=1.0 / 16.0, k_new=None, v_new=None, stream=None):
+        """q, out: fp16 [n_seq][T][hq][256]; ws: a device tensor of at least decode_ws_bytes bytes; k_new, v_new
+        (optional): the step's new cells [n_seq][T][h_kv][256], appended by the launch."""
+        import torch
         sp, k1 = _i32_array(slots)
         cp, k2 = _i64_array(ctx)
         hq = q.shape[2]
-        return check(lib().fnkv_attn_decode(self.h, len(slots), sp, cp, T, layer, hq, scale, P(q.data_ptr()),
-                                            P(out.data_ptr()), P(ws.data_ptr()), ws.numel() * ws.element_size(),
+        kp = P(k_new.data_ptr()) if k_new is not None else None
+        vp = P(v_new.data_ptr()) if v_new is not None else None
+        dt = F32 if (k_new is not None and k_new.dtype == torch.float32) else F16
+        return check(lib().fnkv_attn_decode(self.h, len(slots), sp, cp, T, layer, hq, scale, P(q.data_ptr()), kp, vp,
+                                            dt, P(out.data_ptr()), P(ws.data_ptr()), ws.numel() * ws.element_size(),
                                             _stream(stream)))
 
     def prefill(self, slot, layer, ctx, q, out, scale=1.0 / 16.0, stream=None):

@@ -115,13 +115,17 @@ int fnkv_export_q8_0(const fnkv_pool * pool, int32_t slot, int32_t layer, int32_
 int64_t fnkv_decode_workspace_bytes(const fnkv_pool * pool, int32_t n_seq, const int64_t * ctx, int32_t T, int32_t hq);
 
 /* Dense causal attention of T query tokens of each of n_seq sequences over their pooled Q8_0 K/V of `layer`.
- * slots[n_seq], ctx[n_seq] host arrays: sequence i lives in slot slots[i] and holds ctx[i] cells (its T new ones
- * included, already appended); query t of it sits at position ctx[i] - T + t and sees cells 0 .. ctx[i] - T + t.
+ * slots[n_seq], ctx[n_seq] host arrays: sequence i lives in slot slots[i] and holds ctx[i] cells, its T new ones
+ * included; query t of it sits at position ctx[i] - T + t and sees cells 0 .. ctx[i] - T + t.
+ * k_new, v_new (optional, both or neither; dtype new_dtype, [n_seq][T][h_kv][256]): the step's new cells, quantized
+ * (the fnkv_q8_append rule) and written at positions ctx[i] - T .. ctx[i] - 1 by this launch before it reads them, as
+ * the reference's attend writes its rows' cells (attend.h:100-108); null: those cells were appended already.
  * q: fp16 [n_seq][T][hq][256], out: fp16 [n_seq][T][hq][256] (device). Scores q.k * scale (the reference: 1/16),
- * softmax and accumulation in fp32, split-K over pages merged by log-sum-exp. hq = G * h_kv with G * T <= 48. */
+ * softmax and accumulation in fp32, split-K over pages merged by log-sum-exp. hq = G * h_kv with G * T <= 48.
+ * Replaces fn::qsa::attn::attend / attend_lanes (fn/kernels/qsa/attend.h:141, :151) for dense Q8_0 KV. */
 int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx, int32_t T,
-                     int32_t layer, int32_t hq, float scale, const void * q, void * out, void * ws, int64_t ws_bytes,
-                     void * stream);
+                     int32_t layer, int32_t hq, float scale, const void * q, const void * k_new, const void * v_new,
+                     int32_t new_dtype, void * out, void * ws, int64_t ws_bytes, void * stream);
 
 /* ---- chunked-prefill attention (fn/kernels/qsa/qsa_prompt.h:106-124 qsp_attend) ---- */
 

@@ -226,13 +226,14 @@ def attn_f64(q16, k, v, n_ctx, scale=1.0 / 16.0, rows=None):
     return out
 
 
-def attn_ggml(q16, k_blocks, v_blocks, n_ctx, scale=1.0 / 16.0, q_as_q8=False, threads=1):
-    """ggml-semantics CPU flash attention over contiguous block_q8_0 K/V [n_ctx][hkv][d/32][34 B] -> fp16 bits."""
+def attn_ggml(q16, k_blocks, v_blocks, n_ctx, scale=1.0 / 16.0, q_as_q8=False, threads=1, hkv=2):
+    """ggml-semantics CPU flash attention over contiguous block_q8_0 K/V [cells][hkv][d/32][34 B] (at least n_ctx
+    cells) -> fp16 bits [T][hq][d]."""
     q16 = np.ascontiguousarray(q16, dtype=np.uint16)
     T, hq, d = q16.shape
     kb = np.ascontiguousarray(k_blocks, dtype=np.uint8)
     vb = np.ascontiguousarray(v_blocks, dtype=np.uint8)
-    hkv = kb.size // (n_ctx * (d // 32) * 34)
+    assert hkv > 0 and hq % hkv == 0 and kb.size >= n_ctx * hkv * (d // 32) * 34 and vb.size == kb.size
     out = np.empty((T, hq, d), np.uint16)
     lib().or_attn_ggml(_ptr(q16), _ptr(kb), _ptr(vb), n_ctx, T, hq, hkv, d, scale, 1 if q_as_q8 else 0,
                        threads, _ptr(out))

@@ -142,3 +142,40 @@ def test_refusals_enqueue_nothing():
         st.pool.decode([0], [300], 1, 0, q, out, ws[:16])  # workspace too small
     torch.cuda.synchronize()
     assert not out.any()
+
+
+def test_fused_append_matches_separate_append():
+    # the launch that appends its step's new cells (k_new / v_new) gives the same pool bytes and the same outputs,
+    # bitwise, as a separate fnkv_q8_append followed by a launch without them; contexts put the new cells across a
+    # tile edge, a page edge and a split edge
+    T = 5
+    ctxs = [1026, 4098, 300]
+    a = Setup(ctxs, seed=8, order_seed=3)
+    b = Setup(ctxs, seed=8, order_seed=3)
+    q16 = cases.queries(8, (3, T, HQ, 256))
+    kn = torch.from_numpy(cases.queries(9, (3, T, HKV, 256))).cuda()
+    vn = torch.from_numpy(cases.queries(10, (3, T, HKV, 256))).cuda()
+    q = torch.from_numpy(q16).cuda()
+    oa, ob = torch.empty_like(q), torch.empty_like(q)
+    ws = torch.empty(a.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    a.pool.decode(a.slots, ctxs, T, 0, q, oa, ws, k_new=kn, v_new=vn)
+    for i, (s, c) in enumerate(zip(b.slots, ctxs)):
+        b.pool.append(s, 0, c - T, kn[i].contiguous(), vn[i].contiguous())
+    b.pool.decode(b.slots, ctxs, T, 0, q, ob, ws)
+    torch.cuda.synchronize()
+    assert np.array_equal(oa.cpu().numpy().view(np.uint16), ob.cpu().numpy().view(np.uint16))
+    for s, c in zip(a.slots, ctxs):
+        for kv in (0, 1):
+            for h in range(HKV):
+                ea = a.pool.export(s, 0, h, kv, 0, c)
+                eb = b.pool.export(s, 0, h, kv, 0, c)
+                torch.cuda.synchronize()
+                assert torch.equal(ea, eb)
+    # and the outputs against the oracle over the cache with the new cells in place
+    for i, (s, c) in enumerate(zip(a.slots, ctxs)):
+        k16, v16 = cases.kv_rows(8 * 100 + s, c, HKV, 0)
+        k16[c - T:] = kn[i].cpu().numpy()
+        v16[c - T:] = vn[i].cpu().numpy()
+        (_, _, kf), (_, _, vf) = cases.decoded(O, k16, v16)
+        ref = O.attn_f64(q16[i].view(np.uint16), kf, vf, c)
+        assert cases.out_err(oa.cpu().numpy()[i], ref) <= TOL
