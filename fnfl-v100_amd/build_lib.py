@@ -37,7 +37,8 @@ EXTRA = {"append.hip": ["-ffp-contract=off"]}
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *COMMON, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
+    extra_env = os.environ.get("FNKV_EXTRA_FLAGS", "").split()
+    cmd = [hipcc(), *COMMON, *EXTRA.get(src, []), *extra_env, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)

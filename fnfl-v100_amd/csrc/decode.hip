@@ -36,8 +36,18 @@
 
 namespace fnkv {
 
-constexpr int32_t kWaves = 4;
 constexpr float kNegInf = -__builtin_inff();
+constexpr int32_t kCodeBytes = 16384;  // a tile's K and V codes
+constexpr int32_t kScaleBytes = 1024;  // a tile's K and V scales
+constexpr int32_t kGroupLds = kCodeBytes + 2 * kScaleBytes;
+
+// A tile group is NT waves sharing one tile stream, wave r of the group computing row tile r (query rows 16 r ..
+// 16 r + 15); a workgroup holds GR groups (8 waves for NT = 1 and 2, 6 for NT = 3: two waves a SIMD).
+template <int NT> struct dec_shape {
+    static constexpr int GR = NT == 1 ? 8 : NT == 2 ? 4 : 2;
+    static constexpr int WAVES = NT * GR;
+};
+
 
 struct dec_args {
     pool_view pv;
@@ -62,20 +72,79 @@ __device__ __forceinline__ int32_t seq_of(const dec_args & a, int32_t split) {
     return s;
 }
 
-// issue the 17 LDS loads of one tile into buf (a wave's 17,408 B)
-__device__ __forceinline__ void tile_to_lds(const uint8_t * tile, uint8_t * buf, int32_t lane) {
-#pragma unroll
-    for (int32_t i = 0; i < 16; ++i) {
-        lds_load16(tile + i * 1024 + lane * 16, buf + i * 1024);
+// A tile is 17 chunks of 1 KiB: 8 of K codes, 8 of V codes, 1 of scales. The K codes and the scale chunk stream into
+// the group's LDS slot (wave r of a group of NT issuing chunks r, r + NT, ... of those 9); every wave loads the V
+// codes straight into its registers, where they already sit in the PV operand's layout.
+
+template <int NT, int C>
+__device__ __forceinline__ void issue_chunk(const uint8_t * tile, uint8_t * kbuf, uint8_t * sslot, int32_t lane) {
+    if (C < 8) {
+        // four chunks share one base: the immediate offset moves both the global and the LDS address
+        lds_load16<(C & 3) * 1024>(tile + kKCodes + (C >> 2) * 4096 + lane * 16, kbuf + (C >> 2) * 4096);
+    } else {
+        lds_load16<0>(tile + kKScales + lane * 16, sslot);
     }
-    lds_load16(tile + 16384 + lane * 16, buf + 16384);
 }
 
 template <int NT>
-__global__ __launch_bounds__(256, 1) void decode_kernel(dec_args a) {
+__device__ __forceinline__ void issue_k(const uint8_t * tile, uint8_t * kbuf, uint8_t * sslot, int32_t r,
+                                        int32_t lane) {
+    if (NT == 1) {
+        issue_chunk<NT, 0>(tile, kbuf, sslot, lane);
+        issue_chunk<NT, 1>(tile, kbuf, sslot, lane);
+        issue_chunk<NT, 2>(tile, kbuf, sslot, lane);
+        issue_chunk<NT, 3>(tile, kbuf, sslot, lane);
+        issue_chunk<NT, 4>(tile, kbuf, sslot, lane);
+        issue_chunk<NT, 5>(tile, kbuf, sslot, lane);
+        issue_chunk<NT, 6>(tile, kbuf, sslot, lane);
+        issue_chunk<NT, 7>(tile, kbuf, sslot, lane);
+        issue_chunk<NT, 8>(tile, kbuf, sslot, lane);
+    } else {
+#pragma unroll
+        for (int32_t i = 0; i < (9 + NT - 1) / NT; ++i) {
+            const int32_t c = r + i * NT;
+            if (c < 8) {
+                lds_load16<0>(tile + kKCodes + c * 1024 + lane * 16, kbuf + c * 1024);
+            } else if (c == 8) {
+                lds_load16<0>(tile + kKScales + lane * 16, sslot);
+            }
+        }
+    }
+}
+
+// wait until only this wave's share of a tile's K copy (issued after what we wait for) may be outstanding
+template <int NT> __device__ __forceinline__ void wait_part_k(int32_t r) {
+    if (NT == 1) {
+        wait_vmcnt<9>();
+    } else if (NT == 2) {
+        if (r == 0) {
+            wait_vmcnt<5>();
+        } else {
+            wait_vmcnt<4>();
+        }
+    } else {
+        if (r == 2) {
+            wait_vmcnt<2>();
+        } else {
+            wait_vmcnt<3>();
+        }
+    }
+}
+
+template <int NT> __device__ __forceinline__ void group_sync() {
+    if (NT > 1) {
+        __syncthreads();
+    }
+}
+
+template <int NT>
+__global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(dec_args a) {
+    constexpr int GR = dec_shape<NT>::GR;
+    constexpr int WAVES = dec_shape<NT>::WAVES;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
     const int32_t wave = static_cast<int32_t>(threadIdx.x) >> 6;
+    const int32_t grp = wave / NT, rt = wave % NT; // tile group and row tile
     const int32_t j = lane & 15, qg = lane >> 4;
     const int32_t split = static_cast<int32_t>(blockIdx.x);
     const int32_t kvh = static_cast<int32_t>(blockIdx.y);
@@ -85,7 +154,6 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(dec_args a) {
     const int64_t begin = int64_t(sp) * a.split_tokens;
     const int64_t end = ctx < begin + a.split_tokens ? ctx : begin + a.split_tokens;
     const int32_t n_tiles = static_cast<int32_t>((end - begin + kTileTokens - 1) / kTileTokens);
-
     const pool_view & pv = a.pv;
     const int32_t * table = pv.table + int64_t(a.slot[s]) * pv.table_stride;
 
@@ -96,7 +164,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(dec_args a) {
         const int64_t p0 = begin > first_new ? begin : first_new;
         const int32_t nrow = static_cast<int32_t>(end - p0);
         if (nrow > 0) {
-            for (int32_t job = wave; job < 2 * nrow; job += kWaves) {
+            for (int32_t job = wave; job < 2 * nrow; job += WAVES) {
                 const int64_t pos = p0 + (job >> 1);
                 const int32_t kv = job & 1;
                 const int64_t src = ((int64_t(s) * a.T + (pos - first_new)) * pv.h_kv + kvh) * kHeadDim;
@@ -113,233 +181,292 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(dec_args a) {
         }
     }
 
-    // this lane's query rows (one per row tile: row nt * 16 + j) and causal limits; the Q operands go to LDS once
-    // (B operand layout: [nt][block][lane] 16 B) and are read back per use, keeping them out of the registers
-    uint8_t * qlds = smem + kWaves * 2 * kTileBytes;
-    int64_t lim[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const int32_t r = nt * 16 + j;
-        const bool real = r < a.R;
-        const int32_t t = real ? r / a.G : a.T - 1;
-        lim[nt] = ctx - a.T + t;
+    // this wave's query rows (row tile rt: row 16 rt + j) and causal limits; the Q operands go to LDS once (B operand
+    // layout: [row tile][block][lane] 16 B, after the groups' tile buffers) and are read back per use
+    const int32_t row = rt * 16 + j;
+    const bool real_row = row < a.R;
+    const int32_t t_row = real_row ? row / a.G : a.T - 1;
+    const int64_t lim = ctx - a.T + t_row;
+
+    // Q operands (B of S^T = K Q^T: lane (row j, group qg) holds q[row][32 b + 8 qg .. + 7]) in registers, and the
+    // bias operand: K codes enter the MFMA as 1152 + code, so S^T carries 1152 * sum_b s_k[t][b] * sigma_b[row] with
+    // sigma_b the block's sum of q; one MFMA a half computes that sum from the K scales (A: s_k twice) and
+    // sigma_b as hi + lo fp16 (B), and one FMA a score takes it back out.
+    half8 qop[kBlocks];
+    half8 sig; // lane (row j, qg): qg 0: sigma_hi[0..7][row], qg 1: sigma_lo[0..7][row], else 0
+    {
         const uint16_t * qrow =
-            a.q + ((int64_t(s) * a.T + t) * a.hq + int64_t(kvh) * a.G + (real ? r % a.G : 0)) * kHeadDim;
+            a.q + ((int64_t(s) * a.T + t_row) * a.hq + int64_t(kvh) * a.G + (real_row ? row % a.G : 0)) * kHeadDim;
+        float sigma[kBlocks];
 #pragma unroll
-        for (int bb = 0; bb < 2; ++bb) {
-            const int b = 2 * wave + bb;
+        for (int b = 0; b < kBlocks; ++b) {
             u32x4 v = {0, 0, 0, 0};
-            if (real) {
+            if (real_row) {
                 v = *reinterpret_cast<const u32x4 *>(qrow + b * kQK + 8 * qg);
             }
-            *reinterpret_cast<u32x4 *>(qlds + ((nt * kBlocks + b) * 64 + lane) * 16) = v;
+            qop[b] = __builtin_bit_cast(half8, v);
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                sum += static_cast<float>(qop[b][i]);
+            }
+            sum += __shfl_xor(sum, 16);
+            sum += __shfl_xor(sum, 32);
+            sigma[b] = sum;
+        }
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) {
+            const _Float16 hi = static_cast<_Float16>(sigma[b]);
+            const _Float16 lo = static_cast<_Float16>(sigma[b] - static_cast<float>(hi));
+            sig[b] = qg == 0 ? hi : qg == 1 ? lo : static_cast<_Float16>(0.0f);
         }
     }
-    __syncthreads();
 
-    floatx4 acc[NT][16];
-    float m_run[NT], l_run[NT];
+    floatx4 acc[16];
+    floatx4 lv = {0.0f, 0.0f, 0.0f, 0.0f}; // sum_t P[t][row] s_v[t][b]: lane (row j, qg) holds b = 4 qg + r
+    float m_run = kNegInf, l_run = 0.0f;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        m_run[nt] = kNegInf;
-        l_run[nt] = 0.0f;
-#pragma unroll
-        for (int m = 0; m < 16; ++m) {
-            acc[nt][m] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
+    for (int m = 0; m < 16; ++m) {
+        acc[m] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    uint8_t * wbuf = smem + wave * 2 * kTileBytes;
+    // LDS addresses are formed as smem + offset (never through an array of pointers, which would turn the reads
+    // into generic flat loads that wait on every outstanding global load)
+    uint8_t * const gbase = smem + grp * kGroupLds;
+    auto kbuf = [&](int32_t slot) -> uint8_t * { return gbase + slot * 8192; };
+    auto sslot = [&](int32_t slot) -> uint8_t * { return gbase + kCodeBytes + slot * kScaleBytes; };
     const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
+    // the split's pages (at most 64: splits are at most 16,384 cells), lane i holding logical page begin / 256 + i;
+    // a tile's page is then a lane read, not a memory load on the path to its copy
+    const int32_t n_split_pages = static_cast<int32_t>((end - begin + kPageTokens - 1) / kPageTokens);
+    const int32_t split_page = lane < n_split_pages ? table[(begin >> 8) + lane] : 0;
     auto tile_ptr = [&](int32_t ti) -> const uint8_t * {
-        const int64_t tok = begin + int64_t(ti) * kTileTokens;
-        const int32_t phys = table[tok >> 8];
-        return layer_base + int64_t(phys) * pv.page_stride + int64_t((tok & 255) >> 5) * kTileBytes;
+        const int32_t phys = __builtin_amdgcn_readlane(split_page, ti >> 3);
+        return layer_base + int64_t(phys) * pv.page_stride + int64_t(ti & 7) * kTileBytes;
     };
-
-    int32_t ti = wave;
-    if (ti < n_tiles) {
-        tile_to_lds(tile_ptr(ti), wbuf, lane);
-    }
-    int32_t stage = 0;
-    for (; ti < n_tiles; ti += kWaves) {
-        uint8_t * buf = wbuf + stage * kTileBytes;
-        if (ti + kWaves < n_tiles) {
-            tile_to_lds(tile_ptr(ti + kWaves), wbuf + (stage ^ 1) * kTileBytes, lane);
-            wait_vmcnt<17>();
-        } else {
-            wait_vmcnt<0>();
+    u32x4 vreg[8];
+    auto vload = [&](const uint8_t * tile) {
+        // after every earlier instruction that touches memory: the V loads stay younger than the K copy issued
+        // before them, which the vmcnt waits below count on
+        __asm__ __volatile__("" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            vreg[i] = *reinterpret_cast<const u32x4 *>(tile + kVCodes + i * 1024 + lane * 16);
         }
+    };
+    const half8 zero8 = {};
+
+    // One tile of the group's stream per iteration. Tile k's K codes and scales were copied into LDS slot k % 2
+    // during iteration k - 1, its V codes loaded into this wave's registers at the end of iteration k - 1; tile
+    // k + 1's K half starts into the other slot as soon as tile k's has landed, its V codes once PV(k) has read
+    // tile k's.
+    // Every iteration issues the same loads on every path (a group past its last tile re-reads its last tile, an L2
+    // hit), so the vmcnt counts below, and the compiler's own, are exact rather than a path-merge's zero.
+    const int32_t n_iter = (n_tiles + GR - 1) / GR;
+    const int32_t last_tile = n_tiles - 1;
+    {
+        const uint8_t * t0p = tile_ptr(grp < last_tile ? grp : last_tile);
+        issue_k<NT>(t0p, kbuf(0), sslot(0), rt, lane);
+        vload(t0p);
+    }
+    for (int32_t it = 0; it < n_iter; ++it) {
+        const int32_t ti = grp + it * GR;
+        const bool have = ti < n_tiles;
+        const int32_t tn = ti + GR < last_tile ? ti + GR : last_tile;
+        const uint8_t * next_ptr = tile_ptr(tn);
+        wait_vmcnt<8>(); // tile k's K half has landed (only its 8 V loads may be younger)
+        group_sync<NT>(); // ... for every wave of the group; tile k - 1's slot is no longer read
+        issue_k<NT>(next_ptr, kbuf((it + 1) & 1), sslot((it + 1) & 1), rt, lane);
+        if (have) {
+        const uint8_t * kb = kbuf(it & 1);
+        const uint8_t * sc_tile = sslot(it & 1) - kKScales; // scale offsets are tile-relative
         const int64_t tok0 = begin + int64_t(ti) * kTileTokens;
 
         // ---- S^T = K Q^T for the tile's two 16-token halves ----
-        floatx4 sc[NT][2];
+        floatx4 sc[2];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            sc[nt][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-            sc[nt][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
+        for (int h = 0; h < 2; ++h) {
+            // this lane's score rows are tokens 16 h + 4 qg + r; their K scales, all 8 blocks
+            half8 ks[4];
 #pragma unroll
-        for (int ld = 0; ld < 4; ++ld) {
-            const u32x4 k0 = *reinterpret_cast<const u32x4 *>(buf + kKCodes + ld * 1024 + lane * 16);
-            const u32x4 k1 = *reinterpret_cast<const u32x4 *>(buf + kKCodes + 4096 + ld * 1024 + lane * 16);
-            // the K scales of blocks 2 ld, 2 ld + 1 for this lane's score rows (tokens 16 h + 4 qg + r)
-            half2v ks[2][4];
+            for (int r = 0; r < 4; ++r) {
+                ks[r] = *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + 4 * qg + r) * 16);
+            }
+            // the bias term: A = this lane's token row of K scales (twice), B = sigma hi / lo
+            const half8 srow = qg < 2 ? *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + j) * 16)
+                                      : zero8;
+            const floatx4 corr = mfma16(srow, sig, floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+            floatx4 t[kBlocks];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
+            for (int ld = 0; ld < 4; ++ld) {
+                const u32x4 kw = *reinterpret_cast<const u32x4 *>(kb + h * 4096 + ld * 1024 + lane * 16);
+#pragma unroll
+                for (int bb = 0; bb < 2; ++bb) {
+                    const int b = 2 * ld + bb;
+                    const half8 ka = widen8_biased(kw[2 * bb], kw[2 * bb + 1]);
+                    t[b] = mfma16(ka, qop[b], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+                }
+            }
+            floatx4 acc_s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int b = 0; b < kBlocks; ++b) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    ks[h][r] = *reinterpret_cast<const half2v *>(buf + kKScales + (16 * h + 4 * qg + r) * 16 + ld * 4);
+                    acc_s[r] = __builtin_fmaf(static_cast<float>(ks[r][b]), t[b][r], acc_s[r]);
                 }
             }
 #pragma unroll
-            for (int bb = 0; bb < 2; ++bb) {
-                const int b = 2 * ld + bb;
-                const half8 ka0 = widen8(k0[2 * bb], k0[2 * bb + 1]);
-                const half8 ka1 = widen8(k1[2 * bb], k1[2 * bb + 1]);
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    const half8 qb = *reinterpret_cast<const half8 *>(qlds + ((nt * kBlocks + b) * 64 + lane) * 16);
-                    const floatx4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-                    const floatx4 t0 = mfma16(ka0, qb, z);
-                    const floatx4 t1 = mfma16(ka1, qb, z);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        sc[nt][0][r] = __builtin_fmaf(static_cast<float>(ks[0][r][bb]), t0[r], sc[nt][0][r]);
-                        sc[nt][1][r] = __builtin_fmaf(static_cast<float>(ks[1][r][bb]), t1[r], sc[nt][1][r]);
-                    }
-                }
+            for (int r = 0; r < 4; ++r) {
+                sc[h][r] = __builtin_fmaf(-1152.0f, corr[r], acc_s[r]);
             }
         }
 
-        // ---- online softmax (base 2), P as the PV B operand ----
-        float pf[NT][8];
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            float (&v)[8] = pf[nt];
+        // ---- online softmax (base 2); P stays in the registers that feed the PV MFMA ----
+        const int64_t lim_rel64 = lim - tok0;
+        const int32_t lim_rel = lim_rel64 > 64 ? 64 : static_cast<int32_t>(lim_rel64 < -1 ? -1 : lim_rel64);
+        float pf[8];
+        {
             float mx = kNegInf;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int64_t pos = tok0 + 16 * h + 4 * qg + r;
-                    const float x = pos <= lim[nt] ? sc[nt][h][r] * a.c2 : kNegInf;
-                    v[4 * h + r] = x;
+                    const float x = 16 * h + 4 * qg + r <= lim_rel ? sc[h][r] * a.c2 : kNegInf;
+                    pf[4 * h + r] = x;
                     mx = fmaxf(mx, x);
                 }
             }
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = fmaxf(m_run[nt], mx);
+            const float m_new = fmaxf(m_run, mx);
             const float m_use = m_new == kNegInf ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run[nt] - m_use);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
             float lsum = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                v[i] = __builtin_amdgcn_exp2f(v[i] - m_use);
-                lsum += v[i];
+                pf[i] = __builtin_amdgcn_exp2f(pf[i] - m_use);
+                lsum += pf[i];
             }
-            l_run[nt] = __builtin_fmaf(l_run[nt], alpha, lsum);
-            m_run[nt] = m_new;
+            l_run = __builtin_fmaf(l_run, alpha, lsum);
+            m_run = m_new;
             if (__any(alpha != 1.0f)) {
 #pragma unroll
                 for (int m = 0; m < 16; ++m) {
-                    acc[nt][m] *= alpha;
+                    acc[m] *= alpha;
                 }
+                lv *= alpha;
             }
         }
 
+        wait_part_k<NT>(rt); // tile k's V codes (tile k + 1's K copy is younger)
         // ---- O^T += V^T P^T: MFMA tile m covers values 16 m .. 16 m + 15 of block m / 2 ----
+        // P times the block's V scale goes to the matrix core as hi + lo fp16 (fp16 alone would leave a 2^-11
+        // relative error per term, too coarse when a few large cells dominate). The V codes enter as 1152 + code;
+        // lv accumulates sum_t P s_v per block (one MFMA pair a tile) so the bias comes out once, at the end.
+        const half8 pfh = to_half8_rtz(pf);
+        half8 pfl;
+        {
+            float r8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                r8[i] = pf[i] - static_cast<float>(pfh[i]);
+            }
+            pfl = to_half8_rtz(r8);
+        }
+        {
+            // A: lane (block b = j, qg) holds s_v[token(qg, s)][b] for its 8 slots s (zero for b >= 8)
+            const half8 sva = j < 8 ? *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + j * 16) : zero8;
+            lv = mfma16(sva, pfh, lv);
+            lv = mfma16(sva, pfl, lv);
+        }
 #pragma unroll
         for (int ld = 0; ld < 8; ++ld) {
-            const u32x4 vv = *reinterpret_cast<const u32x4 *>(buf + kVCodes + ld * 1024 + lane * 16);
-            const half8 vs = *reinterpret_cast<const half8 *>(buf + kVScales + qg * 128 + ld * 16);
-            // P times the block's V scale in fp32, carried to the MFMA as hi + lo fp16 (fp16 alone would leave a
-            // 2^-11 relative error per term, too coarse when a few large cells dominate)
-            half8 ph[NT], pl[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                float x[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    x[i] = pf[nt][i] * static_cast<float>(vs[i]);
-                }
-                split_hilo(x, ph[nt], pl[nt]);
-            }
-#pragma unroll
-            for (int mm = 0; mm < 2; ++mm) {
-                const half8 va = widen8(vv[2 * mm], vv[2 * mm + 1]);
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    acc[nt][2 * ld + mm] = mfma16(va, ph[nt], acc[nt][2 * ld + mm]);
-                    acc[nt][2 * ld + mm] = mfma16(va, pl[nt], acc[nt][2 * ld + mm]);
-                }
-            }
+            const half8 vs = *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + ld * 16);
+            half8 ph, pl;
+            scale_hilo(pf, pfh, vs, ph, pl);
+            const half8 va0 = widen8_biased(vreg[ld][0], vreg[ld][1]);
+            const half8 va1 = widen8_biased(vreg[ld][2], vreg[ld][3]);
+            acc[2 * ld] = mfma16(va0, ph, acc[2 * ld]);
+            acc[2 * ld + 1] = mfma16(va1, ph, acc[2 * ld + 1]);
+            acc[2 * ld] = mfma16(va0, pl, acc[2 * ld]);
+            acc[2 * ld + 1] = mfma16(va1, pl, acc[2 * ld + 1]);
         }
-        stage ^= 1;
+        }
+        vload(next_ptr);
     }
+    wait_vmcnt<0>();
 
-    // ---- merge the 4 waves in LDS, write the workgroup's partial ----
+    // the V bias: acc[m] carries 1152 * lv[b = m / 2]; lv[b] of this lane's row sits in lane (j, b / 4), element b % 4
+    {
+        float lb[kBlocks];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        l_run[nt] += __shfl_xor(l_run[nt], 16);
-        l_run[nt] += __shfl_xor(l_run[nt], 32);
-    }
-    constexpr int32_t kOStride = kHeadDim + 4;
-    float * ml = reinterpret_cast<float *>(smem);                   // [4 waves][16 rows][2]
-    float * ob = reinterpret_cast<float *>(smem + 4 * 16 * 2 * 4);  // [4 waves][16 rows][kOStride]
-    const int32_t gsplit = split;
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        __syncthreads(); // staging (or the previous row tile) no longer read
-        if (qg == 0) {
-            ml[(wave * 16 + j) * 2 + 0] = m_run[nt];
-            ml[(wave * 16 + j) * 2 + 1] = l_run[nt];
+        for (int b = 0; b < kBlocks; ++b) {
+            lb[b] = __shfl(lv[b & 3], j + 16 * (b >> 2));
         }
-        __syncthreads();
-        float M = kNegInf;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            M = fmaxf(M, ml[(w * 16 + j) * 2]);
-        }
-        const float M_use = M == kNegInf ? 0.0f : M;
-        const float f = __builtin_amdgcn_exp2f(m_run[nt] - M_use);
 #pragma unroll
         for (int m = 0; m < 16; ++m) {
-            *reinterpret_cast<floatx4 *>(ob + (wave * 16 + j) * kOStride + 16 * m + 4 * qg) = acc[nt][m] * f;
+            acc[m] -= 1152.0f * lb[m >> 1];
         }
-        __syncthreads();
-        // thread -> (row, 16 values)
-        const int32_t tid = static_cast<int32_t>(threadIdx.x);
-        const int32_t row = tid >> 4, c0 = (tid & 15) * 16;
-        const int32_t r = nt * 16 + row;
-        if (r < a.R) {
-            const int64_t prow = (int64_t(gsplit) * pv.h_kv + kvh) * a.R + r;
-            float * dst = a.po + prow * kHeadDim + c0;
+    }
+
+    // ---- merge the groups per row tile in LDS, write the workgroup's partial ----
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    constexpr int32_t kOStride = kHeadDim + 4;
+    __syncthreads(); // the tile buffers are no longer read
+    float * ml = reinterpret_cast<float *>(smem);                        // [waves][16 rows][2]
+    float * ob = reinterpret_cast<float *>(smem + WAVES * 16 * 2 * 4);   // [waves][16 rows][kOStride]
+    if (qg == 0) {
+        ml[(wave * 16 + j) * 2 + 0] = m_run;
+        ml[(wave * 16 + j) * 2 + 1] = l_run;
+    }
+    __syncthreads();
+    {
+        float M = kNegInf;
 #pragma unroll
-            for (int c = 0; c < 16; c += 4) {
-                floatx4 sum = *reinterpret_cast<const floatx4 *>(ob + (0 * 16 + row) * kOStride + c0 + c);
+        for (int g = 0; g < GR; ++g) {
+            M = fmaxf(M, ml[((g * NT + rt) * 16 + j) * 2]);
+        }
+        const float f = __builtin_amdgcn_exp2f(m_run - (M == kNegInf ? 0.0f : M));
 #pragma unroll
-                for (int w = 1; w < kWaves; ++w) {
-                    sum += *reinterpret_cast<const floatx4 *>(ob + (w * 16 + row) * kOStride + c0 + c);
-                }
-                *reinterpret_cast<floatx4 *>(dst + c) = sum;
+        for (int m = 0; m < 16; ++m) {
+            *reinterpret_cast<floatx4 *>(ob + (wave * 16 + j) * kOStride + 16 * m + 4 * qg) = acc[m] * f;
+        }
+    }
+    __syncthreads();
+    // thread -> (row tile, row, 16 values): NT * 16 rows x 256 values over the workgroup's threads
+    for (int32_t item = static_cast<int32_t>(threadIdx.x); item < NT * 16 * 16; item += 64 * WAVES) {
+        const int32_t rtile = item / 256, rrow = (item / 16) % 16, c0 = (item % 16) * 16;
+        const int32_t r = rtile * 16 + rrow;
+        if (r >= a.R) {
+            continue;
+        }
+        const int64_t prow = (int64_t(split) * pv.h_kv + kvh) * a.R + r;
+        float * dst = a.po + prow * kHeadDim + c0;
+#pragma unroll
+        for (int c = 0; c < 16; c += 4) {
+            floatx4 sum = *reinterpret_cast<const floatx4 *>(ob + ((0 * NT + rtile) * 16 + rrow) * kOStride + c0 + c);
+#pragma unroll
+            for (int g = 1; g < GR; ++g) {
+                sum += *reinterpret_cast<const floatx4 *>(ob + ((g * NT + rtile) * 16 + rrow) * kOStride + c0 + c);
             }
-            if ((tid & 15) == 0) {
-                float Mr = kNegInf;
+            *reinterpret_cast<floatx4 *>(dst + c) = sum;
+        }
+        if ((item & 15) == 0) {
+            float Mr = kNegInf;
 #pragma unroll
-                for (int w = 0; w < kWaves; ++w) {
-                    Mr = fmaxf(Mr, ml[(w * 16 + row) * 2]);
-                }
-                const float Mr_use = Mr == kNegInf ? 0.0f : Mr;
-                float L = 0.0f;
-#pragma unroll
-                for (int w = 0; w < kWaves; ++w) {
-                    L += ml[(w * 16 + row) * 2 + 1] * __builtin_amdgcn_exp2f(ml[(w * 16 + row) * 2] - Mr_use);
-                }
-                a.pml[prow * 2 + 0] = Mr;
-                a.pml[prow * 2 + 1] = L;
+            for (int g = 0; g < GR; ++g) {
+                Mr = fmaxf(Mr, ml[((g * NT + rtile) * 16 + rrow) * 2]);
             }
+            const float Mr_use = Mr == kNegInf ? 0.0f : Mr;
+            float L = 0.0f;
+#pragma unroll
+            for (int g = 0; g < GR; ++g) {
+                const int32_t w = g * NT + rtile;
+                L += ml[(w * 16 + rrow) * 2 + 1] * __builtin_amdgcn_exp2f(ml[(w * 16 + rrow) * 2] - Mr_use);
+            }
+            a.pml[prow * 2 + 0] = Mr;
+            a.pml[prow * 2 + 1] = L;
         }
     }
 }
@@ -413,6 +540,15 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
     }
 }
 
+// LDS of a decode launch: the groups' tile buffers, or the merge's (m, l) and partial rows, whichever is larger
+int32_t decode_lds(int32_t nt) {
+    const int32_t waves = nt == 1 ? dec_shape<1>::WAVES : nt == 2 ? dec_shape<2>::WAVES : dec_shape<3>::WAVES;
+    const int32_t gr = waves / nt;
+    const int32_t tiles = gr * kGroupLds;
+    const int32_t merge = waves * 16 * 2 * 4 + waves * 16 * (kHeadDim + 4) * 4;
+    return tiles > merge ? tiles : merge;
+}
+
 int32_t device_cus(int32_t device) {
     static int32_t cache[64] = {0};
     if (device < 0 || device >= 64) {
@@ -434,7 +570,7 @@ int32_t device_cus(int32_t device) {
 int32_t choose_split(int32_t n_seq, const int64_t * ctx, int32_t h_kv, int32_t cus) {
     int32_t best = kPageTokens;
     double best_cost = 1e300;
-    for (int32_t st = kPageTokens; st <= 16384; st *= 2) {
+    for (int32_t st = kPageTokens; st <= 64 * kPageTokens; st *= 2) { // a split's pages fit one wave's lanes
         int64_t wgs = 0;
         for (int32_t i = 0; i < n_seq; ++i) {
             wgs += (ctx[i] + st - 1) / st;
@@ -547,7 +683,6 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
     hipStream_t st = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<uint32_t>(pl.total), static_cast<uint32_t>(p->h_kv()));
     const int32_t NT = (R + 15) / 16;
-    const size_t lds = size_t(fnkv::kWaves) * 2 * fnkv::kTileBytes + size_t(NT) * fnkv::kBlocks * 64 * 16;
     static bool attr_set[64] = {false};
     const int32_t dev = p->device();
     if (dev >= 0 && dev < 64 && !attr_set[dev]) {
@@ -555,21 +690,24 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
         hipGetDevice(&cur);
         hipSetDevice(dev);
         hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::decode_kernel<1>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
+                            hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::decode_lds(1));
         hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::decode_kernel<2>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
+                            hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::decode_lds(2));
         hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::decode_kernel<3>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
+                            hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::decode_lds(3));
         hipGetLastError();
         hipSetDevice(cur);
         attr_set[dev] = true;
     }
     if (NT == 1) {
-        hipLaunchKernelGGL(fnkv::decode_kernel<1>, grid, dim3(256), lds, st, a);
+        hipLaunchKernelGGL(fnkv::decode_kernel<1>, grid, dim3(64 * fnkv::dec_shape<1>::WAVES), fnkv::decode_lds(1),
+                           st, a);
     } else if (NT == 2) {
-        hipLaunchKernelGGL(fnkv::decode_kernel<2>, grid, dim3(256), lds, st, a);
+        hipLaunchKernelGGL(fnkv::decode_kernel<2>, grid, dim3(64 * fnkv::dec_shape<2>::WAVES), fnkv::decode_lds(2),
+                           st, a);
     } else {
-        hipLaunchKernelGGL(fnkv::decode_kernel<3>, grid, dim3(256), lds, st, a);
+        hipLaunchKernelGGL(fnkv::decode_kernel<3>, grid, dim3(64 * fnkv::dec_shape<3>::WAVES), fnkv::decode_lds(3),
+                           st, a);
     }
     fnkv::merge_args m;
     m.po = a.po;

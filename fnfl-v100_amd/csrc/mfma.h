@@ -57,10 +57,49 @@ __device__ __forceinline__ void split_hilo(const float (&x)[8], half8 & hi, half
     lo = __builtin_bit_cast(half8, l);
 }
 
-// a wave's 64 x 16 B from global memory straight into LDS at lds_base + 16 lane (no registers)
-__device__ __forceinline__ void lds_load16(const void * gptr, void * lds_base) {
+// 8 codes as the fp16 values 1152 + code (one byte permute per two codes): the operand when the 1152 bias is folded
+// out elsewhere (into the MFMA's C input, or by an MFMA against the constant -1152)
+__device__ __forceinline__ half8 widen8_biased(uint32_t lo, uint32_t hi) {
+    u32x4 r;
+    r[0] = __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u);
+    r[1] = __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u);
+    r[2] = __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u);
+    r[3] = __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u);
+    return __builtin_bit_cast(half8, r);
+}
+
+// p (8 fp32 values, and the same rounded toward zero to fp16) times s (8 fp16) as hi + lo fp16: hi = fp16(ph * s)
+// (packed multiply), lo = the fp32 remainder p * s - hi (one fused multiply-add, exact to fp32) rounded toward zero.
+// hi + lo carries p * s to about 2^-19 relative.
+__device__ __forceinline__ void scale_hilo(const float (&p)[8], half8 ph, half8 s, half8 & hi, half8 & lo) {
+    typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+    hi = ph * s;
+    u32x4 l;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float r0 = __builtin_fmaf(p[2 * i], static_cast<float>(s[2 * i]), -static_cast<float>(hi[2 * i]));
+        const float r1 =
+            __builtin_fmaf(p[2 * i + 1], static_cast<float>(s[2 * i + 1]), -static_cast<float>(hi[2 * i + 1]));
+        l[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+    }
+    lo = __builtin_bit_cast(half8, l);
+}
+
+// 8 fp32 values rounded toward zero to fp16
+__device__ __forceinline__ half8 to_half8_rtz(const float (&x)[8]) {
+    u32x4 h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x[2 * i], x[2 * i + 1]));
+    }
+    return __builtin_bit_cast(half8, h);
+}
+
+// a wave's 64 x 16 B from global memory straight into LDS at lds_base + 16 lane (no registers); OFF (< 4096) is added
+// to both the global and the LDS address
+template <int OFF = 0> __device__ __forceinline__ void lds_load16(const void * gptr, void * lds_base) {
     typedef __attribute__((address_space(3))) void lds_void;
-    __builtin_amdgcn_global_load_lds(gptr, (lds_void *)lds_base, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(gptr, (lds_void *)lds_base, 16, OFF, 0);
 }
 
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
