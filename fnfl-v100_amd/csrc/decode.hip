@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <vector>
 
 namespace fnkv {
@@ -596,6 +597,13 @@ struct dec_plan {
 dec_plan plan_decode(const kv_pool & p, int32_t n_seq, const int64_t * ctx, int32_t R) {
     dec_plan pl;
     pl.split_tokens = choose_split(n_seq, ctx, p.h_kv(), device_cus(p.device()));
+    // tuning knob: FNKV_SPLIT_TOKENS (a multiple of 256, at most 16,384) overrides the chosen split size
+    if (const char * e = std::getenv("FNKV_SPLIT_TOKENS")) {
+        const int32_t v = std::atoi(e);
+        if (v >= kPageTokens && v <= 64 * kPageTokens && v % kPageTokens == 0) {
+            pl.split_tokens = v;
+        }
+    }
     pl.split0[0] = 0;
     for (int32_t i = 0; i < n_seq; ++i) {
         pl.split0[i + 1] = pl.split0[i] + static_cast<int32_t>((ctx[i] + pl.split_tokens - 1) / pl.split_tokens);
