@@ -108,6 +108,9 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=20261201)
+    ap.add_argument("--T", type=int, default=None, help="override the config's query tokens a sequence")
+    ap.add_argument("--ctxs", default=None, help="override the config's contexts (comma-separated cells)")
+    ap.add_argument("--no-append", action="store_true", help="attend only (the step's cells appended beforehand)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the path is measured on one MI355X); --gpus must be 1",
@@ -121,6 +124,11 @@ def main():
 
     cfg = CONFIGS[args.config]
     ctxs, T, layers = cfg["ctxs"], cfg["T"], cfg["layers"]
+    if args.T is not None:
+        T = args.T
+    if args.ctxs is not None:
+        ctxs = [int(c) for c in args.ctxs.split(",")]
+    workload = cfg["workload"] if (args.T is None and args.ctxs is None) else f"custom: contexts {ctxs}, T={T}, {layers} layers"
     torch.cuda.set_device(0)
     pool, slots = make_pool(torch, fnkv, cases, ctxs, T, layers, args.seed)
     g = torch.Generator(device="cuda")
@@ -134,7 +142,8 @@ def main():
 
     def step():
         for layer in range(layers):
-            pool.decode(slots, ctxs, T, layer, q[layer], out[layer], ws, k_new=kn[layer], v_new=vn[layer])
+            pool.decode(slots, ctxs, T, layer, q[layer], out[layer], ws, k_new=None if args.no_append else kn[layer],
+                        v_new=None if args.no_append else vn[layer])
 
     step()  # first call sets up the kernels' attributes outside any capture
     torch.cuda.synchronize()
@@ -187,7 +196,7 @@ def main():
         "vs_baseline": None,
         "dtype": "q8_0 KV (int8 codes + fp16 scales), fp16 Q/O, fp32 accumulate",
         "data": "synthetic (seeded N(0,1) K/V with 4 of 256 channels x8, N(0,1) Q)",
-        "config": {"workload": cfg["workload"], "contexts": ctxs, "T": T, "layers": layers, "q_heads": HQ,
+        "config": {"workload": workload, "contexts": ctxs, "T": T, "layers": layers, "q_heads": HQ,
                    "kv_heads": HKV, "head_dim": D, "page_tokens": 256, "hip_graph": graph is not None},
         "gb_s": round(bytes_layer * layers * args.steps / wall / 1e9, 3),
         "roofline": {

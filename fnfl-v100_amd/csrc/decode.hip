@@ -33,6 +33,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 #include <vector>
 
 namespace fnkv {
@@ -63,7 +64,35 @@ struct dec_args {
     int32_t slot[FNKV_MAX_SEQS];
     int64_t ctx[FNKV_MAX_SEQS];
     int32_t split0[FNKV_MAX_SEQS + 1]; // first split of each sequence; split0[n_seq] = total
+#ifdef FNKV_TIMING
+    uint64_t * ts; // per workgroup: 16 real-time stamps (instrumented builds only)
+#endif
 };
+
+#ifdef FNKV_TIMING
+#define FNKV_STAMP(k)                                                                                                \
+    do {                                                                                                             \
+        if (a.ts != nullptr && threadIdx.x == 0) {                                                                   \
+            a.ts[(blockIdx.y * gridDim.x + blockIdx.x) * 16 + (k)] = __builtin_amdgcn_s_memrealtime();                   \
+        }                                                                                                            \
+        __builtin_amdgcn_s_waitcnt(0);                                                                               \
+    } while (0)
+#define FNKV_STAMP_WAVE()                                                                                            \
+    do {                                                                                                             \
+        if (a.ts != nullptr && (threadIdx.x & 63) == 0) {                                                            \
+            a.ts[(blockIdx.y * gridDim.x + blockIdx.x) * 16 + 8 + (threadIdx.x >> 6)] =                              \
+                __builtin_amdgcn_s_memrealtime();                                                                    \
+        }                                                                                                            \
+        __builtin_amdgcn_s_waitcnt(0);                                                                               \
+    } while (0)
+#else
+#define FNKV_STAMP_WAVE()                                                                                            \
+    do {                                                                                                             \
+    } while (0)
+#define FNKV_STAMP(k)                                                                                                \
+    do {                                                                                                             \
+    } while (0)
+#endif
 
 __device__ __forceinline__ int32_t seq_of(const dec_args & a, int32_t split) {
     int32_t s = 0;
@@ -134,8 +163,174 @@ template <int NT> __device__ __forceinline__ void wait_part_k(int32_t r) {
 
 template <int NT> __device__ __forceinline__ void group_sync() {
     if (NT > 1) {
-        __syncthreads();
+        barrier_keep_loads();
     }
+}
+
+// The step's new cells ctx - T .. ctx - 1 that fall in this split [begin, end): quantized and written here (each
+// position lies in exactly one split, so one workgroup writes it and only that workgroup reads it in this launch).
+// The barrier's workgroup-scope release / acquire makes the stores visible to the workgroup's own later loads; an
+// agent-scope fence would write back and invalidate the whole L2 under every other workgroup's stream.
+template <int WAVES>
+__device__ __forceinline__ void append_new_cells(const dec_args & a, const int32_t * table, int32_t s, int32_t kvh,
+                                                 int64_t ctx, int64_t begin, int64_t end, int32_t wave,
+                                                 int32_t lane) {
+    if (a.k_new == nullptr) {
+        return;
+    }
+    const pool_view & pv = a.pv;
+    const int64_t first_new = ctx - a.T;
+    const int64_t p0 = begin > first_new ? begin : first_new;
+    const int32_t nrow = static_cast<int32_t>(end - p0);
+    if (nrow <= 0) {
+        return;
+    }
+    for (int32_t job = wave; job < 2 * nrow; job += WAVES) {
+        const int64_t pos = p0 + (job >> 1);
+        const int32_t kv = job & 1;
+        const int64_t src = ((int64_t(s) * a.T + (pos - first_new)) * pv.h_kv + kvh) * kHeadDim;
+        float x[4];
+        if (a.new_f32) {
+            load4<true>(static_cast<const float *>(kv ? a.v_new : a.k_new) + src, lane, x);
+        } else {
+            load4<false>(static_cast<const uint16_t *>(kv ? a.v_new : a.k_new) + src, lane, x);
+        }
+        quantize_store(x, lane, tile_of(pv, table, a.layer, kvh, pos), static_cast<int32_t>(pos & 31), kv);
+    }
+    __syncthreads();
+}
+
+// Query row tile rt (row 16 rt + j of the G T rows of KV head kvh; padding rows read as zero and take the last
+// token's causal limit): the Q operands (B of S^T = K Q^T: lane (row j, group qg) holds q[row][32 b + 8 qg .. + 7])
+// and the bias operand. K codes enter the MFMA as 1152 + code, so S^T carries 1152 * sum_b s_k[t][b] * sigma_b[row]
+// with sigma_b the block's sum of q; one MFMA a half computes that sum from the K scales (A: s_k twice) and sigma_b as
+// hi + lo fp16 (B: lane (row j, qg) holds sigma_hi for qg 0, sigma_lo for qg 1, else 0), and one FMA a score takes it
+// back out. lim: the row's last visible cell.
+__device__ __forceinline__ void load_q_operands(const dec_args & a, int32_t s, int32_t kvh, int32_t rt, int32_t j,
+                                                int32_t qg, half8 (&qop)[kBlocks], half8 & sig, int64_t & lim) {
+    const int32_t row = rt * 16 + j;
+    const bool real_row = row < a.R;
+    const int32_t t_row = real_row ? row / a.G : a.T - 1;
+    lim = a.ctx[s] - a.T + t_row;
+    const uint16_t * qrow =
+        a.q + ((int64_t(s) * a.T + t_row) * a.hq + int64_t(kvh) * a.G + (real_row ? row % a.G : 0)) * kHeadDim;
+    float sigma[kBlocks];
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b) {
+        u32x4 v = {0, 0, 0, 0};
+        if (real_row) {
+            v = *reinterpret_cast<const u32x4 *>(qrow + b * kQK + 8 * qg);
+        }
+        qop[b] = __builtin_bit_cast(half8, v);
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            sum += static_cast<float>(qop[b][i]);
+        }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        sigma[b] = sum;
+    }
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b) {
+        const _Float16 hi = static_cast<_Float16>(sigma[b]);
+        const _Float16 lo = static_cast<_Float16>(sigma[b] - static_cast<float>(hi));
+        sig[b] = qg == 0 ? hi : qg == 1 ? lo : static_cast<_Float16>(0.0f);
+    }
+}
+
+// S^T = K Q^T for a tile's two 16-token halves from its K codes (kb) and scales (sc_tile + kKScales ...) in LDS:
+// sc[h][r] is the score of token 16 h + 4 qg + r against this lane's row j, unscaled (q . k)
+// The Q operand of block b comes from qop(b): registers, or LDS where registers are short.
+template <typename QOP>
+__device__ __forceinline__ void tile_scores(const uint8_t * kb, const uint8_t * sc_tile, const QOP & qop, half8 sig,
+                                            int32_t j, int32_t qg, int32_t lane, floatx4 (&sc)[2]) {
+    const half8 zero8 = {};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        // this lane's score rows are tokens 16 h + 4 qg + r; their K scales, all 8 blocks
+        half8 ks[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            ks[r] = *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + 4 * qg + r) * 16);
+        }
+        // the bias term: A = this lane's token row of K scales (twice), B = sigma hi / lo
+        const half8 srow =
+            qg < 2 ? *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + j) * 16) : zero8;
+        const floatx4 corr = mfma16(srow, sig, floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+        floatx4 acc_s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) { // blocks 4 hb .. 4 hb + 3 (fewer live results)
+            floatx4 t[4];
+#pragma unroll
+            for (int ld = 2 * hb; ld < 2 * hb + 2; ++ld) {
+                const u32x4 kw = *reinterpret_cast<const u32x4 *>(kb + h * 4096 + ld * 1024 + lane * 16);
+#pragma unroll
+                for (int bb = 0; bb < 2; ++bb) {
+                    const int b = 2 * ld + bb;
+                    const half8 ka = widen8_biased(kw[2 * bb], kw[2 * bb + 1]);
+                    t[b - 4 * hb] = mfma16(ka, qop(b), floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+                }
+            }
+#pragma unroll
+            for (int b = 4 * hb; b < 4 * hb + 4; ++b) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    acc_s[r] = __builtin_fmaf(static_cast<float>(ks[r][b]), t[b - 4 * hb][r], acc_s[r]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sc[h][r] = __builtin_fmaf(-1152.0f, corr[r], acc_s[r]);
+        }
+        __builtin_amdgcn_sched_barrier(0); // one half's operands live at a time
+    }
+}
+
+// Online softmax (base 2) of a tile's scores for this lane's row, tokens past lim_rel (tile-relative) masked. The
+// row's reference m_run moves only when the tile's max exceeds it by more than kLazyLog2 (then alpha = 2^(m_old - m),
+// the factor the row's accumulators take before this tile's terms; else alpha = 1), so the rescale of the
+// accumulators is rare; the weights pf[4 h + r] = 2^(c2 sc - m_run) stay <= 2^kLazyLog2 = 64, which keeps a weight
+// times a V scale (at most 65504 / 127) inside fp16. alpha is the same in the row's four lanes.
+constexpr float kLazyLog2 = 6.0f;
+__device__ __forceinline__ void tile_softmax(const floatx4 (&sc)[2], int32_t lim_rel, float c2, int32_t qg,
+                                             float & m_run, float & l_run, float (&pf)[8], float & alpha) {
+    float mx = kNegInf;
+    if (__all(lim_rel >= 31)) { // the whole tile is visible to every row of the wave
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pf[4 * h + r] = sc[h][r] * c2;
+                mx = fmaxf(mx, pf[4 * h + r]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float x = 16 * h + 4 * qg + r <= lim_rel ? sc[h][r] * c2 : kNegInf;
+                pf[4 * h + r] = x;
+                mx = fmaxf(mx, x);
+            }
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const bool move = mx > m_run + kLazyLog2; // m_run = -inf: any visible score moves it
+    const float m_new = move ? mx : m_run;
+    const float m_use = m_new == kNegInf ? 0.0f : m_new;
+    alpha = move ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
+    float lsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        pf[i] = __builtin_amdgcn_exp2f(pf[i] - m_use);
+        lsum += pf[i];
+    }
+    l_run = __builtin_fmaf(l_run, alpha, lsum);
+    m_run = m_new;
 }
 
 template <int NT>
@@ -144,7 +339,8 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     constexpr int WAVES = dec_shape<NT>::WAVES;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
-    const int32_t wave = static_cast<int32_t>(threadIdx.x) >> 6;
+    // the wave index is uniform in a wave; readfirstlane tells the compiler so (scalar registers, no waterfall loops)
+    const int32_t wave = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(threadIdx.x) >> 6);
     const int32_t grp = wave / NT, rt = wave % NT; // tile group and row tile
     const int32_t j = lane & 15, qg = lane >> 4;
     const int32_t split = static_cast<int32_t>(blockIdx.x);
@@ -157,71 +353,14 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     const int32_t n_tiles = static_cast<int32_t>((end - begin + kTileTokens - 1) / kTileTokens);
     const pool_view & pv = a.pv;
     const int32_t * table = pv.table + int64_t(a.slot[s]) * pv.table_stride;
+    FNKV_STAMP(0);
 
-    // the step's new cells ctx - T .. ctx - 1 that fall in this split: quantized and written here (each position lies
-    // in exactly one split, so one workgroup writes it), then made visible to this workgroup's own reads
-    if (a.k_new != nullptr) {
-        const int64_t first_new = ctx - a.T;
-        const int64_t p0 = begin > first_new ? begin : first_new;
-        const int32_t nrow = static_cast<int32_t>(end - p0);
-        if (nrow > 0) {
-            for (int32_t job = wave; job < 2 * nrow; job += WAVES) {
-                const int64_t pos = p0 + (job >> 1);
-                const int32_t kv = job & 1;
-                const int64_t src = ((int64_t(s) * a.T + (pos - first_new)) * pv.h_kv + kvh) * kHeadDim;
-                float x[4];
-                if (a.new_f32) {
-                    load4<true>(static_cast<const float *>(kv ? a.v_new : a.k_new) + src, lane, x);
-                } else {
-                    load4<false>(static_cast<const uint16_t *>(kv ? a.v_new : a.k_new) + src, lane, x);
-                }
-                quantize_store(x, lane, tile_of(pv, table, a.layer, kvh, pos), static_cast<int32_t>(pos & 31), kv);
-            }
-            __threadfence();
-            __syncthreads();
-        }
-    }
-
-    // this wave's query rows (row tile rt: row 16 rt + j) and causal limits; the Q operands go to LDS once (B operand
-    // layout: [row tile][block][lane] 16 B, after the groups' tile buffers) and are read back per use
-    const int32_t row = rt * 16 + j;
-    const bool real_row = row < a.R;
-    const int32_t t_row = real_row ? row / a.G : a.T - 1;
-    const int64_t lim = ctx - a.T + t_row;
-
-    // Q operands (B of S^T = K Q^T: lane (row j, group qg) holds q[row][32 b + 8 qg .. + 7]) in registers, and the
-    // bias operand: K codes enter the MFMA as 1152 + code, so S^T carries 1152 * sum_b s_k[t][b] * sigma_b[row] with
-    // sigma_b the block's sum of q; one MFMA a half computes that sum from the K scales (A: s_k twice) and
-    // sigma_b as hi + lo fp16 (B), and one FMA a score takes it back out.
+    append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, wave, lane);
+    FNKV_STAMP(1);
     half8 qop[kBlocks];
-    half8 sig; // lane (row j, qg): qg 0: sigma_hi[0..7][row], qg 1: sigma_lo[0..7][row], else 0
-    {
-        const uint16_t * qrow =
-            a.q + ((int64_t(s) * a.T + t_row) * a.hq + int64_t(kvh) * a.G + (real_row ? row % a.G : 0)) * kHeadDim;
-        float sigma[kBlocks];
-#pragma unroll
-        for (int b = 0; b < kBlocks; ++b) {
-            u32x4 v = {0, 0, 0, 0};
-            if (real_row) {
-                v = *reinterpret_cast<const u32x4 *>(qrow + b * kQK + 8 * qg);
-            }
-            qop[b] = __builtin_bit_cast(half8, v);
-            float sum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                sum += static_cast<float>(qop[b][i]);
-            }
-            sum += __shfl_xor(sum, 16);
-            sum += __shfl_xor(sum, 32);
-            sigma[b] = sum;
-        }
-#pragma unroll
-        for (int b = 0; b < kBlocks; ++b) {
-            const _Float16 hi = static_cast<_Float16>(sigma[b]);
-            const _Float16 lo = static_cast<_Float16>(sigma[b] - static_cast<float>(hi));
-            sig[b] = qg == 0 ? hi : qg == 1 ? lo : static_cast<_Float16>(0.0f);
-        }
-    }
+    half8 sig;
+    int64_t lim;
+    load_q_operands(a, s, kvh, rt, j, qg, qop, sig, lim);
 
     floatx4 acc[16];
     floatx4 lv = {0.0f, 0.0f, 0.0f, 0.0f}; // sum_t P[t][row] s_v[t][b]: lane (row j, qg) holds b = 4 qg + r
@@ -265,6 +404,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     // hit), so the vmcnt counts below, and the compiler's own, are exact rather than a path-merge's zero.
     const int32_t n_iter = (n_tiles + GR - 1) / GR;
     const int32_t last_tile = n_tiles - 1;
+    FNKV_STAMP(2);
     {
         const uint8_t * t0p = tile_ptr(grp < last_tile ? grp : last_tile);
         issue_k<NT>(t0p, kbuf(0), sslot(0), rt, lane);
@@ -283,73 +423,16 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         const uint8_t * sc_tile = sslot(it & 1) - kKScales; // scale offsets are tile-relative
         const int64_t tok0 = begin + int64_t(ti) * kTileTokens;
 
-        // ---- S^T = K Q^T for the tile's two 16-token halves ----
         floatx4 sc[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            // this lane's score rows are tokens 16 h + 4 qg + r; their K scales, all 8 blocks
-            half8 ks[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                ks[r] = *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + 4 * qg + r) * 16);
-            }
-            // the bias term: A = this lane's token row of K scales (twice), B = sigma hi / lo
-            const half8 srow = qg < 2 ? *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + j) * 16)
-                                      : zero8;
-            const floatx4 corr = mfma16(srow, sig, floatx4{0.0f, 0.0f, 0.0f, 0.0f});
-            floatx4 t[kBlocks];
-#pragma unroll
-            for (int ld = 0; ld < 4; ++ld) {
-                const u32x4 kw = *reinterpret_cast<const u32x4 *>(kb + h * 4096 + ld * 1024 + lane * 16);
-#pragma unroll
-                for (int bb = 0; bb < 2; ++bb) {
-                    const int b = 2 * ld + bb;
-                    const half8 ka = widen8_biased(kw[2 * bb], kw[2 * bb + 1]);
-                    t[b] = mfma16(ka, qop[b], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
-                }
-            }
-            floatx4 acc_s = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int b = 0; b < kBlocks; ++b) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    acc_s[r] = __builtin_fmaf(static_cast<float>(ks[r][b]), t[b][r], acc_s[r]);
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                sc[h][r] = __builtin_fmaf(-1152.0f, corr[r], acc_s[r]);
-            }
-        }
+        tile_scores(kb, sc_tile, [&](int b) { return qop[b]; }, sig, j, qg, lane, sc);
 
         // ---- online softmax (base 2); P stays in the registers that feed the PV MFMA ----
         const int64_t lim_rel64 = lim - tok0;
         const int32_t lim_rel = lim_rel64 > 64 ? 64 : static_cast<int32_t>(lim_rel64 < -1 ? -1 : lim_rel64);
         float pf[8];
         {
-            float mx = kNegInf;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float x = 16 * h + 4 * qg + r <= lim_rel ? sc[h][r] * a.c2 : kNegInf;
-                    pf[4 * h + r] = x;
-                    mx = fmaxf(mx, x);
-                }
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = fmaxf(m_run, mx);
-            const float m_use = m_new == kNegInf ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-            float lsum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                pf[i] = __builtin_amdgcn_exp2f(pf[i] - m_use);
-                lsum += pf[i];
-            }
-            l_run = __builtin_fmaf(l_run, alpha, lsum);
-            m_run = m_new;
+            float alpha;
+            tile_softmax(sc, lim_rel, a.c2, qg, m_run, l_run, pf, alpha);
             if (__any(alpha != 1.0f)) {
 #pragma unroll
                 for (int m = 0; m < 16; ++m) {
@@ -396,6 +479,8 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         vload(next_ptr);
     }
     wait_vmcnt<0>();
+    FNKV_STAMP(3);
+    FNKV_STAMP_WAVE();
 
     // the V bias: acc[m] carries 1152 * lv[b = m / 2]; lv[b] of this lane's row sits in lane (j, b / 4), element b % 4
     {
@@ -415,6 +500,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     l_run += __shfl_xor(l_run, 32);
     constexpr int32_t kOStride = kHeadDim + 4;
     __syncthreads(); // the tile buffers are no longer read
+    FNKV_STAMP(5);
     float * ml = reinterpret_cast<float *>(smem);                        // [waves][16 rows][2]
     float * ob = reinterpret_cast<float *>(smem + WAVES * 16 * 2 * 4);   // [waves][16 rows][kOStride]
     if (qg == 0) {
@@ -435,6 +521,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         }
     }
     __syncthreads();
+    FNKV_STAMP(6);
     // thread -> (row tile, row, 16 values): NT * 16 rows x 256 values over the workgroup's threads
     for (int32_t item = static_cast<int32_t>(threadIdx.x); item < NT * 16 * 16; item += 64 * WAVES) {
         const int32_t rtile = item / 256, rrow = (item / 16) % 16, c0 = (item % 16) * 16;
@@ -470,6 +557,329 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
             a.pml[prow * 2 + 1] = L;
         }
     }
+    FNKV_STAMP(4);
+}
+
+// ---- G T > 16 rows: a group of NT waves shares each tile; rows split for QK, value blocks split for PV ----
+//
+// Wave w of a group computes S^T and the online softmax of query row tile w (rows 16 w .. 16 w + 15) from the
+// group's K copy in LDS, and hands its P (as fp16 hi + lo, the PV operand) and the per-row rescale factor to the
+// group's other waves through LDS. Then every wave accumulates O^T for ALL the group's row tiles over its own share
+// of the value blocks (NT = 2: 4 blocks each; NT = 3: 3, 3, 2), from V codes it loaded into its registers: each V byte
+// is loaded once, widened once, and a wave's accumulators stay at 64 - 72 registers. K streams through a ring of SK
+// LDS slots (SK - 1 tiles ahead), V through two register buffers (two tiles ahead); the loop is unrolled by two so
+// the buffers are fixed registers. The Q operands, the same for every group, sit once in LDS.
+template <int NT> struct rows_shape {
+    static constexpr int GR = NT == 2 ? 4 : 2;                      // tile groups a workgroup
+    static constexpr int WAVES = NT * GR;
+    static constexpr int SK = NT == 2 ? 3 : 6;                      // K ring slots a group
+    static constexpr int NBM = (kBlocks + NT - 1) / NT;             // value blocks a wave (the last may own fewer)
+    static constexpr int CK = (9 + NT - 1) / NT;                    // 1 KiB K chunks a wave issues a tile
+    static constexpr int KSLOT = kCodeBytes / 2 + kScaleBytes;      // K codes, then the tile's K and V scales
+    static constexpr int PX = 2 * NT * 64 * 32;                     // P: [parity][row tile][lane] ph, pl
+    static constexpr int AX = 2 * NT * 16 * 4;                      // rescale factors: [parity][row tile][row]
+    static constexpr int GROUP_LDS = SK * KSLOT + PX + AX;
+    static constexpr int Q_LDS = NT * kBlocks * 64 * 16;            // Q operands of all row tiles, shared by the groups
+    // loads a wave has issued after tile k's K chunks when it waits for them (top of iteration k), and after tile
+    // k's V codes when it waits for those (before PV of iteration k)
+    static constexpr int WAIT_K = NBM + (SK - 2) * (CK + NBM);
+    static constexpr int WAIT_V = 2 * CK + NBM;
+};
+
+template <int NT>
+__global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_kernel(dec_args a) {
+    using SH = rows_shape<NT>;
+    constexpr int GR = SH::GR, WAVES = SH::WAVES, SK = SH::SK, NBM = SH::NBM, CK = SH::CK;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
+    // the wave index is uniform in a wave; readfirstlane tells the compiler so (scalar registers, no waterfall loops)
+    const int32_t wave = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(threadIdx.x) >> 6);
+    const int32_t grp = wave / NT, w = wave % NT; // tile group; this wave's row tile and block share
+    const int32_t j = lane & 15, qg = lane >> 4;
+    const int32_t split = static_cast<int32_t>(blockIdx.x);
+    const int32_t kvh = static_cast<int32_t>(blockIdx.y);
+    const int32_t s = seq_of(a, split);
+    const int32_t sp = split - a.split0[s];
+    const int64_t ctx = a.ctx[s];
+    const int64_t begin = int64_t(sp) * a.split_tokens;
+    const int64_t end = ctx < begin + a.split_tokens ? ctx : begin + a.split_tokens;
+    const int32_t n_tiles = static_cast<int32_t>((end - begin + kTileTokens - 1) / kTileTokens);
+    const pool_view & pv = a.pv;
+    const int32_t * table = pv.table + int64_t(a.slot[s]) * pv.table_stride;
+    FNKV_STAMP(0);
+    append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, wave, lane);
+    FNKV_STAMP(1);
+
+    half8 sig;
+    int64_t lim;
+    uint8_t * const qlds = smem + GR * SH::GROUP_LDS; // [row tile][block][lane] 16 B
+    {
+        half8 qop[kBlocks];
+        load_q_operands(a, s, kvh, w, j, qg, qop, sig, lim);
+        if (grp == 0) { // read before the first tile by the loop's first barrier
+#pragma unroll
+            for (int b = 0; b < kBlocks; ++b) {
+                *reinterpret_cast<half8 *>(qlds + (w * kBlocks + b) * 1024 + lane * 16) = qop[b];
+            }
+        }
+    }
+    auto qop_lds = [&](int b) { return *reinterpret_cast<const half8 *>(qlds + (w * kBlocks + b) * 1024 + lane * 16); };
+
+    const int32_t b0 = NT == 2 ? 4 * w : 3 * w; // this wave's value blocks b0 .. b0 + nb - 1
+    const int32_t nb = NT == 2 ? 4 : (w < 2 ? 3 : 2);
+    floatx4 acc[NT][NBM][2];
+    floatx4 lv[NT];
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt) {
+        lv[rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < NBM; ++i) {
+            acc[rt][i][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            acc[rt][i][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    float m_run = kNegInf, l_run = 0.0f; // row tile w
+
+    // LDS of the group, addressed as smem + offset (never through arrays of pointers)
+    const uint32_t gofs = static_cast<uint32_t>(grp * SH::GROUP_LDS);
+    auto kslot = [&](int32_t slot) -> uint8_t * { return smem + gofs + slot * SH::KSLOT; };
+    auto pslot = [&](int32_t par, int32_t rt) -> uint8_t * {
+        return smem + gofs + SK * SH::KSLOT + (par * NT + rt) * 2048;
+    };
+    auto aslot = [&](int32_t par, int32_t rt) -> float * {
+        return reinterpret_cast<float *>(smem + gofs + SK * SH::KSLOT + SH::PX + (par * NT + rt) * 64);
+    };
+
+    const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
+    const int32_t n_split_pages = static_cast<int32_t>((end - begin + kPageTokens - 1) / kPageTokens);
+    const int32_t split_page = lane < n_split_pages ? table[(begin >> 8) + lane] : 0;
+    const int32_t last_tile = n_tiles - 1;
+    auto tile_ptr = [&](int32_t k) -> const uint8_t * { // the group's tile of iteration k (the last tile past the end)
+        int32_t ti = grp + k * GR;
+        ti = ti < last_tile ? ti : last_tile;
+        const int32_t phys = __builtin_amdgcn_readlane(split_page, ti >> 3);
+        return layer_base + int64_t(phys) * pv.page_stride + int64_t(ti & 7) * kTileBytes;
+    };
+    const int32_t lane16 = lane * 16;
+    // chunk c of a tile (c < 8: K codes, c = 8: the scales) into its place in a ring slot
+    auto issue_chunk = [&](const uint8_t * tile, uint8_t * dst, int32_t c) {
+        const rsrc_t r = make_rsrc(tile, kTileBytes);
+        if (c < 8) {
+            buf_lds16(r, dst + c * 1024, lane16, kKCodes + c * 1024);
+        } else {
+            buf_lds16(r, dst + kCodeBytes / 2, lane16, kKScales);
+        }
+    };
+    // this wave's chunks c = w, w + NT, ... of a tile; past the ninth chunk it copies its first chunk again (the same
+    // bytes to the same place), which keeps every wave's count at CK
+    auto issue_k = [&](const uint8_t * tile, int32_t slot) {
+        uint8_t * dst = kslot(slot);
+#pragma unroll
+        for (int32_t i = 0; i < CK; ++i) {
+            const int32_t c = w + i * NT;
+            issue_chunk(tile, dst, c <= 8 ? c : w);
+        }
+    };
+    // the prologue's placeholders for V loads before tile 0: NBM more copies of this wave's first chunk of a tile
+    // whose K copy it has just issued
+    auto issue_placeholder = [&](const uint8_t * tile, int32_t slot) {
+#pragma unroll
+        for (int32_t i = 0; i < NBM; ++i) {
+            issue_chunk(tile, kslot(slot), w);
+        }
+    };
+    u32x4 vbuf0[NBM], vbuf1[NBM];
+    auto load_v = [&](const uint8_t * tile, u32x4 (&vb)[NBM]) {
+        __asm__ __volatile__("" ::: "memory"); // younger than every load issued before (the waits count on it)
+        const rsrc_t r = make_rsrc(tile, kTileBytes);
+#pragma unroll
+        for (int32_t i = 0; i < NBM; ++i) {
+            const int32_t b = b0 + i < kBlocks ? b0 + i : kBlocks - 1;
+            vb[i] = buf_load16(r, lane16, kVCodes + b * 1024);
+        }
+    };
+
+    // Issue order, per wave, identical in the prologue and every iteration: K(k + SK - 1), then V(k + 2), for
+    // k = -(SK - 1) .. -1 in the prologue (placeholders where k + 2 < 0), then one pair an iteration.
+    const int32_t n_iter = (((n_tiles + GR - 1) / GR) + 1) & ~1;
+#pragma unroll
+    for (int32_t k = -(SK - 1); k < 0; ++k) {
+        issue_k(tile_ptr(k + SK - 1), k + SK - 1);
+        if (k + 2 == 0) {
+            load_v(tile_ptr(0), vbuf0);
+        } else if (k + 2 == 1) {
+            load_v(tile_ptr(1), vbuf1);
+        } else {
+            issue_placeholder(tile_ptr(k + SK - 1), k + SK - 1);
+        }
+    }
+    FNKV_STAMP(2);
+
+    const half8 zero8 = {};
+    auto iteration = [&](auto par_c, int32_t k, u32x4 (&vb)[NBM]) {
+        constexpr int32_t par = decltype(par_c)::value; // k & 1
+        const bool have = grp + k * GR < n_tiles;
+        wait_vmcnt<SH::WAIT_K>(); // this wave's chunks of tile k's K copy have landed
+        barrier_keep_loads();     // ... every wave's; slot (k - 1) % SK and P buffers of k - 2 are free
+        issue_k(tile_ptr(k + SK - 1), (k + SK - 1) % SK);
+        const uint8_t * kb = kslot(k % SK);
+        const uint8_t * sc_tile = kb + kCodeBytes / 2 - kKScales; // scale offsets are tile-relative
+        if (have) {
+            const int64_t tok0 = begin + int64_t(grp + k * GR) * kTileTokens;
+            floatx4 sc[2];
+            tile_scores(kb, sc_tile, qop_lds, sig, j, qg, lane, sc);
+            const int64_t lim_rel64 = lim - tok0;
+            const int32_t lim_rel = lim_rel64 > 64 ? 64 : static_cast<int32_t>(lim_rel64 < -1 ? -1 : lim_rel64);
+            float pf[8];
+            float alpha;
+            tile_softmax(sc, lim_rel, a.c2, qg, m_run, l_run, pf, alpha);
+            half8 ph, pl;
+            split_hilo(pf, ph, pl);
+            u32x4 * px = reinterpret_cast<u32x4 *>(pslot(par, w) + lane * 32);
+            px[0] = __builtin_bit_cast(u32x4, ph);
+            px[1] = __builtin_bit_cast(u32x4, pl);
+            if (qg == 0) {
+                aslot(par, w)[j] = alpha;
+            }
+        }
+        barrier_keep_loads(); // every row tile's P and factors are in LDS
+        if (have) {
+            wait_vmcnt<SH::WAIT_V>(); // tile k's V codes (tile k + 1's K copy and V codes are younger)
+            const half8 sva =
+                j < 8 ? *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + j * 16) : zero8;
+            half8 ph[NT], pl[NT];
+#pragma unroll
+            for (int32_t rt = 0; rt < NT; ++rt) {
+                const u32x4 * px = reinterpret_cast<const u32x4 *>(pslot(par, rt) + lane * 32);
+                ph[rt] = __builtin_bit_cast(half8, px[0]);
+                pl[rt] = __builtin_bit_cast(half8, px[1]);
+                const float alpha = aslot(par, rt)[j];
+                if (__any(alpha != 1.0f)) {
+#pragma unroll
+                    for (int32_t i = 0; i < NBM; ++i) {
+                        acc[rt][i][0] *= alpha;
+                        acc[rt][i][1] *= alpha;
+                    }
+                    lv[rt] *= alpha;
+                }
+                lv[rt] = mfma16(sva, ph[rt], lv[rt]);
+                lv[rt] = mfma16(sva, pl[rt], lv[rt]);
+            }
+#pragma unroll
+            for (int32_t i = 0; i < NBM; ++i) {
+                if (i < nb) {
+                    const half8 vs =
+                        *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + (b0 + i) * 16);
+                    const half8 va0 = widen8_biased(vb[i][0], vb[i][1]);
+                    const half8 va1 = widen8_biased(vb[i][2], vb[i][3]);
+#pragma unroll
+                    for (int32_t rt = 0; rt < NT; ++rt) {
+                        half8 hi, lo;
+                        scale_hilo_pk(ph[rt], pl[rt], vs, hi, lo);
+                        acc[rt][i][0] = mfma16(va0, hi, acc[rt][i][0]);
+                        acc[rt][i][1] = mfma16(va1, hi, acc[rt][i][1]);
+                        acc[rt][i][0] = mfma16(va0, lo, acc[rt][i][0]);
+                        acc[rt][i][1] = mfma16(va1, lo, acc[rt][i][1]);
+                    }
+                }
+            }
+        }
+        load_v(tile_ptr(k + 2), vb);
+    };
+    for (int32_t k = 0; k < n_iter; k += 2) {
+        iteration(std::integral_constant<int32_t, 0>(), k, vbuf0);
+        iteration(std::integral_constant<int32_t, 1>(), k + 1, vbuf1);
+    }
+    wait_vmcnt<0>();
+    FNKV_STAMP(3);
+    FNKV_STAMP_WAVE();
+
+    // the V bias: acc[rt][i] carries 1152 * lv[rt][b0 + i]; lv[rt][b] of this lane's row sits in lane (j, b / 4),
+    // element b % 4
+#pragma unroll
+    for (int32_t rt = 0; rt < NT; ++rt) {
+        float lb[kBlocks];
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) {
+            lb[b] = __shfl(lv[rt][b & 3], j + 16 * (b >> 2));
+        }
+#pragma unroll
+        for (int32_t i = 0; i < NBM; ++i) {
+            float l = lb[0];
+#pragma unroll
+            for (int b = 1; b < kBlocks; ++b) {
+                l = b0 + i == b ? lb[b] : l;
+            }
+            acc[rt][i][0] -= 1152.0f * l;
+            acc[rt][i][1] -= 1152.0f * l;
+        }
+    }
+
+    // ---- merge the groups in LDS, write the workgroup's partial ----
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    constexpr int32_t kRows = NT * 16;
+    constexpr int32_t kOStride = kHeadDim + 4;
+    __syncthreads(); // the ring and exchange buffers are no longer read
+    float * ml = reinterpret_cast<float *>(smem);                     // [group][row][2]
+    float * ob = reinterpret_cast<float *>(smem + GR * kRows * 2 * 4); // [group][row][kOStride]
+    if (qg == 0) {
+        ml[(grp * kRows + w * 16 + j) * 2 + 0] = m_run;
+        ml[(grp * kRows + w * 16 + j) * 2 + 1] = l_run;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int32_t rt = 0; rt < NT; ++rt) {
+        float M = kNegInf;
+#pragma unroll
+        for (int g = 0; g < GR; ++g) {
+            M = fmaxf(M, ml[(g * kRows + rt * 16 + j) * 2]);
+        }
+        const float f = __builtin_amdgcn_exp2f(ml[(grp * kRows + rt * 16 + j) * 2] - (M == kNegInf ? 0.0f : M));
+        float * orow = ob + (grp * kRows + rt * 16 + j) * kOStride;
+#pragma unroll
+        for (int32_t i = 0; i < NBM; ++i) {
+            if (i < nb) {
+                *reinterpret_cast<floatx4 *>(orow + (b0 + i) * 32 + 4 * qg) = acc[rt][i][0] * f;
+                *reinterpret_cast<floatx4 *>(orow + (b0 + i) * 32 + 16 + 4 * qg) = acc[rt][i][1] * f;
+            }
+        }
+    }
+    __syncthreads();
+    // thread -> (row, 16 values): kRows x 256 values over the workgroup's threads
+    for (int32_t item = static_cast<int32_t>(threadIdx.x); item < kRows * 16; item += 64 * WAVES) {
+        const int32_t r = item / 16, c0 = (item % 16) * 16;
+        if (r >= a.R) {
+            continue;
+        }
+        const int64_t prow = (int64_t(split) * pv.h_kv + kvh) * a.R + r;
+        float * dst = a.po + prow * kHeadDim + c0;
+#pragma unroll
+        for (int c = 0; c < 16; c += 4) {
+            floatx4 sum = *reinterpret_cast<const floatx4 *>(ob + r * kOStride + c0 + c);
+#pragma unroll
+            for (int g = 1; g < GR; ++g) {
+                sum += *reinterpret_cast<const floatx4 *>(ob + (g * kRows + r) * kOStride + c0 + c);
+            }
+            *reinterpret_cast<floatx4 *>(dst + c) = sum;
+        }
+        if ((item & 15) == 0) {
+            float Mr = kNegInf;
+#pragma unroll
+            for (int g = 0; g < GR; ++g) {
+                Mr = fmaxf(Mr, ml[(g * kRows + r) * 2]);
+            }
+            const float Mr_use = Mr == kNegInf ? 0.0f : Mr;
+            float L = 0.0f;
+#pragma unroll
+            for (int g = 0; g < GR; ++g) {
+                L += ml[(g * kRows + r) * 2 + 1] * __builtin_amdgcn_exp2f(ml[(g * kRows + r) * 2] - Mr_use);
+            }
+            a.pml[prow * 2 + 0] = Mr;
+            a.pml[prow * 2 + 1] = L;
+        }
+    }
+    FNKV_STAMP(4);
 }
 
 // Fold the splits of each (sequence, KV head, row): one workgroup a (row, 32 values); 256 threads = 8 float4
@@ -543,11 +953,17 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
 
 // LDS of a decode launch: the groups' tile buffers, or the merge's (m, l) and partial rows, whichever is larger
 int32_t decode_lds(int32_t nt) {
-    const int32_t waves = nt == 1 ? dec_shape<1>::WAVES : nt == 2 ? dec_shape<2>::WAVES : dec_shape<3>::WAVES;
-    const int32_t gr = waves / nt;
-    const int32_t tiles = gr * kGroupLds;
-    const int32_t merge = waves * 16 * 2 * 4 + waves * 16 * (kHeadDim + 4) * 4;
-    return tiles > merge ? tiles : merge;
+    if (nt == 1) {
+        constexpr int32_t waves = dec_shape<1>::WAVES;
+        const int32_t tiles = dec_shape<1>::GR * kGroupLds;
+        const int32_t merge = waves * 16 * 2 * 4 + waves * 16 * (kHeadDim + 4) * 4;
+        return tiles > merge ? tiles : merge;
+    }
+    const int32_t gr = nt == 2 ? rows_shape<2>::GR : rows_shape<3>::GR;
+    const int32_t ring = gr * (nt == 2 ? rows_shape<2>::GROUP_LDS : rows_shape<3>::GROUP_LDS) +
+                         (nt == 2 ? rows_shape<2>::Q_LDS : rows_shape<3>::Q_LDS);
+    const int32_t merge = gr * nt * 16 * 2 * 4 + gr * nt * 16 * (kHeadDim + 4) * 4;
+    return ring > merge ? ring : merge;
 }
 
 int32_t device_cus(int32_t device) {
@@ -617,6 +1033,11 @@ dec_plan plan_decode(const kv_pool & p, int32_t n_seq, const int64_t * ctx, int3
 } // namespace fnkv
 
 using fnkv::set_error;
+
+#ifdef FNKV_TIMING
+static uint64_t * g_timing = nullptr;
+extern "C" void fnkv_debug_timing(void * buf) { g_timing = static_cast<uint64_t *>(buf); }
+#endif
 
 extern "C" {
 
@@ -688,6 +1109,9 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
     for (int32_t i = 0; i <= FNKV_MAX_SEQS; ++i) {
         a.split0[i] = i <= n_seq ? pl.split0[i] : pl.total;
     }
+#ifdef FNKV_TIMING
+    a.ts = g_timing;
+#endif
     hipStream_t st = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<uint32_t>(pl.total), static_cast<uint32_t>(p->h_kv()));
     const int32_t NT = (R + 15) / 16;
@@ -699,9 +1123,9 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
         hipSetDevice(dev);
         hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::decode_kernel<1>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::decode_lds(1));
-        hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::decode_kernel<2>),
+        hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::decode_rows_kernel<2>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::decode_lds(2));
-        hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::decode_kernel<3>),
+        hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::decode_rows_kernel<3>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::decode_lds(3));
         hipGetLastError();
         hipSetDevice(cur);
@@ -711,11 +1135,11 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
         hipLaunchKernelGGL(fnkv::decode_kernel<1>, grid, dim3(64 * fnkv::dec_shape<1>::WAVES), fnkv::decode_lds(1),
                            st, a);
     } else if (NT == 2) {
-        hipLaunchKernelGGL(fnkv::decode_kernel<2>, grid, dim3(64 * fnkv::dec_shape<2>::WAVES), fnkv::decode_lds(2),
-                           st, a);
+        hipLaunchKernelGGL(fnkv::decode_rows_kernel<2>, grid, dim3(64 * fnkv::rows_shape<2>::WAVES),
+                           fnkv::decode_lds(2), st, a);
     } else {
-        hipLaunchKernelGGL(fnkv::decode_kernel<3>, grid, dim3(64 * fnkv::dec_shape<3>::WAVES), fnkv::decode_lds(3),
-                           st, a);
+        hipLaunchKernelGGL(fnkv::decode_rows_kernel<3>, grid, dim3(64 * fnkv::rows_shape<3>::WAVES),
+                           fnkv::decode_lds(3), st, a);
     }
     fnkv::merge_args m;
     m.po = a.po;

@@ -85,6 +85,15 @@ __device__ __forceinline__ void scale_hilo(const float (&p)[8], half8 ph, half8 
     lo = __builtin_bit_cast(half8, l);
 }
 
+// (ph + pl) times s (8 fp16 each) as hi + lo fp16 with packed fp16 arithmetic only: hi = fp16(ph * s), the exact
+// remainder ph * s - hi (a fused multiply-add; exact while it is not subnormal), then lo = fp16(pl * s + remainder).
+// With ph + pl carrying p to 2^-20, hi + lo carries p * s to about 2^-20 relative.
+__device__ __forceinline__ void scale_hilo_pk(half8 ph, half8 pl, half8 s, half8 & hi, half8 & lo) {
+    hi = ph * s;
+    const half8 rem = __builtin_elementwise_fma(ph, s, -hi);
+    lo = __builtin_elementwise_fma(pl, s, rem);
+}
+
 // 8 fp32 values rounded toward zero to fp16
 __device__ __forceinline__ half8 to_half8_rtz(const float (&x)[8]) {
     u32x4 h;
@@ -102,11 +111,41 @@ template <int OFF = 0> __device__ __forceinline__ void lds_load16(const void * g
     __builtin_amdgcn_global_load_lds(gptr, (lds_void *)lds_base, 16, OFF, 0);
 }
 
+// Buffer-resource loads: the tile's address lives in four SGPRs, so a lane's address is one VGPR offset (lane * 16)
+// plus scalar and immediate offsets, with no 64-bit address arithmetic in VGPRs. The descriptor is a raw buffer
+// (stride 0) of `bytes` bytes with the 32-bit data format gfx9 raw loads need.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void * base, int32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
+}
+// 16 B a lane at base + voff + soff into registers
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, int32_t voff, int32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+// a wave's 64 x 16 B at base + soff + 16 lane straight into LDS at lds_base + 16 lane
+__device__ __forceinline__ void buf_lds16(rsrc_t r, void * lds_base, int32_t voff, int32_t soff) {
+    typedef __attribute__((address_space(3))) void lds_void;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_base, 16, voff, soff, 0, 0);
+}
+
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
 // lgkmcnt 11:8)
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// The workgroup's waves meet at an s_barrier after their LDS reads have returned (lgkmcnt(0)) but with their global
+// loads still in flight: __syncthreads would also wait for every outstanding global load, prefetches included. The
+// empty asm statements keep the compiler from moving memory accesses across the barrier. LDS data written by a
+// global_load_lds is visible to the other waves once the issuing wave has waited for it (vmcnt) before the barrier.
+__device__ __forceinline__ void barrier_keep_loads() {
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (0 << 8));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    __asm__ __volatile__("" ::: "memory");
 }
 
 } // namespace fnkv
