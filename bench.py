@@ -13,9 +13,14 @@ algorithmic HBM bytes, the roofline of the attention launch, and the CPU baselin
 attention, multithreaded, on a bounded sample) measured in the same run.
 """
 import argparse
+import csv
+import glob
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -35,7 +40,17 @@ CONFIGS = {
     "cfg2v": dict(ctxs=[262144], T=5, layers=1,
                   workload="cfg2: 1 seq 262,144 cells, verify T=5, 1 layer, scattered pages"),
     "cfg0": dict(ctxs=[4096], T=1, layers=1, workload="cfg0: 1 seq 4,096 cells, decode T=1, 1 layer"),
+    "cfg3": dict(ctxs=[131072 + 2048], T=2048, layers=1, prefill=True,
+                 workload="cfg3: 2,048-token fp16 chunk appended at depth 131,072 and attended causally over 133,120 "
+                          "cells (chunked prefill, matrix cores), 1 layer"),
 }
+PEAK_MFMA_F16_TFLOPS = 2500.0  # dense fp16 matrix-core peak
+
+
+def prefill_flops(ctx, rows):
+    """4 d flops a visible (query, key) pair and query head: QK^T and PV, 2 d each"""
+    pairs = sum(ctx - rows + t + 1 for t in range(rows))
+    return 4 * D * HQ * pairs
 
 
 def algorithmic_bytes(ctxs, T):
@@ -99,6 +114,183 @@ def cpu_baseline(ctxs, T, layers, seed, threads):
     }
 
 
+COPY_BYTES = 1 << 30  # the calibration copy: 1 GiB read, 1 GiB written
+
+
+def traffic_child(args, torch, run_step):
+    """The child of a counter pass: the workload's launches (eager, a few steps), then a plain elementwise copy of
+    COPY_BYTES (torch.neg into a second buffer) three times, whose counter readings calibrate the counter's unit."""
+    for _ in range(3):
+        run_step()
+    torch.cuda.synchronize()
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+
+
+def _counter_means(out_dir):
+    """rocprofv3 counter CSV -> {kernel name: mean counter value per dispatch}"""
+    sums, counts = {}, {}
+    for f in glob.glob(os.path.join(out_dir, "**", "*counter_collection.csv"), recursive=True):
+        with open(f) as fh:
+            for row in csv.DictReader(fh):
+                k = row.get("Kernel_Name", "")
+                sums[k] = sums.get(k, 0.0) + float(row.get("Counter_Value", 0.0))
+                counts[k] = counts.get(k, 0) + 1
+    return {k: sums[k] / counts[k] for k in sums}
+
+
+def measure_traffic(argv):
+    """HBM bytes of one fnkv_attn_decode launch (decode + merge kernels) from two rocprofv3 counter passes over a child
+    run of the same workload: FETCH_SIZE, then WRITE_SIZE (KiB a dispatch), each scaled by bytes / reading of the
+    same counter for the calibration copy of known size in the same child. Runs before this process touches the GPU.
+    Returns (traffic bytes, detail dict) or (None, reason)."""
+    rocprof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(rocprof):
+        return None, "rocprofv3 not found"
+    env = dict(os.environ, TMPDIR="/tmp")
+    detail = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out_dir = tempfile.mkdtemp(prefix="fnkv_pmc_", dir="/tmp")
+        cmd = [rocprof, "--pmc", counter, "--output-format", "csv", "-d", out_dir, "-o", "run", "--",
+               sys.executable, os.path.abspath(__file__), "--traffic-child", *argv]
+        try:
+            r = subprocess.run(cmd, timeout=180, capture_output=True, text=True, env=env, cwd="/tmp")
+        except subprocess.TimeoutExpired:
+            return None, f"{counter} pass timed out"
+        means = _counter_means(out_dir)
+        shutil.rmtree(out_dir, ignore_errors=True)
+        if r.returncode != 0 or not means:
+            return None, f"{counter} pass failed ({r.returncode})"
+        launch = sum(v for k, v in means.items() if "decode" in k and "fnkv" in k)
+        launch += sum(v for k, v in means.items() if "merge_kernel" in k)
+        copy = [v for k, v in means.items() if "neg" in k.lower()]
+        if not copy or copy[0] <= 0 or launch <= 0:
+            return None, f"{counter}: kernels not found in the counter output"
+        factor = COPY_BYTES / (copy[0] * 1024.0)
+        detail[counter] = {"kib_per_launch": round(launch, 1), "copy_kib": round(copy[0], 1),
+                           "scale_bytes_per_kib": round(factor, 2), "bytes_per_launch": int(launch * 1024 * factor)}
+    total = detail["FETCH_SIZE"]["bytes_per_launch"] + detail["WRITE_SIZE"]["bytes_per_launch"]
+    return total, detail
+
+
+def run_prefill(args, cfg):
+    """one step = the chunk's Q8_0 append (fnkv_q8_append) + its causal attention over the whole
+    context (fnkv_attn_prefill), captured in a HIP graph; the roofline is the matrix cores' (algorithmic flops)."""
+    import numpy as np
+    import torch
+
+    import cases
+    import fnkv
+
+    ctx, rows = cfg["ctxs"][0], cfg["T"]
+    depth = ctx - rows
+    torch.cuda.set_device(0)
+    pool = fnkv.Pool(2, -(-ctx // 256) + 8, 1, HKV)
+    cases.scatter_ensure(pool, [0], [ctx], args.seed, churn=0.2)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(args.seed)
+    kv = []
+    for _ in range(2):
+        x = torch.randn((ctx, HKV, D), generator=g, device="cuda", dtype=torch.float32)
+        ch = torch.randperm(D, generator=g, device="cuda")[:4]
+        x[:, :, ch] *= 8.0
+        kv.append(x.half())
+    pool.append(0, 0, 0, kv[0][:depth].contiguous(), kv[1][:depth].contiguous())
+    kc, vc = kv[0][depth:].contiguous(), kv[1][depth:].contiguous()
+    q = torch.randn((rows, HQ, D), generator=g, device="cuda").half()
+    out = torch.empty_like(q)
+
+    def step():
+        pool.append(0, 0, depth, kc, vc)
+        pool.prefill(0, 0, ctx, q, out)
+
+    step()
+    torch.cuda.synchronize()
+    graph = None
+    if not args.no_graph:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+    run = graph.replay if graph is not None else step
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        run()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = ev0.elapsed_time(ev1) / 1e3
+    assert torch.isfinite(out.float()).all().item(), "non-finite attention output"
+    flops = prefill_flops(ctx, rows)
+    step_s = gpu_s / args.steps
+    tflops = flops / step_s / 1e12
+    line = {
+        "metric": "chunked-prefill attention over the Q8_0 paged KV: tokens/s and matrix-core TFLOP/s",
+        "value": round(rows * args.steps / wall, 3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0 KV dequantized to fp16 hi + lo, fp16 Q/O, fp32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V with 4 of 256 channels x8, N(0,1) Q)",
+        "config": {"workload": cfg["workload"], "context": ctx, "chunk": rows, "q_heads": HQ, "kv_heads": HKV,
+                   "head_dim": D, "page_tokens": 256, "hip_graph": graph is not None},
+        "roofline": {
+            "kernel": "fnkv_q8_append + fnkv_attn_prefill (append_kernel + prefill_kernel), per step",
+            "bound": "mfma",
+            "achieved": round(tflops, 3),
+            "peak": PEAK_MFMA_F16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_MFMA_F16_TFLOPS, 4),
+            "traffic": None,
+            "flops_per_step": flops,
+            "step_us": round(step_s * 1e6, 3),
+        },
+    }
+    if not args.no_cpu:
+        import oracle as O
+        threads = max(1, min(16, os.cpu_count() or 1))
+        sample = 16
+        (kq, kd, _), (vq, vd, _) = cases.decoded(O, kv[0].cpu().numpy(), kv[1].cpu().numpy())
+        kb, vb = O.to_block_q8_0(kq, kd), O.to_block_q8_0(vq, vd)
+        q16 = q[-sample:].cpu().numpy().view(np.uint16)
+        O.attn_ggml(q16[:1], kb, vb, 2048, threads=threads)
+        t1 = time.perf_counter()
+        O.attn_ggml(q16, kb, vb, ctx, threads=threads)
+        dt = time.perf_counter() - t1
+        sample_flops = 4 * D * HQ * sum(ctx - sample + t + 1 for t in range(sample))
+        cpu_step = dt * flops / sample_flops
+        line["cpu_baseline"] = {
+            "value": round(rows / cpu_step, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"the chunk's last {sample} of {rows} query rows over the full context, fp32-Q ggml-semantics "
+                      f"flash attention (oracle/fnkv_oracle.c or_attn_ggml), {threads} threads, {dt:.2f} s, scaled "
+                      f"by visible pairs to the chunk",
+            "tflops": round(sample_flops / dt / 1e12, 4),
+        }
+    print(json.dumps(line), flush=True)
+    pool.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -111,11 +303,21 @@ def main():
     ap.add_argument("--T", type=int, default=None, help="override the config's query tokens a sequence")
     ap.add_argument("--ctxs", default=None, help="override the config's contexts (comma-separated cells)")
     ap.add_argument("--no-append", action="store_true", help="attend only (the step's cells appended beforehand)")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes (traffic: null)")
+    ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the path is measured on one MI355X); --gpus must be 1",
               file=sys.stderr)
         sys.exit(2)
+    if CONFIGS[args.config].get("prefill"):
+        run_prefill(args, CONFIGS[args.config])
+        return
+
+    traffic, traffic_detail = None, "skipped (--no-traffic)"
+    if not args.traffic_child and not args.no_traffic:
+        passthrough = [a for a in sys.argv[1:] if a not in ("--no-cpu",)]
+        traffic, traffic_detail = measure_traffic(passthrough)
 
     import torch
 
@@ -147,6 +349,10 @@ def main():
 
     step()  # first call sets up the kernels' attributes outside any capture
     torch.cuda.synchronize()
+    if args.traffic_child:
+        traffic_child(args, torch, step)
+        pool.close()
+        return
     graph = None
     if not args.no_graph:
         s = torch.cuda.Stream()
@@ -206,7 +412,8 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_detail": traffic_detail,
             "bytes_per_launch": bytes_layer,
             "launch_us": round(launch_s * 1e6, 3),
         },
