@@ -2,7 +2,7 @@
 
 hipcc compiles each source to an object (in parallel) and links the shared library next to this file. Every HIP
 source is compiled with packed-fp32 instructions disabled (their hand-written forms are avoided on this target) and
-with the matrix-core instructions in their VGPR form (the decode kernel's accumulators stay in VGPRs when they fit).
+with per-file flags (below).
 """
 import concurrent.futures
 import os
@@ -19,7 +19,6 @@ ARCH = os.environ.get("FNKV_ARCH", "gfx950")
 COMMON = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-result",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-I", os.path.join(HERE, "..", "include"),
 ]
 
@@ -31,8 +30,10 @@ def hipcc():
     return "hipcc"
 
 
-# per-file flags: the quantizer must not fuse x * id into the rounding test (ggml rounds the product first)
-EXTRA = {"append.hip": ["-ffp-contract=off"]}
+# per-file flags: the quantizer must not fuse x * id into the rounding test (ggml rounds the product first); the
+# attention kernels run two waves a SIMD and keep their matrix-core accumulators in ordinary registers (VGPR form)
+VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+EXTRA = {"append.hip": ["-ffp-contract=off"], "decode.hip": VGPR_MFMA, "prefill.hip": VGPR_MFMA}
 
 
 def _compile(src):

@@ -26,6 +26,7 @@
 #include "layout.h"
 #include "mfma.h"
 #include "q8_0.h"
+#include "decode_common.h"
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -38,11 +39,6 @@
 
 namespace fnkv {
 
-constexpr float kNegInf = -__builtin_inff();
-constexpr int32_t kCodeBytes = 16384;  // a tile's K and V codes
-constexpr int32_t kScaleBytes = 1024;  // a tile's K and V scales
-constexpr int32_t kGroupLds = kCodeBytes + 2 * kScaleBytes;
-
 // A tile group is NT waves sharing one tile stream, wave r of the group computing row tile r (query rows 16 r ..
 // 16 r + 15); a workgroup holds GR groups (8 waves for NT = 1 and 2, 6 for NT = 3: two waves a SIMD).
 template <int NT> struct dec_shape {
@@ -50,57 +46,6 @@ template <int NT> struct dec_shape {
     static constexpr int WAVES = NT * GR;
 };
 
-
-struct dec_args {
-    pool_view pv;
-    const uint16_t * q; // fp16 [n_seq][T][hq][256]
-    const void * k_new; // optional [n_seq][T][h_kv][256] fp16 / fp32: the step's new cells, appended by the launch
-    const void * v_new;
-    int32_t new_f32;
-    float * po;         // [total_splits][h_kv][R][256] partial accumulators
-    float * pml;        // [total_splits][h_kv][R][2] partial (m, l), base-2 domain
-    float c2;           // scale * log2(e)
-    int32_t layer, T, G, hq, R, n_seq, split_tokens;
-    int32_t slot[FNKV_MAX_SEQS];
-    int64_t ctx[FNKV_MAX_SEQS];
-    int32_t split0[FNKV_MAX_SEQS + 1]; // first split of each sequence; split0[n_seq] = total
-#ifdef FNKV_TIMING
-    uint64_t * ts; // per workgroup: 16 real-time stamps (instrumented builds only)
-#endif
-};
-
-#ifdef FNKV_TIMING
-#define FNKV_STAMP(k)                                                                                                \
-    do {                                                                                                             \
-        if (a.ts != nullptr && threadIdx.x == 0) {                                                                   \
-            a.ts[(blockIdx.y * gridDim.x + blockIdx.x) * 16 + (k)] = __builtin_amdgcn_s_memrealtime();                   \
-        }                                                                                                            \
-        __builtin_amdgcn_s_waitcnt(0);                                                                               \
-    } while (0)
-#define FNKV_STAMP_WAVE()                                                                                            \
-    do {                                                                                                             \
-        if (a.ts != nullptr && (threadIdx.x & 63) == 0) {                                                            \
-            a.ts[(blockIdx.y * gridDim.x + blockIdx.x) * 16 + 8 + (threadIdx.x >> 6)] =                              \
-                __builtin_amdgcn_s_memrealtime();                                                                    \
-        }                                                                                                            \
-        __builtin_amdgcn_s_waitcnt(0);                                                                               \
-    } while (0)
-#else
-#define FNKV_STAMP_WAVE()                                                                                            \
-    do {                                                                                                             \
-    } while (0)
-#define FNKV_STAMP(k)                                                                                                \
-    do {                                                                                                             \
-    } while (0)
-#endif
-
-__device__ __forceinline__ int32_t seq_of(const dec_args & a, int32_t split) {
-    int32_t s = 0;
-    while (s + 1 < a.n_seq && a.split0[s + 1] <= split) {
-        ++s;
-    }
-    return s;
-}
 
 // A tile is 17 chunks of 1 KiB: 8 of K codes, 8 of V codes, 1 of scales. The K codes and the scale chunk stream into
 // the group's LDS slot (wave r of a group of NT issuing chunks r, r + NT, ... of those 9); every wave loads the V
@@ -165,172 +110,6 @@ template <int NT> __device__ __forceinline__ void group_sync() {
     if (NT > 1) {
         barrier_keep_loads();
     }
-}
-
-// The step's new cells ctx - T .. ctx - 1 that fall in this split [begin, end): quantized and written here (each
-// position lies in exactly one split, so one workgroup writes it and only that workgroup reads it in this launch).
-// The barrier's workgroup-scope release / acquire makes the stores visible to the workgroup's own later loads; an
-// agent-scope fence would write back and invalidate the whole L2 under every other workgroup's stream.
-template <int WAVES>
-__device__ __forceinline__ void append_new_cells(const dec_args & a, const int32_t * table, int32_t s, int32_t kvh,
-                                                 int64_t ctx, int64_t begin, int64_t end, int32_t wave,
-                                                 int32_t lane) {
-    if (a.k_new == nullptr) {
-        return;
-    }
-    const pool_view & pv = a.pv;
-    const int64_t first_new = ctx - a.T;
-    const int64_t p0 = begin > first_new ? begin : first_new;
-    const int32_t nrow = static_cast<int32_t>(end - p0);
-    if (nrow <= 0) {
-        return;
-    }
-    for (int32_t job = wave; job < 2 * nrow; job += WAVES) {
-        const int64_t pos = p0 + (job >> 1);
-        const int32_t kv = job & 1;
-        const int64_t src = ((int64_t(s) * a.T + (pos - first_new)) * pv.h_kv + kvh) * kHeadDim;
-        float x[4];
-        if (a.new_f32) {
-            load4<true>(static_cast<const float *>(kv ? a.v_new : a.k_new) + src, lane, x);
-        } else {
-            load4<false>(static_cast<const uint16_t *>(kv ? a.v_new : a.k_new) + src, lane, x);
-        }
-        quantize_store(x, lane, tile_of(pv, table, a.layer, kvh, pos), static_cast<int32_t>(pos & 31), kv);
-    }
-    __syncthreads();
-}
-
-// Query row tile rt (row 16 rt + j of the G T rows of KV head kvh; padding rows read as zero and take the last
-// token's causal limit): the Q operands (B of S^T = K Q^T: lane (row j, group qg) holds q[row][32 b + 8 qg .. + 7])
-// and the bias operand. K codes enter the MFMA as 1152 + code, so S^T carries 1152 * sum_b s_k[t][b] * sigma_b[row]
-// with sigma_b the block's sum of q; one MFMA a half computes that sum from the K scales (A: s_k twice) and sigma_b as
-// hi + lo fp16 (B: lane (row j, qg) holds sigma_hi for qg 0, sigma_lo for qg 1, else 0), and one FMA a score takes it
-// back out. lim: the row's last visible cell.
-__device__ __forceinline__ void load_q_operands(const dec_args & a, int32_t s, int32_t kvh, int32_t rt, int32_t j,
-                                                int32_t qg, half8 (&qop)[kBlocks], half8 & sig, int64_t & lim) {
-    const int32_t row = rt * 16 + j;
-    const bool real_row = row < a.R;
-    const int32_t t_row = real_row ? row / a.G : a.T - 1;
-    lim = a.ctx[s] - a.T + t_row;
-    const uint16_t * qrow =
-        a.q + ((int64_t(s) * a.T + t_row) * a.hq + int64_t(kvh) * a.G + (real_row ? row % a.G : 0)) * kHeadDim;
-    float sigma[kBlocks];
-#pragma unroll
-    for (int b = 0; b < kBlocks; ++b) {
-        u32x4 v = {0, 0, 0, 0};
-        if (real_row) {
-            v = *reinterpret_cast<const u32x4 *>(qrow + b * kQK + 8 * qg);
-        }
-        qop[b] = __builtin_bit_cast(half8, v);
-        float sum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            sum += static_cast<float>(qop[b][i]);
-        }
-        sum += __shfl_xor(sum, 16);
-        sum += __shfl_xor(sum, 32);
-        sigma[b] = sum;
-    }
-#pragma unroll
-    for (int b = 0; b < kBlocks; ++b) {
-        const _Float16 hi = static_cast<_Float16>(sigma[b]);
-        const _Float16 lo = static_cast<_Float16>(sigma[b] - static_cast<float>(hi));
-        sig[b] = qg == 0 ? hi : qg == 1 ? lo : static_cast<_Float16>(0.0f);
-    }
-}
-
-// S^T = K Q^T for a tile's two 16-token halves from its K codes (kb) and scales (sc_tile + kKScales ...) in LDS:
-// sc[h][r] is the score of token 16 h + 4 qg + r against this lane's row j, unscaled (q . k)
-// The Q operand of block b comes from qop(b): registers, or LDS where registers are short.
-template <typename QOP>
-__device__ __forceinline__ void tile_scores(const uint8_t * kb, const uint8_t * sc_tile, const QOP & qop, half8 sig,
-                                            int32_t j, int32_t qg, int32_t lane, floatx4 (&sc)[2]) {
-    const half8 zero8 = {};
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        // this lane's score rows are tokens 16 h + 4 qg + r; their K scales, all 8 blocks
-        half8 ks[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            ks[r] = *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + 4 * qg + r) * 16);
-        }
-        // the bias term: A = this lane's token row of K scales (twice), B = sigma hi / lo
-        const half8 srow =
-            qg < 2 ? *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + j) * 16) : zero8;
-        const floatx4 corr = mfma16(srow, sig, floatx4{0.0f, 0.0f, 0.0f, 0.0f});
-        floatx4 acc_s = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) { // blocks 4 hb .. 4 hb + 3 (fewer live results)
-            floatx4 t[4];
-#pragma unroll
-            for (int ld = 2 * hb; ld < 2 * hb + 2; ++ld) {
-                const u32x4 kw = *reinterpret_cast<const u32x4 *>(kb + h * 4096 + ld * 1024 + lane * 16);
-#pragma unroll
-                for (int bb = 0; bb < 2; ++bb) {
-                    const int b = 2 * ld + bb;
-                    const half8 ka = widen8_biased(kw[2 * bb], kw[2 * bb + 1]);
-                    t[b - 4 * hb] = mfma16(ka, qop(b), floatx4{0.0f, 0.0f, 0.0f, 0.0f});
-                }
-            }
-#pragma unroll
-            for (int b = 4 * hb; b < 4 * hb + 4; ++b) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    acc_s[r] = __builtin_fmaf(static_cast<float>(ks[r][b]), t[b - 4 * hb][r], acc_s[r]);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            sc[h][r] = __builtin_fmaf(-1152.0f, corr[r], acc_s[r]);
-        }
-        __builtin_amdgcn_sched_barrier(0); // one half's operands live at a time
-    }
-}
-
-// Online softmax (base 2) of a tile's scores for this lane's row, tokens past lim_rel (tile-relative) masked. The
-// row's reference m_run moves only when the tile's max exceeds it by more than kLazyLog2 (then alpha = 2^(m_old - m),
-// the factor the row's accumulators take before this tile's terms; else alpha = 1), so the rescale of the
-// accumulators is rare; the weights pf[4 h + r] = 2^(c2 sc - m_run) stay <= 2^kLazyLog2 = 64, which keeps a weight
-// times a V scale (at most 65504 / 127) inside fp16. alpha is the same in the row's four lanes.
-constexpr float kLazyLog2 = 6.0f;
-__device__ __forceinline__ void tile_softmax(const floatx4 (&sc)[2], int32_t lim_rel, float c2, int32_t qg,
-                                             float & m_run, float & l_run, float (&pf)[8], float & alpha) {
-    float mx = kNegInf;
-    if (__all(lim_rel >= 31)) { // the whole tile is visible to every row of the wave
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                pf[4 * h + r] = sc[h][r] * c2;
-                mx = fmaxf(mx, pf[4 * h + r]);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float x = 16 * h + 4 * qg + r <= lim_rel ? sc[h][r] * c2 : kNegInf;
-                pf[4 * h + r] = x;
-                mx = fmaxf(mx, x);
-            }
-        }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const bool move = mx > m_run + kLazyLog2; // m_run = -inf: any visible score moves it
-    const float m_new = move ? mx : m_run;
-    const float m_use = m_new == kNegInf ? 0.0f : m_new;
-    alpha = move ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
-    float lsum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        pf[i] = __builtin_amdgcn_exp2f(pf[i] - m_use);
-        lsum += pf[i];
-    }
-    l_run = __builtin_fmaf(l_run, alpha, lsum);
-    m_run = m_new;
 }
 
 template <int NT>
@@ -496,8 +275,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     }
 
     // ---- merge the groups per row tile in LDS, write the workgroup's partial ----
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    l_run = rows_sum(l_run);
     constexpr int32_t kOStride = kHeadDim + 4;
     __syncthreads(); // the tile buffers are no longer read
     FNKV_STAMP(5);
@@ -568,7 +346,9 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
 // of the value blocks (NT = 2: 4 blocks each; NT = 3: 3, 3, 2), from V codes it loaded into its registers: each V byte
 // is loaded once, widened once, and a wave's accumulators stay at 64 - 72 registers. K streams through a ring of SK
 // LDS slots (SK - 1 tiles ahead), V through two register buffers (two tiles ahead); the loop is unrolled by two so
-// the buffers are fixed registers. The Q operands, the same for every group, sit once in LDS.
+// the buffers are fixed registers. The Q operands stay in registers at NT = 2 and sit once in LDS at NT = 3. The
+// groups of the second half run half an iteration behind the first (see the loop), so the two waves sharing a SIMD
+// are in different phases.
 template <int NT> struct rows_shape {
     static constexpr int GR = NT == 2 ? 4 : 2;                      // tile groups a workgroup
     static constexpr int WAVES = NT * GR;
@@ -579,7 +359,7 @@ template <int NT> struct rows_shape {
     static constexpr int PX = 2 * NT * 64 * 32;                     // P: [parity][row tile][lane] ph, pl
     static constexpr int AX = 2 * NT * 16 * 4;                      // rescale factors: [parity][row tile][row]
     static constexpr int GROUP_LDS = SK * KSLOT + PX + AX;
-    static constexpr int Q_LDS = NT * kBlocks * 64 * 16;            // Q operands of all row tiles, shared by the groups
+    static constexpr int Q_LDS = NT == 2 ? 0 : NT * kBlocks * 64 * 16; // Q operands (NT = 3), shared by the groups
     // loads a wave has issued after tile k's K chunks when it waits for them (top of iteration k), and after tile
     // k's V codes when it waits for those (before PV of iteration k)
     static constexpr int WAIT_K = NBM + (SK - 2) * (CK + NBM);
@@ -612,8 +392,14 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
 
     half8 sig;
     int64_t lim;
+    // the Q operands: in registers at NT = 2; at NT = 3 registers are short and they sit once in LDS (after the
+    // groups' buffers), the same for every group
+    constexpr bool kQReg = NT == 2;
+    half8 qreg[kQReg ? kBlocks : 1];
     uint8_t * const qlds = smem + GR * SH::GROUP_LDS; // [row tile][block][lane] 16 B
-    {
+    if constexpr (kQReg) {
+        load_q_operands(a, s, kvh, w, j, qg, qreg, sig, lim);
+    } else {
         half8 qop[kBlocks];
         load_q_operands(a, s, kvh, w, j, qg, qop, sig, lim);
         if (grp == 0) { // read before the first tile by the loop's first barrier
@@ -623,7 +409,13 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
             }
         }
     }
-    auto qop_lds = [&](int b) { return *reinterpret_cast<const half8 *>(qlds + (w * kBlocks + b) * 1024 + lane * 16); };
+    auto qop_lds = [&](int b) {
+        if constexpr (kQReg) {
+            return qreg[b];
+        } else {
+            return *reinterpret_cast<const half8 *>(qlds + (w * kBlocks + b) * 1024 + lane * 16);
+        }
+    };
 
     const int32_t b0 = NT == 2 ? 4 * w : 3 * w; // this wave's value blocks b0 .. b0 + nb - 1
     const int32_t nb = NT == 2 ? 4 : (w < 2 ? 3 : 2);
@@ -699,98 +491,163 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
         }
     };
 
-    // Issue order, per wave, identical in the prologue and every iteration: K(k + SK - 1), then V(k + 2), for
-    // k = -(SK - 1) .. -1 in the prologue (placeholders where k + 2 < 0), then one pair an iteration.
+    // The groups of the workgroup's second half run half an iteration behind the first half (their PV of tile
+    // k - 1 falls between the barriers where the first half computes tile k's scores, and their scores of tile k
+    // where the first half accumulates PV of tile k). Each SIMD holds one wave of each half, so the matrix-core
+    // heavy PV of one overlaps the VALU-heavy scores and softmax of the other instead of both doing the same phase.
+    // Every wave passes the same barriers: two an iteration, n_iter + 1 iterations.
     const int32_t n_iter = (((n_tiles + GR - 1) / GR) + 1) & ~1;
-#pragma unroll
-    for (int32_t k = -(SK - 1); k < 0; ++k) {
-        issue_k(tile_ptr(k + SK - 1), k + SK - 1);
-        if (k + 2 == 0) {
-            load_v(tile_ptr(0), vbuf0);
-        } else if (k + 2 == 1) {
-            load_v(tile_ptr(1), vbuf1);
-        } else {
-            issue_placeholder(tile_ptr(k + SK - 1), k + SK - 1);
-        }
-    }
-    FNKV_STAMP(2);
-
+    const bool late = grp >= GR / 2;
     const half8 zero8 = {};
-    auto iteration = [&](auto par_c, int32_t k, u32x4 (&vb)[NBM]) {
-        constexpr int32_t par = decltype(par_c)::value; // k & 1
-        const bool have = grp + k * GR < n_tiles;
-        wait_vmcnt<SH::WAIT_K>(); // this wave's chunks of tile k's K copy have landed
-        barrier_keep_loads();     // ... every wave's; slot (k - 1) % SK and P buffers of k - 2 are free
-        issue_k(tile_ptr(k + SK - 1), (k + SK - 1) % SK);
+    FNKV_PHASE_DECL();
+
+    // scores and softmax of tile k (row tile w) -> P and the rescale factor into the exchange buffers of parity PAR
+    auto qk_phase = [&](auto par_c, int32_t k) {
+        constexpr int32_t par = decltype(par_c)::value;
+        if (grp + k * GR >= n_tiles) {
+            return;
+        }
         const uint8_t * kb = kslot(k % SK);
         const uint8_t * sc_tile = kb + kCodeBytes / 2 - kKScales; // scale offsets are tile-relative
-        if (have) {
-            const int64_t tok0 = begin + int64_t(grp + k * GR) * kTileTokens;
-            floatx4 sc[2];
-            tile_scores(kb, sc_tile, qop_lds, sig, j, qg, lane, sc);
-            const int64_t lim_rel64 = lim - tok0;
-            const int32_t lim_rel = lim_rel64 > 64 ? 64 : static_cast<int32_t>(lim_rel64 < -1 ? -1 : lim_rel64);
-            float pf[8];
-            float alpha;
-            tile_softmax(sc, lim_rel, a.c2, qg, m_run, l_run, pf, alpha);
-            half8 ph, pl;
-            split_hilo(pf, ph, pl);
-            u32x4 * px = reinterpret_cast<u32x4 *>(pslot(par, w) + lane * 32);
-            px[0] = __builtin_bit_cast(u32x4, ph);
-            px[1] = __builtin_bit_cast(u32x4, pl);
-            if (qg == 0) {
-                aslot(par, w)[j] = alpha;
+        const int64_t tok0 = begin + int64_t(grp + k * GR) * kTileTokens;
+        floatx4 sc[2];
+        tile_scores(kb, sc_tile, qop_lds, sig, j, qg, lane, sc);
+        const int64_t lim_rel64 = lim - tok0;
+        const int32_t lim_rel = lim_rel64 > 64 ? 64 : static_cast<int32_t>(lim_rel64 < -1 ? -1 : lim_rel64);
+        float pf[8];
+        float alpha;
+        tile_softmax(sc, lim_rel, a.c2, qg, m_run, l_run, pf, alpha);
+        half8 ph, pl;
+        split_hilo(pf, ph, pl);
+        u32x4 * px = reinterpret_cast<u32x4 *>(pslot(par, w) + lane * 32);
+        px[0] = __builtin_bit_cast(u32x4, ph);
+        px[1] = __builtin_bit_cast(u32x4, pl);
+        if (qg == 0) {
+            aslot(par, w)[j] = alpha;
+        }
+    };
+    // O^T += V^T P^T of tile k over this wave's value blocks, for every row tile, from the exchange buffers of
+    // parity PAR and the V codes in vb
+    auto pv_phase = [&](auto par_c, int32_t k, u32x4 (&vb)[NBM]) {
+        constexpr int32_t par = decltype(par_c)::value;
+        if (k < 0 || grp + k * GR >= n_tiles) {
+            return;
+        }
+        wait_vmcnt<SH::WAIT_V>(); // tile k's V codes (the K copies and V codes issued after them may be pending)
+        const uint8_t * sc_tile = kslot(k % SK) + kCodeBytes / 2 - kKScales;
+        const half8 sva = j < 8 ? *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + j * 16) : zero8;
+        half8 ph[NT], pl[NT];
+#pragma unroll
+        for (int32_t rt = 0; rt < NT; ++rt) {
+            const u32x4 * px = reinterpret_cast<const u32x4 *>(pslot(par, rt) + lane * 32);
+            ph[rt] = __builtin_bit_cast(half8, px[0]);
+            pl[rt] = __builtin_bit_cast(half8, px[1]);
+            const float alpha = aslot(par, rt)[j];
+            if (__any(alpha != 1.0f)) {
+#pragma unroll
+                for (int32_t i = 0; i < NBM; ++i) {
+                    acc[rt][i][0] *= alpha;
+                    acc[rt][i][1] *= alpha;
+                }
+                lv[rt] *= alpha;
+            }
+            lv[rt] = mfma16(sva, ph[rt], lv[rt]);
+            lv[rt] = mfma16(sva, pl[rt], lv[rt]);
+        }
+#pragma unroll
+        for (int32_t i = 0; i < NBM; ++i) {
+            if (i < nb) {
+                const half8 vs = *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + (b0 + i) * 16);
+                const half8 va0 = widen8_biased(vb[i][0], vb[i][1]);
+                const half8 va1 = widen8_biased(vb[i][2], vb[i][3]);
+                half8 hi[NT], lo[NT];
+#pragma unroll
+                for (int32_t rt = 0; rt < NT; ++rt) {
+                    scale_hilo_pk(ph[rt], pl[rt], vs, hi[rt], lo[rt]);
+                }
+                // the hi terms of every row tile, then the lo terms: dependent MFMAs 2 NT apart
+#pragma unroll
+                for (int32_t rt = 0; rt < NT; ++rt) {
+                    acc[rt][i][0] = mfma16(va0, hi[rt], acc[rt][i][0]);
+                    acc[rt][i][1] = mfma16(va1, hi[rt], acc[rt][i][1]);
+                }
+#pragma unroll
+                for (int32_t rt = 0; rt < NT; ++rt) {
+                    acc[rt][i][0] = mfma16(va0, lo[rt], acc[rt][i][0]);
+                    acc[rt][i][1] = mfma16(va1, lo[rt], acc[rt][i][1]);
+                }
             }
         }
+    };
+
+    // First half. Issue order, identical in the prologue and every iteration: K(k + SK - 1), then V(k + 2)
+    // (k = -(SK - 1) .. -1 in the prologue, placeholders where k + 2 < 0). Iteration k: [wait K(k), barrier A,
+    // issue K(k + SK - 1) into the slot of tile k - 1, scores of k] [barrier B, PV of k, issue V(k + 2)].
+    auto early_iteration = [&](auto par_c, int32_t k, u32x4 (&vb)[NBM]) {
+        FNKV_PHASE(0 + (k > 0 ? 7 : 0));
+        wait_vmcnt<SH::WAIT_K>(); // this wave's chunks of tile k's K copy have landed
+        FNKV_PHASE(1);
+        barrier_keep_loads();     // ... every wave's; slot (k - 1) % SK and P buffers of k - 2 are free
+        FNKV_PHASE(2);
+        issue_k(tile_ptr(k + SK - 1), (k + SK - 1) % SK);
+        qk_phase(par_c, k);
+        FNKV_PHASE(3);
         barrier_keep_loads(); // every row tile's P and factors are in LDS
-        if (have) {
-            wait_vmcnt<SH::WAIT_V>(); // tile k's V codes (tile k + 1's K copy and V codes are younger)
-            const half8 sva =
-                j < 8 ? *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + j * 16) : zero8;
-            half8 ph[NT], pl[NT];
-#pragma unroll
-            for (int32_t rt = 0; rt < NT; ++rt) {
-                const u32x4 * px = reinterpret_cast<const u32x4 *>(pslot(par, rt) + lane * 32);
-                ph[rt] = __builtin_bit_cast(half8, px[0]);
-                pl[rt] = __builtin_bit_cast(half8, px[1]);
-                const float alpha = aslot(par, rt)[j];
-                if (__any(alpha != 1.0f)) {
-#pragma unroll
-                    for (int32_t i = 0; i < NBM; ++i) {
-                        acc[rt][i][0] *= alpha;
-                        acc[rt][i][1] *= alpha;
-                    }
-                    lv[rt] *= alpha;
-                }
-                lv[rt] = mfma16(sva, ph[rt], lv[rt]);
-                lv[rt] = mfma16(sva, pl[rt], lv[rt]);
-            }
-#pragma unroll
-            for (int32_t i = 0; i < NBM; ++i) {
-                if (i < nb) {
-                    const half8 vs =
-                        *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + (b0 + i) * 16);
-                    const half8 va0 = widen8_biased(vb[i][0], vb[i][1]);
-                    const half8 va1 = widen8_biased(vb[i][2], vb[i][3]);
-#pragma unroll
-                    for (int32_t rt = 0; rt < NT; ++rt) {
-                        half8 hi, lo;
-                        scale_hilo_pk(ph[rt], pl[rt], vs, hi, lo);
-                        acc[rt][i][0] = mfma16(va0, hi, acc[rt][i][0]);
-                        acc[rt][i][1] = mfma16(va1, hi, acc[rt][i][1]);
-                        acc[rt][i][0] = mfma16(va0, lo, acc[rt][i][0]);
-                        acc[rt][i][1] = mfma16(va1, lo, acc[rt][i][1]);
-                    }
-                }
-            }
-        }
+        FNKV_PHASE(4);
+        pv_phase(par_c, k, vb);
+        FNKV_PHASE(6);
         load_v(tile_ptr(k + 2), vb);
     };
-    for (int32_t k = 0; k < n_iter; k += 2) {
-        iteration(std::integral_constant<int32_t, 0>(), k, vbuf0);
-        iteration(std::integral_constant<int32_t, 1>(), k + 1, vbuf1);
+    // Second half. Issue order: V(k + 1), then K(k + SK - 1) (prologue k = -(SK - 1) .. -1, placeholders where
+    // k + 1 < 0). Iteration k: [barrier A, PV of k - 1, issue V(k + 1)] [wait K(k), barrier B, issue K(k + SK - 1)
+    // into the slot of tile k - 1, scores of k].
+    auto late_iteration = [&](auto par_c, int32_t k, u32x4 (&vb_prev)[NBM]) {
+        constexpr int32_t par = decltype(par_c)::value;
+        barrier_keep_loads(); // P of tile k - 1 is in LDS
+        pv_phase(std::integral_constant<int32_t, 1 - par>(), k - 1, vb_prev);
+        load_v(tile_ptr(k + 1), vb_prev);
+        wait_vmcnt<SH::WAIT_K>(); // this wave's chunks of tile k's K copy have landed
+        barrier_keep_loads();     // ... every wave's; PV of k - 1 no longer reads slot (k - 1) % SK
+        issue_k(tile_ptr(k + SK - 1), (k + SK - 1) % SK);
+        qk_phase(par_c, k);
+    };
+
+    if (!late) {
+#pragma unroll
+        for (int32_t k = -(SK - 1); k < 0; ++k) {
+            issue_k(tile_ptr(k + SK - 1), k + SK - 1);
+            if (k + 2 == 0) {
+                load_v(tile_ptr(0), vbuf0);
+            } else if (k + 2 == 1) {
+                load_v(tile_ptr(1), vbuf1);
+            } else {
+                issue_placeholder(tile_ptr(k + SK - 1), k + SK - 1);
+            }
+        }
+        FNKV_STAMP(2);
+        for (int32_t k = 0; k < n_iter; k += 2) {
+            early_iteration(std::integral_constant<int32_t, 0>(), k, vbuf0);
+            early_iteration(std::integral_constant<int32_t, 1>(), k + 1, vbuf1);
+        }
+        early_iteration(std::integral_constant<int32_t, 0>(), n_iter, vbuf0); // past the end: barriers only
+    } else {
+#pragma unroll
+        for (int32_t k = -(SK - 1); k < 0; ++k) {
+            if (k + 1 == 0) {
+                load_v(tile_ptr(0), vbuf0);
+            } else {
+                issue_placeholder(tile_ptr(k + SK - 1), k + SK - 1); // the copy issued just below
+            }
+            issue_k(tile_ptr(k + SK - 1), k + SK - 1);
+        }
+        for (int32_t k = 0; k < n_iter; k += 2) {
+            late_iteration(std::integral_constant<int32_t, 0>(), k, vbuf1);
+            late_iteration(std::integral_constant<int32_t, 1>(), k + 1, vbuf0);
+        }
+        late_iteration(std::integral_constant<int32_t, 0>(), n_iter, vbuf1); // PV of the last tile
     }
     wait_vmcnt<0>();
+    FNKV_PHASE_STORE();
     FNKV_STAMP(3);
     FNKV_STAMP_WAVE();
 
@@ -816,8 +673,7 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
     }
 
     // ---- merge the groups in LDS, write the workgroup's partial ----
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    l_run = rows_sum(l_run);
     constexpr int32_t kRows = NT * 16;
     constexpr int32_t kOStride = kHeadDim + 4;
     __syncthreads(); // the ring and exchange buffers are no longer read

@@ -1,0 +1,266 @@
+// Shared by the decode kernels (decode.hip): launch arguments, the fused append of the step's new
+// cells, the Q operands, the score and softmax steps of one 32-token tile.
+#pragma once
+
+#include "../../include/fnkv.h"
+#include "common.h"
+#include "layout.h"
+#include "mfma.h"
+#include "q8_0.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace fnkv {
+
+constexpr float kNegInf = -__builtin_inff();
+constexpr int32_t kCodeBytes = 16384;  // a tile's K and V codes
+constexpr int32_t kScaleBytes = 1024;  // a tile's K and V scales
+constexpr int32_t kGroupLds = kCodeBytes + 2 * kScaleBytes;
+
+struct dec_args {
+    pool_view pv;
+    const uint16_t * q; // fp16 [n_seq][T][hq][256]
+    const void * k_new; // optional [n_seq][T][h_kv][256] fp16 / fp32: the step's new cells, appended by the launch
+    const void * v_new;
+    int32_t new_f32;
+    float * po;         // [total_splits][h_kv][R][256] partial accumulators
+    float * pml;        // [total_splits][h_kv][R][2] partial (m, l), base-2 domain
+    float c2;           // scale * log2(e)
+    int32_t layer, T, G, hq, R, n_seq, split_tokens;
+    int32_t slot[FNKV_MAX_SEQS];
+    int64_t ctx[FNKV_MAX_SEQS];
+    int32_t split0[FNKV_MAX_SEQS + 1]; // first split of each sequence; split0[n_seq] = total
+#ifdef FNKV_TIMING
+    uint64_t * ts; // per workgroup: 16 real-time stamps (instrumented builds only)
+#endif
+};
+
+#ifdef FNKV_TIMING
+#define FNKV_STAMP(k)                                                                                                \
+    do {                                                                                                             \
+        if (a.ts != nullptr && threadIdx.x == 0) {                                                                   \
+            a.ts[(blockIdx.y * gridDim.x + blockIdx.x) * 16 + (k)] = __builtin_amdgcn_s_memrealtime();                   \
+        }                                                                                                            \
+        __builtin_amdgcn_s_waitcnt(0);                                                                               \
+    } while (0)
+#define FNKV_STAMP_WAVE()                                                                                            \
+    do {                                                                                                             \
+        if (a.ts != nullptr && (threadIdx.x & 63) == 0) {                                                            \
+            a.ts[(blockIdx.y * gridDim.x + blockIdx.x) * 16 + 8 + (threadIdx.x >> 6)] =                              \
+                __builtin_amdgcn_s_memrealtime();                                                                    \
+        }                                                                                                            \
+        __builtin_amdgcn_s_waitcnt(0);                                                                               \
+    } while (0)
+// phase clocks of wave 0 (20-bit shader cycle counter, no memory counters touched), summed over the loop
+#define FNKV_PHASE_DECL() uint32_t ph_last = 0, ph_sum[8] = {0, 0, 0, 0, 0, 0, 0, 0}
+#define FNKV_PHASE(p)                                                                                                \
+    do {                                                                                                             \
+        const uint32_t now = static_cast<uint32_t>(__builtin_amdgcn_s_memtime());                                  \
+        if ((p) > 0) {                                                                                               \
+            ph_sum[(p)-1] += now - ph_last;                                                                          \
+        }                                                                                                            \
+        ph_last = now;                                                                                               \
+    } while (0)
+#define FNKV_PHASE_STORE()                                                                                           \
+    do {                                                                                                             \
+        if (a.ts != nullptr && threadIdx.x == 0) {                                                                   \
+            for (int p_ = 0; p_ < 8; ++p_) {                                                                         \
+                a.ts[4096 * 16 + (blockIdx.y * gridDim.x + blockIdx.x) * 8 + p_] = ph_sum[p_];                        \
+            }                                                                                                        \
+        }                                                                                                            \
+    } while (0)
+#else
+#define FNKV_PHASE_DECL()                                                                                            \
+    do {                                                                                                             \
+    } while (0)
+#define FNKV_PHASE(p)                                                                                                \
+    do {                                                                                                             \
+    } while (0)
+#define FNKV_PHASE_STORE()                                                                                           \
+    do {                                                                                                             \
+    } while (0)
+#define FNKV_STAMP_WAVE()                                                                                            \
+    do {                                                                                                             \
+    } while (0)
+#define FNKV_STAMP(k)                                                                                                \
+    do {                                                                                                             \
+    } while (0)
+#endif
+
+__device__ __forceinline__ int32_t seq_of(const dec_args & a, int32_t split) {
+    int32_t s = 0;
+    while (s + 1 < a.n_seq && a.split0[s + 1] <= split) {
+        ++s;
+    }
+    return s;
+}
+
+// The step's new cells ctx - T .. ctx - 1 that fall in this split [begin, end): quantized and written here (each
+// position lies in exactly one split, so one workgroup writes it and only that workgroup reads it in this launch).
+// The barrier's workgroup-scope release / acquire makes the stores visible to the workgroup's own later loads; an
+// agent-scope fence would write back and invalidate the whole L2 under every other workgroup's stream.
+template <int WAVES>
+__device__ __forceinline__ void append_new_cells(const dec_args & a, const int32_t * table, int32_t s, int32_t kvh,
+                                                 int64_t ctx, int64_t begin, int64_t end, int32_t wave,
+                                                 int32_t lane) {
+    if (a.k_new == nullptr) {
+        return;
+    }
+    const pool_view & pv = a.pv;
+    const int64_t first_new = ctx - a.T;
+    const int64_t p0 = begin > first_new ? begin : first_new;
+    const int32_t nrow = static_cast<int32_t>(end - p0);
+    if (nrow <= 0) {
+        return;
+    }
+    for (int32_t job = wave; job < 2 * nrow; job += WAVES) {
+        const int64_t pos = p0 + (job >> 1);
+        const int32_t kv = job & 1;
+        const int64_t src = ((int64_t(s) * a.T + (pos - first_new)) * pv.h_kv + kvh) * kHeadDim;
+        float x[4];
+        if (a.new_f32) {
+            load4<true>(static_cast<const float *>(kv ? a.v_new : a.k_new) + src, lane, x);
+        } else {
+            load4<false>(static_cast<const uint16_t *>(kv ? a.v_new : a.k_new) + src, lane, x);
+        }
+        quantize_store(x, lane, tile_of(pv, table, a.layer, kvh, pos), static_cast<int32_t>(pos & 31), kv);
+    }
+    __syncthreads();
+}
+
+// Query row tile rt (row 16 rt + j of the G T rows of KV head kvh; padding rows read as zero and take the last
+// token's causal limit): the Q operands (B of S^T = K Q^T: lane (row j, group qg) holds q[row][32 b + 8 qg .. + 7])
+// and the bias operand. K codes enter the MFMA as 1152 + code, so S^T carries 1152 * sum_b s_k[t][b] * sigma_b[row]
+// with sigma_b the block's sum of q; one MFMA a half computes that sum from the K scales (A: s_k twice) and sigma_b as
+// hi + lo fp16 (B: lane (row j, qg) holds sigma_hi for qg 0, sigma_lo for qg 1, else 0), and one FMA a score takes it
+// back out. lim: the row's last visible cell.
+__device__ __forceinline__ void load_q_operands(const dec_args & a, int32_t s, int32_t kvh, int32_t rt, int32_t j,
+                                                int32_t qg, half8 (&qop)[kBlocks], half8 & sig, int64_t & lim) {
+    const int32_t row = rt * 16 + j;
+    const bool real_row = row < a.R;
+    const int32_t t_row = real_row ? row / a.G : a.T - 1;
+    lim = a.ctx[s] - a.T + t_row;
+    const uint16_t * qrow =
+        a.q + ((int64_t(s) * a.T + t_row) * a.hq + int64_t(kvh) * a.G + (real_row ? row % a.G : 0)) * kHeadDim;
+    float sigma[kBlocks];
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b) {
+        u32x4 v = {0, 0, 0, 0};
+        if (real_row) {
+            v = *reinterpret_cast<const u32x4 *>(qrow + b * kQK + 8 * qg);
+        }
+        qop[b] = __builtin_bit_cast(half8, v);
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            sum += static_cast<float>(qop[b][i]);
+        }
+        sum = rows_sum(sum);
+        sigma[b] = sum;
+    }
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b) {
+        const _Float16 hi = static_cast<_Float16>(sigma[b]);
+        const _Float16 lo = static_cast<_Float16>(sigma[b] - static_cast<float>(hi));
+        sig[b] = qg == 0 ? hi : qg == 1 ? lo : static_cast<_Float16>(0.0f);
+    }
+}
+
+// S^T = K Q^T for a tile's two 16-token halves from its K codes (kb) and scales (sc_tile + kKScales ...) in LDS:
+// sc[h][r] is the score of token 16 h + 4 qg + r against this lane's row j, unscaled (q . k)
+// The Q operand of block b comes from qop(b): registers, or LDS where registers are short.
+template <typename QOP>
+__device__ __forceinline__ void tile_scores(const uint8_t * kb, const uint8_t * sc_tile, const QOP & qop, half8 sig,
+                                            int32_t j, int32_t qg, int32_t lane, floatx4 (&sc)[2]) {
+    const half8 zero8 = {};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        // this lane's score rows are tokens 16 h + 4 qg + r; their K scales, all 8 blocks
+        half8 ks[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            ks[r] = *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + 4 * qg + r) * 16);
+        }
+        // the bias term: A = this lane's token row of K scales (twice), B = sigma hi / lo
+        const half8 srow =
+            qg < 2 ? *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + j) * 16) : zero8;
+        const floatx4 corr = mfma16(srow, sig, floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+        floatx4 acc_s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) { // blocks 4 hb .. 4 hb + 3 (fewer live results)
+            floatx4 t[4];
+#pragma unroll
+            for (int ld = 2 * hb; ld < 2 * hb + 2; ++ld) {
+                const u32x4 kw = *reinterpret_cast<const u32x4 *>(kb + h * 4096 + ld * 1024 + lane * 16);
+#pragma unroll
+                for (int bb = 0; bb < 2; ++bb) {
+                    const int b = 2 * ld + bb;
+                    const half8 ka = widen8_biased(kw[2 * bb], kw[2 * bb + 1]);
+                    t[b - 4 * hb] = mfma16(ka, qop(b), floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+                }
+            }
+#pragma unroll
+            for (int b = 4 * hb; b < 4 * hb + 4; ++b) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    acc_s[r] = __builtin_fmaf(static_cast<float>(ks[r][b]), t[b - 4 * hb][r], acc_s[r]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sc[h][r] = __builtin_fmaf(-1152.0f, corr[r], acc_s[r]);
+        }
+        __builtin_amdgcn_sched_barrier(0); // one half's operands live at a time
+    }
+}
+
+// Online softmax (base 2) of a tile's scores for this lane's row, tokens past lim_rel (tile-relative) masked. The
+// row's reference m_run moves only when the tile's max exceeds it by more than kLazyLog2 (then alpha = 2^(m_old - m),
+// the factor the row's accumulators take before this tile's terms; else alpha = 1), so the rescale of the
+// accumulators is rare; the weights pf[4 h + r] = 2^(c2 sc - m_run) stay <= 2^kLazyLog2 = 64, which keeps a weight
+// times a V scale (at most 65504 / 127) inside fp16. alpha is the same in the row's four lanes.
+constexpr float kLazyLog2 = 6.0f;
+__device__ __forceinline__ void tile_softmax(const floatx4 (&sc)[2], int32_t lim_rel, float c2, int32_t qg,
+                                             float & m_run, float & l_run, float (&pf)[8], float & alpha) {
+    // the max runs on the raw scores (c2 > 0 keeps the order); each weight is one FMA and one exp2
+    float raw[8];
+    float mx = kNegInf;
+    if (__all(lim_rel >= 31)) { // the whole tile is visible to every row of the wave
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                raw[4 * h + r] = sc[h][r];
+                mx = fmaxf(mx, raw[4 * h + r]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float x = 16 * h + 4 * qg + r <= lim_rel ? sc[h][r] : kNegInf;
+                raw[4 * h + r] = x;
+                mx = fmaxf(mx, x);
+            }
+        }
+    }
+    mx = rows_max(mx) * c2;
+    const bool move = mx > m_run + kLazyLog2; // m_run = -inf: any visible score moves it
+    const float m_new = move ? mx : m_run;
+    const float m_use = m_new == kNegInf ? 0.0f : m_new;
+    alpha = move ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
+    float lsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        pf[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(raw[i], c2, -m_use));
+        lsum += pf[i];
+    }
+    l_run = __builtin_fmaf(l_run, alpha, lsum);
+    m_run = m_new;
+}
+
+} // namespace fnkv

@@ -47,8 +47,9 @@ __device__ __forceinline__ void split_hilo(const float (&x)[8], half8 & hi, half
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const fp16x2 hv = __builtin_amdgcn_cvt_pkrtz(x[2 * i], x[2 * i + 1]);
-        const float r0 = x[2 * i] - static_cast<float>(hv[0]);
-        const float r1 = x[2 * i + 1] - static_cast<float>(hv[1]);
+        // x - hi as one mixed-precision FMA each (hi read as fp16), exact
+        const float r0 = __builtin_fmaf(static_cast<float>(hv[0]), -1.0f, x[2 * i]);
+        const float r1 = __builtin_fmaf(static_cast<float>(hv[1]), -1.0f, x[2 * i + 1]);
         const fp16x2 lv = __builtin_amdgcn_cvt_pkrtz(r0, r1);
         h[i] = __builtin_bit_cast(uint32_t, hv);
         l[i] = __builtin_bit_cast(uint32_t, lv);
@@ -92,6 +93,21 @@ __device__ __forceinline__ void scale_hilo_pk(half8 ph, half8 pl, half8 s, half8
     hi = ph * s;
     const half8 rem = __builtin_elementwise_fma(ph, s, -hi);
     lo = __builtin_elementwise_fma(pl, s, rem);
+}
+
+// x combined across the wave's four 16-lane rows (lanes l, l ^ 16, l ^ 32, l ^ 48) by two lane swaps on the VALU
+// (v_permlane16_swap, v_permlane32_swap), without the LDS round trip of a shuffle
+__device__ __forceinline__ float rows_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // 8 fp32 values rounded toward zero to fp16

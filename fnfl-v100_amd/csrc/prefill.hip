@@ -213,8 +213,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(pf_args a) {
                     mx = fmaxf(mx, x);
                 }
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = rows_max(mx);
             const float m_new = fmaxf(m_run[nt], mx);
             const float m_use = m_new == kPfNegInf ? 0.0f : m_new;
             const float alpha = __builtin_amdgcn_exp2f(m_run[nt] - m_use);
@@ -253,8 +252,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(pf_args a) {
 #pragma unroll
     for (int nt = 0; nt < kPfNT; ++nt) {
         float l = l_run[nt];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
+        l = rows_sum(l);
         const int32_t r = (wave * kPfNT + nt) * 16 + j;
         const int32_t t = t_first + r / a.G;
         if (t < a.rows) {
