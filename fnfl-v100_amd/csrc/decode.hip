@@ -739,7 +739,9 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
 }
 
 // Fold the splits of each (sequence, KV head, row): one workgroup a (row, 32 values); 256 threads = 8 float4
-// columns x 32 split groups, each group summing its splits in order, the groups folded in order (deterministic).
+// columns x 32 split groups. Group g folds splits g, g + 32, ... in order with a running max (all its loads
+// independent, so they are in flight together: one memory round trip), then the 32 groups fold in order in LDS
+// (deterministic: the same order for every launch).
 struct merge_args {
     const float * po;
     const float * pml;
@@ -750,8 +752,8 @@ struct merge_args {
 
 __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
     __shared__ float sM[32];
-    __shared__ floatx4 sA[32][8];
     __shared__ float sL[32];
+    __shared__ floatx4 sA[32][8];
     const int32_t tid = static_cast<int32_t>(threadIdx.x);
     const int32_t c4 = tid & 7, g = tid >> 3;
     const int32_t chunk = static_cast<int32_t>(blockIdx.x) & 7;
@@ -761,39 +763,39 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
     const int32_t kvh = rest % a.h_kv;
     const int32_t s = rest / a.h_kv;
     const int32_t s0 = a.split0[s], n = a.split0[s + 1] - s0;
-    float M = kNegInf;
-    for (int32_t i = g; i < n; i += 32) {
-        M = fmaxf(M, a.pml[((int64_t(s0 + i) * a.h_kv + kvh) * a.R + r) * 2]);
-    }
-    if (c4 == 0) {
-        sM[g] = M;
-    }
-    __syncthreads();
-    M = kNegInf;
-    for (int32_t i = 0; i < 32; ++i) {
-        M = fmaxf(M, sM[i]);
-    }
-    const float M_use = M == kNegInf ? 0.0f : M;
+    float m = kNegInf, l = 0.0f;
     floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
-    float L = 0.0f;
+#pragma unroll 4
     for (int32_t i = g; i < n; i += 32) {
         const int64_t prow = (int64_t(s0 + i) * a.h_kv + kvh) * a.R + r;
-        const float w = __builtin_amdgcn_exp2f(a.pml[prow * 2] - M_use);
-        L = __builtin_fmaf(a.pml[prow * 2 + 1], w, L);
+        const float2 ml = *reinterpret_cast<const float2 *>(a.pml + prow * 2);
         const floatx4 o = *reinterpret_cast<const floatx4 *>(a.po + prow * kHeadDim + chunk * 32 + c4 * 4);
-        A += o * w;
+        const float m_new = fmaxf(m, ml.x);
+        const float m_use = m_new == kNegInf ? 0.0f : m_new;
+        const float f_old = __builtin_amdgcn_exp2f(m - m_use);
+        const float f_new = __builtin_amdgcn_exp2f(ml.x - m_use);
+        A = A * f_old + o * f_new;
+        l = __builtin_fmaf(l, f_old, ml.y * f_new);
+        m = m_new;
     }
     sA[g][c4] = A;
     if (c4 == 0) {
-        sL[g] = L;
+        sM[g] = m;
+        sL[g] = l;
     }
     __syncthreads();
     if (tid < 8) {
-        floatx4 As = sA[0][tid];
-        float Ls = sL[0];
-        for (int32_t i = 1; i < 32; ++i) {
-            As += sA[i][tid];
-            Ls += sL[i];
+        float M = kNegInf;
+        for (int32_t i = 0; i < 32; ++i) {
+            M = fmaxf(M, sM[i]);
+        }
+        const float M_use = M == kNegInf ? 0.0f : M;
+        floatx4 As = {0.0f, 0.0f, 0.0f, 0.0f};
+        float Ls = 0.0f;
+        for (int32_t i = 0; i < 32; ++i) {
+            const float w = __builtin_amdgcn_exp2f(sM[i] - M_use);
+            As += sA[i][tid] * w;
+            Ls = __builtin_fmaf(sL[i], w, Ls);
         }
         const int32_t t = r / a.G, h = kvh * a.G + r % a.G;
         uint16_t * o = a.out + ((int64_t(s) * a.T + t) * a.hq + h) * kHeadDim + chunk * 32 + tid * 4;
