@@ -9,11 +9,13 @@
 //
 // How (MI355X): matrix-core bound (4 d flops a visible (query, key) pair and head), so K/V tiles are dequantized once
 // a workgroup and shared by all its query rows.
-//   * A workgroup (4 waves) owns 128 query rows (128 / G query tokens x the G heads of one KV head); each wave owns
-//     two 16-row tiles. Its waves walk the key tiles (32 tokens) in order up to the block's last query position.
+//   * A workgroup (8 waves, two a SIMD, so one wave's matrix-core work overlaps the other's VALU work) owns 128 query
+//     rows (128 / G query tokens x the G heads of one KV head); each wave owns one 16-row tile. Its waves walk the
+//     key tiles (32 tokens) in order up to the block's last query position.
 //   * Each tile streams HBM -> LDS (17 direct 1 KiB loads split over the waves, double-buffered), is dequantized once
-//     into fp16 hi / lo MFMA operand planes in LDS (codes widened exactly, times the scale in fp32, split), and then
-//     every wave runs S^T = K Q^T (two v_mfma_f32_16x16x32_f16 a block a 16-token half: K hi, K lo) and
+//     into fp16 MFMA operand planes in LDS (double-buffered: tile k + 1's while tile k is computed): K as code x
+//     scale rounded once to fp16 (the reference's prompt attention rounds its K operand the same way), V exactly as
+//     hi + lo fp16; then every wave runs S^T = K Q^T (one v_mfma_f32_16x16x32_f16 a block a 16-token half) and
 //     O^T += V^T P^T (three a 16-value tile: Vhi Phi, Vlo Phi, Vhi Plo) on it.
 //   * The softmax (base 2) runs on the S^T registers exactly as in the decode kernel; P feeds the PV MFMA in place.
 #include "../../include/fnkv.h"
@@ -28,12 +30,13 @@
 
 namespace fnkv {
 
-constexpr int32_t kPfWaves = 4;
-constexpr int32_t kPfNT = 2;                         // 16-row tiles a wave
+constexpr int32_t kPfWaves = 8;                      // two a SIMD
+constexpr int32_t kPfNT = 1;                         // 16-row tiles a wave
 constexpr int32_t kPfRows = kPfWaves * kPfNT * 16;   // 128 rows a workgroup
-constexpr int32_t kPfStage = kTileBytes;             // one code tile
+constexpr int32_t kPfStage = 8 * 1024 + 1024;        // a tile's K codes, then its K and V scales
 constexpr int32_t kPfPlane = 16 * 1024;             // one fp16 operand plane of a tile (K or V, hi or lo)
-constexpr int32_t kPfLds = 2 * kPfStage + 4 * kPfPlane;
+constexpr int32_t kPfSet = 4 * kPfPlane;             // a tile's planes: K hi, K lo, V hi, V lo
+constexpr int32_t kPfLds = 2 * kPfStage + 2 * kPfSet; // staging and planes, both double-buffered
 constexpr float kPfNegInf = -__builtin_inff();
 
 struct pf_args {
@@ -45,22 +48,23 @@ struct pf_args {
     int32_t rows, G, hq, layer, slot;
 };
 
-template <bool LAST>
+// a tile's K codes (8 chunks of 1 KiB) and its scales chunk into a staging slot: wave w copies chunks w, w + 4,
+// wave 0 also the scales
 __device__ __forceinline__ void pf_issue(const uint8_t * tile, uint8_t * stage, int32_t wave, int32_t lane) {
-    // the tile's 17 chunks of 1 KiB: wave w issues chunks w, w + 4, ...
 #pragma unroll
-    for (int32_t c = 0; c < 5; ++c) {
+    for (int32_t c = 0; c < 8 / kPfWaves; ++c) {
         const int32_t ch = wave + c * kPfWaves;
-        if (ch < 17) {
-            lds_load16(tile + ch * 1024 + lane * 16, stage + ch * 1024);
-        }
+        lds_load16(tile + kKCodes + ch * 1024 + lane * 16, stage + ch * 1024);
+    }
+    if (wave == 0) {
+        lds_load16(tile + kKScales + lane * 16, stage + 8 * 1024);
     }
 }
 
-__global__ __launch_bounds__(256, 1) void prefill_kernel(pf_args a) {
+__global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
-    const int32_t wave = static_cast<int32_t>(threadIdx.x) >> 6;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(threadIdx.x) >> 6);
     const int32_t j = lane & 15, qg = lane >> 4;
     const int32_t kvh = static_cast<int32_t>(blockIdx.y);
     const int32_t tok_per_wg = kPfRows / a.G;
@@ -109,74 +113,63 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(pf_args a) {
         const int32_t phys = table[tok >> 8];
         return layer_base + int64_t(phys) * pv.page_stride + int64_t((tok & 255) >> 5) * kTileBytes;
     };
-    uint8_t * stage_base = smem;
-    uint8_t * planes = smem + 2 * kPfStage;
+    uint8_t * const stage_base = smem;
+    uint8_t * const plane_base = smem + 2 * kPfStage;
 
-    if (n_tiles > 0) {
-        pf_issue<false>(tile_ptr(0), stage_base, wave, lane);
-    }
-    for (int32_t ti = 0; ti < n_tiles; ++ti) {
-        uint8_t * st = stage_base + (ti & 1) * kPfStage;
-        uint8_t * pl = planes; // one set: the barriers above and below order its writers and readers
-        if (ti + 1 < n_tiles) {
-            pf_issue<false>(tile_ptr(ti + 1), stage_base + ((ti + 1) & 1) * kPfStage, wave, lane);
-            // this wave issued 4 or 5 chunks for the next tile; its chunks of this tile are older than those
-            if (wave == 0) {
-                wait_vmcnt<5>();
-            } else {
-                wait_vmcnt<4>();
-            }
-        } else {
-            wait_vmcnt<0>();
-        }
-        __syncthreads(); // every wave's chunks of tile ti have landed
-
-        // ---- dequantize: wave w converts K chunks (h, ld) = w and w + 4, V chunks ld = w and w + 4 ----
+    // tile ti's K codes and scales (staging slot ti & 1) and V codes (vreg: this wave's V chunk) -> the fp16 operand
+    // planes (set ti & 1), each value exactly as hi + lo (code x scale has 8 x 11 significant bits): hi = fp16(code
+    // x scale), lo = the remainder by one fused multiply-add. Wave w converts K chunk (h, ld) = w and V chunk ld = w.
+    auto dequant = [&](int32_t ti, const u32x4 (&vreg)[8 / kPfWaves]) {
+        const uint8_t * st = stage_base + (ti & 1) * kPfStage;
+        const uint8_t * ksc = st + 8 * 1024;  // K scales [32 tokens][8 blocks]
+        const uint8_t * vsc = ksc + 512;      // V scales [4 lane groups][8 blocks][8 slots]
+        uint8_t * pl = plane_base + (ti & 1) * kPfSet;
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const int32_t kc = wave + 4 * c; // K chunk: h = kc / 4, ld = kc % 4
+        for (int32_t c = 0; c < 8 / kPfWaves; ++c) {
+            const int32_t kc = wave + c * kPfWaves; // K chunk: h = kc / 4, ld = kc % 4
             const int32_t h = kc >> 2, ld = kc & 3;
-            const u32x4 w = *reinterpret_cast<const u32x4 *>(st + kKCodes + kc * 1024 + lane * 16);
+            const u32x4 w = *reinterpret_cast<const u32x4 *>(st + kc * 1024 + lane * 16);
             // this lane's row is token 16 h + j; blocks 2 ld and 2 ld + 1
-            const half2v s2 = *reinterpret_cast<const half2v *>(st + kKScales + (16 * h + j) * 16 + ld * 4);
+            const half2v s2 = *reinterpret_cast<const half2v *>(ksc + (16 * h + j) * 16 + ld * 4);
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb) {
                 const int32_t b = 2 * ld + bb;
                 const half8 code = widen8(w[2 * bb], w[2 * bb + 1]);
-                const float sc = static_cast<float>(s2[bb]);
-                float x[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    x[i] = static_cast<float>(code[i]) * sc;
-                }
-                half8 hi, lo;
-                split_hilo(x, hi, lo);
+                const half8 sv = {s2[bb], s2[bb], s2[bb], s2[bb], s2[bb], s2[bb], s2[bb], s2[bb]};
+                const half8 hi = code * sv;
+                const half8 lo = __builtin_elementwise_fma(code, sv, -hi);
                 const int32_t off = ((h * kBlocks + b) * 64 + lane) * 16;
                 *reinterpret_cast<half8 *>(pl + off) = hi;
                 *reinterpret_cast<half8 *>(pl + kPfPlane + off) = lo;
             }
-            const int32_t vc = wave + 4 * c; // V chunk ld = vc: MFMA tiles m = 2 vc, 2 vc + 1 of block vc
-            const u32x4 vw = *reinterpret_cast<const u32x4 *>(st + kVCodes + vc * 1024 + lane * 16);
-            const half8 vs = *reinterpret_cast<const half8 *>(st + kVScales + qg * 128 + vc * 16);
+        }
+#pragma unroll
+        for (int32_t c = 0; c < 8 / kPfWaves; ++c) {
+            const int32_t vc = wave + c * kPfWaves; // V chunk ld = vc: MFMA tiles m = 2 vc, 2 vc + 1 of block vc
+            const half8 vs = *reinterpret_cast<const half8 *>(vsc + qg * 128 + vc * 16);
 #pragma unroll
             for (int mm = 0; mm < 2; ++mm) {
-                const half8 code = widen8(vw[2 * mm], vw[2 * mm + 1]);
-                float x[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    x[i] = static_cast<float>(code[i]) * static_cast<float>(vs[i]);
-                }
-                half8 hi, lo;
-                split_hilo(x, hi, lo);
+                const half8 code = widen8(vreg[c][2 * mm], vreg[c][2 * mm + 1]);
+                const half8 hi = code * vs;
+                const half8 lo = __builtin_elementwise_fma(code, vs, -hi);
                 const int32_t off = ((2 * vc + mm) * 64 + lane) * 16;
                 *reinterpret_cast<half8 *>(pl + 2 * kPfPlane + off) = hi;
                 *reinterpret_cast<half8 *>(pl + 3 * kPfPlane + off) = lo;
             }
         }
-        __syncthreads(); // the operand planes are complete
+    };
+    auto load_v = [&](int32_t ti, u32x4 (&vreg)[8 / kPfWaves]) { // this wave's V chunks of tile ti
+        const uint8_t * t = tile_ptr(ti) + kVCodes + lane * 16;
+#pragma unroll
+        for (int32_t c = 0; c < 8 / kPfWaves; ++c) {
+            vreg[c] = *reinterpret_cast<const u32x4 *>(t + (wave + c * kPfWaves) * 1024);
+        }
+    };
 
+    // tile ti on planes set ti & 1: scores, online softmax, PV
+    auto compute = [&](int32_t ti) {
+        const uint8_t * pl = plane_base + (ti & 1) * kPfSet;
         const int64_t tok0 = int64_t(ti) * kTileTokens;
-        // ---- S^T = K Q^T ----
         floatx4 sc[kPfNT][2];
 #pragma unroll
         for (int nt = 0; nt < kPfNT; ++nt) {
@@ -197,7 +190,6 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(pf_args a) {
                 }
             }
         }
-        // ---- online softmax (base 2), P split hi + lo ----
         half8 ph[kPfNT], plo[kPfNT];
 #pragma unroll
         for (int nt = 0; nt < kPfNT; ++nt) {
@@ -208,19 +200,19 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(pf_args a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int64_t pos = tok0 + 16 * h + 4 * qg + r;
-                    const float x = pos <= lim[nt] ? sc[nt][h][r] * a.c2 : kPfNegInf;
+                    const float x = pos <= lim[nt] ? sc[nt][h][r] : kPfNegInf;
                     v[4 * h + r] = x;
                     mx = fmaxf(mx, x);
                 }
             }
-            mx = rows_max(mx);
+            mx = rows_max(mx) * a.c2;
             const float m_new = fmaxf(m_run[nt], mx);
             const float m_use = m_new == kPfNegInf ? 0.0f : m_new;
             const float alpha = __builtin_amdgcn_exp2f(m_run[nt] - m_use);
             float lsum = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                v[i] = __builtin_amdgcn_exp2f(v[i] - m_use);
+                v[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[i], a.c2, -m_use));
                 lsum += v[i];
             }
             split_hilo(v, ph[nt], plo[nt]);
@@ -233,7 +225,6 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(pf_args a) {
                 }
             }
         }
-        // ---- O^T += V^T P^T ----
 #pragma unroll
         for (int m = 0; m < 16; ++m) {
             const int32_t off = (m * 64 + lane) * 16;
@@ -246,6 +237,39 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(pf_args a) {
                 acc[nt][m] = mfma16(vhi, plo[nt], acc[nt][m]);
             }
         }
+    };
+
+    // Iteration ti: [tile ti + 1's data has landed; barrier] [copy tile ti + 2's K codes and scales into the staging
+    // slot tile ti used] [dequantize tile ti + 1 into the other plane set, load this wave's V chunk of tile ti + 2]
+    // [compute tile ti]: the VALU-heavy dequantization of the next tile and the matrix-core work on this one are
+    // independent, so one wave's overlaps the other's.
+    u32x4 vreg[8 / kPfWaves] = {};
+    if (n_tiles > 0) {
+        pf_issue(tile_ptr(0), stage_base, wave, lane);
+        load_v(0, vreg);
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (n_tiles > 1) {
+            pf_issue(tile_ptr(1), stage_base + kPfStage, wave, lane);
+        }
+        dequant(0, vreg);
+        if (n_tiles > 1) {
+            load_v(1, vreg);
+        }
+    }
+    for (int32_t ti = 0; ti < n_tiles; ++ti) {
+        wait_vmcnt<0>(); // tile ti + 1's copy and V chunks (the last loads issued)
+        __syncthreads(); // ... every wave's; planes ti complete; staging slot ti & 1 and planes (ti + 1) & 1 free
+        if (ti + 2 < n_tiles) {
+            pf_issue(tile_ptr(ti + 2), stage_base + (ti & 1) * kPfStage, wave, lane);
+        }
+        if (ti + 1 < n_tiles) {
+            dequant(ti + 1, vreg);
+            if (ti + 2 < n_tiles) {
+                load_v(ti + 2, vreg);
+            }
+        }
+        compute(ti);
     }
 
     // ---- normalise and write ----
@@ -329,7 +353,7 @@ int fnkv_attn_prefill(const fnkv_pool * pool, int32_t slot, int32_t layer, int64
         attr_set[dev] = true;
     }
     const dim3 grid(static_cast<uint32_t>((rows + tok_per_wg - 1) / tok_per_wg), static_cast<uint32_t>(p->h_kv()));
-    hipLaunchKernelGGL(fnkv::prefill_kernel, grid, dim3(256), fnkv::kPfLds, static_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL(fnkv::prefill_kernel, grid, dim3(64 * fnkv::kPfWaves), fnkv::kPfLds, static_cast<hipStream_t>(stream), a);
     if (hipGetLastError() != hipSuccess) {
         set_error("fnkv_attn_prefill: launch failed");
         return FNKV_ERR_HIP;
