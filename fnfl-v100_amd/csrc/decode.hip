@@ -489,6 +489,7 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
             const int32_t b = b0 + i < kBlocks ? b0 + i : kBlocks - 1;
             vb[i] = buf_load16(r, lane16, kVCodes + b * 1024);
         }
+        keep_issued(); // older than every load issued after
     };
 
     // The groups of the workgroup's second half run half an iteration behind the first half (their PV of tile

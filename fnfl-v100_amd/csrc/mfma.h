@@ -120,11 +120,18 @@ __device__ __forceinline__ half8 to_half8_rtz(const float (&x)[8]) {
     return __builtin_bit_cast(half8, h);
 }
 
+// The kernels wait for their LDS copies by counting the loads issued after them (s_waitcnt vmcnt(n)), so every copy
+// must be issued, in program order. LLVM models a copy as a plain store to its LDS pointer: it deletes one that a later
+// identical copy overwrites (the duplicate copies that keep a wave's count uniform) and may move register loads across
+// it. The empty asm after each copy reads and writes all memory as far as the compiler knows, which forbids both.
+__device__ __forceinline__ void keep_issued() { __asm__ __volatile__("" ::: "memory"); }
+
 // a wave's 64 x 16 B from global memory straight into LDS at lds_base + 16 lane (no registers); OFF (< 4096) is added
 // to both the global and the LDS address
 template <int OFF = 0> __device__ __forceinline__ void lds_load16(const void * gptr, void * lds_base) {
     typedef __attribute__((address_space(3))) void lds_void;
     __builtin_amdgcn_global_load_lds(gptr, (lds_void *)lds_base, 16, OFF, 0);
+    keep_issued();
 }
 
 // Buffer-resource loads: the tile's address lives in four SGPRs, so a lane's address is one VGPR offset (lane * 16)
@@ -142,6 +149,7 @@ __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, int32_t voff, int32_t soff
 __device__ __forceinline__ void buf_lds16(rsrc_t r, void * lds_base, int32_t voff, int32_t soff) {
     typedef __attribute__((address_space(3))) void lds_void;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_base, 16, voff, soff, 0, 0);
+    keep_issued();
 }
 
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,

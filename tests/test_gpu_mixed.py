@@ -1,0 +1,160 @@
+"""a mixed 8-sequence pool step with page churn — three finished sequences free their pages first
+(a fragmented free list), two sequences append and attend a 4,096-token prefill chunk, six verify T = 5 — all in one
+shared pool, every layer. Parity against the oracle's fp64 attention over the decoded cache (max-abs 2e-3) at
+contexts the oracle finishes in seconds; at BASELINE's full contexts (1K..196K) the same step is checked through
+properties that do not need the oracle (finite outputs, the verify launch over six sequences against each sequence
+launched alone, the prefill chunk's last rows against a T = 5 verify of the same cells)."""
+import numpy as np
+import pytest
+
+import cases
+import fnkv
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+TOL = 2e-3
+HQ, HKV, D = 16, 2, 256
+CHUNK = 4096
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def churned_pool(n_pages, layers, seed):
+    """An 8-slot pool (plus a filler slot) whose free list has holes: three finished sequences take interleaved pages,
+    then give them back."""
+    pool = fnkv.Pool(9, n_pages, layers, HKV)
+    rng = np.random.default_rng([seed, 4])
+    finished = [5, 6, 7]
+    sizes = {s: int(rng.integers(8, 40)) for s in finished}
+    have = {s: 0 for s in finished}
+    while any(have[s] < sizes[s] for s in finished):
+        s = int(rng.choice([x for x in finished if have[x] < sizes[x]]))
+        have[s] += 1
+        assert pool.ensure(s, have[s] * 256)[0] == 0
+    for s in finished:
+        assert pool.trim(s, 0) == 0
+    return pool
+
+
+def verify_inputs(seed, n, T):
+    q = cases.queries(seed, (n, T, HQ, D))
+    rng = np.random.default_rng([seed, 5])
+    kn = rng.standard_normal((n, T, HKV, D), dtype=np.float32).astype(np.float16)
+    vn = rng.standard_normal((n, T, HKV, D), dtype=np.float32).astype(np.float16)
+    return q, kn, vn
+
+
+def test_config4_mixed_step_parity():
+    seed, layers, T = 4, 2, 5
+    rng = np.random.default_rng([seed, 1])
+    pf_slots, vf_slots = [0, 1], [2, 3, 4, 5, 6, 7]
+    pf_depth = [int(rng.integers(1000, 6000)) for _ in pf_slots]
+    vf_ctx = [int(rng.integers(1024, 24 * 1024)) for _ in vf_slots]  # BASELINE draws 1K..196K; scaled for the oracle
+    n_pages = sum(-(-(d + CHUNK) // 256) for d in pf_depth) + sum(-(-c // 256) for c in vf_ctx) + 120
+    pool = churned_pool(n_pages, layers, seed)
+    ctx_of = {}
+    for s, d in zip(pf_slots, pf_depth):
+        ctx_of[s] = d + CHUNK
+    for s, c in zip(vf_slots, vf_ctx):
+        ctx_of[s] = c
+    cases.scatter_ensure(pool, pf_slots + vf_slots, [ctx_of[s] for s in pf_slots + vf_slots], seed)
+    dec = {}
+    for layer in range(layers):
+        for s in pf_slots + vf_slots:
+            c = ctx_of[s]
+            k16, v16 = cases.kv_rows(seed * 100 + s, c, HKV, layer)
+            if s in vf_slots:  # the verify step's T new cells arrive with the launch
+                k16[c - T:], v16[c - T:] = 0, 0
+            upto = c - CHUNK if s in pf_slots else c - T
+            pool.append(s, layer, 0, torch.from_numpy(k16[:upto]).cuda(), torch.from_numpy(v16[:upto]).cuda())
+            dec[(s, layer)] = (k16, v16)
+    q_v, kn, vn = verify_inputs(seed, len(vf_slots), T)
+    errs = {}
+    for layer in range(layers):
+        # the two prefill chunks: append, then attend
+        for s in pf_slots:
+            c = ctx_of[s]
+            k16, v16 = dec[(s, layer)]
+            pool.append(s, layer, c - CHUNK, torch.from_numpy(k16[c - CHUNK:]).cuda(),
+                        torch.from_numpy(v16[c - CHUNK:]).cuda())
+            q16 = cases.queries(seed * 10 + s + layer, (CHUNK, HQ, D))
+            out = torch.empty((CHUNK, HQ, D), dtype=torch.float16, device="cuda")
+            pool.prefill(s, layer, c, torch.from_numpy(q16).cuda(), out)
+            torch.cuda.synchronize()
+            rows = [0, 1, 777, 2048, CHUNK - 2, CHUNK - 1]
+            (_, _, kf), (_, _, vf) = cases.decoded(O, k16, v16)
+            ref = O.attn_f64(q16.view(np.uint16), kf, vf, c, rows=rows)
+            errs[("prefill", layer, s)] = cases.out_err(out.cpu().numpy()[rows], ref)
+        # the six verify steps in one launch, their new cells appended by it
+        q = torch.from_numpy(q_v).cuda()
+        out = torch.empty_like(q)
+        ctxs = [ctx_of[s] for s in vf_slots]
+        ws = torch.empty(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+        pool.decode(vf_slots, ctxs, T, layer, q, out, ws, k_new=torch.from_numpy(kn).cuda(),
+                    v_new=torch.from_numpy(vn).cuda())
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        for i, s in enumerate(vf_slots):
+            c = ctx_of[s]
+            k16, v16 = dec[(s, layer)]
+            k16 = k16.copy()
+            v16 = v16.copy()
+            k16[c - T:], v16[c - T:] = kn[i], vn[i]
+            (_, _, kf), (_, _, vf) = cases.decoded(O, k16, v16)
+            ref = O.attn_f64(q_v[i].view(np.uint16), kf, vf, c)
+            errs[("verify", layer, s)] = cases.out_err(got[i], ref)
+    worst = max(errs.values())
+    assert np.isfinite(worst) and worst <= TOL, errs
+
+
+def test_config4_full_contexts_properties():
+    seed, layers, T = 41, 1, 5
+    rng = np.random.default_rng([seed, 1])
+    pf_slots, vf_slots = [0, 1], [2, 3, 4, 5, 6, 7]
+    pf_depth = [int(rng.integers(1024, 196 * 1024)) for _ in pf_slots]
+    vf_ctx = [int(rng.integers(1024, 196 * 1024)) for _ in vf_slots]
+    ctx_of = dict(zip(pf_slots, [d + CHUNK for d in pf_depth]))
+    ctx_of.update(zip(vf_slots, vf_ctx))
+    n_pages = sum(-(-c // 256) for c in ctx_of.values()) + 120
+    pool = churned_pool(n_pages, layers, seed)
+    order = pf_slots + vf_slots
+    cases.scatter_ensure(pool, order, [ctx_of[s] for s in order], seed)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    for s in order:
+        x = torch.randn((2, ctx_of[s], HKV, D), generator=g, device="cuda").half()
+        pool.append(s, 0, 0, x[0].contiguous(), x[1].contiguous())
+    # the prefill chunks: finite; the chunk's last five rows agree with a T = 5 verify over the same cells
+    for s in pf_slots:
+        c = ctx_of[s]
+        q = torch.randn((CHUNK, HQ, D), generator=g, device="cuda").half()
+        out = torch.empty_like(q)
+        pool.prefill(s, 0, c, q, out)
+        qv = q[None, -5:].contiguous()
+        ov = torch.empty_like(qv)
+        ws = torch.empty(pool.decode_ws_bytes([c], 5, HQ), dtype=torch.uint8, device="cuda")
+        pool.decode([s], [c], 5, 0, qv, ov, ws)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out.float()).all().item()
+        assert (ov[0].float() - out[-5:].float()).abs().max().item() <= 2 * TOL
+    # the six verify steps in one launch against each launched alone
+    q = torch.randn((len(vf_slots), T, HQ, D), generator=g, device="cuda").half()
+    ctxs = [ctx_of[s] for s in vf_slots]
+    out = torch.empty_like(q)
+    ws = torch.empty(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    pool.decode(vf_slots, ctxs, T, 0, q, out, ws)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all().item()
+    for i, s in enumerate(vf_slots):
+        one = torch.empty_like(q[i:i + 1])
+        ws1 = torch.empty(pool.decode_ws_bytes([ctxs[i]], T, HQ), dtype=torch.uint8, device="cuda")
+        pool.decode([s], [ctxs[i]], T, 0, q[i:i + 1].contiguous(), one, ws1)
+        torch.cuda.synchronize()
+        assert (one[0].float() - out[i].float()).abs().max().item() <= 2 * TOL
