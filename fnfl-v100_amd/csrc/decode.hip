@@ -132,14 +132,18 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     const int32_t n_tiles = static_cast<int32_t>((end - begin + kTileTokens - 1) / kTileTokens);
     const pool_view & pv = a.pv;
     const int32_t * table = pv.table + int64_t(a.slot[s]) * pv.table_stride;
+    // the split's pages (at most 64: splits are at most 16,384 cells), lane i holding logical page begin / 256 + i;
+    // a tile's page is then a lane read, not a memory load on the path to its copy. Loaded first: the page table, the
+    // Q rows and the first tile are then one memory latency each but overlapped, not three in a row.
+    const int32_t n_split_pages = static_cast<int32_t>((end - begin + kPageTokens - 1) / kPageTokens);
+    const int32_t split_page = lane < n_split_pages ? table[(begin >> 8) + lane] : 0;
     FNKV_STAMP(0);
 
     append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, wave, lane);
     FNKV_STAMP(1);
     half8 qop[kBlocks];
-    half8 sig;
     int64_t lim;
-    load_q_operands(a, s, kvh, rt, j, qg, qop, sig, lim);
+    load_q_operands(a, s, kvh, rt, j, qg, qop, lim);
 
     floatx4 acc[16];
     floatx4 lv = {0.0f, 0.0f, 0.0f, 0.0f}; // sum_t P[t][row] s_v[t][b]: lane (row j, qg) holds b = 4 qg + r
@@ -155,10 +159,6 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     auto kbuf = [&](int32_t slot) -> uint8_t * { return gbase + slot * 8192; };
     auto sslot = [&](int32_t slot) -> uint8_t * { return gbase + kCodeBytes + slot * kScaleBytes; };
     const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
-    // the split's pages (at most 64: splits are at most 16,384 cells), lane i holding logical page begin / 256 + i;
-    // a tile's page is then a lane read, not a memory load on the path to its copy
-    const int32_t n_split_pages = static_cast<int32_t>((end - begin + kPageTokens - 1) / kPageTokens);
-    const int32_t split_page = lane < n_split_pages ? table[(begin >> 8) + lane] : 0;
     auto tile_ptr = [&](int32_t ti) -> const uint8_t * {
         const int32_t phys = __builtin_amdgcn_readlane(split_page, ti >> 3);
         return layer_base + int64_t(phys) * pv.page_stride + int64_t(ti & 7) * kTileBytes;
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         __asm__ __volatile__("" ::: "memory");
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            vreg[i] = *reinterpret_cast<const u32x4 *>(tile + kVCodes + i * 1024 + lane * 16);
+            vreg[i] = stream_load16(tile + kVCodes + i * 1024 + lane * 16);
         }
     };
     const half8 zero8 = {};
@@ -189,6 +189,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         issue_k<NT>(t0p, kbuf(0), sslot(0), rt, lane);
         vload(t0p);
     }
+    const half8 sig = q_sums(qop, qg);
     for (int32_t it = 0; it < n_iter; ++it) {
         const int32_t ti = grp + it * GR;
         const bool have = ti < n_tiles;
@@ -386,29 +387,22 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
     const int32_t n_tiles = static_cast<int32_t>((end - begin + kTileTokens - 1) / kTileTokens);
     const pool_view & pv = a.pv;
     const int32_t * table = pv.table + int64_t(a.slot[s]) * pv.table_stride;
+    // the split's pages, lane i holding logical page begin / 256 + i, loaded first (with the Q rows below, and the
+    // first tiles issued before the Q sums wait: overlapped latencies, not three in a row)
+    const int32_t n_split_pages = static_cast<int32_t>((end - begin + kPageTokens - 1) / kPageTokens);
+    const int32_t split_page = lane < n_split_pages ? table[(begin >> 8) + lane] : 0;
     FNKV_STAMP(0);
     append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, wave, lane);
     FNKV_STAMP(1);
 
-    half8 sig;
+    half8 sig; // set once the first tiles are issued
     int64_t lim;
     // the Q operands: in registers at NT = 2; at NT = 3 registers are short and they sit once in LDS (after the
     // groups' buffers), the same for every group
     constexpr bool kQReg = NT == 2;
-    half8 qreg[kQReg ? kBlocks : 1];
+    half8 qreg[kBlocks];
     uint8_t * const qlds = smem + GR * SH::GROUP_LDS; // [row tile][block][lane] 16 B
-    if constexpr (kQReg) {
-        load_q_operands(a, s, kvh, w, j, qg, qreg, sig, lim);
-    } else {
-        half8 qop[kBlocks];
-        load_q_operands(a, s, kvh, w, j, qg, qop, sig, lim);
-        if (grp == 0) { // read before the first tile by the loop's first barrier
-#pragma unroll
-            for (int b = 0; b < kBlocks; ++b) {
-                *reinterpret_cast<half8 *>(qlds + (w * kBlocks + b) * 1024 + lane * 16) = qop[b];
-            }
-        }
-    }
+    load_q_operands(a, s, kvh, w, j, qg, qreg, lim);
     auto qop_lds = [&](int b) {
         if constexpr (kQReg) {
             return qreg[b];
@@ -443,8 +437,6 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
     };
 
     const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
-    const int32_t n_split_pages = static_cast<int32_t>((end - begin + kPageTokens - 1) / kPageTokens);
-    const int32_t split_page = lane < n_split_pages ? table[(begin >> 8) + lane] : 0;
     const int32_t last_tile = n_tiles - 1;
     auto tile_ptr = [&](int32_t k) -> const uint8_t * { // the group's tile of iteration k (the last tile past the end)
         int32_t ti = grp + k * GR;
@@ -613,6 +605,20 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
         qk_phase(par_c, k);
     };
 
+    // after the prologue's copies are issued: the bias operand from the Q rows, and at NT = 3 the Q operands into
+    // LDS (group 0's waves; read after the loop's first barrier)
+    auto q_finish = [&]() {
+        sig = q_sums(qreg, qg);
+        if constexpr (!kQReg) {
+            if (grp == 0) {
+#pragma unroll
+                for (int b = 0; b < kBlocks; ++b) {
+                    *reinterpret_cast<half8 *>(qlds + (w * kBlocks + b) * 1024 + lane * 16) = qreg[b];
+                }
+            }
+        }
+    };
+
     if (!late) {
 #pragma unroll
         for (int32_t k = -(SK - 1); k < 0; ++k) {
@@ -625,6 +631,7 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
                 issue_placeholder(tile_ptr(k + SK - 1), k + SK - 1);
             }
         }
+        q_finish();
         FNKV_STAMP(2);
         for (int32_t k = 0; k < n_iter; k += 2) {
             early_iteration(std::integral_constant<int32_t, 0>(), k, vbuf0);
@@ -641,6 +648,7 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
             }
             issue_k(tile_ptr(k + SK - 1), k + SK - 1);
         }
+        q_finish();
         for (int32_t k = 0; k < n_iter; k += 2) {
             late_iteration(std::integral_constant<int32_t, 0>(), k, vbuf1);
             late_iteration(std::integral_constant<int32_t, 1>(), k + 1, vbuf0);

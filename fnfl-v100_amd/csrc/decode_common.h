@@ -42,6 +42,9 @@ struct dec_args {
     do {                                                                                                             \
         if (a.ts != nullptr && threadIdx.x == 0) {                                                                   \
             a.ts[(blockIdx.y * gridDim.x + blockIdx.x) * 16 + (k)] = __builtin_amdgcn_s_memrealtime();                   \
+            a.ts[(blockIdx.y * gridDim.x + blockIdx.x) * 16 + 7] =                                                       \
+                (uint64_t(__builtin_amdgcn_s_getreg((15 << 11) | 20)) << 32) |                                           \
+                uint64_t(__builtin_amdgcn_s_getreg((31 << 11) | 4));                                                     \
         }                                                                                                            \
         __builtin_amdgcn_s_waitcnt(0);                                                                               \
     } while (0)
@@ -136,15 +139,15 @@ __device__ __forceinline__ void append_new_cells(const dec_args & a, const int32
 // with sigma_b the block's sum of q; one MFMA a half computes that sum from the K scales (A: s_k twice) and sigma_b as
 // hi + lo fp16 (B: lane (row j, qg) holds sigma_hi for qg 0, sigma_lo for qg 1, else 0), and one FMA a score takes it
 // back out. lim: the row's last visible cell.
+// load_q_operands only issues the loads; q_sums reads them, so a kernel can issue its first tile copies in between.
 __device__ __forceinline__ void load_q_operands(const dec_args & a, int32_t s, int32_t kvh, int32_t rt, int32_t j,
-                                                int32_t qg, half8 (&qop)[kBlocks], half8 & sig, int64_t & lim) {
+                                                int32_t qg, half8 (&qop)[kBlocks], int64_t & lim) {
     const int32_t row = rt * 16 + j;
     const bool real_row = row < a.R;
     const int32_t t_row = real_row ? row / a.G : a.T - 1;
     lim = a.ctx[s] - a.T + t_row;
     const uint16_t * qrow =
         a.q + ((int64_t(s) * a.T + t_row) * a.hq + int64_t(kvh) * a.G + (real_row ? row % a.G : 0)) * kHeadDim;
-    float sigma[kBlocks];
 #pragma unroll
     for (int b = 0; b < kBlocks; ++b) {
         u32x4 v = {0, 0, 0, 0};
@@ -152,20 +155,29 @@ __device__ __forceinline__ void load_q_operands(const dec_args & a, int32_t s, i
             v = *reinterpret_cast<const u32x4 *>(qrow + b * kQK + 8 * qg);
         }
         qop[b] = __builtin_bit_cast(half8, v);
+    }
+}
+
+// sig: the row's per-block sums of q (the bias correction's operand), as fp16 hi (qg = 0) and lo (qg = 1) parts
+__device__ __forceinline__ half8 q_sums(const half8 (&qop)[kBlocks], int32_t qg) {
+    float sigma[kBlocks];
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b) {
         float sum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             sum += static_cast<float>(qop[b][i]);
         }
-        sum = rows_sum(sum);
-        sigma[b] = sum;
+        sigma[b] = rows_sum(sum);
     }
+    half8 sig;
 #pragma unroll
     for (int b = 0; b < kBlocks; ++b) {
         const _Float16 hi = static_cast<_Float16>(sigma[b]);
         const _Float16 lo = static_cast<_Float16>(sigma[b] - static_cast<float>(hi));
         sig[b] = qg == 0 ? hi : qg == 1 ? lo : static_cast<_Float16>(0.0f);
     }
+    return sig;
 }
 
 // S^T = K Q^T for a tile's two 16-token halves from its K codes (kb) and scales (sc_tile + kKScales ...) in LDS:

@@ -179,3 +179,30 @@ def test_fused_append_matches_separate_append():
         (_, _, kf), (_, _, vf) = cases.decoded(O, k16, v16)
         ref = O.attn_f64(q16[i].view(np.uint16), kf, vf, c)
         assert cases.out_err(oa.cpu().numpy()[i], ref) <= TOL
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 5])
+def test_first_launch_matches_reruns(T):
+    # A launch on a freshly filled pool (cold TLB and caches, the slowest copies) gives the same bits as warm reruns:
+    # the kernels' load-count waits must cover every copy whatever its latency. Deep contexts, so each workgroup runs
+    # many iterations of its copy ring.
+    for ctx in (112927, 262144):
+        pool = fnkv.Pool(2, -(-ctx // 256) + 8, 1, HKV)
+        try:
+            cases.scatter_ensure(pool, [0], [ctx], 3, 0.3)
+            g = torch.Generator(device="cuda")
+            g.manual_seed(ctx + T)
+            x = torch.randn((2, ctx, HKV, 256), generator=g, device="cuda").half()
+            pool.append(0, 0, 0, x[0].contiguous(), x[1].contiguous())
+            q = torch.randn((1, T, HQ, 256), generator=g, device="cuda").half()
+            ws = torch.empty(pool.decode_ws_bytes([ctx], T, HQ), dtype=torch.uint8, device="cuda")
+            outs = []
+            for _ in range(6):
+                out = torch.full_like(q, float("nan"))
+                pool.decode([0], [ctx], T, 0, q, out, ws)
+                torch.cuda.synchronize()
+                outs.append(out.cpu().numpy().view(np.uint16))
+            assert all(np.array_equal(outs[0], o) for o in outs[1:]), (ctx, T)
+            assert np.isfinite(outs[0].view(np.float16).astype(np.float32)).all()
+        finally:
+            pool.close()
