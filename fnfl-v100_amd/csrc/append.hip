@@ -1,6 +1,7 @@
-// The Q8_0 append (new K/V rows quantized into the pool) and the export back to ggml's block_q8_0.
+// The append (new K/V rows quantized into the pool) and the exports back to ggml's block_q8_0 and to KV8's arrays.
 //
-// The quantization rule is q8_0.h's (ggml's quantize_row_q8_0_ref, bit for bit). The reference's device writers of its
+// The quantization rule is the pool's: q8_0.h's Q8_0 (ggml's quantize_row_q8_0_ref, bit for bit) or KV8 (FNFL's
+// kv_q8_quantize_group, bit for bit). The reference's device writers of its
 // own KV8 format (fn/kernels/qsa/kv_q8.cuh:244-267, qsa_prompt_attn.cu:90-122) use one warp a row; here one wave64
 // quantizes one 256-value row. This entry point serves chunked prefill and any caller appending outside a decode
 // launch; fnkv_attn_decode appends a step's new rows itself.
@@ -36,7 +37,7 @@ __global__ __launch_bounds__(256) void append_kernel(pool_view pv, int32_t slot,
     }
     const int64_t pos = pos0 + row;
     uint8_t * t = tile_of(pv, pv.table + int64_t(slot) * pv.table_stride, layer, head, pos);
-    quantize_store(x, lane, t, static_cast<int32_t>(pos & 31), kv);
+    quantize_store_fmt(x, lane, t, static_cast<int32_t>(pos & 31), kv, pv.format);
 }
 
 // one wave a cell: its 8 blocks of (layer, head, kv) as 8 x 34 bytes of block_q8_0
@@ -62,6 +63,32 @@ __global__ __launch_bounds__(256) void export_kernel(pool_view pv, int32_t slot,
         const uint16_t s = *reinterpret_cast<const uint16_t *>(t + (kv == 0 ? k_scale_off(tt, b) : v_scale_off(tt, b)));
         o[0] = static_cast<uint8_t>(s & 0xff);
         o[1] = static_cast<uint8_t>(s >> 8);
+    }
+}
+
+// one wave a cell: its 256 codes (int8) and 4 group scales (fp16 bits) of (layer, head, kv) in KV8's form
+__global__ __launch_bounds__(256) void export_kv8_kernel(pool_view pv, int32_t slot, int32_t layer, int32_t head,
+                                                         int32_t kv, int64_t tok0, int32_t n_tok, int8_t * codes,
+                                                         uint16_t * scales) {
+    const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
+    const int64_t i = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (i >= n_tok) {
+        return;
+    }
+    const int64_t pos = tok0 + i;
+    const uint8_t * t = tile_of(pv, pv.table + int64_t(slot) * pv.table_stride, layer, head, pos);
+    const int32_t tt = static_cast<int32_t>(pos & 31);
+    const int32_t d0 = 4 * lane;
+#pragma unroll
+    for (int32_t e = 0; e < 4; ++e) {
+        const int32_t d = d0 + e;
+        const uint8_t u = kv == 0 ? t[k_code_off(tt, d)] : t[v_code_off(tt, d)];
+        codes[i * kHeadDim + d] = static_cast<int8_t>(u ^ 0x80u);
+    }
+    if ((lane & 15) == 0) {
+        const int32_t g = lane >> 4, b = 2 * g; // the group's first block holds its scale
+        scales[i * (kHeadDim / kKV8Group) + g] =
+            *reinterpret_cast<const uint16_t *>(t + (kv == 0 ? k_scale_off(tt, b) : v_scale_off(tt, b)));
     }
 }
 
@@ -126,6 +153,28 @@ int fnkv_export_q8_0(const fnkv_pool * pool, int32_t slot, int32_t layer, int32_
                        static_cast<uint8_t *>(out));
     if (hipGetLastError() != hipSuccess) {
         set_error("fnkv_export_q8_0: launch failed");
+        return FNKV_ERR_HIP;
+    }
+    return FNKV_OK;
+}
+
+int fnkv_export_kv8(const fnkv_pool * pool, int32_t slot, int32_t layer, int32_t head, int32_t kv, int64_t tok0,
+                    int32_t n_tok, void * codes, void * scales, void * stream) {
+    const fnkv::kv_pool * p = fnkv::pool_of(pool);
+    if (p == nullptr || p->format() != fnkv::kFormatKV8 || slot < 0 || slot >= p->pages().n_slots() || layer < 0 ||
+        layer >= p->layers() || head < 0 || head >= p->h_kv() || (kv != 0 && kv != 1) || tok0 < 0 || n_tok < 0 ||
+        codes == nullptr || scales == nullptr || tok0 + n_tok > p->mapped_cells(slot)) {
+        set_error("fnkv_export_kv8: argument outside the contract (a KV8 pool's mapped cells)");
+        return FNKV_ERR_ARG;
+    }
+    if (n_tok == 0) {
+        return FNKV_OK;
+    }
+    hipLaunchKernelGGL(fnkv::export_kv8_kernel, dim3(static_cast<uint32_t>((n_tok + 3) / 4)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), p->view(), slot, layer, head, kv, tok0, n_tok,
+                       static_cast<int8_t *>(codes), static_cast<uint16_t *>(scales));
+    if (hipGetLastError() != hipSuccess) {
+        set_error("fnkv_export_kv8: launch failed");
         return FNKV_ERR_HIP;
     }
     return FNKV_OK;

@@ -128,7 +128,8 @@ __device__ __forceinline__ void append_new_cells(const dec_args & a, const int32
         } else {
             load4<false>(static_cast<const uint16_t *>(kv ? a.v_new : a.k_new) + src, lane, x);
         }
-        quantize_store(x, lane, tile_of(pv, table, a.layer, kvh, pos), static_cast<int32_t>(pos & 31), kv);
+        quantize_store_fmt(x, lane, tile_of(pv, table, a.layer, kvh, pos), static_cast<int32_t>(pos & 31), kv,
+                           pv.format);
     }
     __syncthreads();
 }

@@ -49,7 +49,7 @@ class kv_pool {
     kv_pool & operator=(const kv_pool &) = delete;
 
     bool init(int32_t n_slots, int32_t n_pages, int32_t page_cells, int32_t layers, int32_t h_kv, int64_t slot_cells,
-              int32_t device, std::string & err);
+              int32_t device, std::string & err, int32_t format = kFormatQ8_0);
     bool ensure(int32_t slot, int64_t cells, std::string & err, bool * capacity = nullptr);
     bool trim(int32_t slot, int64_t keep_cells, std::string & err);
     int64_t mapped_cells(int32_t slot) const { return int64_t(pages_.mapped(slot)) * page_cells_; }
@@ -60,6 +60,7 @@ class kv_pool {
     int32_t layers() const { return layers_; }
     int32_t h_kv() const { return h_kv_; }
     int32_t device() const { return device_; }
+    int32_t format() const { return format_; }
     int64_t device_bytes() const { return bytes_; }
     uint8_t * device_base() const { return base_; }
     std::vector<std::string> ledger() const;
@@ -72,6 +73,7 @@ class kv_pool {
     void release_all();
 
     int32_t n_slots_ = 0, page_cells_ = 0, layers_ = 0, h_kv_ = 0, device_ = 0, table_stride_ = 0;
+    int32_t format_ = kFormatQ8_0;
     int64_t slot_cells_ = 0, bytes_ = 0;
     uint8_t * base_ = nullptr;
     int32_t * table_dev_ = nullptr;

@@ -6,6 +6,10 @@
 //   [8192, 16384)  V codes, 32 tokens x 256, arranged for its PV operand
 //   [16384, 16896) K scales, fp16 [32 tokens][8 blocks] (token-major, natural order)
 //   [16896, 17408) V scales, fp16 [4 lane groups][8 blocks][8 slots]
+// Two code formats share the layout (the pool's format, fixed at creation): Q8_0 (ggml's block_q8_0 rule, a scale a
+// 32-value block) and FNFL's KV8 (kv_q8_ref.h: a scale a 64-value group), whose group scale is written at both of the
+// group's 32-value blocks, so every attention kernel reads the two formats the same way and a cell is 1,088 B either
+// way.
 // Codes are stored excess-128 (byte = code + 128 = code ^ 0x80), so the kernels widen them to fp16 with one byte
 // permute (0x6400 | byte is the fp16 value 1024 + byte) and one packed subtract of 1152.
 //
@@ -36,6 +40,9 @@ constexpr int32_t kKScales = 16384;
 constexpr int32_t kVScales = 16896;
 constexpr int32_t kTileBytes = 17408;
 constexpr int64_t kPageBlock = int64_t(kTileBytes) * kTilesPerPage; // 139,264
+constexpr int32_t kFormatQ8_0 = 0; // FNKV_FMT_Q8_0
+constexpr int32_t kFormatKV8 = 1;  // FNKV_FMT_KV8
+constexpr int32_t kKV8Group = 64;  // values a KV8 scale
 
 #if defined(__HIPCC__)
 #define FNKV_HD __host__ __device__ inline
@@ -66,6 +73,7 @@ struct pool_view {
     int64_t page_stride;   // bytes a physical page within a layer: h_kv * kPageBlock
     int32_t table_stride;
     int32_t h_kv;
+    int32_t format; // kFormatQ8_0 or kFormatKV8
 };
 
 } // namespace fnkv

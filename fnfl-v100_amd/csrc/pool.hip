@@ -152,10 +152,14 @@ void kv_pool::release_all() {
 }
 
 bool kv_pool::init(int32_t n_slots, int32_t n_pages, int32_t page_cells, int32_t layers, int32_t h_kv,
-                   int64_t slot_cells, int32_t device, std::string & err) {
+                   int64_t slot_cells, int32_t device, std::string & err, int32_t format) {
     release_all();
     if (n_slots <= 0 || n_pages <= 0 || layers <= 0 || h_kv <= 0) {
         err = "KV pool: slots, pages, layers and heads must be positive";
+        return false;
+    }
+    if (format != kFormatQ8_0 && format != kFormatKV8) {
+        err = "KV pool: unknown code format " + std::to_string(format);
         return false;
     }
     if (page_cells != kPageTokens) {
@@ -172,6 +176,7 @@ bool kv_pool::init(int32_t n_slots, int32_t n_pages, int32_t page_cells, int32_t
         return false;
     }
     n_slots_ = n_slots;
+    format_ = format;
     page_cells_ = page_cells;
     layers_ = layers;
     h_kv_ = h_kv;
@@ -307,9 +312,9 @@ std::vector<std::string> kv_pool::ledger() const {
     char b[512];
     snprintf(b, sizeof b,
              "KV pool: %d pages of %d cells (%lld cells shared by %d slots; a slot's logical range %lld cells); "
-             "%d layers x %d KV heads of Q8_0 K and V, %lld bytes a page, %.3f GiB of HBM on device %d",
+             "%d layers x %d KV heads of %s K and V, %lld bytes a page, %.3f GiB of HBM on device %d",
              pages_.n_pages(), page_cells_, static_cast<long long>(capacity_cells()), n_slots_,
-             static_cast<long long>(slot_cells_), layers_, h_kv_,
+             static_cast<long long>(slot_cells_), layers_, h_kv_, format_ == kFormatKV8 ? "KV8 (group 64)" : "Q8_0",
              static_cast<long long>(int64_t(layers_) * h_kv_ * kPageBlock), double(bytes_) / 1073741824.0, device_);
     out.emplace_back(b);
     snprintf(b, sizeof b, "KV pool: page table %d slots x %d entries (int32); %d of %d pages free", n_slots_,
@@ -326,6 +331,7 @@ pool_view kv_pool::view() const {
     v.layer_stride = int64_t(pages_.n_pages()) * v.page_stride;
     v.table_stride = table_stride_;
     v.h_kv = h_kv_;
+    v.format = format_;
     return v;
 }
 
@@ -357,6 +363,11 @@ int32_t fnkv_reclaim_victim(const fnkv_slot_view * views, int32_t n, int32_t for
 
 int fnkv_pool_create(int32_t n_slots, int32_t n_pages, int32_t page_tokens, int32_t layers, int32_t h_kv,
                      int64_t slot_tokens, int32_t device, fnkv_pool ** out) {
+    return fnkv_pool_create_fmt(n_slots, n_pages, page_tokens, layers, h_kv, slot_tokens, FNKV_FMT_Q8_0, device, out);
+}
+
+int fnkv_pool_create_fmt(int32_t n_slots, int32_t n_pages, int32_t page_tokens, int32_t layers, int32_t h_kv,
+                         int64_t slot_tokens, int32_t format, int32_t device, fnkv_pool ** out) {
     if (out == nullptr) {
         set_error("fnkv_pool_create: null out");
         return FNKV_ERR_ARG;
@@ -364,7 +375,7 @@ int fnkv_pool_create(int32_t n_slots, int32_t n_pages, int32_t page_tokens, int3
     *out = nullptr;
     fnkv_pool * p = new fnkv_pool;
     std::string err;
-    if (!p->p.init(n_slots, n_pages, page_tokens, layers, h_kv, slot_tokens, device, err)) {
+    if (!p->p.init(n_slots, n_pages, page_tokens, layers, h_kv, slot_tokens, device, err, format)) {
         delete p;
         set_error(err);
         return err.find("HBM") != std::string::npos ? FNKV_ERR_HIP : FNKV_ERR_ARG;
@@ -374,6 +385,8 @@ int fnkv_pool_create(int32_t n_slots, int32_t n_pages, int32_t page_tokens, int3
 }
 
 void fnkv_pool_destroy(fnkv_pool * pool) { delete pool; }
+
+int32_t fnkv_pool_format(const fnkv_pool * pool) { return pool == nullptr ? -1 : pool->p.format(); }
 
 int fnkv_pool_ensure(fnkv_pool * pool, int32_t slot, int64_t cells, int32_t * capacity) {
     if (capacity != nullptr) {

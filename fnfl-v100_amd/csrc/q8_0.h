@@ -1,5 +1,5 @@
-// The Q8_0 quantizer of one 256-value row by one wave64, shared by the append kernel and the decode kernel's fused
-// append. Rule, bit for bit ggml's quantize_row_q8_0_ref (ggml/src/ggml-quants.c:274-297) on the fp32 value of each
+// The quantizers of one 256-value row by one wave64 (Q8_0 and KV8), shared by the append kernel and the decode
+// kernel's fused append. Rule, bit for bit ggml's quantize_row_q8_0_ref (ggml/src/ggml-quants.c:274-297) on the fp32 value of each
 // input: per block of 32, amax = max |x|; d = amax / 127 (IEEE division); id = d != 0 ? 1 / d : 0 (IEEE division);
 // code = roundf(x * id) (IEEE product, ties away from zero); the stored scale is fp16(d), round to nearest even
 // (ggml-impl.h:414-438). Lane l holds values 4 l .. 4 l + 3; the 8 lanes of a block reduce amax with cross-lane max.
@@ -85,6 +85,62 @@ __device__ __forceinline__ void quantize_store(const float (&x)[4], int32_t lane
         if ((lane & 7) == 0) {
             *reinterpret_cast<uint16_t *>(tile + v_scale_off(tt, b)) = dh;
         }
+    }
+}
+
+// The KV8 rule, bit for bit FNFL's kv_q8_quantize_group (fn/quant/kv_q8_ref.cpp:72-87; device kv8::quantize8,
+// fn/kernels/qsa/kv_q8.cuh:29-52): per group of 64 values amax = max |x|; the scale is fp16(amax / 127) (IEEE
+// division, round to nearest even), s its exact value; code = 0 when s == 0, else clamp(rint(x / s), -127, 127)
+// (IEEE division, ties to even). The 16 lanes of a group (lanes 16 g .. 16 g + 15) reduce amax; the group's scale is
+// stored at both of its 32-value blocks.
+__device__ __forceinline__ void quantize_store_kv8(const float (&x)[4], int32_t lane, uint8_t * tile, int32_t tt,
+                                                   int32_t kv) {
+#pragma clang fp contract(off)
+    float amax = fmaxf(fmaxf(__builtin_fabsf(x[0]), __builtin_fabsf(x[1])),
+                       fmaxf(__builtin_fabsf(x[2]), __builtin_fabsf(x[3])));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    amax = fmaxf(amax, __shfl_xor(amax, 8));
+    const __half h = __float2half_rn(__fdiv_rn(amax, 127.0f));
+    const float sv = __half2float(h);
+    uint32_t packed = 0;
+    uint8_t bytes[4];
+#pragma unroll
+    for (int32_t e = 0; e < 4; ++e) {
+        int32_t c = 0;
+        if (sv > 0.0f) {
+            const float r = __builtin_rintf(__fdiv_rn(x[e], sv));
+            c = r < -127.0f ? -127 : r > 127.0f ? 127 : static_cast<int32_t>(r);
+        }
+        bytes[e] = static_cast<uint8_t>((c & 0xff) ^ 0x80);
+        packed |= uint32_t(bytes[e]) << (8 * e);
+    }
+    const int32_t d0 = 4 * lane, b = lane >> 3;
+    const uint16_t sh = __half_as_ushort(h);
+    if (kv == 0) {
+        *reinterpret_cast<uint32_t *>(tile + k_code_off(tt, d0)) = packed;
+        if ((lane & 7) == 0) {
+            *reinterpret_cast<uint16_t *>(tile + k_scale_off(tt, b)) = sh;
+        }
+    } else {
+#pragma unroll
+        for (int32_t e = 0; e < 4; ++e) {
+            tile[v_code_off(tt, d0 + e)] = bytes[e];
+        }
+        if ((lane & 7) == 0) {
+            *reinterpret_cast<uint16_t *>(tile + v_scale_off(tt, b)) = sh;
+        }
+    }
+}
+
+// the pool's rule (format: kFormatQ8_0 or kFormatKV8, uniform across the wave)
+__device__ __forceinline__ void quantize_store_fmt(const float (&x)[4], int32_t lane, uint8_t * tile, int32_t tt,
+                                                   int32_t kv, int32_t format) {
+    if (format == kFormatKV8) {
+        quantize_store_kv8(x, lane, tile, tt, kv);
+    } else {
+        quantize_store(x, lane, tile, tt, kv);
     }
 }
 

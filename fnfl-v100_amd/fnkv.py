@@ -12,6 +12,7 @@ LIB_PATH = os.path.join(HERE, "libfnkv.so")
 
 OK, ERR_ARG, ERR_CAPACITY, ERR_HIP = 0, 1, 2, 3
 F16, F32 = 0, 1
+FMT_Q8_0, FMT_KV8 = 0, 1
 PAGE_TOKENS = 256
 HEAD_DIM = 256
 EXPORTS = [
@@ -20,7 +21,7 @@ EXPORTS = [
     "fnkv_pool_mapped_pages", "fnkv_pool_physical", "fnkv_page_table", "fnkv_pool_ledger", "fnkv_pool_test_fail",
     "fnkv_page_block_bytes", "fnkv_pool_device_base", "fnkv_pool_device_bytes", "fnkv_q8_append",
     "fnkv_export_q8_0", "fnkv_decode_workspace_bytes", "fnkv_attn_decode", "fnkv_prefill_workspace_bytes",
-    "fnkv_attn_prefill",
+    "fnkv_attn_prefill", "fnkv_pool_create_fmt", "fnkv_pool_format", "fnkv_export_kv8",
 ]
 
 P = ctypes.c_void_p
@@ -53,6 +54,10 @@ def lib():
         L.fnkv_reclaim_victim.argtypes = [P, I32, I32]
         L.fnkv_pool_create.restype = ctypes.c_int
         L.fnkv_pool_create.argtypes = [I32, I32, I32, I32, I32, I64, I32, ctypes.POINTER(P)]
+        L.fnkv_pool_create_fmt.restype = ctypes.c_int
+        L.fnkv_pool_create_fmt.argtypes = [I32, I32, I32, I32, I32, I64, I32, I32, ctypes.POINTER(P)]
+        L.fnkv_pool_format.restype = I32
+        L.fnkv_pool_format.argtypes = [P]
         L.fnkv_pool_destroy.argtypes = [P]
         L.fnkv_pool_ensure.restype = ctypes.c_int
         L.fnkv_pool_ensure.argtypes = [P, I32, I64, ctypes.POINTER(I32)]
@@ -81,6 +86,8 @@ def lib():
         L.fnkv_q8_append.argtypes = [P, I32, I32, I64, I32, P, P, I32, P]
         L.fnkv_export_q8_0.restype = ctypes.c_int
         L.fnkv_export_q8_0.argtypes = [P, I32, I32, I32, I32, I64, I32, P, P]
+        L.fnkv_export_kv8.restype = ctypes.c_int
+        L.fnkv_export_kv8.argtypes = [P, I32, I32, I32, I32, I64, I32, P, P, P]
         L.fnkv_decode_workspace_bytes.restype = I64
         L.fnkv_decode_workspace_bytes.argtypes = [P, I32, P, I32, I32]
         L.fnkv_attn_decode.restype = ctypes.c_int
@@ -135,11 +142,13 @@ def _i64_array(xs):
 class Pool:
     """The page pool (kv_pool.h:63-138) and the kernels that read and write it."""
 
-    def __init__(self, n_slots, n_pages, layers, h_kv, slot_tokens=0, device=0, page_tokens=PAGE_TOKENS):
+    def __init__(self, n_slots, n_pages, layers, h_kv, slot_tokens=0, device=0, page_tokens=PAGE_TOKENS,
+                 fmt=FMT_Q8_0):
         h = P()
-        check(lib().fnkv_pool_create(n_slots, n_pages, page_tokens, layers, h_kv, slot_tokens, device,
-                                     ctypes.byref(h)))
+        check(lib().fnkv_pool_create_fmt(n_slots, n_pages, page_tokens, layers, h_kv, slot_tokens, fmt, device,
+                                         ctypes.byref(h)))
         self.h = h
+        self.fmt = fmt
         self.n_slots, self.n_pages, self.layers, self.h_kv = n_slots, n_pages, layers, h_kv
 
     def close(self):
@@ -208,6 +217,15 @@ class Pool:
         check(lib().fnkv_export_q8_0(self.h, slot, layer, head, kv, tok0, n_tok, P(out.data_ptr()),
                                      _stream(stream)))
         return out
+
+    def export_kv8(self, slot, layer, head, kv, tok0, n_tok, stream=None):
+        """KV8 pool -> (int8 codes [n_tok][256], uint16 group scales [n_tok][4]) device tensors."""
+        import torch
+        codes = torch.empty((n_tok, HEAD_DIM), dtype=torch.int8, device="cuda")
+        scales = torch.empty((n_tok, HEAD_DIM // 64), dtype=torch.int16, device="cuda")
+        check(lib().fnkv_export_kv8(self.h, slot, layer, head, kv, tok0, n_tok, P(codes.data_ptr()),
+                                    P(scales.data_ptr()), _stream(stream)))
+        return codes, scales
 
     def decode_ws_bytes(self, ctx, T, hq):
         ptr, keep = _i64_array(ctx)

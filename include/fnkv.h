@@ -35,6 +35,10 @@ enum fnkv_status {
 
 enum fnkv_dtype { FNKV_F16 = 0, FNKV_F32 = 1 };
 
+/* the pool's code format: ggml's Q8_0 (a fp16 scale a 32-value block, ggml-quants.c:274-297), or FNFL's KV8 (a fp16
+ * scale a 64-value group, divide and round to even, fn/quant/kv_q8_ref.h:5-13, fn/kernels/qsa/kv_q8.cuh:1-12) */
+enum fnkv_format { FNKV_FMT_Q8_0 = 0, FNKV_FMT_KV8 = 1 };
+
 typedef struct fnkv_pool fnkv_pool;
 
 /* the message of the calling thread's last failed call ("" when none) */
@@ -63,6 +67,12 @@ int32_t fnkv_reclaim_victim(const fnkv_slot_view * views, int32_t n, int32_t for
  * Device memory on `device`: n_pages * layers * h_kv * fnkv_page_block_bytes(). page_tokens must be 256. */
 int fnkv_pool_create(int32_t n_slots, int32_t n_pages, int32_t page_tokens, int32_t layers, int32_t h_kv,
                      int64_t slot_tokens, int32_t device, fnkv_pool ** out);
+/* kv_pool::init for a pool of either code format (format: enum fnkv_format). The reference's KV8 class is its
+ * --fnfl-kv-format q8 pool (fn/kernels/qsa/kv_q8.cuh:8-11, state.h:88-91); fnkv_pool_create is this with FNKV_FMT_Q8_0. */
+int fnkv_pool_create_fmt(int32_t n_slots, int32_t n_pages, int32_t page_tokens, int32_t layers, int32_t h_kv,
+                         int64_t slot_tokens, int32_t format, int32_t device, fnkv_pool ** out);
+/* the pool's code format (enum fnkv_format); -1 for null */
+int32_t fnkv_pool_format(const fnkv_pool * pool);
 /* kv_pool::~kv_pool (kv_pool.cpp:162-205); null is a no-op */
 void fnkv_pool_destroy(fnkv_pool * pool);
 
@@ -96,8 +106,9 @@ int64_t fnkv_pool_device_bytes(const fnkv_pool * pool);
 
 /* ---- the append (fn/kernels/qsa/qsa_prompt.h:90-104 qsp_kv, attend.cu:218-260 prepare) ---- */
 
-/* Quantizes rows new K and V rows (k, v: [rows][h_kv][256] of dtype, device) into Q8_0 by ggml's
- * quantize_row_q8_0_ref rule (ggml-quants.c:274-297) and writes them at the slot's positions pos0 .. pos0 + rows - 1
+/* Quantizes rows new K and V rows (k, v: [rows][h_kv][256] of dtype, device) by the pool's rule — Q8_0: ggml's
+ * quantize_row_q8_0_ref (ggml-quants.c:274-297); KV8: kv_q8_quantize_group (fn/quant/kv_q8_ref.cpp:72-87, device
+ * kv8::quantize8, fn/kernels/qsa/kv_q8.cuh:29-52) — and writes them at the slot's positions pos0 .. pos0 + rows - 1
  * of `layer` through the page table (cell pos: logical page pos / 256, offset pos % 256). The positions must be
  * mapped (fnkv_pool_ensure). */
 int fnkv_q8_append(fnkv_pool * pool, int32_t slot, int32_t layer, int64_t pos0, int32_t rows, const void * k,
@@ -107,6 +118,12 @@ int fnkv_q8_append(fnkv_pool * pool, int32_t slot, int32_t layer, int64_t pos0, 
  * block, 8 blocks a cell) into out (device, n_tok * 272 bytes): the interchange form of the stored codes. */
 int fnkv_export_q8_0(const fnkv_pool * pool, int32_t slot, int32_t layer, int32_t head, int32_t kv, int64_t tok0,
                      int32_t n_tok, void * out, void * stream);
+
+/* Reads the slot's cells tok0 .. tok0 + n_tok - 1 of (layer, head, kv) of a KV8 pool back in the reference's KV8
+ * form: codes int8 [n_tok][256] and the group scales fp16 bits [n_tok][4] (device), the arrays the reference keeps
+ * cell-major (kv_q8.cuh:8-11). */
+int fnkv_export_kv8(const fnkv_pool * pool, int32_t slot, int32_t layer, int32_t head, int32_t kv, int64_t tok0,
+                    int32_t n_tok, void * codes, void * scales, void * stream);
 
 /* ---- decode / speculative verify attention (fn/kernels/qsa/attend.h:97-151 attend, attend_lanes) ---- */
 

@@ -71,3 +71,13 @@ def out_err(got, ref):
     g = np.asarray(got, np.float64)
     r = np.asarray(ref, np.float64)
     return float(np.max(np.abs(g - r) - half_ulp_f16(np.maximum(np.abs(g), np.abs(r)))))
+
+
+def decoded_kv8(oracle, k16, v16):
+    """The oracle's KV8 codes, group scales and decoded fp32 values (code x scale, exact) of fp16 K and V rows."""
+    out = []
+    for x in (k16, v16):
+        c, s = oracle.kv8_quantize(x.astype(np.float32))
+        sf = s.view(np.float16).astype(np.float32)
+        out.append((c, s, c.astype(np.float32) * np.repeat(sf, 64, axis=-1)))
+    return out[0], out[1]
