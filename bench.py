@@ -202,10 +202,12 @@ def run_prefill(args, cfg):
     kc, vc = kv[0][depth:].contiguous(), kv[1][depth:].contiguous()
     q = torch.randn((rows, HQ, D), generator=g, device="cuda").half()
     out = torch.empty_like(q)
+    ws_n = pool.prefill_ws_bytes(ctx, rows, HQ)
+    ws = torch.empty(max(ws_n, 16), dtype=torch.uint8, device="cuda") if ws_n > 0 else False
 
     def step():
         pool.append(0, 0, depth, kc, vc)
-        pool.prefill(0, 0, ctx, q, out)
+        pool.prefill(0, 0, ctx, q, out, ws=ws)
 
     step()
     torch.cuda.synchronize()
@@ -256,7 +258,7 @@ def run_prefill(args, cfg):
         "config": {"workload": cfg["workload"], "context": ctx, "chunk": rows, "q_heads": HQ, "kv_heads": HKV,
                    "head_dim": D, "page_tokens": 256, "hip_graph": graph is not None},
         "roofline": {
-            "kernel": "fnkv_q8_append + fnkv_attn_prefill (append_kernel + prefill_kernel), per step",
+            "kernel": "fnkv_q8_append + fnkv_attn_prefill (append_kernel + prefill_kernel + prefill_merge_kernel), per step",
             "bound": "mfma",
             "achieved": round(tflops, 3),
             "peak": PEAK_MFMA_F16_TFLOPS,

@@ -12,5 +12,7 @@ namespace fnkv {
 void set_error(const std::string & e);
 const char * last_error();
 const kv_pool * pool_of(const fnkv_pool * p);
+// compute units of a device (cached)
+int32_t device_cus(int32_t device);
 
 } // namespace fnkv

@@ -26,13 +26,14 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 
 namespace fnkv {
 
 constexpr int32_t kPfWaves = 8;                      // two a SIMD
-constexpr int32_t kPfNT = 1;                         // 16-row tiles a wave
-constexpr int32_t kPfRows = kPfWaves * kPfNT * 16;   // 128 rows a workgroup
+constexpr int32_t kPfNT = 2;                         // 16-row tiles a wave (each plane read serves both)
+constexpr int32_t kPfRows = kPfWaves * kPfNT * 16;   // 256 rows a workgroup
 constexpr int32_t kPfStage = 8 * 1024 + 1024;        // a tile's K codes, then its K and V scales
 constexpr int32_t kPfPlane = 16 * 1024;             // one fp16 operand plane of a tile (K or V, hi or lo)
 constexpr int32_t kPfSet = 4 * kPfPlane;             // a tile's planes: K hi, K lo, V hi, V lo
@@ -43,9 +44,12 @@ struct pf_args {
     pool_view pv;
     const uint16_t * q; // fp16 [rows][hq][256]
     uint16_t * out;     // fp16 [rows][hq][256]
+    float * po;         // split partials (n_split > 1): acc [split][h_kv][row blocks * kPfRows][256]
+    float * pml;        // ... and (m, l) [split][h_kv][row blocks * kPfRows][2]
     float c2;           // scale * log2(e)
     int64_t ctx;        // cells of the sequence (the chunk included)
     int32_t rows, G, hq, layer, slot;
+    int32_t n_split, split_tiles; // key tiles split over blockIdx.z: split z takes tiles z * split_tiles ..
 };
 
 // a tile's K codes (8 chunks of 1 KiB) and its scales chunk into a staging slot: wave w copies chunks w, w + 4,
@@ -72,7 +76,10 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
     const int64_t pos_first = a.ctx - a.rows; // position of query token 0
     const int32_t t_last = min(a.rows, t_first + tok_per_wg) - 1;
     const int64_t key_end = pos_first + t_last + 1; // keys the block's last query sees
-    const int32_t n_tiles = static_cast<int32_t>((key_end + kTileTokens - 1) / kTileTokens);
+    const int32_t n_tiles_all = static_cast<int32_t>((key_end + kTileTokens - 1) / kTileTokens);
+    // this workgroup's key tiles: its split's share of those the block's queries see
+    const int32_t ts0 = static_cast<int32_t>(blockIdx.z) * a.split_tiles;
+    const int32_t n_tiles = max(0, min(n_tiles_all, ts0 + a.split_tiles) - ts0);
 
     // Q operands (B of S^T = K Q^T) of this wave's two row tiles, and each row's causal limit
     half8 qop[kPfNT][kBlocks];
@@ -108,8 +115,8 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
     const pool_view & pv = a.pv;
     const int32_t * table = pv.table + int64_t(a.slot) * pv.table_stride;
     const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
-    auto tile_ptr = [&](int32_t ti) -> const uint8_t * {
-        const int64_t tok = int64_t(ti) * kTileTokens;
+    auto tile_ptr = [&](int32_t li) -> const uint8_t * { // the split's li-th tile
+        const int64_t tok = int64_t(ts0 + li) * kTileTokens;
         const int32_t phys = table[tok >> 8];
         return layer_base + int64_t(phys) * pv.page_stride + int64_t((tok & 255) >> 5) * kTileBytes;
     };
@@ -169,7 +176,7 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
     // tile ti on planes set ti & 1: scores, online softmax, PV
     auto compute = [&](int32_t ti) {
         const uint8_t * pl = plane_base + (ti & 1) * kPfSet;
-        const int64_t tok0 = int64_t(ti) * kTileTokens;
+        const int64_t tok0 = int64_t(ts0 + ti) * kTileTokens;
         floatx4 sc[kPfNT][2];
 #pragma unroll
         for (int nt = 0; nt < kPfNT; ++nt) {
@@ -272,7 +279,25 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
         compute(ti);
     }
 
-    // ---- normalise and write ----
+    // ---- one split: normalise and write; several: the unnormalised partial (acc, m, l) for the merge ----
+    if (a.n_split > 1) {
+        const int64_t prow0 = (int64_t(blockIdx.z) * gridDim.y + kvh) * (int64_t(gridDim.x) * kPfRows) +
+                              int64_t(blockIdx.x) * kPfRows;
+#pragma unroll
+        for (int nt = 0; nt < kPfNT; ++nt) {
+            const float l = rows_sum(l_run[nt]);
+            const int64_t prow = prow0 + (wave * kPfNT + nt) * 16 + j;
+            float * po = a.po + prow * kHeadDim + 4 * qg;
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                *reinterpret_cast<floatx4 *>(po + 16 * m) = acc[nt][m];
+            }
+            if (qg == 0) {
+                *reinterpret_cast<float2 *>(a.pml + prow * 2) = float2{m_run[nt], l};
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int nt = 0; nt < kPfNT; ++nt) {
         float l = l_run[nt];
@@ -295,6 +320,73 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
     }
 }
 
+// Folds the splits' partials of each (query token, head): M = max m_z, L = sum l_z 2^(m_z - M), O = sum acc_z
+// 2^(m_z - M) / L, in split order. A thread takes 4 values of one row; 64 threads a row.
+__global__ __launch_bounds__(256) void prefill_merge_kernel(pf_args a, int32_t rows_pad) {
+    const int32_t tid = static_cast<int32_t>(threadIdx.x);
+    const int64_t item = int64_t(blockIdx.x) * 4 + (tid >> 6); // (kvh, row) over h_kv x rows_pad
+    const int32_t c4 = (tid & 63) * 4;
+    const int32_t h_kv = a.pv.h_kv;
+    if (item >= int64_t(h_kv) * rows_pad) {
+        return;
+    }
+    const int32_t kvh = static_cast<int32_t>(item / rows_pad);
+    const int32_t R = static_cast<int32_t>(item % rows_pad);
+    const int32_t tok_per_wg = kPfRows / a.G;
+    const int32_t blk = R / kPfRows, r = R % kPfRows;
+    const int32_t t = blk * tok_per_wg + r / a.G;
+    if (t >= a.rows) {
+        return;
+    }
+    float M = kPfNegInf;
+    for (int32_t z = 0; z < a.n_split; ++z) {
+        M = fmaxf(M, a.pml[((int64_t(z) * h_kv + kvh) * rows_pad + R) * 2]);
+    }
+    const float M_use = M == kPfNegInf ? 0.0f : M;
+    float L = 0.0f;
+    floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int32_t z = 0; z < a.n_split; ++z) {
+        const int64_t prow = (int64_t(z) * h_kv + kvh) * rows_pad + R;
+        const float2 ml = *reinterpret_cast<const float2 *>(a.pml + prow * 2);
+        const float f = __builtin_amdgcn_exp2f(ml.x - M_use);
+        L = __builtin_fmaf(ml.y, f, L);
+        A += *reinterpret_cast<const floatx4 *>(a.po + prow * kHeadDim + c4) * f;
+    }
+    const float inv = 1.0f / L;
+    uint16_t * o = a.out + (int64_t(t) * a.hq + int64_t(kvh) * a.G + r % a.G) * kHeadDim + c4;
+    uint2 pk;
+    pk.x = uint32_t(__half_as_ushort(__float2half_rn(A[0] * inv))) |
+           (uint32_t(__half_as_ushort(__float2half_rn(A[1] * inv))) << 16);
+    pk.y = uint32_t(__half_as_ushort(__float2half_rn(A[2] * inv))) |
+           (uint32_t(__half_as_ushort(__float2half_rn(A[3] * inv))) << 16);
+    *reinterpret_cast<uint2 *>(o) = pk;
+}
+
+// The launch shape: row blocks of kPfRows rows, and the key split that fills the device (a split keeps at least 16
+// tiles); the workspace the splits' partials need (0 for one split).
+struct pf_plan {
+    int32_t row_blocks = 0, n_split = 1, split_tiles = 0, rows_pad = 0;
+    int64_t ws_bytes = 0;
+};
+pf_plan plan_prefill(const kv_pool & p, int64_t ctx, int32_t rows, int32_t G) {
+    pf_plan pl;
+    const int32_t tok_per_wg = kPfRows / G;
+    pl.row_blocks = (rows + tok_per_wg - 1) / tok_per_wg;
+    pl.rows_pad = pl.row_blocks * kPfRows;
+    const int32_t max_tiles = static_cast<int32_t>((ctx + kTileTokens - 1) / kTileTokens);
+    const int32_t base = pl.row_blocks * p.h_kv();
+    const int32_t cus = device_cus(p.device());
+    int32_t ns = (cus + base - 1) / base;
+    ns = std::min(ns, std::max(1, max_tiles / 16));
+    ns = std::min(ns, 64);
+    pl.n_split = std::max(1, ns);
+    pl.split_tiles = (max_tiles + pl.n_split - 1) / pl.n_split;
+    if (pl.n_split > 1) {
+        pl.ws_bytes = int64_t(pl.n_split) * p.h_kv() * pl.rows_pad * (kHeadDim + 2) * 4;
+    }
+    return pl;
+}
+
 } // namespace fnkv
 
 using fnkv::set_error;
@@ -302,16 +394,16 @@ using fnkv::set_error;
 extern "C" {
 
 int64_t fnkv_prefill_workspace_bytes(const fnkv_pool * pool, int64_t ctx, int32_t rows, int32_t hq) {
-    (void)ctx;
-    (void)rows;
-    (void)hq;
-    return pool == nullptr ? -1 : 0;
+    const fnkv::kv_pool * p = fnkv::pool_of(pool);
+    if (p == nullptr || rows <= 0 || ctx < rows || hq <= 0 || hq % p->h_kv() != 0 ||
+        fnkv::kPfRows % (hq / p->h_kv()) != 0) {
+        return -1;
+    }
+    return fnkv::plan_prefill(*p, ctx, rows, hq / p->h_kv()).ws_bytes;
 }
 
 int fnkv_attn_prefill(const fnkv_pool * pool, int32_t slot, int32_t layer, int64_t ctx, int32_t rows, int32_t hq,
                       float scale, const void * q, void * out, void * ws, int64_t ws_bytes, void * stream) {
-    (void)ws;
-    (void)ws_bytes;
     const fnkv::kv_pool * p = fnkv::pool_of(pool);
     if (p == nullptr || slot < 0 || slot >= p->pages().n_slots() || layer < 0 || layer >= p->layers() || rows <= 0 ||
         ctx < rows || ctx > p->mapped_cells(slot) || hq <= 0 || hq % p->h_kv() != 0 || q == nullptr ||
@@ -339,7 +431,16 @@ int fnkv_attn_prefill(const fnkv_pool * pool, int32_t slot, int32_t layer, int64
     a.hq = hq;
     a.layer = layer;
     a.slot = slot;
-    const int32_t tok_per_wg = fnkv::kPfRows / G;
+    fnkv::pf_plan pl = fnkv::plan_prefill(*p, ctx, rows, G);
+    if (pl.n_split > 1 && (ws == nullptr || ws_bytes < pl.ws_bytes || (reinterpret_cast<uintptr_t>(ws) & 15) != 0)) {
+        // no (or too small a) workspace: one split, written directly
+        pl.n_split = 1;
+        pl.split_tiles = static_cast<int32_t>((ctx + fnkv::kTileTokens - 1) / fnkv::kTileTokens);
+    }
+    a.n_split = pl.n_split;
+    a.split_tiles = pl.split_tiles;
+    a.po = static_cast<float *>(ws);
+    a.pml = a.po == nullptr ? nullptr : a.po + int64_t(pl.n_split) * p->h_kv() * pl.rows_pad * fnkv::kHeadDim;
     static bool attr_set[64] = {false};
     const int32_t dev = p->device();
     if (dev >= 0 && dev < 64 && !attr_set[dev]) {
@@ -352,8 +453,15 @@ int fnkv_attn_prefill(const fnkv_pool * pool, int32_t slot, int32_t layer, int64
         hipSetDevice(cur);
         attr_set[dev] = true;
     }
-    const dim3 grid(static_cast<uint32_t>((rows + tok_per_wg - 1) / tok_per_wg), static_cast<uint32_t>(p->h_kv()));
-    hipLaunchKernelGGL(fnkv::prefill_kernel, grid, dim3(64 * fnkv::kPfWaves), fnkv::kPfLds, static_cast<hipStream_t>(stream), a);
+    const dim3 grid(static_cast<uint32_t>(pl.row_blocks), static_cast<uint32_t>(p->h_kv()),
+                    static_cast<uint32_t>(pl.n_split));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(fnkv::prefill_kernel, grid, dim3(64 * fnkv::kPfWaves), fnkv::kPfLds, st, a);
+    if (pl.n_split > 1) {
+        const int64_t items = int64_t(p->h_kv()) * pl.rows_pad;
+        hipLaunchKernelGGL(fnkv::prefill_merge_kernel, dim3(static_cast<uint32_t>((items + 3) / 4)), dim3(256), 0, st,
+                           a, pl.rows_pad);
+    }
     if (hipGetLastError() != hipSuccess) {
         set_error("fnkv_attn_prefill: launch failed");
         return FNKV_ERR_HIP;

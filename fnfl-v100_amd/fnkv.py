@@ -245,8 +245,17 @@ class Pool:
                                             dt, P(out.data_ptr()), P(ws.data_ptr()), ws.numel() * ws.element_size(),
                                             _stream(stream)))
 
-    def prefill(self, slot, layer, ctx, q, out, scale=1.0 / 16.0, stream=None):
-        """q, out: fp16 [rows][hq][256]: the chunk's queries at positions ctx - rows .. ctx - 1."""
+    def prefill_ws_bytes(self, ctx, rows, hq):
+        return lib().fnkv_prefill_workspace_bytes(self.h, ctx, rows, hq)
+
+    def prefill(self, slot, layer, ctx, q, out, scale=1.0 / 16.0, stream=None, ws=None):
+        """q, out: fp16 [rows][hq][256]: the chunk's queries at positions ctx - rows .. ctx - 1. ws: a device tensor
+        of at least prefill_ws_bytes bytes (None: allocated here; False: none, one key split)."""
+        import torch
         rows, hq = q.shape[0], q.shape[1]
+        if ws is None:
+            n = self.prefill_ws_bytes(ctx, rows, hq)
+            ws = torch.empty(max(n, 16), dtype=torch.uint8, device=q.device) if n > 0 else False
+        wp, wn = (P(ws.data_ptr()), ws.numel() * ws.element_size()) if ws is not False else (None, 0)
         return check(lib().fnkv_attn_prefill(self.h, slot, layer, ctx, rows, hq, scale, P(q.data_ptr()),
-                                             P(out.data_ptr()), None, 0, _stream(stream)))
+                                             P(out.data_ptr()), wp, wn, _stream(stream)))

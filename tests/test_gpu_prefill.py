@@ -73,3 +73,20 @@ def test_config3_chunk_at_depth_131072():
     _, got, err, _ = prefill_case(131072, rows, seed=3, check_rows=check)
     assert np.isfinite(got).all()
     assert err <= TOL
+
+
+def test_prefill_key_splits_agree_with_one_split():
+    # the launch splits the keys over workgroups when the row blocks alone do not fill the device (a workspace holds
+    # the partials); without a workspace it runs one split: both within the tolerance, of the oracle and each other
+    depth, rows = 20000, 300
+    pool, got, err, (q16, kf, vf, ctx) = prefill_case(depth, rows, seed=91, check_rows=[0, 150, 299])
+    assert pool.prefill_ws_bytes(ctx, rows, HQ) > 0  # this shape splits
+    assert err <= TOL
+    q = torch.from_numpy(q16).cuda()
+    one = torch.empty_like(q)
+    pool.prefill(0, 0, ctx, q, one, ws=False)
+    torch.cuda.synchronize()
+    one = one.cpu().numpy()
+    ref = O.attn_f64(q16.view(np.uint16), kf, vf, ctx, rows=[0, 150, 299])
+    assert cases.out_err(one[[0, 150, 299]], ref) <= TOL
+    assert np.abs(one.astype(np.float32) - got.astype(np.float32)).max() <= 2 * TOL
