@@ -2,22 +2,23 @@
 // positions ctx - rows .. ctx - 1) attend causally to the sequence's cells 0 .. ctx - 1 of one layer in the pool.
 //
 // What it computes (the reference's prompt attention, fn/kernels/qsa/qsa_prompt.h:50-58 and qsa_prompt_attn.cu:
-// 229-436, made dense and causal, on BASELINE's Q8_0 format): S = Q K^T * scale, online softmax, O = P V, fp16 out.
-// The reference rounds its K/V operand to fp16 once (q4_h4, qsa_prompt_attn.cu:195-207) and P to fp16, within a loose
-// 2e-2 bound; here K and V (code x scale, exact in fp32: 8 x 11 bits) and P go to the matrix cores as hi + lo fp16
-// pairs, so the products carry ~22 bits and the result meets 2e-3 against fp64 even when a few cells dominate.
+// 229-436, made dense and causal, on the pool's codes): S = Q K^T * scale, online softmax, O = P V, fp16 out. The
+// reference rounds its K/V operand to fp16 once (q4_h4, qsa_prompt_attn.cu:195-207) and P to fp16, within a loose
+// 2e-2 bound; here every product carries ~22 bits, so the result meets 2e-3 against fp64 even when a few cells
+// dominate: K goes to the matrix cores exactly as hi + lo fp16 (code x scale has 8 x 11 significant bits), V as its
+// codes (exact in fp16) against P x (the token's V scale) as hi + lo fp16.
 //
 // How (MI355X): matrix-core bound (4 d flops a visible (query, key) pair and head), so K/V tiles are dequantized once
 // a workgroup and shared by all its query rows.
-//   * A workgroup (8 waves, two a SIMD, so one wave's matrix-core work overlaps the other's VALU work) owns 128 query
-//     rows (128 / G query tokens x the G heads of one KV head); each wave owns one 16-row tile. Its waves walk the
-//     key tiles (32 tokens) in order up to the block's last query position.
-//   * Each tile streams HBM -> LDS (17 direct 1 KiB loads split over the waves, double-buffered), is dequantized once
-//     into fp16 MFMA operand planes in LDS (double-buffered: tile k + 1's while tile k is computed): K as code x
-//     scale rounded once to fp16 (the reference's prompt attention rounds its K operand the same way), V exactly as
-//     hi + lo fp16; then every wave runs S^T = K Q^T (one v_mfma_f32_16x16x32_f16 a block a 16-token half) and
-//     O^T += V^T P^T (three a 16-value tile: Vhi Phi, Vlo Phi, Vhi Plo) on it.
-//   * The softmax (base 2) runs on the S^T registers exactly as in the decode kernel; P feeds the PV MFMA in place.
+//   * A workgroup (8 waves, two a SIMD, so one wave's matrix-core work overlaps the other's VALU work) owns 256 query
+//     rows (256 / G query tokens x the G heads of one KV head); each wave owns two 16-row tiles, so each operand
+//     read from LDS feeds two MFMAs. Its waves walk the key tiles (32 tokens) of the workgroup's key split in order;
+//     the splits (blockIdx.z) fill the device when the row blocks alone do not, and a merge kernel folds them.
+//   * Each tile streams HBM -> LDS (16 direct 1 KiB loads of codes split over the waves into a double-buffered
+//     staging slot; the scales chunk into a 4-entry ring), is converted once into fp16 operand planes (K hi, K lo, V
+//     codes; double-buffered: tile k + 1's while tile k is computed); then every wave runs S^T = K Q^T (two
+//     v_mfma_f32_16x16x32_f16 a block, half and row tile) and O^T += V^T (P s_v)^T (two a 16-value tile and row tile).
+//   * The softmax (base 2) runs on the S^T registers as in the decode kernel; P feeds the PV MFMA in place.
 #include "../../include/fnkv.h"
 #include "common.h"
 #include "layout.h"
@@ -34,10 +35,11 @@ namespace fnkv {
 constexpr int32_t kPfWaves = 8;                      // two a SIMD
 constexpr int32_t kPfNT = 2;                         // 16-row tiles a wave (each plane read serves both)
 constexpr int32_t kPfRows = kPfWaves * kPfNT * 16;   // 256 rows a workgroup
-constexpr int32_t kPfStage = 8 * 1024 + 1024;        // a tile's K codes, then its K and V scales
-constexpr int32_t kPfPlane = 16 * 1024;             // one fp16 operand plane of a tile (K or V, hi or lo)
-constexpr int32_t kPfSet = 4 * kPfPlane;             // a tile's planes: K hi, K lo, V hi, V lo
-constexpr int32_t kPfLds = 2 * kPfStage + 2 * kPfSet; // staging and planes, both double-buffered
+constexpr int32_t kPfStage = 16 * 1024;              // a tile's K codes, then its V codes
+constexpr int32_t kPfPlane = 16 * 1024;             // one fp16 operand plane of a tile
+constexpr int32_t kPfSet = 3 * kPfPlane;             // a tile's planes: K hi, K lo, V codes
+constexpr int32_t kPfScaleRing = 4;                  // tiles' scale chunks (K then V scales, 1 KiB), a ring
+constexpr int32_t kPfLds = 2 * kPfStage + 2 * kPfSet + kPfScaleRing * 1024; // staging and planes double-buffered
 constexpr float kPfNegInf = -__builtin_inff();
 
 struct pf_args {
@@ -52,16 +54,17 @@ struct pf_args {
     int32_t n_split, split_tiles; // key tiles split over blockIdx.z: split z takes tiles z * split_tiles ..
 };
 
-// a tile's K codes (8 chunks of 1 KiB) and its scales chunk into a staging slot: wave w copies chunks w, w + 4,
-// wave 0 also the scales
-__device__ __forceinline__ void pf_issue(const uint8_t * tile, uint8_t * stage, int32_t wave, int32_t lane) {
+// a tile's 16 code chunks of 1 KiB (K, then V) into a staging slot (wave w copies chunks w and w + 8) and its scales
+// chunk into its place in the scale ring (wave 0)
+__device__ __forceinline__ void pf_issue(const uint8_t * tile, uint8_t * stage, uint8_t * scales, int32_t wave,
+                                         int32_t lane) {
 #pragma unroll
-    for (int32_t c = 0; c < 8 / kPfWaves; ++c) {
+    for (int32_t c = 0; c < 16 / kPfWaves; ++c) {
         const int32_t ch = wave + c * kPfWaves;
-        lds_load16(tile + kKCodes + ch * 1024 + lane * 16, stage + ch * 1024);
+        lds_load16(tile + ch * 1024 + lane * 16, stage + ch * 1024);
     }
     if (wave == 0) {
-        lds_load16(tile + kKScales + lane * 16, stage + 8 * 1024);
+        lds_load16(tile + kKScales + lane * 16, scales);
     }
 }
 
@@ -83,13 +86,13 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
 
     // Q operands (B of S^T = K Q^T) of this wave's two row tiles, and each row's causal limit
     half8 qop[kPfNT][kBlocks];
-    int64_t lim[kPfNT];
+    int32_t lim[kPfNT]; // each row's last visible cell, relative to the split's first
 #pragma unroll
     for (int nt = 0; nt < kPfNT; ++nt) {
         const int32_t r = (wave * kPfNT + nt) * 16 + j;
         const int32_t t = t_first + r / a.G;
         const bool real = t < a.rows;
-        lim[nt] = real ? pos_first + t : pos_first + t_last;
+        lim[nt] = static_cast<int32_t>((real ? pos_first + t : pos_first + t_last) - int64_t(ts0) * kTileTokens);
         const uint16_t * qrow = a.q + (int64_t(real ? t : t_last) * a.hq + int64_t(kvh) * a.G + r % a.G) * kHeadDim;
 #pragma unroll
         for (int b = 0; b < kBlocks; ++b) {
@@ -122,14 +125,16 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
     };
     uint8_t * const stage_base = smem;
     uint8_t * const plane_base = smem + 2 * kPfStage;
+    uint8_t * const ring_base = plane_base + 2 * kPfSet;
+    auto ring = [&](int32_t li) { return ring_base + (li & (kPfScaleRing - 1)) * 1024; };
 
-    // tile ti's K codes and scales (staging slot ti & 1) and V codes (vreg: this wave's V chunk) -> the fp16 operand
-    // planes (set ti & 1), each value exactly as hi + lo (code x scale has 8 x 11 significant bits): hi = fp16(code
-    // x scale), lo = the remainder by one fused multiply-add. Wave w converts K chunk (h, ld) = w and V chunk ld = w.
-    auto dequant = [&](int32_t ti, const u32x4 (&vreg)[8 / kPfWaves]) {
+    // tile ti's codes and scales (staging slot ti & 1) -> the fp16 operand planes (set ti & 1): K exactly as hi + lo
+    // (code x scale has 8 x 11 significant bits: hi = fp16(code x scale), lo = the remainder by one fused
+    // multiply-add), V as its codes (exact) with the V scales beside them. Wave w converts K chunk (h, ld) = w and V
+    // chunk ld = w.
+    auto dequant = [&](int32_t ti) {
         const uint8_t * st = stage_base + (ti & 1) * kPfStage;
-        const uint8_t * ksc = st + 8 * 1024;  // K scales [32 tokens][8 blocks]
-        const uint8_t * vsc = ksc + 512;      // V scales [4 lane groups][8 blocks][8 slots]
+        const uint8_t * ksc = ring(ti); // K scales [32 tokens][8 blocks]
         uint8_t * pl = plane_base + (ti & 1) * kPfSet;
 #pragma unroll
         for (int32_t c = 0; c < 8 / kPfWaves; ++c) {
@@ -153,30 +158,18 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
 #pragma unroll
         for (int32_t c = 0; c < 8 / kPfWaves; ++c) {
             const int32_t vc = wave + c * kPfWaves; // V chunk ld = vc: MFMA tiles m = 2 vc, 2 vc + 1 of block vc
-            const half8 vs = *reinterpret_cast<const half8 *>(vsc + qg * 128 + vc * 16);
+            const u32x4 w = *reinterpret_cast<const u32x4 *>(st + kVCodes + vc * 1024 + lane * 16);
 #pragma unroll
             for (int mm = 0; mm < 2; ++mm) {
-                const half8 code = widen8(vreg[c][2 * mm], vreg[c][2 * mm + 1]);
-                const half8 hi = code * vs;
-                const half8 lo = __builtin_elementwise_fma(code, vs, -hi);
                 const int32_t off = ((2 * vc + mm) * 64 + lane) * 16;
-                *reinterpret_cast<half8 *>(pl + 2 * kPfPlane + off) = hi;
-                *reinterpret_cast<half8 *>(pl + 3 * kPfPlane + off) = lo;
+                *reinterpret_cast<half8 *>(pl + 2 * kPfPlane + off) = widen8(w[2 * mm], w[2 * mm + 1]);
             }
-        }
-    };
-    auto load_v = [&](int32_t ti, u32x4 (&vreg)[8 / kPfWaves]) { // this wave's V chunks of tile ti
-        const uint8_t * t = tile_ptr(ti) + kVCodes + lane * 16;
-#pragma unroll
-        for (int32_t c = 0; c < 8 / kPfWaves; ++c) {
-            vreg[c] = *reinterpret_cast<const u32x4 *>(t + (wave + c * kPfWaves) * 1024);
         }
     };
 
     // tile ti on planes set ti & 1: scores, online softmax, PV
     auto compute = [&](int32_t ti) {
         const uint8_t * pl = plane_base + (ti & 1) * kPfSet;
-        const int64_t tok0 = int64_t(ts0 + ti) * kTileTokens;
         floatx4 sc[kPfNT][2];
 #pragma unroll
         for (int nt = 0; nt < kPfNT; ++nt) {
@@ -202,14 +195,25 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
         for (int nt = 0; nt < kPfNT; ++nt) {
             float v[8];
             float mx = kPfNegInf;
+            const int32_t rel = lim[nt] - ti * kTileTokens - 4 * qg; // this lane's tokens 16 h + r visible: <= rel
+            if (__all(rel >= 16 + 3)) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
+                for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int64_t pos = tok0 + 16 * h + 4 * qg + r;
-                    const float x = pos <= lim[nt] ? sc[nt][h][r] : kPfNegInf;
-                    v[4 * h + r] = x;
-                    mx = fmaxf(mx, x);
+                    for (int r = 0; r < 4; ++r) {
+                        v[4 * h + r] = sc[nt][h][r];
+                        mx = fmaxf(mx, sc[nt][h][r]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float x = 16 * h + r <= rel ? sc[nt][h][r] : kPfNegInf;
+                        v[4 * h + r] = x;
+                        mx = fmaxf(mx, x);
+                    }
                 }
             }
             mx = rows_max(mx) * a.c2;
@@ -232,17 +236,24 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
                 }
             }
         }
+        // O^T += V^T (P x s_v)^T, block by block: the V codes exact in fp16, P times the block's V scale (per
+        // token) as hi + lo fp16 (packed-fp16 TwoProduct: the pair carries ~22 bits)
 #pragma unroll
-        for (int m = 0; m < 16; ++m) {
-            const int32_t off = (m * 64 + lane) * 16;
-            const half8 vhi = *reinterpret_cast<const half8 *>(pl + 2 * kPfPlane + off);
-            const half8 vlo = *reinterpret_cast<const half8 *>(pl + 3 * kPfPlane + off);
+        for (int b = 0; b < kBlocks; ++b) {
+            // V scales [4 lane groups][8 blocks][8 slots] after the K scales
+            const half8 vs = *reinterpret_cast<const half8 *>(ring(ti) + 512 + qg * 128 + b * 16);
+            const half8 vc0 = *reinterpret_cast<const half8 *>(pl + 2 * kPfPlane + ((2 * b) * 64 + lane) * 16);
+            const half8 vc1 = *reinterpret_cast<const half8 *>(pl + 2 * kPfPlane + ((2 * b + 1) * 64 + lane) * 16);
 #pragma unroll
             for (int nt = 0; nt < kPfNT; ++nt) {
-                acc[nt][m] = mfma16(vhi, ph[nt], acc[nt][m]);
-                acc[nt][m] = mfma16(vlo, ph[nt], acc[nt][m]);
-                acc[nt][m] = mfma16(vhi, plo[nt], acc[nt][m]);
+                half8 shi, slo;
+                scale_hilo_pk(ph[nt], plo[nt], vs, shi, slo);
+                acc[nt][2 * b] = mfma16(vc0, shi, acc[nt][2 * b]);
+                acc[nt][2 * b + 1] = mfma16(vc1, shi, acc[nt][2 * b + 1]);
+                acc[nt][2 * b] = mfma16(vc0, slo, acc[nt][2 * b]);
+                acc[nt][2 * b + 1] = mfma16(vc1, slo, acc[nt][2 * b + 1]);
             }
+            __builtin_amdgcn_sched_barrier(0); // one block's operands live at a time
         }
     };
 
@@ -250,31 +261,23 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
     // slot tile ti used] [dequantize tile ti + 1 into the other plane set, load this wave's V chunk of tile ti + 2]
     // [compute tile ti]: the VALU-heavy dequantization of the next tile and the matrix-core work on this one are
     // independent, so one wave's overlaps the other's.
-    u32x4 vreg[8 / kPfWaves] = {};
     if (n_tiles > 0) {
-        pf_issue(tile_ptr(0), stage_base, wave, lane);
-        load_v(0, vreg);
+        pf_issue(tile_ptr(0), stage_base, ring(0), wave, lane);
         wait_vmcnt<0>();
         __syncthreads();
         if (n_tiles > 1) {
-            pf_issue(tile_ptr(1), stage_base + kPfStage, wave, lane);
+            pf_issue(tile_ptr(1), stage_base + kPfStage, ring(1), wave, lane);
         }
-        dequant(0, vreg);
-        if (n_tiles > 1) {
-            load_v(1, vreg);
-        }
+        dequant(0);
     }
     for (int32_t ti = 0; ti < n_tiles; ++ti) {
-        wait_vmcnt<0>(); // tile ti + 1's copy and V chunks (the last loads issued)
+        wait_vmcnt<0>(); // tile ti + 1's copy (the last loads issued)
         __syncthreads(); // ... every wave's; planes ti complete; staging slot ti & 1 and planes (ti + 1) & 1 free
         if (ti + 2 < n_tiles) {
-            pf_issue(tile_ptr(ti + 2), stage_base + (ti & 1) * kPfStage, wave, lane);
+            pf_issue(tile_ptr(ti + 2), stage_base + (ti & 1) * kPfStage, ring(ti + 2), wave, lane);
         }
         if (ti + 1 < n_tiles) {
-            dequant(ti + 1, vreg);
-            if (ti + 2 < n_tiles) {
-                load_v(ti + 2, vreg);
-            }
+            dequant(ti + 1);
         }
         compute(ti);
     }

@@ -146,12 +146,15 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
 
 /* ---- chunked-prefill attention (fn/kernels/qsa/qsa_prompt.h:106-124 qsp_attend) ---- */
 
+/* the workspace a prefill launch of this shape uses (bytes; 0: none; -1: a shape outside the contract) */
 int64_t fnkv_prefill_workspace_bytes(const fnkv_pool * pool, int64_t ctx, int32_t rows, int32_t hq);
 
 /* Causal attention of `rows` query tokens (positions ctx - rows .. ctx - 1 of the slot, already appended) over the
- * slot's cells 0 .. ctx - 1 of `layer`, on the matrix cores: K and V dequantized to fp16 (code x scale, rounded once,
- * as the reference's prompt attention does, qsa_prompt.h:55-58), QK^T and PV in fp16 with fp32 accumulation.
- * q: fp16 [rows][hq][256], out: fp16 [rows][hq][256]. */
+ * slot's cells 0 .. ctx - 1 of `layer`, on the matrix cores with fp32 accumulation: K as exact hi + lo fp16 operands,
+ * V as its codes against P x V-scale in hi + lo fp16 (the reference's prompt attention rounds its operands to fp16
+ * once, qsa_prompt.h:55-58; this keeps ~22 bits a product). q: fp16 [rows][hq][256], out: fp16 [rows][hq][256].
+ * ws: fnkv_prefill_workspace_bytes bytes of device memory (no zeroing needed) for the key-split partials when the
+ * query rows alone do not fill the device; null (or smaller): one split, no workspace. */
 int fnkv_attn_prefill(const fnkv_pool * pool, int32_t slot, int32_t layer, int64_t ctx, int32_t rows, int32_t hq,
                       float scale, const void * q, void * out, void * ws, int64_t ws_bytes, void * stream);
 
