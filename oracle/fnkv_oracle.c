@@ -7,11 +7,11 @@
  *
  * What each function restates (paths relative to the reference checkout):
  *   or_f32_to_f16 / or_f16_to_f32   ggml/src/ggml-impl.h:391-438 (fp32 <-> fp16, round to nearest even, subnormals,
- *                                   NaN -> 0x7e00 | sign); fn/quant/kv_q8_ref.cpp:10-86 is the same rounding.
+ *                                   NaN -> 0x7e00 | sign); fn/quant/kv_q8_ref.cpp:10-43 is the same rounding.
  *   or_q8_0_quantize                ggml/src/ggml-quants.c:274-297 quantize_row_q8_0_ref (blocks of 32:
  *                                   d = amax / 127, id = d ? 1 / d : 0, qs = roundf(x * id), stored fp16(d)).
  *   or_q8_0_dequantize              ggml/src/ggml-quants.c:551-565 dequantize_row_q8_0 (y = qs * fp32(d)).
- *   or_kv8_quantize                 fn/quant/kv_q8_ref.cpp:116-137 (FNFL's group-64 rule: s = fp16(amax / 127),
+ *   or_kv8_quantize                 fn/quant/kv_q8_ref.cpp:72-93 (FNFL's group-64 rule: s = fp16(amax / 127),
  *                                   code = clamp(nearbyint(x / s), -127, 127)).
  *   or_pages_*                      fn/model/kv_pool.cpp:85-144 kv_pages (pages_for, take, give, physical).
  *   or_reclaim_victim               fn/model/kv_pool.cpp:146-158 kv_reclaim_victim.

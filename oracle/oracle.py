@@ -124,7 +124,7 @@ def q8_0_dequantize(qs, d):
 
 
 def kv8_quantize(x):
-    """FNFL's group-64 rule (kv_q8_ref.cpp:116-137) -> (codes, scales)."""
+    """FNFL's group-64 rule (kv_q8_ref.cpp:72-93) -> (codes, scales)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     codes = np.empty(x.shape, np.int8)
     sc = np.empty(x.shape[:-1] + (x.shape[-1] // 64,), np.uint16)

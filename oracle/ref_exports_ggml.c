@@ -5,9 +5,9 @@
  *   fnkv_ref_q8_0_quantize   ggml/src/ggml-quants.c:274-297 quantize_row_q8_0_ref (block_q8_0 AoS out, 34 B a block)
  *   fnkv_ref_q8_0_dequantize ggml/src/ggml-quants.c:551-565 dequantize_row_q8_0
  *   fnkv_ref_f32_to_f16 / fnkv_ref_f16_to_f32   ggml/src/ggml-impl.h:391-438 (static inline in the header)
- *   fnkv_ref_kv8_quantize    fn/quant/kv_q8_ref.cpp:133-137 kv_q8_quantize (FNFL's group-64 rule)
- *   fnkv_ref_f16_bits_rn / fnkv_ref_f16_value   fn/quant/kv_q8_ref.cpp:10-114
- *   fnkv_ref_stress_rows     fn/quant/kv_q8_ref.cpp:139-213 kv_q8_stress_rows
+ *   fnkv_ref_kv8_quantize    fn/quant/kv_q8_ref.cpp:89-93 kv_q8_quantize (FNFL's group-64 rule)
+ *   fnkv_ref_f16_bits_rn / fnkv_ref_f16_value   fn/quant/kv_q8_ref.cpp:10-70
+ *   fnkv_ref_stress_rows     fn/quant/kv_q8_ref.cpp:99-169 kv_q8_stress_rows
  */
 
 #include <stdint.h>

@@ -7,7 +7,7 @@ exists: `python tests/golden/make_golden.py`. The GPU box never runs it; the tes
 
 Fixtures:
   q8_0_golden.npz   quantize_row_q8_0_ref (ggml-quants.c:274-297) on
-                      stress: kv_q8_stress_rows(0x6b5638, 8) (kv_q8_ref.cpp:139-213; the seed of qa2_test.cpp:1011)
+                      stress: kv_q8_stress_rows(0x6b5638, 8) (kv_q8_ref.cpp:99-169; the seed of qa2_test.cpp:1011)
                       allf16: every finite fp16 value, in bit order, as fp32 (1,984 blocks: each exponent range)
                       ties:   blocks whose x * id land exactly on k + 0.5 (roundf's ties away from zero)
                       rows:   seeded fp16 K/V rows, N(0, 1) with 4 of 256 channels x8 (BASELINE's distribution)
@@ -15,7 +15,7 @@ Fixtures:
                     (dequantize_row_q8_0, ggml-quants.c:551-565)
   f16_golden.npz    ggml_compute_fp32_to_fp16 (ggml-impl.h:414-438) on 40,000 seeded fp32 bit patterns plus edge
                     values; ggml_compute_fp16_to_fp32 (ggml-impl.h:391-412) on all 65,536 halves
-  kv8_golden.npz    FNFL's own KV8 rule kv_q8_quantize (kv_q8_ref.cpp:116-137) on the stress rows and the fp16 rows
+  kv8_golden.npz    FNFL's own KV8 rule kv_q8_quantize (kv_q8_ref.cpp:72-93) on the stress rows and the fp16 rows
 """
 import os
 import sys
