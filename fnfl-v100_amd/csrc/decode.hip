@@ -112,7 +112,7 @@ template <int NT> __device__ __forceinline__ void group_sync() {
     }
 }
 
-template <int NT>
+template <int NT, bool SP>
 __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(dec_args a) {
     constexpr int GR = dec_shape<NT>::GR;
     constexpr int WAVES = dec_shape<NT>::WAVES;
@@ -129,14 +129,17 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     const int64_t ctx = a.ctx[s];
     const int64_t begin = int64_t(sp) * a.split_tokens;
     const int64_t end = ctx < begin + a.split_tokens ? ctx : begin + a.split_tokens;
-    const int32_t n_tiles = static_cast<int32_t>((end - begin + kTileTokens - 1) / kTileTokens);
     const pool_view & pv = a.pv;
     const int32_t * table = pv.table + int64_t(a.slot[s]) * pv.table_stride;
-    // the split's pages (at most 64: splits are at most 16,384 cells), lane i holding logical page begin / 256 + i;
-    // a tile's page is then a lane read, not a memory load on the path to its copy. Loaded first: the page table, the
-    // Q rows and the first tile are then one memory latency each but overlapped, not three in a row.
-    const int32_t n_split_pages = static_cast<int32_t>((end - begin + kPageTokens - 1) / kPageTokens);
-    const int32_t split_page = lane < n_split_pages ? table[(begin >> 8) + lane] : 0;
+    // the split's tiles (at most 64), lane i holding tile i's page: a tile's page is then a lane read, not a memory
+    // load on the path to its copy. Loaded first: the page table, the Q rows and the first tile are then one memory
+    // latency each but overlapped, not three in a row.
+    split_src<SP> src;
+    src.init(a, table, split, begin, end, lane);
+    const int32_t n_tiles = src.n_tiles;
+    if (SP && n_tiles == 0) {
+        return; // past the selection's tiles (the merge reads only the splits that hold some)
+    }
     FNKV_STAMP(0);
 
     append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, wave, lane);
@@ -159,10 +162,8 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     auto kbuf = [&](int32_t slot) -> uint8_t * { return gbase + slot * 8192; };
     auto sslot = [&](int32_t slot) -> uint8_t * { return gbase + kCodeBytes + slot * kScaleBytes; };
     const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
-    auto tile_ptr = [&](int32_t ti) -> const uint8_t * {
-        const int32_t phys = __builtin_amdgcn_readlane(split_page, ti >> 3);
-        return layer_base + int64_t(phys) * pv.page_stride + int64_t(ti & 7) * kTileBytes;
-    };
+    auto tile_ptr = [&](int32_t ti) -> const uint8_t * { return layer_base + src.tile_off(pv, ti); };
+    const int32_t t_row = t_of_row(a, rt, j);
     u32x4 vreg[8];
     auto vload = [&](const uint8_t * tile) {
         // after every earlier instruction that touches memory: the V loads stay younger than the K copy issued
@@ -201,7 +202,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         if (have) {
         const uint8_t * kb = kbuf(it & 1);
         const uint8_t * sc_tile = sslot(it & 1) - kKScales; // scale offsets are tile-relative
-        const int64_t tok0 = begin + int64_t(ti) * kTileTokens;
+        const int64_t tok0 = src.tok0(ti);
 
         floatx4 sc[2];
         tile_scores(kb, sc_tile, [&](int b) { return qop[b]; }, sig, j, qg, lane, sc);
@@ -212,7 +213,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         float pf[8];
         {
             float alpha;
-            tile_softmax(sc, lim_rel, a.c2, qg, m_run, l_run, pf, alpha);
+            tile_softmax(sc, lim_rel, a.c2, qg, m_run, l_run, pf, alpha, src.vis(ti, t_row, qg));
             if (__any(alpha != 1.0f)) {
 #pragma unroll
                 for (int m = 0; m < 16; ++m) {
@@ -367,7 +368,7 @@ template <int NT> struct rows_shape {
     static constexpr int WAIT_V = 2 * CK + NBM;
 };
 
-template <int NT>
+template <int NT, bool SP>
 __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_kernel(dec_args a) {
     using SH = rows_shape<NT>;
     constexpr int GR = SH::GR, WAVES = SH::WAVES, SK = SH::SK, NBM = SH::NBM, CK = SH::CK;
@@ -384,13 +385,16 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
     const int64_t ctx = a.ctx[s];
     const int64_t begin = int64_t(sp) * a.split_tokens;
     const int64_t end = ctx < begin + a.split_tokens ? ctx : begin + a.split_tokens;
-    const int32_t n_tiles = static_cast<int32_t>((end - begin + kTileTokens - 1) / kTileTokens);
     const pool_view & pv = a.pv;
     const int32_t * table = pv.table + int64_t(a.slot[s]) * pv.table_stride;
-    // the split's pages, lane i holding logical page begin / 256 + i, loaded first (with the Q rows below, and the
-    // first tiles issued before the Q sums wait: overlapped latencies, not three in a row)
-    const int32_t n_split_pages = static_cast<int32_t>((end - begin + kPageTokens - 1) / kPageTokens);
-    const int32_t split_page = lane < n_split_pages ? table[(begin >> 8) + lane] : 0;
+    // the split's tiles, lane i holding tile i's page, loaded first (with the Q rows below, and the first tiles
+    // issued before the Q sums wait: overlapped latencies, not three in a row)
+    split_src<SP> src;
+    src.init(a, table, split, begin, end, lane);
+    const int32_t n_tiles = src.n_tiles;
+    if (SP && n_tiles == 0) {
+        return; // past the selection's tiles (the merge reads only the splits that hold some)
+    }
     FNKV_STAMP(0);
     append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, wave, lane);
     FNKV_STAMP(1);
@@ -441,9 +445,9 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
     auto tile_ptr = [&](int32_t k) -> const uint8_t * { // the group's tile of iteration k (the last tile past the end)
         int32_t ti = grp + k * GR;
         ti = ti < last_tile ? ti : last_tile;
-        const int32_t phys = __builtin_amdgcn_readlane(split_page, ti >> 3);
-        return layer_base + int64_t(phys) * pv.page_stride + int64_t(ti & 7) * kTileBytes;
+        return layer_base + src.tile_off(pv, ti);
     };
+    const int32_t t_row = t_of_row(a, w, j);
     const int32_t lane16 = lane * 16;
     // chunk c of a tile (c < 8: K codes, c = 8: the scales) into its place in a ring slot
     auto issue_chunk = [&](const uint8_t * tile, uint8_t * dst, int32_t c) {
@@ -502,14 +506,14 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
         }
         const uint8_t * kb = kslot(k % SK);
         const uint8_t * sc_tile = kb + kCodeBytes / 2 - kKScales; // scale offsets are tile-relative
-        const int64_t tok0 = begin + int64_t(grp + k * GR) * kTileTokens;
+        const int64_t tok0 = src.tok0(grp + k * GR);
         floatx4 sc[2];
         tile_scores(kb, sc_tile, qop_lds, sig, j, qg, lane, sc);
         const int64_t lim_rel64 = lim - tok0;
         const int32_t lim_rel = lim_rel64 > 64 ? 64 : static_cast<int32_t>(lim_rel64 < -1 ? -1 : lim_rel64);
         float pf[8];
         float alpha;
-        tile_softmax(sc, lim_rel, a.c2, qg, m_run, l_run, pf, alpha);
+        tile_softmax(sc, lim_rel, a.c2, qg, m_run, l_run, pf, alpha, src.vis(grp + k * GR, t_row, qg));
         half8 ph, pl;
         split_hilo(pf, ph, pl);
         u32x4 * px = reinterpret_cast<u32x4 *>(pslot(par, w) + lane * 32);
@@ -751,14 +755,6 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
 // columns x 32 split groups. Group g folds splits g, g + 32, ... in order with a running max (all its loads
 // independent, so they are in flight together: one memory round trip), then the 32 groups fold in order in LDS
 // (deterministic: the same order for every launch).
-struct merge_args {
-    const float * po;
-    const float * pml;
-    uint16_t * out; // fp16 [n_seq][T][hq][256]
-    int32_t T, G, hq, R, h_kv, n_seq;
-    int32_t split0[FNKV_MAX_SEQS + 1];
-};
-
 __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
     __shared__ float sM[32];
     __shared__ float sL[32];
@@ -771,7 +767,12 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
     rest /= a.R;
     const int32_t kvh = rest % a.h_kv;
     const int32_t s = rest / a.h_kv;
-    const int32_t s0 = a.split0[s], n = a.split0[s + 1] - s0;
+    const int32_t s0 = a.split0[s];
+    int32_t n = a.split0[s + 1] - s0;
+    if (a.sel_n != nullptr) { // a sparse launch: only the splits that hold selected tiles ran
+        const int32_t used = (*a.sel_n + a.sel_split - 1) / a.sel_split;
+        n = used < n ? used : n;
+    }
     float m = kNegInf, l = 0.0f;
     floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
@@ -897,6 +898,41 @@ dec_plan plan_decode(const kv_pool & p, int32_t n_seq, const int64_t * ctx, int3
     return pl;
 }
 
+void launch_merge(const merge_args & m, hipStream_t st) {
+    hipLaunchKernelGGL(merge_kernel, dim3(static_cast<uint32_t>(m.n_seq * m.h_kv * m.R * 8)), dim3(256), 0, st, m);
+}
+
+// the decode kernel for NT row tiles (sparse or dense), its LDS attribute set once per device
+template <bool SP> void launch_decode(const kv_pool & p, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
+    static bool attr_set[64] = {false};
+    const int32_t dev = p.device();
+    if (dev >= 0 && dev < 64 && !attr_set[dev]) {
+        int32_t cur = 0;
+        (void)hipGetDevice(&cur);
+        (void)hipSetDevice(dev);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<1, SP>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(1));
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<2, SP>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(2));
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<3, SP>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3));
+        (void)hipGetLastError();
+        (void)hipSetDevice(cur);
+        attr_set[dev] = true;
+    }
+    if (NT == 1) {
+        hipLaunchKernelGGL((decode_kernel<1, SP>), grid, dim3(64 * dec_shape<1>::WAVES), decode_lds(1), st, a);
+    } else if (NT == 2) {
+        hipLaunchKernelGGL((decode_rows_kernel<2, SP>), grid, dim3(64 * rows_shape<2>::WAVES), decode_lds(2), st, a);
+    } else {
+        hipLaunchKernelGGL((decode_rows_kernel<3, SP>), grid, dim3(64 * rows_shape<3>::WAVES), decode_lds(3), st, a);
+    }
+}
+
+void launch_decode_sparse(const kv_pool & p, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
+    launch_decode<true>(p, NT, grid, a, st);
+}
+
 } // namespace fnkv
 
 using fnkv::set_error;
@@ -969,6 +1005,10 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
     a.R = R;
     a.n_seq = n_seq;
     a.split_tokens = pl.split_tokens;
+    a.sel_tiles = nullptr;
+    a.sel_masks = nullptr;
+    a.sel_n = nullptr;
+    a.sel_split = 0;
     for (int32_t i = 0; i < FNKV_MAX_SEQS; ++i) {
         a.slot[i] = i < n_seq ? slots[i] : 0;
         a.ctx[i] = i < n_seq ? ctx[i] : 0;
@@ -981,33 +1021,7 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
 #endif
     hipStream_t st = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<uint32_t>(pl.total), static_cast<uint32_t>(p->h_kv()));
-    const int32_t NT = (R + 15) / 16;
-    static bool attr_set[64] = {false};
-    const int32_t dev = p->device();
-    if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-        int32_t cur = 0;
-        hipGetDevice(&cur);
-        hipSetDevice(dev);
-        hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::decode_kernel<1>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::decode_lds(1));
-        hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::decode_rows_kernel<2>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::decode_lds(2));
-        hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::decode_rows_kernel<3>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::decode_lds(3));
-        hipGetLastError();
-        hipSetDevice(cur);
-        attr_set[dev] = true;
-    }
-    if (NT == 1) {
-        hipLaunchKernelGGL(fnkv::decode_kernel<1>, grid, dim3(64 * fnkv::dec_shape<1>::WAVES), fnkv::decode_lds(1),
-                           st, a);
-    } else if (NT == 2) {
-        hipLaunchKernelGGL(fnkv::decode_rows_kernel<2>, grid, dim3(64 * fnkv::rows_shape<2>::WAVES),
-                           fnkv::decode_lds(2), st, a);
-    } else {
-        hipLaunchKernelGGL(fnkv::decode_rows_kernel<3>, grid, dim3(64 * fnkv::rows_shape<3>::WAVES),
-                           fnkv::decode_lds(3), st, a);
-    }
+    fnkv::launch_decode<false>(*p, (R + 15) / 16, grid, a, st);
     fnkv::merge_args m;
     m.po = a.po;
     m.pml = a.pml;
@@ -1018,11 +1032,12 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
     m.R = R;
     m.h_kv = p->h_kv();
     m.n_seq = n_seq;
+    m.sel_n = nullptr;
+    m.sel_split = 0;
     for (int32_t i = 0; i <= FNKV_MAX_SEQS; ++i) {
         m.split0[i] = a.split0[i];
     }
-    hipLaunchKernelGGL(fnkv::merge_kernel, dim3(static_cast<uint32_t>(n_seq * p->h_kv() * R * 8)), dim3(256), 0, st,
-                       m);
+    fnkv::launch_merge(m, st);
     if (hipGetLastError() != hipSuccess) {
         set_error("fnkv_attn_decode: launch failed");
         return FNKV_ERR_HIP;

@@ -32,6 +32,13 @@ struct dec_args {
     int32_t slot[FNKV_MAX_SEQS];
     int64_t ctx[FNKV_MAX_SEQS];
     int32_t split0[FNKV_MAX_SEQS + 1]; // first split of each sequence; split0[n_seq] = total
+    // a sparse launch (one sequence): the ascending union of the logical tiles the rows' selections touch, each
+    // row's 4-cell blocks in it (row t's 8 bits at bit 8 t of .x for t < 4, of .y for t = 4), their count (device),
+    // and the entries a split takes (split s: entries s * sel_split ..)
+    const int32_t * sel_tiles;
+    const uint2 * sel_masks;
+    const int32_t * sel_n;
+    int32_t sel_split;
 #ifdef FNKV_TIMING
     uint64_t * ts; // per workgroup: 16 real-time stamps (instrumented builds only)
 #endif
@@ -91,6 +98,91 @@ struct dec_args {
     do {                                                                                                             \
     } while (0)
 #endif
+
+// The tiles a workgroup walks. Dense: its split's consecutive cells begin .. end, lane i holding the physical page
+// of the split's logical page i. Sparse: entries e0 .. e0 + n_tiles - 1 of the selection's tile list, lane i holding
+// entry i's logical tile, physical page and row masks. Tile ti of the walk is then a lane read either way.
+template <bool SP> struct split_src {
+    int32_t n_tiles = 0;
+    int32_t page_lane = 0;
+    int32_t tile_lane = 0;
+    uint32_t mlo_lane = 0, mhi_lane = 0;
+    int64_t begin = 0;
+
+    __device__ __forceinline__ void init(const dec_args & a, const int32_t * table, int32_t split, int64_t b,
+                                         int64_t e, int32_t lane) {
+        if constexpr (SP) {
+            const int32_t e0 = split * a.sel_split;
+            const int32_t left = *a.sel_n - e0;
+            n_tiles = left < 0 ? 0 : left < a.sel_split ? left : a.sel_split;
+            if (lane < n_tiles) {
+                tile_lane = a.sel_tiles[e0 + lane];
+                const uint2 m = a.sel_masks[e0 + lane];
+                mlo_lane = m.x;
+                mhi_lane = m.y;
+                page_lane = table[tile_lane >> 3];
+            }
+        } else {
+            begin = b;
+            n_tiles = static_cast<int32_t>((e - b + kTileTokens - 1) / kTileTokens);
+            const int32_t n_pages = static_cast<int32_t>((e - b + kPageTokens - 1) / kPageTokens);
+            page_lane = lane < n_pages ? table[(b >> 8) + lane] : 0;
+        }
+    }
+    // byte offset of walk tile ti within the (layer, head) plane of the pool
+    __device__ __forceinline__ int64_t tile_off(const pool_view & pv, int32_t ti) const {
+        if constexpr (SP) {
+            const int32_t phys = __builtin_amdgcn_readlane(page_lane, ti);
+            const int32_t t8 = __builtin_amdgcn_readlane(tile_lane, ti) & 7;
+            return int64_t(phys) * pv.page_stride + int64_t(t8) * kTileBytes;
+        } else {
+            const int32_t phys = __builtin_amdgcn_readlane(page_lane, ti >> 3);
+            return int64_t(phys) * pv.page_stride + int64_t(ti & 7) * kTileBytes;
+        }
+    }
+    // the first cell of walk tile ti
+    __device__ __forceinline__ int64_t tok0(int32_t ti) const {
+        if constexpr (SP) {
+            return int64_t(__builtin_amdgcn_readlane(tile_lane, ti)) * kTileTokens;
+        } else {
+            return begin + int64_t(ti) * kTileTokens;
+        }
+    }
+    // the visibility bits of tile_softmax for this lane (query row of step token t_row, lane group qg)
+    __device__ __forceinline__ uint32_t vis(int32_t ti, int32_t t_row, int32_t qg) const {
+        if constexpr (SP) {
+            const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int32_t>(mlo_lane), ti));
+            const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int32_t>(mhi_lane), ti));
+            const uint32_t byte = t_row < 4 ? (lo >> (8 * t_row)) : hi;
+            return ((byte >> qg) & 1u) | (((byte >> (4 + qg)) & 1u) << 1);
+        } else {
+            return 3u;
+        }
+    }
+};
+
+// the step token of this lane's query row (rt * 16 + j); padding rows take the last
+__device__ __forceinline__ int32_t t_of_row(const dec_args & a, int32_t rt, int32_t j) {
+    const int32_t row = rt * 16 + j;
+    return row < a.R ? row / a.G : a.T - 1;
+}
+
+// the split merge's arguments (merge_kernel): partials of n_seq sequences, split0 as in dec_args; for a sparse
+// launch sel_n / sel_split bound the splits that ran
+struct merge_args {
+    const float * po;
+    const float * pml;
+    uint16_t * out; // fp16 [n_seq][T][hq][256]
+    int32_t T, G, hq, R, h_kv, n_seq;
+    int32_t split0[FNKV_MAX_SEQS + 1];
+    const int32_t * sel_n;
+    int32_t sel_split;
+};
+
+class kv_pool;
+// host: the merge launch, and the sparse instantiation of the decode kernels (decode.hip)
+void launch_merge(const merge_args & m, hipStream_t st);
+void launch_decode_sparse(const kv_pool & p, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st);
 
 __device__ __forceinline__ int32_t seq_of(const dec_args & a, int32_t split) {
     int32_t s = 0;
@@ -181,51 +273,59 @@ __device__ __forceinline__ half8 q_sums(const half8 (&qop)[kBlocks], int32_t qg)
     return sig;
 }
 
-// S^T = K Q^T for a tile's two 16-token halves from its K codes (kb) and scales (sc_tile + kKScales ...) in LDS:
-// sc[h][r] is the score of token 16 h + 4 qg + r against this lane's row j, unscaled (q . k)
+// S^T = K Q^T for one 16-token half h of a tile from its K codes (kb) and scales (sc_tile + kKScales ...) in LDS:
+// the returned r-th value is the score of token 16 h + 4 qg + r against this lane's row j, unscaled (q . k).
 // The Q operand of block b comes from qop(b): registers, or LDS where registers are short.
+template <typename QOP>
+__device__ __forceinline__ floatx4 tile_scores_half(const uint8_t * kb, const uint8_t * sc_tile, const QOP & qop,
+                                                    half8 sig, int32_t j, int32_t qg, int32_t lane, int32_t h) {
+    const half8 zero8 = {};
+    // this lane's score rows are tokens 16 h + 4 qg + r; their K scales, all 8 blocks
+    half8 ks[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        ks[r] = *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + 4 * qg + r) * 16);
+    }
+    // the bias term: A = this lane's token row of K scales (twice), B = sigma hi / lo
+    const half8 srow = qg < 2 ? *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + j) * 16) : zero8;
+    const floatx4 corr = mfma16(srow, sig, floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+    floatx4 acc_s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) { // blocks 4 hb .. 4 hb + 3 (fewer live results)
+        floatx4 t[4];
+#pragma unroll
+        for (int ld = 2 * hb; ld < 2 * hb + 2; ++ld) {
+            const u32x4 kw = *reinterpret_cast<const u32x4 *>(kb + h * 4096 + ld * 1024 + lane * 16);
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) {
+                const int b = 2 * ld + bb;
+                const half8 ka = widen8_biased(kw[2 * bb], kw[2 * bb + 1]);
+                t[b - 4 * hb] = mfma16(ka, qop(b), floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+            }
+        }
+#pragma unroll
+        for (int b = 4 * hb; b < 4 * hb + 4; ++b) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                acc_s[r] = __builtin_fmaf(static_cast<float>(ks[r][b]), t[b - 4 * hb][r], acc_s[r]);
+            }
+        }
+    }
+    floatx4 sc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        sc[r] = __builtin_fmaf(-1152.0f, corr[r], acc_s[r]);
+    }
+    return sc;
+}
+
+// both halves: sc[h][r] is the score of token 16 h + 4 qg + r against this lane's row j
 template <typename QOP>
 __device__ __forceinline__ void tile_scores(const uint8_t * kb, const uint8_t * sc_tile, const QOP & qop, half8 sig,
                                             int32_t j, int32_t qg, int32_t lane, floatx4 (&sc)[2]) {
-    const half8 zero8 = {};
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        // this lane's score rows are tokens 16 h + 4 qg + r; their K scales, all 8 blocks
-        half8 ks[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            ks[r] = *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + 4 * qg + r) * 16);
-        }
-        // the bias term: A = this lane's token row of K scales (twice), B = sigma hi / lo
-        const half8 srow =
-            qg < 2 ? *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + j) * 16) : zero8;
-        const floatx4 corr = mfma16(srow, sig, floatx4{0.0f, 0.0f, 0.0f, 0.0f});
-        floatx4 acc_s = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) { // blocks 4 hb .. 4 hb + 3 (fewer live results)
-            floatx4 t[4];
-#pragma unroll
-            for (int ld = 2 * hb; ld < 2 * hb + 2; ++ld) {
-                const u32x4 kw = *reinterpret_cast<const u32x4 *>(kb + h * 4096 + ld * 1024 + lane * 16);
-#pragma unroll
-                for (int bb = 0; bb < 2; ++bb) {
-                    const int b = 2 * ld + bb;
-                    const half8 ka = widen8_biased(kw[2 * bb], kw[2 * bb + 1]);
-                    t[b - 4 * hb] = mfma16(ka, qop(b), floatx4{0.0f, 0.0f, 0.0f, 0.0f});
-                }
-            }
-#pragma unroll
-            for (int b = 4 * hb; b < 4 * hb + 4; ++b) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    acc_s[r] = __builtin_fmaf(static_cast<float>(ks[r][b]), t[b - 4 * hb][r], acc_s[r]);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            sc[h][r] = __builtin_fmaf(-1152.0f, corr[r], acc_s[r]);
-        }
+        sc[h] = tile_scores_half(kb, sc_tile, qop, sig, j, qg, lane, h);
         __builtin_amdgcn_sched_barrier(0); // one half's operands live at a time
     }
 }
@@ -236,12 +336,14 @@ __device__ __forceinline__ void tile_scores(const uint8_t * kb, const uint8_t * 
 // accumulators is rare; the weights pf[4 h + r] = 2^(c2 sc - m_run) stay <= 2^kLazyLog2 = 64, which keeps a weight
 // times a V scale (at most 65504 / 127) inside fp16. alpha is the same in the row's four lanes.
 constexpr float kLazyLog2 = 6.0f;
+// vis: bit h set when this lane's 4 cells of half h (one 4-cell block) are in its row's selection (dense: 3).
 __device__ __forceinline__ void tile_softmax(const floatx4 (&sc)[2], int32_t lim_rel, float c2, int32_t qg,
-                                             float & m_run, float & l_run, float (&pf)[8], float & alpha) {
+                                             float & m_run, float & l_run, float (&pf)[8], float & alpha,
+                                             uint32_t vis = 3) {
     // the max runs on the raw scores (c2 > 0 keeps the order); each weight is one FMA and one exp2
     float raw[8];
     float mx = kNegInf;
-    if (__all(lim_rel >= 31)) { // the whole tile is visible to every row of the wave
+    if (__all(lim_rel >= 31 && vis == 3)) { // the whole tile is visible to every row of the wave
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -255,7 +357,7 @@ __device__ __forceinline__ void tile_softmax(const floatx4 (&sc)[2], int32_t lim
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float x = 16 * h + 4 * qg + r <= lim_rel ? sc[h][r] : kNegInf;
+                const float x = (16 * h + 4 * qg + r <= lim_rel && ((vis >> h) & 1u)) ? sc[h][r] : kNegInf;
                 raw[4 * h + r] = x;
                 mx = fmaxf(mx, x);
             }

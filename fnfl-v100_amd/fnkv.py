@@ -22,6 +22,7 @@ EXPORTS = [
     "fnkv_page_block_bytes", "fnkv_pool_device_base", "fnkv_pool_device_bytes", "fnkv_q8_append",
     "fnkv_export_q8_0", "fnkv_decode_workspace_bytes", "fnkv_attn_decode", "fnkv_prefill_workspace_bytes",
     "fnkv_attn_prefill", "fnkv_pool_create_fmt", "fnkv_pool_format", "fnkv_export_kv8",
+    "fnkv_sparse_workspace_bytes", "fnkv_attn_sparse",
 ]
 
 P = ctypes.c_void_p
@@ -92,6 +93,10 @@ def lib():
         L.fnkv_decode_workspace_bytes.argtypes = [P, I32, P, I32, I32]
         L.fnkv_attn_decode.restype = ctypes.c_int
         L.fnkv_attn_decode.argtypes = [P, I32, P, P, I32, I32, I32, ctypes.c_float, P, P, P, I32, P, P, I64, P]
+        L.fnkv_sparse_workspace_bytes.restype = I64
+        L.fnkv_sparse_workspace_bytes.argtypes = [P, I64, I32, I32]
+        L.fnkv_attn_sparse.restype = ctypes.c_int
+        L.fnkv_attn_sparse.argtypes = [P, I32, I64, I32, I32, I32, ctypes.c_float, P, P, P, P, P, I32, P, P, I64, P]
         L.fnkv_prefill_workspace_bytes.restype = I64
         L.fnkv_prefill_workspace_bytes.argtypes = [P, I64, I32, I32]
         L.fnkv_attn_prefill.restype = ctypes.c_int
@@ -243,6 +248,25 @@ class Pool:
         dt = F32 if (k_new is not None and k_new.dtype == torch.float32) else F16
         return check(lib().fnkv_attn_decode(self.h, len(slots), sp, cp, T, layer, hq, scale, P(q.data_ptr()), kp, vp,
                                             dt, P(out.data_ptr()), P(ws.data_ptr()), ws.numel() * ws.element_size(),
+                                            _stream(stream)))
+
+    def sparse_ws_bytes(self, depth, T, hq):
+        return lib().fnkv_sparse_workspace_bytes(self.h, depth, T, hq)
+
+    def sparse(self, slot, depth, layer, q, body, offsets, out, ws=None, scale=1.0 / 16.0, k_new=None, v_new=None,
+               stream=None):
+        """QSA attention: q, out fp16 [T][hq][256]; body int32/uint32 device words, offsets int32 device [T + 1]
+        (qsa.h layout); k_new, v_new (optional) [T][h_kv][256]: the rows' own cells."""
+        import torch
+        T, hq = q.shape[0], q.shape[1]
+        if ws is None:
+            ws = torch.empty(max(16, self.sparse_ws_bytes(depth, T, hq)), dtype=torch.uint8, device=q.device)
+        kp = P(k_new.data_ptr()) if k_new is not None else None
+        vp = P(v_new.data_ptr()) if v_new is not None else None
+        dt = F32 if (k_new is not None and k_new.dtype == torch.float32) else F16
+        return check(lib().fnkv_attn_sparse(self.h, slot, depth, T, layer, hq, scale, P(q.data_ptr()),
+                                            P(body.data_ptr()), P(offsets.data_ptr()), kp, vp, dt,
+                                            P(out.data_ptr()), P(ws.data_ptr()), ws.numel() * ws.element_size(),
                                             _stream(stream)))
 
     def prefill_ws_bytes(self, ctx, rows, hq):

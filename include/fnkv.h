@@ -144,6 +144,24 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
                      int32_t layer, int32_t hq, float scale, const void * q, const void * k_new, const void * v_new,
                      int32_t new_dtype, void * out, void * ws, int64_t ws_bytes, void * stream);
 
+/* ---- sparse (QSA) attention at decode rows (fn/kernels/qsa/attend.h:97-141 attend over a selection body) ---- */
+
+/* The workspace a sparse launch at this depth needs (bytes; no zeroing needed); -1 outside the contract. */
+int64_t fnkv_sparse_workspace_bytes(const fnkv_pool * pool, int64_t depth, int32_t T, int32_t hq);
+
+/* Attention of T (1..5) query rows of the sequence in `slot`, row t at position depth + t, each over its own
+ * selection: body (device, U32 words) in the reference's selected-block layout (fn/kernels/qsa/qsa.h:77-81): row t
+ * has K = min((q + 1) / 4, 512) ascending 4-cell block IDs and its tail cells 4 ((q + 1) / 4) .. q, the rows packed in
+ * order (2 + K + tail words each). offsets (device, I32 [T + 1]) is the reference's byte-offset array; the launch
+ * derives the same offsets from depth and T (they depend on nothing else) and reads no word past the body. Block IDs
+ * outside the row's whole blocks are ignored. k_new / v_new (optional, [T][h_kv][256] of new_dtype): the rows' own
+ * cells, written at depth .. depth + T - 1 before any row reads (a row's selection need not include them). q, out:
+ * fp16 [T][hq][256]; scores q.k * scale, softmax and accumulation in fp32, over the pool's codes exactly as the dense
+ * launch. depth + T <= 262,176 and mapped. */
+int fnkv_attn_sparse(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq,
+                     float scale, const void * q, const void * body, const void * offsets, const void * k_new,
+                     const void * v_new, int32_t new_dtype, void * out, void * ws, int64_t ws_bytes, void * stream);
+
 /* ---- chunked-prefill attention (fn/kernels/qsa/qsa_prompt.h:106-124 qsp_attend) ---- */
 
 /* the workspace a prefill launch of this shape uses (bytes; 0: none; -1: a shape outside the contract) */

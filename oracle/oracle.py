@@ -226,6 +226,57 @@ def attn_f64(q16, k, v, n_ctx, scale=1.0 / 16.0, rows=None):
     return out
 
 
+def attn_f64_cells(q16, k, v, cells, scale=1.0 / 16.0):
+    """FP64 attention of each query row over its own list of cells (the QSA attention's math, attend.h:16-18:
+    softmax_c(q . K[c] * scale) . V[c] over row t's selected cells). q16: uint16 [T][hq][d]; k, v: float32
+    [n][hkv][d] (decoded cache); cells: T int arrays -> float64 [T][hq][d]."""
+    q = np.ascontiguousarray(q16, dtype=np.uint16).view(np.float16).astype(np.float64)
+    T, hq, d = q.shape
+    hkv = k.shape[1]
+    G = hq // hkv
+    out = np.empty((T, hq, d), np.float64)
+    for t in range(T):
+        c = np.asarray(cells[t], dtype=np.int64)
+        kk = k[c].astype(np.float64)  # [n][hkv][d]
+        vv = v[c].astype(np.float64)
+        for h in range(hq):
+            s = (kk[:, h // G, :] @ q[t, h]) * scale
+            p = np.exp(s - s.max())
+            out[t, h] = (p @ vv[:, h // G, :]) / p.sum()
+    return out
+
+
+def qsa_body(depth, T, seed, clustered=False):
+    """A selection body in the reference's layout (qsa.h:77-81) for rows t at positions q = depth + t: K =
+    min((q + 1) / 4, 512) distinct ascending 4-cell blocks among the row's whole blocks, then the tail cells
+    4 ((q + 1) / 4) .. q. -> (uint32 words, int32 byte offsets [T + 1], the rows' cell lists)."""
+    rng = np.random.default_rng([seed, 17])
+    words, offsets, cells = [], [0], []
+    for t in range(T):
+        q = depth + t
+        n_vis = (q + 1) // 4
+        K = min(n_vis, 512)
+        if clustered and n_vis > K:
+            # a sink, a local window and a few runs, as selections tend to be
+            runs = [np.arange(0, min(16, n_vis)), np.arange(max(0, n_vis - 64), n_vis)]
+            while sum(r.size for r in runs) < 2 * K:
+                s0 = int(rng.integers(0, n_vis))
+                runs.append(np.arange(s0, min(n_vis, s0 + int(rng.integers(8, 64)))))
+            pool = np.unique(np.concatenate(runs))
+            blocks = np.sort(rng.choice(pool, size=min(K, pool.size), replace=False))
+            if blocks.size < K:
+                rest = np.setdiff1d(np.arange(n_vis), blocks)
+                blocks = np.sort(np.concatenate([blocks, rng.choice(rest, K - blocks.size, replace=False)]))
+        else:
+            blocks = np.sort(rng.choice(n_vis, size=K, replace=False)) if K else np.zeros(0, np.int64)
+        tail = np.arange(4 * n_vis, q + 1)
+        row = [K, tail.size] + [int(b) for b in blocks] + [int(c) for c in tail]
+        words += row
+        offsets.append(offsets[-1] + 4 * len(row))
+        cells.append(np.concatenate([(4 * blocks[:, None] + np.arange(4)[None, :]).reshape(-1), tail]))
+    return np.array(words, np.uint32), np.array(offsets, np.int32), cells
+
+
 def attn_ggml(q16, k_blocks, v_blocks, n_ctx, scale=1.0 / 16.0, q_as_q8=False, threads=1, hkv=2):
     """ggml-semantics CPU flash attention over contiguous block_q8_0 K/V [cells][hkv][d/32][34 B] (at least n_ctx
     cells) -> fp16 bits [T][hq][d]."""

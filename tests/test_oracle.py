@@ -197,3 +197,35 @@ def test_attn_ggml_path_within_tolerance():
     got8 = O.attn_ggml(q16, kb, vb, n, q_as_q8=True, threads=4).view(np.float16).astype(np.float64)
     # Q itself quantized to Q8_0 (ggml's vec_dot operand): a documented divergence of ~2.6e-2 here, bounded loosely
     assert np.abs(got8 - ref).max() <= 5e-2
+
+
+def test_attn_f64_cells_pinned_by_the_dense_form():
+    # over every causal cell of each row the per-row-cells form is the dense form (itself pinned above by closed
+    # forms and brute force); one selected cell returns its V row; the order of a row's cells does not matter
+    rng = np.random.default_rng(5)
+    n, T, hq, hkv, d = 70, 3, 4, 2, 32
+    k = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    q16 = rng.standard_normal((T, hq, d)).astype(np.float16).view(np.uint16)
+    cells = [np.arange(n - T + t + 1) for t in range(T)]
+    np.testing.assert_allclose(O.attn_f64_cells(q16, k, v, cells), O.attn_f64(q16, k, v, n), rtol=0, atol=1e-12)
+    one = O.attn_f64_cells(q16, k, v, [np.array([7])] * T)
+    assert np.allclose(one[:, 0], v[7, 0][None, :]) and np.allclose(one[:, 3], v[7, 1][None, :])
+    perm = [rng.permutation(c) for c in cells]
+    np.testing.assert_allclose(O.attn_f64_cells(q16, k, v, perm), O.attn_f64(q16, k, v, n), rtol=0, atol=1e-12)
+
+
+def test_qsa_body_layout():
+    # qsa.h:77-81: 2 + K + tail words a row, K = min((q + 1) / 4, 512), blocks ascending and whole, tail 4 n_vis .. q
+    for depth, T in ((0, 1), (2, 5), (2045, 3), (9000, 5)):
+        words, offs, cells = O.qsa_body(depth, T, seed=depth)
+        assert offs[0] == 0 and offs[-1] == 4 * words.size
+        for t in range(T):
+            q = depth + t
+            row = words[offs[t] // 4: offs[t + 1] // 4]
+            K, tail = int(row[0]), int(row[1])
+            assert K == min((q + 1) // 4, 512) and tail == (q + 1) % 4 and row.size == 2 + K + tail
+            blocks = row[2:2 + K].astype(np.int64)
+            assert np.all(np.diff(blocks) > 0) and (K == 0 or 4 * blocks[-1] + 3 <= q)
+            assert list(row[2 + K:]) == list(range(4 * ((q + 1) // 4), q + 1))
+            assert cells[t].size == 4 * K + tail and cells[t].max() <= q
