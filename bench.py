@@ -43,6 +43,11 @@ CONFIGS = {
     "cfg3": dict(ctxs=[131072 + 2048], T=2048, layers=1, prefill=True,
                  workload="cfg3: 2,048-token fp16 chunk appended at depth 131,072 and attended causally over 133,120 "
                           "cells (chunked prefill, matrix cores), 1 layer"),
+    "qsa3": dict(depth=196608 - 3, T=3, layers=12, sparse=True,
+                 workload="qsa3: sparse (QSA) attention, 3 rows at 196,608 cells, each over its own 512 blocks + tail "
+                          "(random, rows disjoint: the reference's QA2 shape), 12 layers"),
+    "qsa1": dict(depth=196608 - 1, T=1, layers=12, sparse=True,
+                 workload="qsa1: sparse (QSA) attention, 1 row at 196,608 cells over 512 blocks + tail, 12 layers"),
 }
 PEAK_MFMA_F16_TFLOPS = 2500.0  # dense fp16 matrix-core peak
 
@@ -293,6 +298,126 @@ def run_prefill(args, cfg):
     pool.close()
 
 
+def run_sparse(args, cfg):
+    """Sparse (QSA) attention: one step = for each of the 12 layers one fnkv_attn_sparse launch (the rows' own cells
+    written, each row attending to its 512 selected blocks and tail), captured in a HIP graph. Algorithmic bytes: the
+    selected cells' K and V (both heads), Q in and O out, the new cells' write."""
+    import numpy as np
+    import torch
+
+    import cases
+    import fnkv
+    import oracle as O
+
+    depth, T, layers = cfg["depth"], cfg["T"], cfg["layers"]
+    ctx = depth + T
+    torch.cuda.set_device(0)
+    pool, slots = make_pool(torch, fnkv, cases, [ctx], T, layers, args.seed)
+    bodies, cells = [], []
+    for layer in range(layers):
+        w, o, c = O.qsa_body(depth, T, args.seed + layer)
+        bodies.append((torch.from_numpy(w.view(np.int32)).cuda(), torch.from_numpy(o).cuda()))
+        cells.append(c)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(args.seed + 7)
+    q = torch.randn((layers, T, HQ, D), generator=g, device="cuda").half()
+    kn = torch.randn((layers, T, HKV, D), generator=g, device="cuda").half()
+    vn = torch.randn((layers, T, HKV, D), generator=g, device="cuda").half()
+    out = torch.empty_like(q)
+    ws = torch.empty(pool.sparse_ws_bytes(depth, T, HQ), dtype=torch.uint8, device="cuda")
+
+    def step():
+        for layer in range(layers):
+            pool.sparse(0, depth, layer, q[layer], bodies[layer][0], bodies[layer][1], out[layer], ws=ws,
+                        k_new=kn[layer], v_new=vn[layer])
+
+    step()
+    torch.cuda.synchronize()
+    graph = None
+    if not args.no_graph:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+    run = graph.replay if graph is not None else step
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        run()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = ev0.elapsed_time(ev1) / 1e3
+    assert torch.isfinite(out.float()).all().item(), "non-finite attention output"
+    sel = sum(sum(c.size for c in cl) for cl in cells) / layers  # selected cells a layer, all rows
+    bytes_layer = int(sel * BYTES_PER_CELL_LAYER + T * HQ * D * 2 * 2 + T * (BYTES_PER_CELL_LAYER + 2 * HKV * D * 2))
+    launch_s = gpu_s / (args.steps * layers)
+    achieved = bytes_layer / launch_s / 1e9
+    tiles = len(np.unique(np.concatenate([c // 32 for c in cells[0]])))
+    line = {
+        "metric": "sparse (QSA) decode attention over the Q8_0 pool: tokens/s + achieved GB/s of the selected cells",
+        "value": round(T * args.steps / wall, 3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0 KV (int8 codes + fp16 scales), fp16 Q/O, fp32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V with 4 of 256 channels x8, N(0,1) Q; random selections)",
+        "config": {"workload": cfg["workload"], "cells": ctx, "rows": T, "layers": layers, "q_heads": HQ,
+                   "kv_heads": HKV, "head_dim": D, "selected_cells_per_layer": int(sel),
+                   "tiles_read_per_layer_per_head": tiles, "hip_graph": graph is not None},
+        "roofline": {
+            "kernel": "fnkv_attn_sparse launch (sparse_plan_kernel + decode kernel + merge_kernel), per layer",
+            "bound": "hbm",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "traffic_note": f"whole 17,408 B tiles are read: {tiles} a head a layer for {int(sel)} selected cells",
+            "bytes_per_launch": bytes_layer,
+            "launch_us": round(launch_s * 1e6, 3),
+        },
+    }
+    if not args.no_cpu:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        k16, v16 = cases.kv_rows(args.seed, ctx, HKV)
+        q16 = cases.queries(args.seed, (T, HQ, D)).view(np.uint16)
+        t_layer = 0.0
+        for t in range(T):
+            c = cells[0][t]
+            (kq, kd, _), (vq, vd, _) = cases.decoded(O, k16[c], v16[c])
+            kb, vb = O.to_block_q8_0(kq, kd), O.to_block_q8_0(vq, vd)
+            O.attn_ggml(q16[t:t + 1], kb, vb, c.size, threads=threads)
+            t1 = time.perf_counter()
+            O.attn_ggml(q16[t:t + 1], kb, vb, c.size, threads=threads)
+            t_layer += time.perf_counter() - t1
+        line["cpu_baseline"] = {
+            "value": round(T / (t_layer * layers), 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"1 of {layers} layers: each row's selected cells gathered, fp32-Q ggml-semantics flash attention "
+                      f"over them (oracle/fnkv_oracle.c or_attn_ggml), {threads} threads, {t_layer * 1e3:.2f} ms a "
+                      f"layer x {layers}",
+        }
+    print(json.dumps(line), flush=True)
+    pool.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -314,6 +439,9 @@ def main():
         sys.exit(2)
     if CONFIGS[args.config].get("prefill"):
         run_prefill(args, CONFIGS[args.config])
+        return
+    if CONFIGS[args.config].get("sparse"):
+        run_sparse(args, CONFIGS[args.config])
         return
 
     traffic, traffic_detail = None, "skipped (--no-traffic)"

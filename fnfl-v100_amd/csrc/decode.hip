@@ -134,19 +134,28 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     // the split's tiles (at most 64), lane i holding tile i's page: a tile's page is then a lane read, not a memory
     // load on the path to its copy. Loaded first: the page table, the Q rows and the first tile are then one memory
     // latency each but overlapped, not three in a row.
+    half8 qop[kBlocks];
+    int64_t lim;
+    if constexpr (SP) { // the Q rows' latency hidden behind the selection's build
+        load_q_operands(a, s, kvh, rt, j, qg, qop, lim);
+    }
     split_src<SP> src;
-    src.init(a, table, split, begin, end, lane);
+    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * kGroupLds);
     const int32_t n_tiles = src.n_tiles;
     if (SP && n_tiles == 0) {
         return; // past the selection's tiles (the merge reads only the splits that hold some)
     }
     FNKV_STAMP(0);
 
-    append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, wave, lane);
+    if constexpr (SP) {
+        append_owned_cells<WAVES>(a, table, kvh, ctx, src.new_mine, wave, lane);
+    } else {
+        append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, wave, lane);
+    }
     FNKV_STAMP(1);
-    half8 qop[kBlocks];
-    int64_t lim;
-    load_q_operands(a, s, kvh, rt, j, qg, qop, lim);
+    if constexpr (!SP) {
+        load_q_operands(a, s, kvh, rt, j, qg, qop, lim);
+    }
 
     floatx4 acc[16];
     floatx4 lv = {0.0f, 0.0f, 0.0f, 0.0f}; // sum_t P[t][row] s_v[t][b]: lane (row j, qg) holds b = 4 qg + r
@@ -182,7 +191,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     // tile k's.
     // Every iteration issues the same loads on every path (a group past its last tile re-reads its last tile, an L2
     // hit), so the vmcnt counts below, and the compiler's own, are exact rather than a path-merge's zero.
-    const int32_t n_iter = (n_tiles + GR - 1) / GR;
+    const int32_t n_iter = (((n_tiles + GR - 1) / GR) + 1) & ~1;
     const int32_t last_tile = n_tiles - 1;
     FNKV_STAMP(2);
     {
@@ -389,24 +398,36 @@ __global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_ker
     const int32_t * table = pv.table + int64_t(a.slot[s]) * pv.table_stride;
     // the split's tiles, lane i holding tile i's page, loaded first (with the Q rows below, and the first tiles
     // issued before the Q sums wait: overlapped latencies, not three in a row)
-    split_src<SP> src;
-    src.init(a, table, split, begin, end, lane);
-    const int32_t n_tiles = src.n_tiles;
-    if (SP && n_tiles == 0) {
-        return; // past the selection's tiles (the merge reads only the splits that hold some)
+    if constexpr (SP) {
+        FNKV_STAMP(6);
     }
-    FNKV_STAMP(0);
-    append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, wave, lane);
-    FNKV_STAMP(1);
-
     half8 sig; // set once the first tiles are issued
     int64_t lim;
     // the Q operands: in registers at NT = 2; at NT = 3 registers are short and they sit once in LDS (after the
     // groups' buffers), the same for every group
     constexpr bool kQReg = NT == 2;
     half8 qreg[kBlocks];
+    if constexpr (SP) { // the Q rows' latency hidden behind the selection's build
+        load_q_operands(a, s, kvh, w, j, qg, qreg, lim);
+    }
+    split_src<SP, NT == 2> src; // NT = 3 is short of registers: its entries stay in LDS
+    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * SH::GROUP_LDS + SH::Q_LDS);
+    const int32_t n_tiles = src.n_tiles;
+    if (SP && n_tiles == 0) {
+        return; // past the selection's tiles (the merge reads only the splits that hold some)
+    }
+    FNKV_STAMP(0);
+    if constexpr (SP) {
+        append_owned_cells<WAVES>(a, table, kvh, ctx, src.new_mine, wave, lane);
+    } else {
+        append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, wave, lane);
+    }
+    FNKV_STAMP(1);
+
     uint8_t * const qlds = smem + GR * SH::GROUP_LDS; // [row tile][block][lane] 16 B
-    load_q_operands(a, s, kvh, w, j, qg, qreg, lim);
+    if constexpr (!SP) {
+        load_q_operands(a, s, kvh, w, j, qg, qreg, lim);
+    }
     auto qop_lds = [&](int b) {
         if constexpr (kQReg) {
             return qreg[b];
@@ -770,7 +791,8 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
     const int32_t s0 = a.split0[s];
     int32_t n = a.split0[s + 1] - s0;
     if (a.sel_n != nullptr) { // a sparse launch: only the splits that hold selected tiles ran
-        const int32_t used = (*a.sel_n + a.sel_split - 1) / a.sel_split;
+        const int32_t S = sparse_split_size(*a.sel_n, n);
+        const int32_t used = (*a.sel_n + S - 1) / S;
         n = used < n ? used : n;
     }
     float m = kNegInf, l = 0.0f;
@@ -825,13 +847,13 @@ int32_t decode_lds(int32_t nt) {
         constexpr int32_t waves = dec_shape<1>::WAVES;
         const int32_t tiles = dec_shape<1>::GR * kGroupLds;
         const int32_t merge = waves * 16 * 2 * 4 + waves * 16 * (kHeadDim + 4) * 4;
-        return tiles > merge ? tiles : merge;
+        return std::max(std::max(tiles + kSelSlice, merge), kSelLds);
     }
     const int32_t gr = nt == 2 ? rows_shape<2>::GR : rows_shape<3>::GR;
     const int32_t ring = gr * (nt == 2 ? rows_shape<2>::GROUP_LDS : rows_shape<3>::GROUP_LDS) +
                          (nt == 2 ? rows_shape<2>::Q_LDS : rows_shape<3>::Q_LDS);
     const int32_t merge = gr * nt * 16 * 2 * 4 + gr * nt * 16 * (kHeadDim + 4) * 4;
-    return ring > merge ? ring : merge;
+    return std::max(std::max(ring + kSelSlice, merge), kSelLds);
 }
 
 int32_t device_cus(int32_t device) {
@@ -940,6 +962,9 @@ using fnkv::set_error;
 #ifdef FNKV_TIMING
 static uint64_t * g_timing = nullptr;
 extern "C" void fnkv_debug_timing(void * buf) { g_timing = static_cast<uint64_t *>(buf); }
+namespace fnkv {
+uint64_t * timing_buffer() { return g_timing; }
+}
 #endif
 
 extern "C" {
@@ -1005,8 +1030,7 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
     a.R = R;
     a.n_seq = n_seq;
     a.split_tokens = pl.split_tokens;
-    a.sel_tiles = nullptr;
-    a.sel_masks = nullptr;
+    a.sel_body = nullptr;
     a.sel_n = nullptr;
     a.sel_split = 0;
     for (int32_t i = 0; i < FNKV_MAX_SEQS; ++i) {

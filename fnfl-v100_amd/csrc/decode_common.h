@@ -32,12 +32,11 @@ struct dec_args {
     int32_t slot[FNKV_MAX_SEQS];
     int64_t ctx[FNKV_MAX_SEQS];
     int32_t split0[FNKV_MAX_SEQS + 1]; // first split of each sequence; split0[n_seq] = total
-    // a sparse launch (one sequence): the ascending union of the logical tiles the rows' selections touch, each
-    // row's 4-cell blocks in it (row t's 8 bits at bit 8 t of .x for t < 4, of .y for t = 4), their count (device),
-    // and the entries a split takes (split s: entries s * sel_split ..)
-    const int32_t * sel_tiles;
-    const uint2 * sel_masks;
-    const int32_t * sel_n;
+    // a sparse launch (one sequence, rows at positions ctx - T ..): the rows' selection bodies (qsa.h layout) and
+    // where split 0 of head 0 stores the length of the selection's tile list for the merge (the list's entries are
+    // spread over the launched splits: sparse_split_size; sel_split is the host's bound on a split's entries)
+    const uint32_t * sel_body;
+    int32_t * sel_n;
     int32_t sel_split;
 #ifdef FNKV_TIMING
     uint64_t * ts; // per workgroup: 16 real-time stamps (instrumented builds only)
@@ -57,7 +56,7 @@ struct dec_args {
     } while (0)
 #define FNKV_STAMP_WAVE()                                                                                            \
     do {                                                                                                             \
-        if (a.ts != nullptr && (threadIdx.x & 63) == 0) {                                                            \
+        if (a.ts != nullptr && (threadIdx.x & 63) == 0 && a.sel_body == nullptr) {                                   \
             a.ts[(blockIdx.y * gridDim.x + blockIdx.x) * 16 + 8 + (threadIdx.x >> 6)] =                              \
                 __builtin_amdgcn_s_memrealtime();                                                                    \
         }                                                                                                            \
@@ -99,28 +98,199 @@ struct dec_args {
     } while (0)
 #endif
 
+// A sparse launch's selection as the workgroup sees it. Every workgroup rebuilds it in LDS from the bodies (a few
+// KB): row t's 8 block bits of each 32-cell tile (bit 8 t of mlo for t < 4, of mhi for t = 4), a 4-cell block a bit;
+// the tiles any row selected, in ascending order, are the list whose entries the splits take in turn. Rebuilding
+// costs each workgroup one read of the bodies, which replaces the launch (and the memory round trip) that a separate
+// planning kernel would add.
+constexpr int32_t kSelMaxCells = 262144 + 32;                                     // the reference's max_cells
+constexpr int32_t kSelMaxTiles = (kSelMaxCells + kTileTokens - 1) / kTileTokens; // 8,193
+constexpr int32_t kSelTopBlocks = 512;                                            // blocks a row (qsa.h)
+constexpr int32_t kSelMaxRows = 5;
+constexpr int32_t kSelMaxThreads = 512;
+
+// list entries a split takes when n_sel entries go to n_splits splits (at most 64: the host launches enough splits)
+__host__ __device__ inline int32_t sparse_split_size(int32_t n_sel, int32_t n_splits) {
+    const int32_t s = (n_sel + n_splits - 1) / n_splits;
+    return s < 1 ? 1 : s;
+}
+constexpr int32_t kSelLds = 2 * kSelMaxTiles * 4 + kSelMaxThreads * 4 + 64; // the build's scratch
+constexpr int32_t kSelSlice = 64 * 8; // a split's entries (logical tile | row 4's bits << 16, rows 0-3's bits)
+
+template <int32_t THREADS>
+__device__ void sparse_build(const dec_args & a, uint8_t * smem, uint2 * slice, int32_t split, int32_t & n_tiles,
+                             int32_t & tile_l, int32_t & rank_of_new) {
+    static_assert(THREADS <= kSelMaxThreads, "prefix array size");
+    uint32_t * mlo = reinterpret_cast<uint32_t *>(smem);
+    uint32_t * mhi = mlo + kSelMaxTiles;
+    int32_t * base = reinterpret_cast<int32_t *>(mhi + kSelMaxTiles); // [THREADS] each thread's first entry
+    int32_t * total = base + kSelMaxThreads; // [1 + kSelMaxRows]
+    const int32_t tid = static_cast<int32_t>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+    const int64_t ctx = a.ctx[0], depth = ctx - a.T;
+    const int32_t n_ctx_tiles = static_cast<int32_t>((ctx + kTileTokens - 1) / kTileTokens);
+    // Row t at position q sees block b whole when 4 b + 3 <= q; its tail (cells 4 n_vis .. q, n_vis = (q + 1) / 4)
+    // is block n_vis up to its own position, which the causal limit cuts. The layout follows from depth and T alone
+    // (qsa.h:77-81): row t's words start after the earlier rows' 2 + K + tail, so nothing past a row is read, and
+    // entries outside the row's whole blocks are ignored.
+    // Each row's block count follows from its position (K = min(n_vis, 512)), so every row's block IDs are read in
+    // one flat loop (one memory round trip, not one a row); the words' K field is not needed.
+    int32_t row_off[kSelMaxRows + 1], row_k[kSelMaxRows];
+    int32_t n_entries = 0;
+    {
+        int32_t off = 0;
+#pragma unroll
+        for (int32_t t = 0; t < kSelMaxRows; ++t) {
+            const int64_t q = depth + t;
+            const int32_t n_vis = static_cast<int32_t>((q + 1) / 4);
+            const int32_t k_full = t < a.T ? (n_vis < kSelTopBlocks ? n_vis : kSelTopBlocks) : 0;
+            row_off[t] = n_entries;
+            row_k[t] = off; // the row's first block word
+            n_entries += k_full;
+            off += t < a.T ? 2 + k_full + static_cast<int32_t>((q + 1) % 4) : 0;
+        }
+        row_off[kSelMaxRows] = n_entries;
+    }
+    // all of a thread's loads first (at most kPer), then their bits: one memory round trip
+    constexpr int32_t kPer = (kSelMaxRows * kSelTopBlocks + THREADS - 1) / THREADS;
+    int32_t blk[kPer], row[kPer];
+#pragma unroll
+    for (int32_t k = 0; k < kPer; ++k) {
+        const int32_t i = tid + k * THREADS;
+        int32_t t = 0, e0 = 0, w0 = row_k[0]; // the entry's row, its first entry and its first block word
+#pragma unroll
+        for (int32_t r = 1; r < kSelMaxRows; ++r) {
+            const bool in = i >= row_off[r];
+            t = in ? r : t;
+            e0 = in ? row_off[r] : e0;
+            w0 = in ? row_k[r] : w0;
+        }
+        row[k] = t;
+        blk[k] = i < n_entries ? static_cast<int32_t>(a.sel_body[w0 + 2 + (i - e0)]) : -1;
+    }
+    // the bitmap zeroed while the loads are in flight
+    for (int32_t i = tid; i < n_ctx_tiles; i += THREADS) {
+        mlo[i] = 0u;
+        mhi[i] = 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int32_t k = 0; k < kPer; ++k) {
+        const int32_t t = row[k], b = blk[k];
+        const int32_t n_vis = static_cast<int32_t>((depth + t + 1) / 4);
+        if (b >= 0 && b < n_vis) {
+            atomicOr(&(t < 4 ? mlo : mhi)[b >> 3], 1u << (8 * (t & 3) + (b & 7)));
+        }
+    }
+    if (tid < a.T) {
+        const int64_t q = depth + tid;
+        const int32_t n_vis = static_cast<int32_t>((q + 1) / 4);
+        if ((q + 1) % 4 != 0) {
+            atomicOr(&(tid < 4 ? mlo : mhi)[n_vis >> 3], 1u << (8 * (tid & 3) + (n_vis & 7)));
+        }
+    }
+    __syncthreads();
+    // the list: thread i scans tiles i * PER .. (i + 1) * PER - 1 (PER odd, so the threads' reads fall in distinct
+    // banks; the tiles' nonzero flags kept as bits of one register); a block-wide exclusive scan of the counts gives
+    // each thread its first entry
+    constexpr int32_t PER = ((kSelMaxTiles + THREADS - 1) / THREADS) | 1;
+    static_assert(PER <= 32, "one bit a tile");
+    const int32_t t0 = tid * PER;
+    uint32_t bits = 0;
+#pragma unroll
+    for (int32_t k = 0; k < PER; ++k) {
+        const int32_t i = t0 + k;
+        const uint32_t v = i < n_ctx_tiles ? (mlo[i] | mhi[i]) : 0u;
+        bits |= (v != 0u ? 1u : 0u) << k;
+    }
+    const int32_t cnt = __builtin_popcount(bits);
+    int32_t incl = cnt;
+#pragma unroll
+    for (int32_t o = 1; o < 64; o <<= 1) {
+        const int32_t y = __shfl_up(incl, o);
+        incl += lane >= o ? y : 0;
+    }
+    if (lane == 63) {
+        base[wave] = incl; // wave totals
+    }
+    int32_t * owner = total + 1; // [kSelMaxRows] the split that writes new cell t (0 when no row selects its tile)
+    if (tid < kSelMaxRows) {
+        owner[tid] = 0;
+    }
+    __syncthreads();
+    int32_t wbase = 0, n_sel = 0;
+    for (int32_t w = 0; w < THREADS / 64; ++w) {
+        wbase += w < wave ? base[w] : 0;
+        n_sel += base[w];
+    }
+    const int32_t first = wbase + incl - cnt;
+    // the entries spread over all the launched splits (S each, the last ones short), so every workgroup gets work
+    const int32_t S = sparse_split_size(n_sel, static_cast<int32_t>(gridDim.x));
+    // this split's entries, and the owners of the new cells' tiles
+    const int32_t e0 = split * S;
+    const int32_t tile_new0 = static_cast<int32_t>(depth >> 5), tile_new1 = static_cast<int32_t>((ctx - 1) >> 5);
+    int32_t pos = first;
+    uint32_t rest = bits;
+    while (rest != 0u) {
+        const int32_t k = __builtin_ctz(rest);
+        rest &= rest - 1u;
+        const int32_t i = t0 + k;
+        if (pos >= e0 && pos < e0 + S) {
+            slice[pos - e0] = uint2{static_cast<uint32_t>(i) | ((mhi[i] & 0xffu) << 16), mlo[i]};
+        }
+        if (i >= tile_new0 && i <= tile_new1) {
+#pragma unroll
+            for (int32_t t = 0; t < kSelMaxRows; ++t) {
+                if (t < a.T && static_cast<int32_t>((depth + t) >> 5) == i) {
+                    owner[t] = pos / S;
+                }
+            }
+        }
+        ++pos;
+    }
+    __syncthreads();
+    const int32_t left = n_sel - e0;
+    n_tiles = left < 0 ? 0 : left < S ? left : S;
+    if (lane < n_tiles) {
+        tile_l = static_cast<int32_t>(slice[lane].x & 0xffffu);
+    }
+    if (split == 0 && blockIdx.y == 0 && tid == 0) {
+        *a.sel_n = n_sel;
+    }
+    int32_t mine = 0; // the new cells this split writes (bit t: cell depth + t)
+#pragma unroll
+    for (int32_t t = 0; t < kSelMaxRows; ++t) {
+        mine |= (t < a.T && owner[t] == split) ? (1 << t) : 0;
+    }
+    rank_of_new = mine;
+    __syncthreads(); // the LDS is the ring's from here
+}
+
 // The tiles a workgroup walks. Dense: its split's consecutive cells begin .. end, lane i holding the physical page
-// of the split's logical page i. Sparse: entries e0 .. e0 + n_tiles - 1 of the selection's tile list, lane i holding
-// entry i's logical tile, physical page and row masks. Tile ti of the walk is then a lane read either way.
-template <bool SP> struct split_src {
+// of the split's logical page i. Sparse: entries e0 .. e0 + n_tiles - 1 of the selection's tile list, kept in LDS
+// (slice: past the ring) and, with LANES, also in lanes (lane i: entry i); lane i holds entry i's physical page.
+// Tile ti of the walk is then a lane read (without LANES, plus one LDS read) either way.
+template <bool SP, bool LANES = true> struct split_src {
     int32_t n_tiles = 0;
     int32_t page_lane = 0;
-    int32_t tile_lane = 0;
-    uint32_t mlo_lane = 0, mhi_lane = 0;
+    int32_t new_mine = 0; // sparse: the new cells (bit t: cell ctx - T + t) this workgroup writes
     int64_t begin = 0;
+    const uint2 * slice = nullptr;
+    uint32_t ent_x = 0, ent_y = 0; // sparse with LANES: lane i holds entry i (register reads instead of LDS reads)
 
+    template <int32_t THREADS>
     __device__ __forceinline__ void init(const dec_args & a, const int32_t * table, int32_t split, int64_t b,
-                                         int64_t e, int32_t lane) {
+                                         int64_t e, int32_t lane, uint8_t * smem, uint8_t * slice_lds) {
         if constexpr (SP) {
-            const int32_t e0 = split * a.sel_split;
-            const int32_t left = *a.sel_n - e0;
-            n_tiles = left < 0 ? 0 : left < a.sel_split ? left : a.sel_split;
+            uint2 * sl = reinterpret_cast<uint2 *>(slice_lds);
+            int32_t tile_l = 0;
+            sparse_build<THREADS>(a, smem, sl, split, n_tiles, tile_l, new_mine);
+            slice = sl;
             if (lane < n_tiles) {
-                tile_lane = a.sel_tiles[e0 + lane];
-                const uint2 m = a.sel_masks[e0 + lane];
-                mlo_lane = m.x;
-                mhi_lane = m.y;
-                page_lane = table[tile_lane >> 3];
+                page_lane = table[tile_l >> 3];
+                if constexpr (LANES) {
+                    ent_x = sl[lane].x;
+                    ent_y = sl[lane].y;
+                }
             }
         } else {
             begin = b;
@@ -129,11 +299,21 @@ template <bool SP> struct split_src {
             page_lane = lane < n_pages ? table[(b >> 8) + lane] : 0;
         }
     }
+    __device__ __forceinline__ uint2 entry(int32_t ti) const {
+        if constexpr (LANES) {
+            return uint2{static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int32_t>(ent_x), ti)),
+                         static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int32_t>(ent_y), ti))};
+        } else {
+            const uint2 v = slice[ti];
+            return uint2{static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(v.x))),
+                         static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(v.y)))};
+        }
+    }
     // byte offset of walk tile ti within the (layer, head) plane of the pool
     __device__ __forceinline__ int64_t tile_off(const pool_view & pv, int32_t ti) const {
         if constexpr (SP) {
             const int32_t phys = __builtin_amdgcn_readlane(page_lane, ti);
-            const int32_t t8 = __builtin_amdgcn_readlane(tile_lane, ti) & 7;
+            const int32_t t8 = static_cast<int32_t>(entry(ti).x & 7u);
             return int64_t(phys) * pv.page_stride + int64_t(t8) * kTileBytes;
         } else {
             const int32_t phys = __builtin_amdgcn_readlane(page_lane, ti >> 3);
@@ -143,7 +323,7 @@ template <bool SP> struct split_src {
     // the first cell of walk tile ti
     __device__ __forceinline__ int64_t tok0(int32_t ti) const {
         if constexpr (SP) {
-            return int64_t(__builtin_amdgcn_readlane(tile_lane, ti)) * kTileTokens;
+            return int64_t(entry(ti).x & 0xffffu) * kTileTokens;
         } else {
             return begin + int64_t(ti) * kTileTokens;
         }
@@ -151,9 +331,8 @@ template <bool SP> struct split_src {
     // the visibility bits of tile_softmax for this lane (query row of step token t_row, lane group qg)
     __device__ __forceinline__ uint32_t vis(int32_t ti, int32_t t_row, int32_t qg) const {
         if constexpr (SP) {
-            const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int32_t>(mlo_lane), ti));
-            const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int32_t>(mhi_lane), ti));
-            const uint32_t byte = t_row < 4 ? (lo >> (8 * t_row)) : hi;
+            const uint2 en = entry(ti);
+            const uint32_t byte = t_row < 4 ? (en.y >> (8 * t_row)) : (en.x >> 16);
             return ((byte >> qg) & 1u) | (((byte >> (4 + qg)) & 1u) << 1);
         } else {
             return 3u;
@@ -196,6 +375,34 @@ __device__ __forceinline__ int32_t seq_of(const dec_args & a, int32_t split) {
 // position lies in exactly one split, so one workgroup writes it and only that workgroup reads it in this launch).
 // The barrier's workgroup-scope release / acquire makes the stores visible to the workgroup's own later loads; an
 // agent-scope fence would write back and invalidate the whole L2 under every other workgroup's stream.
+// A sparse launch's workgroup writes the new cells set in `mine` (bit t: cell ctx - T + t) for its head.
+template <int WAVES>
+__device__ __forceinline__ void append_owned_cells(const dec_args & a, const int32_t * table, int32_t kvh,
+                                                   int64_t ctx, int32_t mine, int32_t wave, int32_t lane) {
+    if (a.k_new == nullptr || mine == 0) {
+        return;
+    }
+    const pool_view & pv = a.pv;
+    const int64_t first_new = ctx - a.T;
+    for (int32_t job = wave; job < 2 * a.T; job += WAVES) {
+        const int32_t t = job >> 1, kv = job & 1;
+        if (((mine >> t) & 1) == 0) {
+            continue;
+        }
+        const int64_t pos = first_new + t;
+        const int64_t src = (int64_t(t) * pv.h_kv + kvh) * kHeadDim;
+        float x[4];
+        if (a.new_f32) {
+            load4<true>(static_cast<const float *>(kv ? a.v_new : a.k_new) + src, lane, x);
+        } else {
+            load4<false>(static_cast<const uint16_t *>(kv ? a.v_new : a.k_new) + src, lane, x);
+        }
+        quantize_store_fmt(x, lane, tile_of(pv, table, a.layer, kvh, pos), static_cast<int32_t>(pos & 31), kv,
+                           pv.format);
+    }
+    __syncthreads();
+}
+
 template <int WAVES>
 __device__ __forceinline__ void append_new_cells(const dec_args & a, const int32_t * table, int32_t s, int32_t kvh,
                                                  int64_t ctx, int64_t begin, int64_t end, int32_t wave,
