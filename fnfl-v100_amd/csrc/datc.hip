@@ -1,0 +1,547 @@
+// The draft block's dense F16 attention (DA-TC, fn/kernels/draft/draft.h:47-83): the prepare of a round's rows (F32
+// RMS norm and IMROPE of the query heads and of k, the F16 K / V cache writes, q / 16 in F16) and the attention of one
+// row over every cell before it (or over a selection body, SP2), gated by sigmoid(gate) and written in F32 and in the
+// int8 activation format. The caches are flat F16 [max_cells][256] arrays of one KV head, 1,024 B a cell for K and V.
+//
+// How (MI355X):
+//   * prepare: a workgroup a row, a wave a query head (12) and one for k / v; a lane holds 4 of the 256 values.
+//   * attend: a fixed grid of kGrid workgroups of 4 waves (the depth is a device word, so the grid cannot depend on
+//     it); the first A = min(kGrid, ceil(tiles / 4)) take even ranges of 32-cell tiles, wave w every fourth tile of
+//     its group's range. A wave's step, all on the matrix cores (v_mfma_f32_16x16x32_f16):
+//       S^T = K Q^T: K rows straight from HBM into registers (buffer loads; cells past the row read as zeros), the 12
+//         heads (padded to 16) of q16 held in registers for the whole launch; lane l ends with head l % 16's scores
+//         of cells 4 (l / 16) .. + 3 of each 16-cell half, so the online softmax needs no transposition: its max
+//         and sum cross the four 16-lane rows by two lane swaps.
+//       O^T += V^T P^T: the lane's own 8 rounded probabilities are the B operand as they stand (the MFMA's k slots
+//         mapped onto those 8 cells); the V tile comes into LDS by direct global-to-LDS copies (two cells a copy,
+//         rows padded so the transposed reads below are conflict-free) and each lane reads its A operand (8 cells of
+//         one dimension) as 16-bit values. The accumulators hold O^T, so the per-head rescale is the lane's own.
+//     The next tile's K and V are issued before the current one is computed (two register and LDS buffers).
+//     The 4 waves fold into one partial per workgroup in LDS.
+//   * fold: a workgroup per (head, 32-value run): the partials folded in workgroup order with exp(m_c - M), the gate,
+//     the F32 output and the run's activation format.
+// Numerics (draft.h:69-77): exact F16 products, F32 accumulation, P rounded to F16 (nearest even), l the sum of the
+// rounded P; every reduction order is fixed, so reruns are bitwise.
+#include "../../include/fnkv.h"
+#include "common.h"
+#include "mfma.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <string>
+
+namespace fnkv {
+namespace {
+
+constexpr int32_t kHeads = FNKV_DATC_HEADS;
+constexpr int32_t kD = 256;
+constexpr int32_t kQS = FNKV_DATC_QSTRIDE;
+constexpr int32_t kNRot = 64;           // rotated dimensions (fn/kernels/qsa/qsa.h n_rot)
+constexpr float kRmsEps = 1e-6f;        // fn/model/shapes.h:35 rms_eps
+constexpr int32_t kGrid = 256;          // attention workgroups
+constexpr int32_t kWaves = 4;
+constexpr int32_t kTile = 32;           // cells a wave's step
+constexpr int32_t kPartFloats = kHeads * kD + 2 * kHeads; // a workgroup's O [12][256], then m [12] and l [12]
+constexpr int32_t kVPair = 2 * 512 + 16;                  // LDS bytes of two cells' V rows, padded
+constexpr int32_t kVBuf = (kTile / 2) * kVPair;           // a tile's V rows: 16,640 B
+constexpr int32_t kWaveLds = 2 * kVBuf;                   // two tiles a wave
+constexpr int32_t kAttendLds = kWaves * kWaveLds + 2 * kWaves * 16 * 4; // + the waves' m and l
+constexpr int32_t kOStride = kD + 4;                      // floats a head's row of a wave's O in LDS (fold step)
+constexpr int32_t kSelRatio = 4, kSelBlocks = 512;
+constexpr uint32_t kOob = 0x80000000u;                    // a buffer offset past every cache: reads as zero
+
+static_assert(kWaves * kHeads * kOStride * 4 <= kWaves * kWaveLds, "the wave fold reuses the V buffers");
+
+// ---- prepare ----
+
+// The F32 rms norm and IMROPE of one 256-wide row (pinned by the reference as build_norm LLM_NORM_RMS, then
+// ggml_rope_multi with GGML_ROPE_TYPE_IMROPE; fn/kernels/qsa/attend.cu:151-198, imrope.cuh:14-20). A lane holds dims
+// 4 lane .. 4 lane + 3. Rotation pair i (< 32) is dims i and i + 32; its angle is its plane's position times
+// theta_scale^i as the F32 product chain, the plane picked by the sector rule (sections 11, 11, 10, 0).
+__device__ __forceinline__ void norm_rope(float (&y)[4], const float * src, const float * w, const int32_t * pos,
+                                          int32_t stride, int32_t col, float ts, int32_t lane) {
+    const float4 x = reinterpret_cast<const float4 *>(src)[lane];
+    float ss = x.x * x.x;
+    ss = __builtin_fmaf(x.y, x.y, ss);
+    ss = __builtin_fmaf(x.z, x.z, ss);
+    ss = __builtin_fmaf(x.w, x.w, ss);
+#pragma unroll
+    for (int32_t o = 32; o > 0; o >>= 1) {
+        ss += __shfl_xor(ss, o, 64);
+    }
+    const float r = 1.0f / sqrtf(ss * (1.0f / kD) + kRmsEps);
+    const float4 g = reinterpret_cast<const float4 *>(w)[lane];
+    y[0] = x.x * r * g.x;
+    y[1] = x.y * r * g.y;
+    y[2] = x.z * r * g.z;
+    y[3] = x.w * r * g.w;
+    // lane i < 32 forms pair i's angle
+    const int32_t sector = lane & 31;
+    const int32_t plane = sector % 3 == 1 && sector < 33   ? 1
+                          : sector % 3 == 2 && sector < 30 ? 2
+                          : sector % 3 == 0 && sector < 33 ? 0
+                                                           : 3;
+    float theta = static_cast<float>(pos[plane * stride + col]);
+#pragma unroll
+    for (int32_t i = 0; i < kNRot / 2 - 1; ++i) {
+        theta = i < sector ? theta * ts : theta;
+    }
+    float s = 0.0f, c = 0.0f;
+    sincosf(theta, &s, &c);
+    // dims 0..31 sit in lanes 0..7, their partners 32..63 in lanes 8..15
+#pragma unroll
+    for (int32_t e = 0; e < 4; ++e) {
+        const int32_t pair = 4 * (lane & 7) + e;
+        const float ce = __shfl(c, pair, 64);
+        const float se = __shfl(s, pair, 64);
+        const float other = __shfl_xor(y[e], 8, 64);
+        if (lane < 8) {
+            y[e] = y[e] * ce - other * se;
+        } else if (lane < 16) {
+            y[e] = other * se + y[e] * ce;
+        }
+    }
+}
+
+__device__ __forceinline__ uint2 pack4_f16(const float (&x)[4], float scale) {
+    half2v a{static_cast<_Float16>(x[0] * scale), static_cast<_Float16>(x[1] * scale)};
+    half2v b{static_cast<_Float16>(x[2] * scale), static_cast<_Float16>(x[3] * scale)};
+    return make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+}
+
+__global__ __launch_bounds__(64 * (kHeads + 1)) void datc_prepare_kernel(fnkv_datc_prepare_args a, int32_t rows) {
+    const int32_t wave = static_cast<int32_t>(threadIdx.x) / 64, lane = static_cast<int32_t>(threadIdx.x) % 64;
+    const int32_t t = static_cast<int32_t>(blockIdx.x);
+    const int32_t nb = *a.n_before, stride = *a.stride;
+    if (nb < 0 || static_cast<int64_t>(nb) + a.row0 + rows > a.max_cells || a.row0 + rows > stride) {
+        if (threadIdx.x == 0) {
+            atomicOr(a.err, FNKV_DEV_ERR_DRAFT_DEPTH);
+        }
+        return;
+    }
+    const int32_t col = a.row0 + t;
+    float y[4];
+    if (wave < kHeads) {
+        if (a.qfull == nullptr) {
+            return;
+        }
+        norm_rope(y, a.qfull + (t * kHeads + wave) * kQS, a.q_norm, a.pos, stride, col, a.theta_scale, lane);
+        if (a.q_f32 != nullptr) {
+            reinterpret_cast<float4 *>(a.q_f32 + (t * kHeads + wave) * kD)[lane] = make_float4(y[0], y[1], y[2], y[3]);
+        }
+        reinterpret_cast<uint2 *>(a.q16 + (t * kHeads + wave) * kD)[lane] = pack4_f16(y, 1.0f / 16.0f);
+        return;
+    }
+    norm_rope(y, a.kv_k + t * kD, a.k_norm, a.pos, stride, col, a.theta_scale, lane);
+    if (a.k_f32 != nullptr) {
+        reinterpret_cast<float4 *>(a.k_f32 + t * kD)[lane] = make_float4(y[0], y[1], y[2], y[3]);
+    }
+    const int64_t at = (static_cast<int64_t>(nb) + col) * kD;
+    reinterpret_cast<uint2 *>(a.k_cache + at)[lane] = pack4_f16(y, 1.0f);
+    const float4 v4 = reinterpret_cast<const float4 *>(a.kv_v + t * kD)[lane];
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    reinterpret_cast<uint2 *>(a.v_cache + at)[lane] = pack4_f16(v, 1.0f);
+}
+
+// ---- attend ----
+
+// The row's logical cells: n of them; cell i is i (dense) or, SP2, the i-th of the selection (its K blocks' cells,
+// then 4 n_vis .. N + row0). valid false: the launch must write nothing (a depth outside the caches, a body not made
+// at this depth).
+struct datc_shape {
+    int32_t n = 0, K = 0, n_vis = 0, n_tiles = 0, active = 0;
+    bool valid = false;
+};
+
+template <bool SP> __device__ __forceinline__ datc_shape datc_shape_of(const fnkv_datc_attend_args & a) {
+    datc_shape s;
+    const int32_t nb = *a.n_before;
+    const int64_t n64 = static_cast<int64_t>(nb) + a.row0 + 1;
+    s.n_vis = nb / kSelRatio;
+    s.K = SP ? static_cast<int32_t>(a.body[0]) : 0;
+    s.valid = nb >= 0 && n64 <= a.max_cells && (!SP || s.K == min(s.n_vis, kSelBlocks));
+    if (!s.valid) {
+        return s;
+    }
+    s.n = SP ? kSelRatio * s.K + static_cast<int32_t>(n64) - kSelRatio * s.n_vis : static_cast<int32_t>(n64);
+    s.n_tiles = (s.n + kTile - 1) / kTile;
+    s.active = min(kGrid, (s.n_tiles + kWaves - 1) / kWaves);
+    return s;
+}
+
+// logical cell i (< n) to its cache cell
+template <bool SP>
+__device__ __forceinline__ int32_t cell_of(const fnkv_datc_attend_args & a, const datc_shape & s, int32_t i) {
+    if constexpr (!SP) {
+        return i;
+    } else {
+        return i < kSelRatio * s.K ? kSelRatio * static_cast<int32_t>(a.body[2 + i / kSelRatio]) + (i & 3)
+                                   : kSelRatio * s.n_vis + (i - kSelRatio * s.K);
+    }
+}
+
+struct k_tile {
+    u32x4 r[2][8]; // [16-cell half][32-dim slice]: lane l's 8 dims 32 j + 8 (l / 16) .. of cell 16 half + l % 16
+};
+
+// issue one tile's loads: K into registers, V into the wave's LDS buffer (16 copies of two cells)
+template <bool SP>
+__device__ __forceinline__ void issue_tile(const fnkv_datc_attend_args & a, const datc_shape & s, rsrc_t rk, rsrc_t rv,
+                                           int32_t base, k_tile & kt, uint8_t * vbuf, int32_t lane) {
+    // lane l < 32 resolves logical cell base + l (a body word for SP2); the others are taken by lane exchange
+    const int32_t li = base + (lane & 31);
+    const int32_t mine = li < s.n ? cell_of<SP>(a, s, li) : -1;
+    const int32_t g = lane / 16;
+#pragma unroll
+    for (int32_t h = 0; h < 2; ++h) {
+        const int32_t c = __shfl(mine, 16 * h + lane % 16, 64);
+        const uint32_t off = c >= 0 ? static_cast<uint32_t>(c) * 512u + 16u * static_cast<uint32_t>(g) : kOob;
+#pragma unroll
+        for (int32_t j = 0; j < 8; ++j) {
+            kt.r[h][j] = buf_load16(rk, static_cast<int32_t>(off), 64 * j);
+        }
+    }
+#pragma unroll
+    for (int32_t c2 = 0; c2 < kTile / 2; ++c2) {
+        const int32_t c = __shfl(mine, 2 * c2 + lane / 32, 64);
+        const uint32_t off = c >= 0 ? static_cast<uint32_t>(c) * 512u + 16u * static_cast<uint32_t>(lane % 32) : kOob;
+        buf_lds16(rv, vbuf + c2 * kVPair, static_cast<int32_t>(off), 0);
+    }
+}
+
+// one tile's step: scores, the online softmax (m, l of head lane % 16), O^T rescaled and accumulated
+template <bool HAS_NEXT>
+__device__ __forceinline__ void tile_step(const k_tile & kt, const half8 (&qb)[8], const uint8_t * vbuf, int32_t base,
+                                          int32_t n, float & m_run, float & l_run, floatx4 (&o)[16], int32_t lane) {
+    const int32_t g = lane / 16;
+    floatx4 st[2];
+#pragma unroll
+    for (int32_t h = 0; h < 2; ++h) {
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int32_t j = 0; j < 8; ++j) {
+            acc = mfma16(__builtin_bit_cast(half8, kt.r[h][j]), qb[j], acc);
+        }
+        st[h] = acc;
+    }
+    // lane l: head l % 16, cells 16 h + 4 g + i
+    float s[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int32_t h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int32_t i = 0; i < 4; ++i) {
+            const float v = base + 16 * h + 4 * g + i < n ? st[h][i] : -INFINITY;
+            s[4 * h + i] = v;
+            mx = fmaxf(mx, v);
+        }
+    }
+    mx = rows_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    u32x4 pw;
+    float sum = 0.0f;
+#pragma unroll
+    for (int32_t i = 0; i < 4; ++i) {
+        const _Float16 p0 = static_cast<_Float16>(expf(s[2 * i] - m_new));
+        const _Float16 p1 = static_cast<_Float16>(expf(s[2 * i + 1] - m_new));
+        sum += static_cast<float>(p0);
+        sum += static_cast<float>(p1);
+        pw[i] = __builtin_bit_cast(uint32_t, half2v{p0, p1});
+    }
+    sum = rows_sum(sum);
+    const float alpha = expf(m_run - m_new); // 0 for the wave's first tile (m_run = -inf)
+    m_run = m_new;
+    l_run = __builtin_fmaf(l_run, alpha, sum);
+    const half8 pb = __builtin_bit_cast(half8, pw);
+    // V of this tile has landed in LDS once at most the next tile's 32 loads are outstanding
+    if constexpr (HAS_NEXT) {
+        wait_vmcnt<32>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    // A operand of dims 16 db + l % 16: cells 4 g + i (i < 4) and 16 + 4 g + i - 4 (the k-slot order of pb)
+    const uint8_t * vl = vbuf + 2 * g * kVPair + 2 * (lane % 16);
+    constexpr int32_t coff[8] = {0, 512, kVPair, kVPair + 512, 8 * kVPair, 8 * kVPair + 512, 9 * kVPair,
+                                 9 * kVPair + 512};
+#pragma unroll
+    for (int32_t db = 0; db < 16; ++db) {
+        u32x4 va;
+#pragma unroll
+        for (int32_t i = 0; i < 4; ++i) {
+            const uint32_t lo = *reinterpret_cast<const uint16_t *>(vl + 32 * db + coff[2 * i]);
+            const uint32_t hi = *reinterpret_cast<const uint16_t *>(vl + 32 * db + coff[2 * i + 1]);
+            va[i] = lo | (hi << 16);
+        }
+        o[db] = mfma16(__builtin_bit_cast(half8, va), pb, o[db] * alpha);
+    }
+}
+
+template <bool SP> __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend_kernel(fnkv_datc_attend_args a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int32_t wave = static_cast<int32_t>(threadIdx.x) / 64, lane = static_cast<int32_t>(threadIdx.x) % 64;
+    const datc_shape s = datc_shape_of<SP>(a);
+    if (!s.valid) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            atomicOr(a.err, FNKV_DEV_ERR_DRAFT_DEPTH);
+        }
+        return;
+    }
+    const int32_t b = static_cast<int32_t>(blockIdx.x);
+    if (b >= s.active) {
+        return;
+    }
+    const int32_t t0 = static_cast<int32_t>(static_cast<int64_t>(b) * s.n_tiles / s.active);
+    const int32_t t1 = static_cast<int32_t>(static_cast<int64_t>(b + 1) * s.n_tiles / s.active);
+    const int32_t cnt = t1 - t0 > wave ? (t1 - t0 - wave + kWaves - 1) / kWaves : 0;
+    const uint32_t cache_bytes = static_cast<uint32_t>(a.max_cells) * 512u;
+    const rsrc_t rk = make_rsrc(a.k_cache, static_cast<int32_t>(cache_bytes));
+    const rsrc_t rv = make_rsrc(a.v_cache, static_cast<int32_t>(cache_bytes));
+    uint8_t * vb0 = smem + wave * kWaveLds;
+    uint8_t * vb1 = vb0 + kVBuf;
+    // q16 as the B operand: lane l holds head l % 16's dims 32 j + 8 (l / 16) .. + 7 (heads 12..15 zero); loaded
+    // before the first tile so that the wait for it leaves the tile's loads in flight
+    half8 qb[8];
+    {
+        const int32_t h = lane % 16, g = lane / 16;
+#pragma unroll
+        for (int32_t j = 0; j < 8; ++j) {
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (h < kHeads) {
+                v = *reinterpret_cast<const u32x4 *>(a.q16 + h * kD + 32 * j + 8 * g);
+            }
+            qb[j] = __builtin_bit_cast(half8, v);
+        }
+    }
+    k_tile ka, kb;
+    if (cnt > 0) {
+        issue_tile<SP>(a, s, rk, rv, (t0 + wave) * kTile, ka, vb0, lane);
+    }
+    float m_run = -INFINITY, l_run = 0.0f;
+    floatx4 o[16];
+#pragma unroll
+    for (int32_t db = 0; db < 16; ++db) {
+        o[db] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    for (int32_t k = 0; k < cnt; k += 2) {
+        const int32_t base0 = (t0 + wave + kWaves * k) * kTile;
+        if (k + 1 < cnt) {
+            issue_tile<SP>(a, s, rk, rv, base0 + kWaves * kTile, kb, vb1, lane);
+            tile_step<true>(ka, qb, vb0, base0, s.n, m_run, l_run, o, lane);
+        } else {
+            tile_step<false>(ka, qb, vb0, base0, s.n, m_run, l_run, o, lane);
+            break;
+        }
+        const int32_t base1 = base0 + kWaves * kTile;
+        if (k + 2 < cnt) {
+            issue_tile<SP>(a, s, rk, rv, base1 + kWaves * kTile, ka, vb0, lane);
+            tile_step<true>(kb, qb, vb1, base1, s.n, m_run, l_run, o, lane);
+        } else {
+            tile_step<false>(kb, qb, vb1, base1, s.n, m_run, l_run, o, lane);
+        }
+    }
+    // fold the waves: M, the waves' weights, then O summed in wave order
+    float * ml = reinterpret_cast<float *>(smem + kWaves * kWaveLds);
+    if (lane < 16) {
+        ml[wave * 16 + lane] = m_run;
+        ml[kWaves * 16 + wave * 16 + lane] = l_run;
+    }
+    __syncthreads(); // also: every wave is done with its V buffers
+    const int32_t h = lane % 16, g = lane / 16;
+    float M = -INFINITY;
+#pragma unroll
+    for (int32_t w = 0; w < kWaves; ++w) {
+        M = fmaxf(M, ml[w * 16 + h]);
+    }
+    const float scale = expf(m_run - M); // 0 for a wave without tiles
+    float * ow = reinterpret_cast<float *>(smem) + wave * kHeads * kOStride;
+    if (h < kHeads) {
+#pragma unroll
+        for (int32_t db = 0; db < 16; ++db) {
+            *reinterpret_cast<floatx4 *>(ow + h * kOStride + 16 * db + 4 * g) = o[db] * scale;
+        }
+    }
+    __syncthreads();
+    float * part = reinterpret_cast<float *>(a.part) + static_cast<int64_t>(b) * kPartFloats;
+    const int32_t d = static_cast<int32_t>(threadIdx.x);
+    const float * of = reinterpret_cast<const float *>(smem);
+#pragma unroll
+    for (int32_t hh = 0; hh < kHeads; ++hh) {
+        float acc = of[hh * kOStride + d];
+#pragma unroll
+        for (int32_t w = 1; w < kWaves; ++w) {
+            acc += of[w * kHeads * kOStride + hh * kOStride + d];
+        }
+        part[hh * kD + d] = acc;
+    }
+    if (threadIdx.x < kHeads) {
+        float Mh = -INFINITY;
+#pragma unroll
+        for (int32_t w = 0; w < kWaves; ++w) {
+            Mh = fmaxf(Mh, ml[w * 16 + d]);
+        }
+        float L = 0.0f;
+#pragma unroll
+        for (int32_t w = 0; w < kWaves; ++w) {
+            L = __builtin_fmaf(ml[kWaves * 16 + w * 16 + d], expf(ml[w * 16 + d] - Mh), L);
+        }
+        part[kHeads * kD + d] = Mh;
+        part[kHeads * kD + kHeads + d] = L;
+    }
+}
+
+// the fold of (head h, values 32 r .. 32 r + 31): the active partials in workgroup order, the gate, the F32 output and
+// its activation-format run (fn/kernels/act/act_warp.cuh:12-20's rule: amax, d = amax / 127, id = 127 / amax,
+// q = round-to-even of x id clamped to +-127 (NaN: 0), s = d * sum q)
+template <bool SP> __global__ __launch_bounds__(256) void datc_fold_kernel(fnkv_datc_attend_args a) {
+    __shared__ float w_of[kGrid];
+    __shared__ float red[256];
+    __shared__ float accs[8][32];
+    const datc_shape s = datc_shape_of<SP>(a);
+    if (!s.valid) {
+        return;
+    }
+    const int32_t h = static_cast<int32_t>(blockIdx.x) / 8, r = static_cast<int32_t>(blockIdx.x) % 8;
+    const int32_t t = static_cast<int32_t>(threadIdx.x);
+    const float * part = reinterpret_cast<const float *>(a.part);
+    const float m_t = t < s.active ? part[static_cast<int64_t>(t) * kPartFloats + kHeads * kD + h] : -INFINITY;
+    const float l_t = t < s.active ? part[static_cast<int64_t>(t) * kPartFloats + kHeads * kD + kHeads + h] : 0.0f;
+    red[t] = m_t;
+    __syncthreads();
+    for (int32_t o = 128; o > 0; o >>= 1) {
+        if (t < o) {
+            red[t] = fmaxf(red[t], red[t + o]);
+        }
+        __syncthreads();
+    }
+    const float M = red[0];
+    __syncthreads();
+    const float wt = t < s.active ? expf(m_t - M) : 0.0f;
+    w_of[t] = wt;
+    red[t] = l_t * wt;
+    __syncthreads();
+    for (int32_t o = 128; o > 0; o >>= 1) {
+        if (t < o) {
+            red[t] += red[t + o];
+        }
+        __syncthreads();
+    }
+    const float L = red[0];
+    const int32_t grp = t / 32, dl = t % 32;
+    const int32_t dd = h * kD + 32 * r + dl;
+    float acc = 0.0f;
+    for (int32_t c = grp; c < s.active; c += 8) {
+        acc = __builtin_fmaf(part[static_cast<int64_t>(c) * kPartFloats + dd], w_of[c], acc);
+    }
+    accs[grp][dl] = acc;
+    __syncthreads();
+    if (t >= 32) {
+        return;
+    }
+    const float A = ((accs[0][dl] + accs[1][dl]) + (accs[2][dl] + accs[3][dl])) +
+                    ((accs[4][dl] + accs[5][dl]) + (accs[6][dl] + accs[7][dl]));
+    const float gate = a.qfull[h * kQS + kD + 32 * r + dl];
+    const float y = A / L * (1.0f / (1.0f + expf(-gate)));
+    a.out[dd] = y;
+    float amax = fabsf(y);
+#pragma unroll
+    for (int32_t o = 16; o > 0; o >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    }
+    const float dsc = amax / 127.0f;
+    const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
+    const float e = y * id;
+    const int32_t q = e != e ? 0 : static_cast<int32_t>(fminf(fmaxf(__builtin_rintf(e), -127.0f), 127.0f));
+    int32_t sum = q;
+#pragma unroll
+    for (int32_t o = 16; o > 0; o >>= 1) {
+        sum += __shfl_xor(sum, o, 64);
+    }
+    a.codes[dd] = static_cast<int8_t>(q);
+    if (dl == 0) {
+        a.scales[2 * (h * 8 + r)] = dsc;
+        a.scales[2 * (h * 8 + r) + 1] = dsc * static_cast<float>(sum);
+    }
+}
+
+bool aligned(const void * p, uintptr_t n) {
+    return p != nullptr && reinterpret_cast<uintptr_t>(p) % n == 0;
+}
+
+} // namespace
+} // namespace fnkv
+
+using fnkv::set_error;
+
+extern "C" {
+
+float fnkv_rope_theta_scale(void) {
+    return powf(10000000.0f, -2.0f / static_cast<float>(fnkv::kNRot));
+}
+
+int64_t fnkv_datc_part_bytes(void) {
+    return static_cast<int64_t>(sizeof(float)) * fnkv::kGrid * fnkv::kPartFloats;
+}
+
+int fnkv_datc_prepare(int32_t rows, const fnkv_datc_prepare_args * a, void * stream) {
+    using fnkv::aligned;
+    if (a == nullptr || rows < 1 || rows > FNKV_DATC_MAX_ROWS || a->row0 < 0 || a->row0 + rows > FNKV_DATC_MAX_ROWS ||
+        a->max_cells < 1 || !aligned(a->kv_k, 16) || !aligned(a->kv_v, 16) || !aligned(a->k_norm, 16) ||
+        a->n_before == nullptr || a->pos == nullptr || a->stride == nullptr || !aligned(a->k_cache, 16) ||
+        !aligned(a->v_cache, 16) || a->err == nullptr || (a->k_f32 != nullptr && !aligned(a->k_f32, 16)) ||
+        !std::isfinite(a->theta_scale) ||
+        (a->qfull != nullptr && (!aligned(a->qfull, 16) || !aligned(a->q_norm, 16) || !aligned(a->q16, 16) ||
+                                 (a->q_f32 != nullptr && !aligned(a->q_f32, 16))))) {
+        set_error("fnkv_datc_prepare: argument outside the contract");
+        return FNKV_ERR_ARG;
+    }
+    hipLaunchKernelGGL(fnkv::datc_prepare_kernel, dim3(static_cast<uint32_t>(rows)), dim3(64 * (fnkv::kHeads + 1)), 0,
+                       static_cast<hipStream_t>(stream), *a, rows);
+    if (hipGetLastError() != hipSuccess) {
+        set_error("fnkv_datc_prepare: launch failed");
+        return FNKV_ERR_HIP;
+    }
+    return FNKV_OK;
+}
+
+int fnkv_datc_attend(const fnkv_datc_attend_args * a, void * stream) {
+    using fnkv::aligned;
+    // the caches are addressed by 32-bit buffer offsets: at most 4,194,303 cells (2 GiB a cache)
+    if (a == nullptr || a->row0 < 0 || a->row0 >= (a->body != nullptr ? FNKV_DATC_MAX_SPARSE_ROW : FNKV_DATC_MAX_ROWS) ||
+        a->max_cells < 1 || a->max_cells >= (1 << 22) || !aligned(a->q16, 16) || !aligned(a->qfull, 16) ||
+        !aligned(a->k_cache, 16) || !aligned(a->v_cache, 16) || a->n_before == nullptr || !aligned(a->part, 16) ||
+        !aligned(a->out, 16) || a->codes == nullptr || !aligned(a->scales, 8) || a->err == nullptr ||
+        (a->body != nullptr && !aligned(a->body, 4))) {
+        set_error("fnkv_datc_attend: argument outside the contract");
+        return FNKV_ERR_ARG;
+    }
+    static bool attr_set[64] = {false};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev >= 0 && dev < 64 && !attr_set[dev]) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::datc_attend_kernel<false>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::kAttendLds);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::datc_attend_kernel<true>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::kAttendLds);
+        (void)hipGetLastError();
+        attr_set[dev] = true;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (a->body != nullptr) {
+        hipLaunchKernelGGL(fnkv::datc_attend_kernel<true>, dim3(fnkv::kGrid), dim3(64 * fnkv::kWaves),
+                           fnkv::kAttendLds, st, *a);
+        hipLaunchKernelGGL(fnkv::datc_fold_kernel<true>, dim3(fnkv::kHeads * 8), dim3(256), 0, st, *a);
+    } else {
+        hipLaunchKernelGGL(fnkv::datc_attend_kernel<false>, dim3(fnkv::kGrid), dim3(64 * fnkv::kWaves),
+                           fnkv::kAttendLds, st, *a);
+        hipLaunchKernelGGL(fnkv::datc_fold_kernel<false>, dim3(fnkv::kHeads * 8), dim3(256), 0, st, *a);
+    }
+    if (hipGetLastError() != hipSuccess) {
+        set_error("fnkv_datc_attend: launch failed");
+        return FNKV_ERR_HIP;
+    }
+    return FNKV_OK;
+}
+
+} // extern "C"

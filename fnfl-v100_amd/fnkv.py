@@ -22,8 +22,12 @@ EXPORTS = [
     "fnkv_page_block_bytes", "fnkv_pool_device_base", "fnkv_pool_device_bytes", "fnkv_q8_append",
     "fnkv_export_q8_0", "fnkv_decode_workspace_bytes", "fnkv_attn_decode", "fnkv_prefill_workspace_bytes",
     "fnkv_attn_prefill", "fnkv_pool_create_fmt", "fnkv_pool_format", "fnkv_export_kv8",
-    "fnkv_sparse_workspace_bytes", "fnkv_attn_sparse",
+    "fnkv_sparse_workspace_bytes", "fnkv_attn_sparse", "fnkv_rope_theta_scale", "fnkv_datc_part_bytes",
+    "fnkv_datc_prepare", "fnkv_datc_attend",
 ]
+DATC_HEADS = 12
+DATC_QSTRIDE = 512
+DEV_ERR_DRAFT_DEPTH = 1 << 24
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int32
@@ -34,6 +38,19 @@ _lib = None
 
 class SlotView(ctypes.Structure):
     _fields_ = [("active", I32), ("pages", I32), ("released", ctypes.c_uint64)]
+
+
+class DatcPrepareArgs(ctypes.Structure):
+    """fnkv_datc_prepare_args (include/fnkv.h)"""
+    _fields_ = [("qfull", P), ("kv_k", P), ("kv_v", P), ("q_norm", P), ("k_norm", P), ("n_before", P), ("pos", P),
+                ("stride", P), ("row0", I32), ("theta_scale", ctypes.c_float), ("k_cache", P), ("v_cache", P),
+                ("max_cells", I32), ("q16", P), ("q_f32", P), ("k_f32", P), ("err", P)]
+
+
+class DatcAttendArgs(ctypes.Structure):
+    """fnkv_datc_attend_args (include/fnkv.h)"""
+    _fields_ = [("q16", P), ("qfull", P), ("k_cache", P), ("v_cache", P), ("n_before", P), ("row0", I32),
+                ("max_cells", I32), ("part", P), ("out", P), ("codes", P), ("scales", P), ("err", P), ("body", P)]
 
 
 class FnkvError(RuntimeError):
@@ -101,6 +118,14 @@ def lib():
         L.fnkv_prefill_workspace_bytes.argtypes = [P, I64, I32, I32]
         L.fnkv_attn_prefill.restype = ctypes.c_int
         L.fnkv_attn_prefill.argtypes = [P, I32, I32, I64, I32, I32, ctypes.c_float, P, P, P, I64, P]
+        L.fnkv_rope_theta_scale.restype = ctypes.c_float
+        L.fnkv_rope_theta_scale.argtypes = []
+        L.fnkv_datc_part_bytes.restype = I64
+        L.fnkv_datc_part_bytes.argtypes = []
+        L.fnkv_datc_prepare.restype = ctypes.c_int
+        L.fnkv_datc_prepare.argtypes = [I32, ctypes.POINTER(DatcPrepareArgs), P]
+        L.fnkv_datc_attend.restype = ctypes.c_int
+        L.fnkv_datc_attend.argtypes = [ctypes.POINTER(DatcAttendArgs), P]
         _lib = L
     return _lib
 
@@ -283,3 +308,36 @@ class Pool:
         wp, wn = (P(ws.data_ptr()), ws.numel() * ws.element_size()) if ws is not False else (None, 0)
         return check(lib().fnkv_attn_prefill(self.h, slot, layer, ctx, rows, hq, scale, P(q.data_ptr()),
                                              P(out.data_ptr()), wp, wn, _stream(stream)))
+
+
+# ---- DA-TC: the draft block's dense F16 attention (fn/kernels/draft/draft.h:47-83) ----
+
+def _p(t):
+    return P(t.data_ptr()) if t is not None else None
+
+
+def rope_theta_scale():
+    return lib().fnkv_rope_theta_scale()
+
+
+def datc_part_bytes():
+    return lib().fnkv_datc_part_bytes()
+
+
+def datc_prepare(rows, *, kv_k, kv_v, k_norm, n_before, pos, stride, k_cache, v_cache, err, row0=0, qfull=None,
+                 q_norm=None, q16=None, q_f32=None, k_f32=None, theta_scale=None, stream=None):
+    """datc_prepare (draft.h:243): device tensors; n_before, stride int32 [1], pos int32 [4][stride] on the device."""
+    a = DatcPrepareArgs(_p(qfull), _p(kv_k), _p(kv_v), _p(q_norm), _p(k_norm), _p(n_before), _p(pos), _p(stride),
+                        row0, rope_theta_scale() if theta_scale is None else theta_scale, _p(k_cache), _p(v_cache),
+                        k_cache.shape[0], _p(q16), _p(q_f32), _p(k_f32), _p(err))
+    return check(lib().fnkv_datc_prepare(rows, ctypes.byref(a), _stream(stream)))
+
+
+def datc_attend(*, q16, qfull, k_cache, v_cache, n_before, part, out, codes, scales, err, row0=0, body=None,
+                max_cells=None, stream=None):
+    """datc_attend (draft.h:244): q16 the row's [12][256] fp16, qfull the row's [12][512] fp32, out fp32 [3072],
+    codes int8 [3072], scales fp32 [96][2]; body (SP2) a uint32/int32 device tensor or None."""
+    a = DatcAttendArgs(_p(q16), _p(qfull), _p(k_cache), _p(v_cache), _p(n_before), row0,
+                       k_cache.shape[0] if max_cells is None else max_cells, _p(part), _p(out), _p(codes),
+                       _p(scales), _p(err), _p(body))
+    return check(lib().fnkv_datc_attend(ctypes.byref(a), _stream(stream)))

@@ -176,6 +176,77 @@ int64_t fnkv_prefill_workspace_bytes(const fnkv_pool * pool, int64_t ctx, int32_
 int fnkv_attn_prefill(const fnkv_pool * pool, int32_t slot, int32_t layer, int64_t ctx, int32_t rows, int32_t hq,
                       float scale, const void * q, void * out, void * ws, int64_t ws_bytes, void * stream);
 
+/* ---- the draft block's dense F16 attention, DA-TC (fn/kernels/draft/draft.h:47-83, 159-218) ----
+ *
+ * One KV head, its FNKV_DATC_HEADS query heads, flat F16 caches k_cache / v_cache [max_cells][256] owned by the
+ * caller (not the pool). prepare: per row the F32 RMS norm (eps 1e-6) and IMROPE of each query head and of k, the F16
+ * (nearest even) K and V written at cell n_before + row0 + t, q / 16 rounded to F16; attend: the one row row0 over
+ * cells 0 .. n_before + row0 (or over a selection body, SP2), S = q16 . K with exact F16 products and F32
+ * accumulation, the online softmax in F32 with P rounded to F16 and l the sum of the rounded P, P V, the fold of the
+ * partials, then out = o * sigmoid(gate) in F32 and its int8 activation format (32-value runs: codes and {d, s}, the
+ * rule of fn/quant/act_ref.h:10-13). n_before, pos and stride are device words read by the launches (graph
+ * capturable). A cell at or past max_cells (or, SP2, a body whose K is not this depth's) sets FNKV_DEV_ERR_DRAFT_DEPTH
+ * in *err and writes nothing. Arguments outside the contract: FNKV_ERR_ARG, nothing enqueued. */
+#define FNKV_DATC_HEADS 12         /* query heads a KV head (draft.h:166 n_head) */
+#define FNKV_DATC_QSTRIDE 512      /* qfull: [q | gate] a head (draft.h:168 q_stride) */
+#define FNKV_DATC_MAX_ROWS 5       /* rows a prepare (draft.h:159 max_rows) */
+#define FNKV_DATC_MAX_SPARSE_ROW 4 /* SP2: row0 below this (draft.h:178 max_sparse_steps) */
+#define FNKV_DEV_ERR_DRAFT_DEPTH (1u << 24) /* the reference's err_draft_depth bit (fn/xchg/xchg.h:230) */
+
+/* fn::draft::prepare_args (draft.h:192-213) without the exchange-slot releases (release_hc, release_hmix: the card
+ * exchange is not part of this library) */
+typedef struct {
+    const float * qfull;     /* F32 [rows][12][512], or null: K and V only (the catch-up) */
+    const float * kv_k;      /* F32 [rows][256], before the norm */
+    const float * kv_v;      /* F32 [rows][256] */
+    const float * q_norm;    /* [256] */
+    const float * k_norm;    /* [256] */
+    const int32_t * n_before; /* device: cells before the round's rows */
+    const int32_t * pos;     /* device: rope planes [4][*stride] (t, h, w, e) */
+    const int32_t * stride;  /* device: the round's rows */
+    int32_t row0;            /* this launch's first row in the round */
+    float theta_scale;       /* fnkv_rope_theta_scale() */
+    uint16_t * k_cache;      /* F16 [max_cells][256] */
+    uint16_t * v_cache;
+    int32_t max_cells;
+    uint16_t * q16;          /* F16 [rows][12][256]: q / 16; unused without qfull */
+    float * q_f32;           /* optional [rows][12][256]: the F32 q before the scale */
+    float * k_f32;           /* optional [rows][256]: the F32 k before rounding */
+    uint32_t * err;          /* device error word (FNKV_DEV_ERR_DRAFT_DEPTH) */
+} fnkv_datc_prepare_args;
+
+/* fn::draft::attend_args (draft.h:215-235) */
+typedef struct {
+    const uint16_t * q16;    /* the row's prepared q16 [12][256] */
+    const float * qfull;     /* the row's F32 [12][512]: its gates (floats 256..511 of each head) */
+    const uint16_t * k_cache; /* F16 [max_cells][256] */
+    const uint16_t * v_cache;
+    const int32_t * n_before; /* device */
+    int32_t row0;            /* the row's index in the round; its cell is n_before + row0 */
+    int32_t max_cells;
+    void * part;             /* fnkv_datc_part_bytes() of device scratch (no zeroing needed) */
+    float * out;             /* F32 [3072], gated */
+    int8_t * codes;          /* [3072] the activation format */
+    float * scales;          /* [96][2] */
+    uint32_t * err;
+    /* SP2, optional: a select body made at depth N - 1 (N = *n_before): U32 K = min(N / 4, 512), the tail count, then
+     * K ascending block IDs; the row attends the K blocks' cells, then cells 4 (N / 4) .. N + row0 in order (row0 <
+     * FNKV_DATC_MAX_SPARSE_ROW). Null: every cell 0 .. N + row0. */
+    const uint32_t * body;
+} fnkv_datc_attend_args;
+
+/* rope_theta_scale (fn/kernels/qsa/attend.cu:830-832): powf(1e7, -2 / 64) */
+float fnkv_rope_theta_scale(void);
+
+/* part_bytes (draft.h:237): the attend's scratch */
+int64_t fnkv_datc_part_bytes(void);
+
+/* datc_prepare (draft.h:243, datc.cu:560-578): one launch for rows 1..5 (row0 + rows <= 5) */
+int fnkv_datc_prepare(int32_t rows, const fnkv_datc_prepare_args * a, void * stream);
+
+/* datc_attend (draft.h:244, datc.cu:582-604): two launches (the split attention, then the fold with the gate) */
+int fnkv_datc_attend(const fnkv_datc_attend_args * a, void * stream);
+
 #ifdef __cplusplus
 }
 #endif

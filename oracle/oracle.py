@@ -81,6 +81,7 @@ def ref():
         R.fnkv_ref_f16_value.argtypes = [P, I64, P]
         R.fnkv_ref_stress_rows.restype = I64
         R.fnkv_ref_stress_rows.argtypes = [ctypes.c_uint64, I32, P, I64]
+        R.fnkv_ref_act_quantize.argtypes = [P, I32, I32, P, P]
         _ref = R
     return _ref
 
@@ -289,3 +290,109 @@ def attn_ggml(q16, k_blocks, v_blocks, n_ctx, scale=1.0 / 16.0, q_as_q8=False, t
     lib().or_attn_ggml(_ptr(q16), _ptr(kb), _ptr(vb), n_ctx, T, hq, hkv, d, scale, 1 if q_as_q8 else 0,
                        threads, _ptr(out))
     return out
+
+
+# ---- DA-TC: the draft block's dense F16 attention (fn/kernels/draft/draft.h:47-83) ----
+
+N_ROT = 64
+RMS_EPS = 1e-6
+
+
+def imrope_plane(sector):
+    """IMROPE's plane of rotation pair `sector` (fn/kernels/qsa/imrope.cuh:14-20: sections 11, 11, 10, 0
+    interleaved): 1 (h) for sector % 3 == 1 below 33, 2 (w) for % 3 == 2 below 30, 0 (t) for % 3 == 0 below 33,
+    else 3 (e)."""
+    return (1 if sector % 3 == 1 and sector < 33 else 2 if sector % 3 == 2 and sector < 30
+            else 0 if sector % 3 == 0 and sector < 33 else 3)
+
+
+def theta_f32(pos4, i, ts):
+    """Pair i's angle as the reference forms it (attend.cu:172-183; its checker draft_test.cpp:460-472): the plane's
+    position times theta_scale, i times, as an F32 product chain."""
+    th = np.float32(pos4[imrope_plane(i)])
+    ts = np.float32(ts)
+    for _ in range(i):
+        th = np.float32(th * ts)
+    return float(th)
+
+
+def norm_rope_f64(x, w, pos4, ts):
+    """FP64 of the pinned order (draft_test.cpp:474-489): rms_norm(x) * w over 256 values (eps 1e-6), then pair i
+    (< 32) of dims (i, i + 32) rotated by theta_f32(pos4, i, ts)."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    r = 1.0 / np.sqrt(np.dot(x, x) / x.size + RMS_EPS)
+    y = x * r * w
+    half = N_ROT // 2
+    for i in range(half):
+        th = theta_f32(pos4, i, ts)
+        c, s = np.cos(th), np.sin(th)
+        x0, x1 = y[i], y[i + half]
+        y[i] = x0 * c - x1 * s
+        y[i + half] = x0 * s + x1 * c
+    return y
+
+
+def act_quantize(x):
+    """FNFL's int8 activation format (fn/quant/act_ref.cpp:8-29), in F32: per run of 32 values amax = max |x|,
+    d = amax / 127, id = 127 / amax (0 when amax is 0), q = round-half-even(x id) clamped to [-127, 127] (NaN: 0),
+    s = d * sum q. x: float32 [..., k] (k a multiple of 32) -> (codes int8 like x, scales float32 [..., k / 32, 2])."""
+    x = np.ascontiguousarray(x, np.float32)
+    runs = x.reshape(-1, 32)
+    amax = np.fmax.reduce(np.abs(runs), axis=1, initial=np.float32(0.0)).astype(np.float32)  # NaN ignored, as fmax
+    with np.errstate(divide="ignore", invalid="ignore"):
+        d = (amax / np.float32(127.0)).astype(np.float32)
+        idv = np.where(amax > 0, np.float32(127.0) / np.where(amax > 0, amax, np.float32(1.0)),
+                       np.float32(0.0)).astype(np.float32)
+        e = (runs * idv[:, None]).astype(np.float32)
+    q = np.clip(np.rint(e), -127, 127)
+    q = np.where(np.isnan(e), 0, q).astype(np.int32)
+    s = (d * q.sum(axis=1).astype(np.float32)).astype(np.float32)
+    codes = q.astype(np.int8).reshape(x.shape)
+    scales = np.stack([d, s], axis=1).reshape(x.shape[:-1] + (x.shape[-1] // 32, 2))
+    return codes, scales
+
+
+def datc_cells(n_before, row0, body=None):
+    """The cells DA-TC's row row0 attends, in the kernel's logical order (draft.h:228-233, datc.cu:268-283): dense,
+    0 .. n_before + row0; SP2, the body's K blocks' cells (4 b .. 4 b + 3, in body order), then 4 (N / 4) .. N + row0
+    (N = n_before)."""
+    n = n_before + row0 + 1
+    if body is None:
+        return np.arange(n, dtype=np.int64)
+    body = np.asarray(body, np.int64)
+    K = int(body[0])
+    n_vis = n_before // 4
+    blocks = body[2:2 + K]
+    return np.concatenate([(4 * blocks[:, None] + np.arange(4)[None, :]).reshape(-1),
+                           np.arange(4 * n_vis, n, dtype=np.int64)])
+
+
+def datc_attn_f64(q16, gate, k_cache, v_cache, cells, chunk=16384):
+    """FP64 attention of one DA-TC row over the listed cells of the F16 caches, gated (draft_test.cpp:682-709 form):
+    q = 16 * q16 (exact), s_c = q . K[c] / 16, o = softmax(s) V, out = o / (1 + exp(-gate)).
+    q16: uint16 [12][256]; gate: float32 [12][256]; k_cache, v_cache: uint16 [cells][256] -> float64 [12][256].
+    The cells are taken `chunk` at a time (scores first, then the weighted rows), bounding the fp64 copies."""
+    q = np.ascontiguousarray(q16, np.uint16).view(np.float16).astype(np.float64) * 16.0
+    c = np.asarray(cells, np.int64)
+    kc = np.ascontiguousarray(k_cache, np.uint16)
+    vc = np.ascontiguousarray(v_cache, np.uint16)
+    s = np.concatenate([(q @ kc[c[i:i + chunk]].view(np.float16).astype(np.float64).T) / 16.0
+                        for i in range(0, c.size, chunk)], axis=1)  # [12][n]
+    p = np.exp(s - s.max(axis=1, keepdims=True))
+    o = np.zeros((q.shape[0], kc.shape[1]), np.float64)
+    for i in range(0, c.size, chunk):
+        o += p[:, i:i + chunk] @ vc[c[i:i + chunk]].view(np.float16).astype(np.float64)
+    o /= p.sum(axis=1, keepdims=True)
+    return o / (1.0 + np.exp(-np.asarray(gate, np.float64)))
+
+
+def norm_err(ref, got):
+    """max |got - ref| / max |ref| (draft_test.cpp:143-151; NaN counts as infinite)."""
+    ref = np.asarray(ref, np.float64)
+    got = np.asarray(got, np.float64)
+    e = np.abs(got - ref)
+    if np.isnan(e).any():
+        return float("inf")
+    rmax = np.abs(ref).max()
+    return float(e.max() / rmax) if rmax > 0 else float(e.max())

@@ -8,6 +8,8 @@
 //   fnkv_ref_kv8_quantize    fn/quant/kv_q8_ref.cpp:89-93 kv_q8_quantize (FNFL's group-64 rule)
 //   fnkv_ref_f16_bits_rn / fnkv_ref_f16_value   fn/quant/kv_q8_ref.cpp:10-70
 //   fnkv_ref_stress_rows     fn/quant/kv_q8_ref.cpp:99-169 kv_q8_stress_rows
+//   fnkv_ref_act_quantize    fn/quant/act_ref.cpp:8-29 act_quantize_ref (the int8 activation format)
+#include "fn/quant/act_ref.h"
 #include "fn/quant/kv_q8_ref.h"
 
 #include <cstdint>
@@ -35,6 +37,10 @@ int64_t fnkv_ref_stress_rows(uint64_t seed, int32_t random_rows, float * out, in
         std::memcpy(out, v.data(), sizeof(float) * size_t(cap < int64_t(v.size()) ? cap : int64_t(v.size())));
     }
     return int64_t(v.size());
+}
+
+void fnkv_ref_act_quantize(const float * x, int32_t rows, int32_t k, int8_t * codes, float * scales) {
+    fn::quant::act_quantize_ref(x, rows, k, codes, scales);
 }
 
 }  // extern "C"

@@ -16,6 +16,8 @@ Fixtures:
   f16_golden.npz    ggml_compute_fp32_to_fp16 (ggml-impl.h:414-438) on 40,000 seeded fp32 bit patterns plus edge
                     values; ggml_compute_fp16_to_fp32 (ggml-impl.h:391-412) on all 65,536 halves
   kv8_golden.npz    FNFL's own KV8 rule kv_q8_quantize (kv_q8_ref.cpp:72-93) on the stress rows and the fp16 rows
+  act_golden.npz    FNFL's int8 activation format act_quantize_ref (fn/quant/act_ref.cpp:8-29) on seeded rows of the
+                    DA-TC output width (3,072), exact ties (x id = k + 0.5), zero, subnormal, huge, NaN and inf runs
 """
 import os
 import sys
@@ -71,6 +73,27 @@ def tie_blocks():
     return np.concatenate(out).astype(np.float32)
 
 
+def act_inputs():
+    """Runs of 32 for the activation format: seeded rows, ties, and edge runs."""
+    rng = np.random.default_rng(20261202)
+    runs = [rng.uniform(-3.0, 3.0, size=4 * 3072).astype(np.float32)]
+    runs.append(rng.standard_normal(3072).astype(np.float32) * np.float32(1e-3))
+    # amax 127: id = 1, x = k + 0.5 exactly (ties to even); amax 63.5: id = 2
+    runs.append(np.array([127.0] + [(k % 127) + 0.5 for k in range(31)], np.float32))
+    runs.append(np.array([-63.5] + [-((k % 63) + 0.5) / 2.0 for k in range(31)], np.float32))
+    runs.append(np.zeros(32, np.float32))
+    runs.append(np.full(32, 1e-42, np.float32) * np.arange(1, 33, dtype=np.float32))
+    runs.append(np.linspace(-3e38, 3e38, 32, dtype=np.float32))
+    nan = rng.uniform(-1.0, 1.0, 32).astype(np.float32)
+    nan[[3, 17]] = np.nan
+    runs.append(nan)
+    runs.append(np.full(32, np.nan, np.float32))
+    inf = rng.uniform(-1.0, 1.0, 32).astype(np.float32)
+    inf[5] = np.inf
+    runs.append(inf)
+    return np.concatenate(runs).astype(np.float32)
+
+
 def main():
     if not O.ref_available():
         raise SystemExit("oracle/_ref/libfnkv_ref.so missing: run `make -C oracle ref` first")
@@ -114,7 +137,12 @@ def main():
         kv[f"{name}_codes"] = codes
         kv[f"{name}_scales"] = sc
     np.savez_compressed(os.path.join(HERE, "kv8_golden.npz"), **kv)
-    for f in ("q8_0_golden.npz", "f16_golden.npz", "kv8_golden.npz"):
+    act = act_inputs()
+    codes = np.empty(act.size, np.int8)
+    sc = np.empty(act.size // 16, np.float32)
+    R.fnkv_ref_act_quantize(O._ptr(act), 1, act.size, O._ptr(codes), O._ptr(sc))
+    np.savez_compressed(os.path.join(HERE, "act_golden.npz"), x=act, codes=codes, scales_bits=sc.view(np.uint32))
+    for f in ("q8_0_golden.npz", "f16_golden.npz", "kv8_golden.npz", "act_golden.npz"):
         print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")
 
 

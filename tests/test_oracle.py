@@ -13,6 +13,18 @@ What pins each oracle function (oracle/fnkv_oracle.c):
   or_attn_f64          closed forms (one visible key returns its V row; q = 0 returns the visible rows' mean; equal
                        keys give the mean), brute force by numpy on tiny inputs, and key-order invariance
   or_attn_ggml         the fp64 form within 2e-3 (fp32 Q) on a seeded BASELINE-shaped case
+DA-TC (oracle.py):
+  act_quantize         the reference's act_quantize_ref (fn/quant/act_ref.cpp) outputs, bitwise (golden: seeded rows,
+                       exact ties, zero / subnormal / huge / NaN / inf runs)
+  imrope_plane         the sector table written out by hand from imrope.cuh's sections (11, 11, 10, 0)
+  theta_f32            the closed form pos * ts^i in fp64 (the F32 chain within i + 1 ulps)
+  norm_rope_f64        closed forms: at position 0 the rotation is the identity and the row's mean square is
+                       1 / (1 + eps / ms(x)) against w = 1; each pair's norm is preserved; each pair equals the complex
+                       product (y_i + i y_{i+32}) e^(i theta) computed from the position-0 row; distinct planes pick
+                       the sector's position
+  datc_cells           hand-written dense and SP2 lists (the body's blocks' cells, then the tail and the chain)
+  datc_attn_f64        closed forms (one dominant key returns its V row times sigmoid(gate); q = 0 the listed rows'
+                       mean; gate 0 halves the output) and numpy brute force over a tiny case
 """
 import numpy as np
 import pytest
@@ -229,3 +241,93 @@ def test_qsa_body_layout():
             assert np.all(np.diff(blocks) > 0) and (K == 0 or 4 * blocks[-1] + 3 <= q)
             assert list(row[2 + K:]) == list(range(4 * ((q + 1) // 4), q + 1))
             assert cells[t].size == 4 * K + tail and cells[t].max() <= q
+
+
+# ---- DA-TC ----
+
+def test_act_quantize_matches_reference(golden):
+    g = golden("act_golden.npz")
+    codes, scales = O.act_quantize(g["x"])
+    assert np.array_equal(codes, g["codes"])
+    assert np.array_equal(scales.reshape(-1).view(np.uint32), g["scales_bits"])
+
+
+def test_imrope_plane_table():
+    # sections (t 11, h 11, w 10, e 0), interleaved by sector % 3; n_rot 64 has sectors 0..31 only
+    want = [0, 1, 2] * 10 + [0, 1]
+    assert [O.imrope_plane(i) for i in range(32)] == want
+    assert O.imrope_plane(33) == 3 and O.imrope_plane(30) == 0 and O.imrope_plane(32) == 3 and O.imrope_plane(31) == 1
+
+
+def test_theta_f32_chain_closed_form():
+    ts = np.float32(10000000.0) ** np.float32(-2.0 / 64.0)
+    for p in (1, 7, 4095, 196607):
+        for i in range(32):
+            exact = p * float(ts) ** i
+            got = O.theta_f32([p, p, p, p], i, float(ts))
+            assert abs(got - exact) <= (i + 1) * 2.0**-23 * abs(exact) + 1e-300
+
+
+def test_norm_rope_f64_closed_forms():
+    rng = np.random.default_rng(3)
+    ts = float(np.float32(10000000.0) ** np.float32(-2.0 / 64.0))
+    x = rng.uniform(-2, 2, 256).astype(np.float32)
+    w = rng.uniform(0.3, 1.8, 256).astype(np.float32)
+    y0 = O.norm_rope_f64(x, np.ones(256, np.float32), [0, 0, 0, 0], ts)
+    ms = np.mean(x.astype(np.float64) ** 2)
+    assert abs(np.mean(y0**2) - 1.0 / (1.0 + 1e-6 / ms)) < 1e-12
+    assert np.allclose(y0 / x, y0[0] / x[0])  # the identity rotation: a common factor
+    base = O.norm_rope_f64(x, w, [0, 0, 0, 0], ts)
+    pos4 = [5000, 5017, 5034, 1250]
+    y = O.norm_rope_f64(x, w, pos4, ts)
+    a = base[:32] + 1j * base[32:64]
+    b = y[:32] + 1j * y[32:64]
+    th = np.array([O.theta_f32(pos4, i, ts) for i in range(32)])
+    assert np.allclose(np.abs(a), np.abs(b), rtol=1e-13)
+    assert np.allclose(a * np.exp(1j * th), b, rtol=0, atol=1e-12)
+    assert np.array_equal(y[64:], base[64:])
+    # pair i turns by its own plane's position: pair 1 (h) at 5017 * ts (an F32 angle near 3,000: within 1e-3; the
+    # other planes' positions are 10 radians or more away)
+    for i, p in ((1, 5017), (2, 5034), (3, 5000)):
+        d = np.angle(b[i] / a[i]) - np.angle(np.exp(1j * p * float(ts) ** i))
+        assert abs((d + np.pi) % (2 * np.pi) - np.pi) < 1e-3
+
+
+def test_datc_cells_lists():
+    assert O.datc_cells(5, 2).tolist() == list(range(8))
+    # N = 14: n_vis 3 whole blocks, K = 3, tail cells 12, 13 and the chain's row0 + 1 = 2 cells 14, 15
+    body = [3, 2, 0, 1, 2]
+    assert O.datc_cells(14, 1, body).tolist() == list(range(12)) + [12, 13, 14, 15]
+    body = [2, 0, 1, 5, 99]  # K 2 of N / 4 = 6 blocks (a test of the list, not of K's rule)
+    assert O.datc_cells(24, 0, body).tolist() == [4, 5, 6, 7, 20, 21, 22, 23, 24]
+
+
+def test_datc_attn_f64_closed_forms():
+    rng = np.random.default_rng(5)
+    n = 40
+    kc = rng.uniform(-1, 1, (n, 256)).astype(np.float16)
+    vc = rng.uniform(-1.5, 1.5, (n, 256)).astype(np.float16)
+    gate = rng.uniform(-3, 3, (12, 256)).astype(np.float32)
+    cells = np.arange(n)
+    # q = 0: the mean of the listed V rows, times sigmoid(gate)
+    q0 = np.zeros((12, 256), np.float16)
+    o = O.datc_attn_f64(q0.view(np.uint16), gate, kc.view(np.uint16), vc.view(np.uint16), cells)
+    sig = 1.0 / (1.0 + np.exp(-gate.astype(np.float64)))
+    assert np.allclose(o, vc.astype(np.float64).mean(0)[None] * sig, rtol=0, atol=1e-14)
+    # one dominant key: its V row; gate 0 halves it
+    kd = kc.copy()
+    kd[17] = np.float16(4.0)
+    q = np.full((12, 256), 4.0, np.float16)
+    o = O.datc_attn_f64(q.view(np.uint16), np.zeros((12, 256), np.float32), kd.view(np.uint16),
+                        vc.view(np.uint16), cells)
+    assert np.allclose(o, 0.5 * vc[17].astype(np.float64)[None], rtol=0, atol=1e-12)
+    # brute force on a tiny list (a subset, out of order)
+    sub = np.array([3, 9, 1, 30])
+    qr = rng.uniform(-1, 1, (12, 256)).astype(np.float16)
+    o = O.datc_attn_f64(qr.view(np.uint16), gate, kc.view(np.uint16), vc.view(np.uint16), sub)
+    for h in range(12):
+        s = [sum(float(qr[h, d]) * 16.0 * float(kc[c, d]) for d in range(256)) / 16.0 for c in sub]
+        m = max(s)
+        p = [np.exp(v - m) for v in s]
+        ref = sum(pi * vc[c].astype(np.float64) for pi, c in zip(p, sub)) / sum(p) * sig[h]
+        assert np.allclose(o[h], ref, rtol=1e-12, atol=1e-14)
