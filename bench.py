@@ -48,6 +48,11 @@ CONFIGS = {
                           "(random, rows disjoint: the reference's QA2 shape), 12 layers"),
     "qsa1": dict(depth=196608 - 1, T=1, layers=12, sparse=True,
                  workload="qsa1: sparse (QSA) attention, 1 row at 196,608 cells over 512 blocks + tail, 12 layers"),
+    "datc": dict(cells=196608, datc=True,
+                 workload="datc: DA-TC draft step row (prepare with q, dense attention, gate) at 196,608 cells of F16 "
+                          "K/V, 12 query heads, the reference's deepest draft-bench point"),
+    "datc4k": dict(cells=4096, datc=True,
+                   workload="datc4k: DA-TC draft step row at 4,096 cells of F16 K/V (the reference's shallowest point)"),
 }
 PEAK_MFMA_F16_TFLOPS = 2500.0  # dense fp16 matrix-core peak
 
@@ -418,6 +423,149 @@ def run_sparse(args, cfg):
     pool.close()
 
 
+def run_datc(args, cfg):
+    """DA-TC's draft step row (fn/kernels/draft/draft.h:47-83): one step = fnkv_datc_prepare (the row's 12 query heads
+    and its new cell's K / V) then fnkv_datc_attend (the attention over every cell, the fold, the gate), one HIP graph
+    a step. Every cell comes from HBM: the steps rotate over copies of the caches totalling over 1 GB (the reference's
+    warm bench rotates over 200 MB for the V100's 6 MB L2; MI355X's last-level cache is 256 MB). Algorithmic bytes a
+    step: K and V of the cells (1,024 B a cell), the prepare's inputs and outputs, the attend's q16, gates and outputs."""
+    import numpy as np
+    import torch
+
+    import fnkv
+    import oracle as O
+
+    n = cfg["cells"]
+    nb, NHd, HDd = n - 1, fnkv.DATC_HEADS, 256
+    max_cells = n + 8
+    copy_bytes = max_cells * HDd * 2 * 2
+    copies = max(2, min(512, -(-1_200_000_000 // copy_bytes)))
+    torch.cuda.set_device(0)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(args.seed)
+    caches = torch.randn((copies, 2, max_cells, HDd), generator=g, device="cuda").half().view(torch.int16)
+    qfull = torch.empty((1, NHd, 512), device="cuda").uniform_(-3.0, 3.0, generator=g)
+    kv = torch.empty((2, 1, HDd), device="cuda").uniform_(-2.0, 2.0, generator=g)
+    norms = torch.empty((2, HDd), device="cuda").uniform_(0.3, 1.8, generator=g)
+    ints = torch.tensor([nb, 1], dtype=torch.int32, device="cuda")
+    pos = torch.full((4, 1), nb, dtype=torch.int32, device="cuda")
+    q16 = torch.empty((1, NHd, HDd), dtype=torch.int16, device="cuda")
+    part = torch.empty(fnkv.datc_part_bytes() // 4, dtype=torch.float32, device="cuda")
+    out = torch.empty(NHd * HDd, dtype=torch.float32, device="cuda")
+    codes = torch.empty(NHd * HDd, dtype=torch.int8, device="cuda")
+    scales = torch.empty(NHd * HDd // 16, dtype=torch.float32, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def step(i):
+        kc, vc = caches[i][0], caches[i][1]
+        fnkv.datc_prepare(1, kv_k=kv[0], kv_v=kv[1], k_norm=norms[1], n_before=ints[0:1], pos=pos, stride=ints[1:2],
+                          k_cache=kc, v_cache=vc, err=err, qfull=qfull, q_norm=norms[0], q16=q16)
+        fnkv.datc_attend(q16=q16, qfull=qfull, k_cache=kc, v_cache=vc, n_before=ints[0:1], part=part, out=out,
+                         codes=codes, scales=scales, err=err)
+
+    for i in range(copies):
+        step(i)
+    torch.cuda.synchronize()
+    # one graph holds `copies` steps, one on each copy of the caches (the reference's bench times graphs of n_copy
+    # steps, fn/kernels/draft/draft_bench.cu:250-292); K steps = ceil(K / copies) replays
+    replays = max(1, -(-args.steps // copies))
+    warm = max(1, -(-args.warmup // copies))
+    run = None
+    if not args.no_graph:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step(0)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(copies):
+                step(i)
+        torch.cuda.synchronize()
+        run = graph.replay
+    else:
+        def run():
+            for i in range(copies):
+                step(i)
+    for _ in range(warm):
+        run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(replays):
+        run()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = ev0.elapsed_time(ev1) / 1e3
+    n_steps = replays * copies
+    assert int(err.item()) == 0, "DA-TC error word set"
+    assert torch.isfinite(out).all().item(), "non-finite attention output"
+    step_s = gpu_s / n_steps
+    bytes_step = (n * HDd * 2 * 2  # K and V of every cell
+                  + NHd * 512 * 4 + 2 * HDd * 4 + 2 * HDd * 4 + 4 * 4  # prepare: qfull, k / v, norms, positions
+                  + NHd * HDd * 2 + 2 * HDd * 2  # q16 and the new cell written
+                  + NHd * HDd * 2 + NHd * HDd * 4  # attend: q16 and the gates read
+                  + NHd * HDd * 4 + NHd * HDd + NHd * HDd // 16 * 4)  # out, codes, scales written
+    achieved = bytes_step / step_s / 1e9
+    line = {
+        "metric": "DA-TC draft step row (prepare + dense F16 attention + gate): steps/s and achieved GB/s",
+        "value": round(n_steps / wall, 3),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": n_steps,
+        "warmup": warm * copies,
+        "ms_per_step": round(wall / n_steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 K/V and q, f32 accumulate and softmax, f16 P",
+        "data": "synthetic (seeded N(0,1) F16 caches, uniform q / k / v / gates / norms)",
+        "config": {"workload": cfg["workload"], "cells": n, "q_heads": NHd, "head_dim": HDd,
+                   "cache_copies_rotated": copies, "rotated_mb": round(copies * copy_bytes / 1e6),
+                   "steps_per_graph": copies, "hip_graph": not args.no_graph},
+        "roofline": {
+            "kernel": "fnkv_datc_prepare + fnkv_datc_attend (datc_prepare_kernel, datc_attend_kernel, "
+                      "datc_fold_kernel), a step",
+            "bound": "hbm",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": bytes_step,
+            "launch_us": round(step_s * 1e6, 3),
+            "reference_floor_v100_us": round(1.95 + n * 1024 / 1021.6e3, 2),
+        },
+    }
+    if not args.no_cpu:
+        from threadpoolctl import threadpool_limits
+        threads = max(1, min(16, os.cpu_count() or 1))
+        kh = caches[0][0].cpu().numpy().view(np.uint16)
+        vh = caches[0][1].cpu().numpy().view(np.uint16)
+        qh = q16[0].cpu().numpy().view(np.uint16)
+        gate = qfull[0, :, 256:].cpu().numpy()
+        cells = np.arange(n)
+        with threadpool_limits(limits=threads):
+            O.datc_attn_f64(qh, gate, kh, vh, cells)
+            reps, t1 = 0, time.perf_counter()
+            while reps < 3 or time.perf_counter() - t1 < 2.0:
+                O.datc_attn_f64(qh, gate, kh, vh, cells)
+                reps += 1
+            cpu_s = (time.perf_counter() - t1) / reps
+        line["cpu_baseline"] = {
+            "value": round(1.0 / cpu_s, 3), "unit": "steps/s", "cores": threads, "kind": "port",
+            "sample": f"the attention of one step row over all {n} cells in fp64 numpy (oracle/oracle.py "
+                      f"datc_attn_f64, BLAS threads capped at {threads}), {reps} reps, {cpu_s * 1e3:.1f} ms each; the "
+                      f"reference has no CPU path for DA-TC",
+        }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -442,6 +590,9 @@ def main():
         return
     if CONFIGS[args.config].get("sparse"):
         run_sparse(args, CONFIGS[args.config])
+        return
+    if CONFIGS[args.config].get("datc"):
+        run_datc(args, CONFIGS[args.config])
         return
 
     traffic, traffic_detail = None, "skipped (--no-traffic)"

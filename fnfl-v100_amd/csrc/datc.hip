@@ -6,18 +6,19 @@
 // How (MI355X):
 //   * prepare: a workgroup a row, a wave a query head (12) and one for k / v; a lane holds 4 of the 256 values.
 //   * attend: a fixed grid of kGrid workgroups of 4 waves (the depth is a device word, so the grid cannot depend on
-//     it); the first A = min(kGrid, ceil(tiles / 4)) take even ranges of 32-cell tiles, wave w every fourth tile of
-//     its group's range. A wave's step, all on the matrix cores (v_mfma_f32_16x16x32_f16):
+//     it); the first A = min(kGrid, ceil(tiles / 4)) stride over the 32-cell tiles, wave w of workgroup b taking
+//     tiles w + 4 (b + A i), so the workgroups read one window of the caches together (measured: a contiguous range
+//     a workgroup streams ~18% slower). A wave's step, all on the matrix cores (v_mfma_f32_16x16x32_f16):
 //       S^T = K Q^T: K rows straight from HBM into registers (buffer loads; cells past the row read as zeros), the 12
 //         heads (padded to 16) of q16 held in registers for the whole launch; lane l ends with head l % 16's scores
 //         of cells 4 (l / 16) .. + 3 of each 16-cell half, so the online softmax needs no transposition: its max
 //         and sum cross the four 16-lane rows by two lane swaps.
 //       O^T += V^T P^T: the lane's own 8 rounded probabilities are the B operand as they stand (the MFMA's k slots
-//         mapped onto those 8 cells); the V tile comes into LDS by direct global-to-LDS copies (two cells a copy,
-//         rows padded so the transposed reads below are conflict-free) and each lane reads its A operand (8 cells of
-//         one dimension) as 16-bit values. The accumulators hold O^T, so the per-head rescale is the lane's own.
-//     The next tile's K and V are issued before the current one is computed (two register and LDS buffers).
-//     The 4 waves fold into one partial per workgroup in LDS.
+//         mapped onto those 8 cells); the V tile comes into the wave's LDS buffer by direct global-to-LDS copies (two
+//         cells a copy, copies padded apart) and each lane's A operand (8 cells of one dimension) is two transposing
+//         reads (ds_read_b64_tr_b16). The accumulators hold O^T, so the per-head rescale is the lane's own.
+//     The next tile's K (registers) and V (the other LDS buffer) are in flight while one is computed. The 4 waves
+//     fold into one partial per workgroup in LDS.
 //   * fold: a workgroup per (head, 32-value run): the partials folded in workgroup order with exp(m_c - M), the gate,
 //     the F32 output and the run's activation format.
 // Numerics (draft.h:69-77): exact F16 products, F32 accumulation, P rounded to F16 (nearest even), l the sum of the
@@ -44,15 +45,34 @@ constexpr int32_t kGrid = 256;          // attention workgroups
 constexpr int32_t kWaves = 4;
 constexpr int32_t kTile = 32;           // cells a wave's step
 constexpr int32_t kPartFloats = kHeads * kD + 2 * kHeads; // a workgroup's O [12][256], then m [12] and l [12]
-constexpr int32_t kVPair = 2 * 512 + 16;                  // LDS bytes of two cells' V rows, padded
-constexpr int32_t kVBuf = (kTile / 2) * kVPair;           // a tile's V rows: 16,640 B
-constexpr int32_t kWaveLds = 2 * kVBuf;                   // two tiles a wave
-constexpr int32_t kAttendLds = kWaves * kWaveLds + 2 * kWaves * 16 * 4; // + the waves' m and l
-constexpr int32_t kOStride = kD + 4;                      // floats a head's row of a wave's O in LDS (fold step)
+constexpr int32_t kVPair = 2 * 512 + 64;                  // LDS bytes of two cells' V rows, padded
+constexpr int32_t kVBuf = (kTile / 2) * kVPair;           // a tile's V rows: 17,408 B (two a wave)
+constexpr int32_t kOStride = kD + 4;                      // floats a head's row of a wave's O in LDS (wave fold)
+constexpr int32_t kFoldLds = kWaves * kHeads * kOStride * 4; // the waves' O, over the V buffers at the end
+constexpr int32_t kMlLds = kFoldLds > 2 * kWaves * kVBuf ? kFoldLds : 2 * kWaves * kVBuf; // waves' m, l: past both
+constexpr int32_t kAttendLds = kMlLds + 2 * kWaves * 16 * 4;
 constexpr int32_t kSelRatio = 4, kSelBlocks = 512;
 constexpr uint32_t kOob = 0x80000000u;                    // a buffer offset past every cache: reads as zero
+constexpr int32_t kEmptyTile = 1 << 30;                   // a tile base past every row: an empty step
 
-static_assert(kWaves * kHeads * kOStride * 4 <= kWaves * kWaveLds, "the wave fold reuses the V buffers");
+static_assert(kGrid == 256, "the fold: a thread's partial weight, 8 groups of kGrid / 8 partials");
+
+#ifdef FNKV_TIMING
+__device__ uint64_t * g_datc_ts;
+} // namespace
+uint64_t * timing_buffer();
+namespace {
+// instrumented builds: real-time stamps of workgroup `slot`'s phases (16 a workgroup; attend slots 0..255, fold
+// 256..351, prepare 352..)
+#define DATC_STAMP(slot, k)                                                                                          \
+    do {                                                                                                             \
+        if (ts != nullptr && threadIdx.x == 0) {                                                                     \
+            ts[(slot) * 16 + (k)] = __builtin_amdgcn_s_memrealtime();                                                \
+        }                                                                                                            \
+    } while (0)
+#else
+#define DATC_STAMP(slot, k) ((void)0)
+#endif
 
 // ---- prepare ----
 
@@ -114,6 +134,10 @@ __device__ __forceinline__ uint2 pack4_f16(const float (&x)[4], float scale) {
 __global__ __launch_bounds__(64 * (kHeads + 1)) void datc_prepare_kernel(fnkv_datc_prepare_args a, int32_t rows) {
     const int32_t wave = static_cast<int32_t>(threadIdx.x) / 64, lane = static_cast<int32_t>(threadIdx.x) % 64;
     const int32_t t = static_cast<int32_t>(blockIdx.x);
+#ifdef FNKV_TIMING
+    uint64_t * ts = g_datc_ts;
+#endif
+    DATC_STAMP(352 + t, 0);
     const int32_t nb = *a.n_before, stride = *a.stride;
     if (nb < 0 || static_cast<int64_t>(nb) + a.row0 + rows > a.max_cells || a.row0 + rows > stride) {
         if (threadIdx.x == 0) {
@@ -132,6 +156,7 @@ __global__ __launch_bounds__(64 * (kHeads + 1)) void datc_prepare_kernel(fnkv_da
             reinterpret_cast<float4 *>(a.q_f32 + (t * kHeads + wave) * kD)[lane] = make_float4(y[0], y[1], y[2], y[3]);
         }
         reinterpret_cast<uint2 *>(a.q16 + (t * kHeads + wave) * kD)[lane] = pack4_f16(y, 1.0f / 16.0f);
+        DATC_STAMP(352 + t, 1);
         return;
     }
     norm_rope(y, a.kv_k + t * kD, a.k_norm, a.pos, stride, col, a.theta_scale, lane);
@@ -182,21 +207,38 @@ __device__ __forceinline__ int32_t cell_of(const fnkv_datc_attend_args & a, cons
     }
 }
 
+// K of a tile in registers, as the S^T operand
 struct k_tile {
     u32x4 r[2][8]; // [16-cell half][32-dim slice]: lane l's 8 dims 32 j + 8 (l / 16) .. of cell 16 half + l % 16
 };
 
-// issue one tile's loads: K into registers, V into the wave's LDS buffer (16 copies of two cells)
+// LDS byte offset of cell c's V row in a tile buffer: two cells a copy (contiguous), copies kVPair apart
+__device__ __forceinline__ int32_t v_cell_off(int32_t c) {
+    return (c >> 1) * kVPair + (c & 1) * 512;
+}
+
+// issue one tile's 32 loads: K into registers, V into the wave's LDS buffer; cells past the row read as zeros
 template <bool SP>
 __device__ __forceinline__ void issue_tile(const fnkv_datc_attend_args & a, const datc_shape & s, rsrc_t rk, rsrc_t rv,
                                            int32_t base, k_tile & kt, uint8_t * vbuf, int32_t lane) {
-    // lane l < 32 resolves logical cell base + l (a body word for SP2); the others are taken by lane exchange
-    const int32_t li = base + (lane & 31);
-    const int32_t mine = li < s.n ? cell_of<SP>(a, s, li) : -1;
+    // SP2: lane l < 32 resolves logical cell base + l (a body word) and the others take it by lane exchange; dense:
+    // logical cell i is cell i
+    int32_t mine = 0;
+    if constexpr (SP) {
+        const int32_t li = base + (lane & 31);
+        mine = li < s.n ? cell_of<SP>(a, s, li) : -1;
+    }
+    auto cell = [&](int32_t i) {
+        if constexpr (SP) {
+            return __shfl(mine, i, 64);
+        } else {
+            return base + i < s.n ? base + i : -1;
+        }
+    };
     const int32_t g = lane / 16;
 #pragma unroll
     for (int32_t h = 0; h < 2; ++h) {
-        const int32_t c = __shfl(mine, 16 * h + lane % 16, 64);
+        const int32_t c = cell(16 * h + lane % 16);
         const uint32_t off = c >= 0 ? static_cast<uint32_t>(c) * 512u + 16u * static_cast<uint32_t>(g) : kOob;
 #pragma unroll
         for (int32_t j = 0; j < 8; ++j) {
@@ -205,16 +247,49 @@ __device__ __forceinline__ void issue_tile(const fnkv_datc_attend_args & a, cons
     }
 #pragma unroll
     for (int32_t c2 = 0; c2 < kTile / 2; ++c2) {
-        const int32_t c = __shfl(mine, 2 * c2 + lane / 32, 64);
+        const int32_t c = cell(2 * c2 + lane / 32);
         const uint32_t off = c >= 0 ? static_cast<uint32_t>(c) * 512u + 16u * static_cast<uint32_t>(lane % 32) : kOob;
         buf_lds16(rv, vbuf + c2 * kVPair, static_cast<int32_t>(off), 0);
     }
 }
 
-// one tile's step: scores, the online softmax (m, l of head lane % 16), O^T rescaled and accumulated
-template <bool HAS_NEXT>
-__device__ __forceinline__ void tile_step(const k_tile & kt, const half8 (&qb)[8], const uint8_t * vbuf, int32_t base,
-                                          int32_t n, float & m_run, float & l_run, floatx4 (&o)[16], int32_t lane) {
+// 4 fp16 values by the transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group, lane j supplies the
+// address of 4 consecutive values M[j][0..3]; lane i receives M[4 k + i / 4][i % 4] for k = 0..3
+__device__ __forceinline__ u32x2 lds_read_tr4(const uint8_t * p) {
+    typedef short short4v __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) short4v * lds_s4;
+    const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p));
+    return __builtin_bit_cast(u32x2, r);
+}
+
+// one tile's step: the next tile's loads issued (K into kn, V into vnext), then, once this tile's have landed (K in kt,
+// V in vbuf), the scores, the online softmax (m, l of head lane % 16), O^T rescaled and accumulated. The two LDS
+// buffers are distinct restrict pointers here, which tells the compiler that the reads of vbuf do not depend on the
+// copies into vnext: it then waits for this tile's copies only, not for the next tile's.
+template <bool SP, bool NEXT>
+__device__ __forceinline__ void tile_step(const fnkv_datc_attend_args & a, const datc_shape & s, rsrc_t rk, rsrc_t rv,
+                                          const k_tile & kt, k_tile & kn, const uint8_t * __restrict__ vbuf,
+                                          uint8_t * __restrict__ vnext, int32_t base, int32_t next_base,
+                                          const half8 (&qb)[8], float & m_run, float & l_run, floatx4 (&o)[16],
+                                          int32_t lane) {
+    // the next tile's loads go out before anything of this step (the scheduler may not sink them below the scores)
+    if constexpr (NEXT) {
+        issue_tile<SP>(a, s, rk, rv, next_base, kn, vnext, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<32>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#ifdef FNKV_TIMING
+    {
+        uint64_t * ts = g_datc_ts;
+        if (ts != nullptr && threadIdx.x == 0 && ts[blockIdx.x * 16 + 1] == 0) {
+            ts[blockIdx.x * 16 + 1] = __builtin_amdgcn_s_memrealtime();
+        }
+    }
+#endif
+    const int32_t n = s.n;
     const int32_t g = lane / 16;
     floatx4 st[2];
 #pragma unroll
@@ -227,14 +302,14 @@ __device__ __forceinline__ void tile_step(const k_tile & kt, const half8 (&qb)[8
         st[h] = acc;
     }
     // lane l: head l % 16, cells 16 h + 4 g + i
-    float s[8];
+    float sv[8];
     float mx = -INFINITY;
 #pragma unroll
     for (int32_t h = 0; h < 2; ++h) {
 #pragma unroll
         for (int32_t i = 0; i < 4; ++i) {
             const float v = base + 16 * h + 4 * g + i < n ? st[h][i] : -INFINITY;
-            s[4 * h + i] = v;
+            sv[4 * h + i] = v;
             mx = fmaxf(mx, v);
         }
     }
@@ -244,8 +319,8 @@ __device__ __forceinline__ void tile_step(const k_tile & kt, const half8 (&qb)[8
     float sum = 0.0f;
 #pragma unroll
     for (int32_t i = 0; i < 4; ++i) {
-        const _Float16 p0 = static_cast<_Float16>(expf(s[2 * i] - m_new));
-        const _Float16 p1 = static_cast<_Float16>(expf(s[2 * i + 1] - m_new));
+        const _Float16 p0 = static_cast<_Float16>(expf(sv[2 * i] - m_new));
+        const _Float16 p1 = static_cast<_Float16>(expf(sv[2 * i + 1] - m_new));
         sum += static_cast<float>(p0);
         sum += static_cast<float>(p1);
         pw[i] = __builtin_bit_cast(uint32_t, half2v{p0, p1});
@@ -255,25 +330,17 @@ __device__ __forceinline__ void tile_step(const k_tile & kt, const half8 (&qb)[8
     m_run = m_new;
     l_run = __builtin_fmaf(l_run, alpha, sum);
     const half8 pb = __builtin_bit_cast(half8, pw);
-    // V of this tile has landed in LDS once at most the next tile's 32 loads are outstanding
-    if constexpr (HAS_NEXT) {
-        wait_vmcnt<32>();
-    } else {
-        wait_vmcnt<0>();
-    }
-    // A operand of dims 16 db + l % 16: cells 4 g + i (i < 4) and 16 + 4 g + i - 4 (the k-slot order of pb)
-    const uint8_t * vl = vbuf + 2 * g * kVPair + 2 * (lane % 16);
-    constexpr int32_t coff[8] = {0, 512, kVPair, kVPair + 512, 8 * kVPair, 8 * kVPair + 512, 9 * kVPair,
-                                 9 * kVPair + 512};
+    // the A operand of dims 16 db + i (i = l % 16): k slots 8 g .. + 3 are cells 4 g .. + 3, slots 8 g + 4 .. + 7
+    // cells 16 + 4 g .. + 3 (pb's order); lane j = l % 16 of the group addresses cell (j / 4) of each four, dims
+    // 4 (j % 4) .. + 3 of the 16
+    const int32_t j = lane % 16;
+    const uint8_t * r0 = vbuf + v_cell_off(4 * g + j / 4) + 8 * (j % 4);
+    const uint8_t * r1 = vbuf + v_cell_off(16 + 4 * g + j / 4) + 8 * (j % 4);
 #pragma unroll
     for (int32_t db = 0; db < 16; ++db) {
-        u32x4 va;
-#pragma unroll
-        for (int32_t i = 0; i < 4; ++i) {
-            const uint32_t lo = *reinterpret_cast<const uint16_t *>(vl + 32 * db + coff[2 * i]);
-            const uint32_t hi = *reinterpret_cast<const uint16_t *>(vl + 32 * db + coff[2 * i + 1]);
-            va[i] = lo | (hi << 16);
-        }
+        const u32x2 lo = lds_read_tr4(r0 + 32 * db);
+        const u32x2 hi = lds_read_tr4(r1 + 32 * db);
+        const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
         o[db] = mfma16(__builtin_bit_cast(half8, va), pb, o[db] * alpha);
     }
 }
@@ -292,16 +359,21 @@ template <bool SP> __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend
     if (b >= s.active) {
         return;
     }
-    const int32_t t0 = static_cast<int32_t>(static_cast<int64_t>(b) * s.n_tiles / s.active);
-    const int32_t t1 = static_cast<int32_t>(static_cast<int64_t>(b + 1) * s.n_tiles / s.active);
-    const int32_t cnt = t1 - t0 > wave ? (t1 - t0 - wave + kWaves - 1) / kWaves : 0;
+#ifdef FNKV_TIMING
+    uint64_t * ts = g_datc_ts;
+#endif
+    DATC_STAMP(b, 0);
+    // the grid strides over the tiles: wave w of workgroup b takes tiles w + 4 (b + A i), so at any moment the
+    // workgroups read one window of the caches together
+    const int32_t first = wave + kWaves * b, per = kWaves * s.active;
+    const int32_t cnt = s.n_tiles > first ? (s.n_tiles - first + per - 1) / per : 0;
     const uint32_t cache_bytes = static_cast<uint32_t>(a.max_cells) * 512u;
     const rsrc_t rk = make_rsrc(a.k_cache, static_cast<int32_t>(cache_bytes));
     const rsrc_t rv = make_rsrc(a.v_cache, static_cast<int32_t>(cache_bytes));
-    uint8_t * vb0 = smem + wave * kWaveLds;
+    uint8_t * vb0 = smem + wave * 2 * kVBuf;
     uint8_t * vb1 = vb0 + kVBuf;
     // q16 as the B operand: lane l holds head l % 16's dims 32 j + 8 (l / 16) .. + 7 (heads 12..15 zero); loaded
-    // before the first tile so that the wait for it leaves the tile's loads in flight
+    // before the first tile
     half8 qb[8];
     {
         const int32_t h = lane % 16, g = lane / 16;
@@ -314,35 +386,35 @@ template <bool SP> __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend
             qb[j] = __builtin_bit_cast(half8, v);
         }
     }
-    k_tile ka, kb;
-    if (cnt > 0) {
-        issue_tile<SP>(a, s, rk, rv, (t0 + wave) * kTile, ka, vb0, lane);
-    }
+    // one tile in flight while the other is computed; in the loop every step issues its 32 loads (the wave's last
+    // pair may take an empty tile: cells beyond the row, zeros, no memory traffic) and the loop runs whole pairs, so a
+    // step waits for exactly the loads issued before the last 32; an odd last tile is a step of its own that issues
+    // nothing
+    auto tile_base = [&](int32_t k) { return k < cnt ? (first + per * k) * kTile : kEmptyTile; };
     float m_run = -INFINITY, l_run = 0.0f;
     floatx4 o[16];
 #pragma unroll
     for (int32_t db = 0; db < 16; ++db) {
         o[db] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    for (int32_t k = 0; k < cnt; k += 2) {
-        const int32_t base0 = (t0 + wave + kWaves * k) * kTile;
-        if (k + 1 < cnt) {
-            issue_tile<SP>(a, s, rk, rv, base0 + kWaves * kTile, kb, vb1, lane);
-            tile_step<true>(ka, qb, vb0, base0, s.n, m_run, l_run, o, lane);
-        } else {
-            tile_step<false>(ka, qb, vb0, base0, s.n, m_run, l_run, o, lane);
-            break;
+    if (cnt > 0) {
+        k_tile ka, kb;
+        issue_tile<SP>(a, s, rk, rv, tile_base(0), ka, vb0, lane);
+        int32_t k = 0;
+        for (; k + 1 < cnt; k += 2) {
+            tile_step<SP, true>(a, s, rk, rv, ka, kb, vb0, vb1, tile_base(k), tile_base(k + 1), qb, m_run, l_run, o,
+                                lane);
+            tile_step<SP, true>(a, s, rk, rv, kb, ka, vb1, vb0, tile_base(k + 1), tile_base(k + 2), qb, m_run, l_run,
+                                o, lane);
         }
-        const int32_t base1 = base0 + kWaves * kTile;
-        if (k + 2 < cnt) {
-            issue_tile<SP>(a, s, rk, rv, base1 + kWaves * kTile, ka, vb0, lane);
-            tile_step<true>(kb, qb, vb1, base1, s.n, m_run, l_run, o, lane);
-        } else {
-            tile_step<false>(kb, qb, vb1, base1, s.n, m_run, l_run, o, lane);
+        if (k < cnt) {
+            tile_step<SP, false>(a, s, rk, rv, ka, kb, vb0, vb1, tile_base(k), 0, qb, m_run, l_run, o, lane);
         }
+        wait_vmcnt<0>(); // the last (empty) copies land before the fold below reuses the buffers
     }
+    DATC_STAMP(b, 2);
     // fold the waves: M, the waves' weights, then O summed in wave order
-    float * ml = reinterpret_cast<float *>(smem + kWaves * kWaveLds);
+    float * ml = reinterpret_cast<float *>(smem + kMlLds); // a wave still in its last step owns its V buffer
     if (lane < 16) {
         ml[wave * 16 + lane] = m_run;
         ml[kWaves * 16 + wave * 16 + lane] = l_run;
@@ -389,50 +461,66 @@ template <bool SP> __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend
         part[kHeads * kD + d] = Mh;
         part[kHeads * kD + kHeads + d] = L;
     }
+    DATC_STAMP(b, 3);
 }
 
 // the fold of (head h, values 32 r .. 32 r + 31): the active partials in workgroup order, the gate, the F32 output and
 // its activation-format run (fn/kernels/act/act_warp.cuh:12-20's rule: amax, d = amax / 127, id = 127 / amax,
-// q = round-to-even of x id clamped to +-127 (NaN: 0), s = d * sum q)
+// q = round-to-even of x id clamped to +-127 (NaN: 0), s = d * sum q). Thread t takes partials t / 32 + 8 i of value
+// t % 32 and issues all its loads before the reductions that weigh them.
 template <bool SP> __global__ __launch_bounds__(256) void datc_fold_kernel(fnkv_datc_attend_args a) {
+    constexpr int32_t kPer = kGrid / 8;
     __shared__ float w_of[kGrid];
-    __shared__ float red[256];
+    __shared__ float wred[2][4];
     __shared__ float accs[8][32];
     const datc_shape s = datc_shape_of<SP>(a);
     if (!s.valid) {
         return;
     }
     const int32_t h = static_cast<int32_t>(blockIdx.x) / 8, r = static_cast<int32_t>(blockIdx.x) % 8;
-    const int32_t t = static_cast<int32_t>(threadIdx.x);
-    const float * part = reinterpret_cast<const float *>(a.part);
-    const float m_t = t < s.active ? part[static_cast<int64_t>(t) * kPartFloats + kHeads * kD + h] : -INFINITY;
-    const float l_t = t < s.active ? part[static_cast<int64_t>(t) * kPartFloats + kHeads * kD + kHeads + h] : 0.0f;
-    red[t] = m_t;
-    __syncthreads();
-    for (int32_t o = 128; o > 0; o >>= 1) {
-        if (t < o) {
-            red[t] = fmaxf(red[t], red[t + o]);
-        }
-        __syncthreads();
-    }
-    const float M = red[0];
-    __syncthreads();
-    const float wt = t < s.active ? expf(m_t - M) : 0.0f;
-    w_of[t] = wt;
-    red[t] = l_t * wt;
-    __syncthreads();
-    for (int32_t o = 128; o > 0; o >>= 1) {
-        if (t < o) {
-            red[t] += red[t + o];
-        }
-        __syncthreads();
-    }
-    const float L = red[0];
+    const int32_t t = static_cast<int32_t>(threadIdx.x), wave = t / 64;
+#ifdef FNKV_TIMING
+    uint64_t * ts = g_datc_ts;
+#endif
+    DATC_STAMP(256 + blockIdx.x, 0);
     const int32_t grp = t / 32, dl = t % 32;
     const int32_t dd = h * kD + 32 * r + dl;
+    const float * part = reinterpret_cast<const float *>(a.part);
+    float ov[kPer];
+#pragma unroll
+    for (int32_t i = 0; i < kPer; ++i) {
+        const int32_t c = grp + 8 * i;
+        ov[i] = c < s.active ? part[static_cast<int64_t>(c) * kPartFloats + dd] : 0.0f;
+    }
+    const float m_t = t < s.active ? part[static_cast<int64_t>(t) * kPartFloats + kHeads * kD + h] : -INFINITY;
+    const float l_t = t < s.active ? part[static_cast<int64_t>(t) * kPartFloats + kHeads * kD + kHeads + h] : 0.0f;
+    const float gate = t < 32 ? a.qfull[h * kQS + kD + 32 * r + dl] : 0.0f;
+    float mx = m_t;
+#pragma unroll
+    for (int32_t o = 32; o > 0; o >>= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    }
+    if ((t & 63) == 0) {
+        wred[0][wave] = mx;
+    }
+    __syncthreads();
+    const float M = fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3]));
+    const float wt = t < s.active ? expf(m_t - M) : 0.0f;
+    w_of[t] = wt;
+    float lw = l_t * wt;
+#pragma unroll
+    for (int32_t o = 32; o > 0; o >>= 1) {
+        lw += __shfl_xor(lw, o, 64);
+    }
+    if ((t & 63) == 0) {
+        wred[1][wave] = lw;
+    }
+    __syncthreads();
+    const float L = (wred[1][0] + wred[1][1]) + (wred[1][2] + wred[1][3]);
     float acc = 0.0f;
-    for (int32_t c = grp; c < s.active; c += 8) {
-        acc = __builtin_fmaf(part[static_cast<int64_t>(c) * kPartFloats + dd], w_of[c], acc);
+#pragma unroll
+    for (int32_t i = 0; i < kPer; ++i) {
+        acc = __builtin_fmaf(ov[i], w_of[grp + 8 * i], acc);
     }
     accs[grp][dl] = acc;
     __syncthreads();
@@ -441,7 +529,6 @@ template <bool SP> __global__ __launch_bounds__(256) void datc_fold_kernel(fnkv_
     }
     const float A = ((accs[0][dl] + accs[1][dl]) + (accs[2][dl] + accs[3][dl])) +
                     ((accs[4][dl] + accs[5][dl]) + (accs[6][dl] + accs[7][dl]));
-    const float gate = a.qfull[h * kQS + kD + 32 * r + dl];
     const float y = A / L * (1.0f / (1.0f + expf(-gate)));
     a.out[dd] = y;
     float amax = fabsf(y);
@@ -463,6 +550,7 @@ template <bool SP> __global__ __launch_bounds__(256) void datc_fold_kernel(fnkv_
         a.scales[2 * (h * 8 + r)] = dsc;
         a.scales[2 * (h * 8 + r) + 1] = dsc * static_cast<float>(sum);
     }
+    DATC_STAMP(256 + blockIdx.x, 1);
 }
 
 bool aligned(const void * p, uintptr_t n) {
@@ -496,6 +584,13 @@ int fnkv_datc_prepare(int32_t rows, const fnkv_datc_prepare_args * a, void * str
         set_error("fnkv_datc_prepare: argument outside the contract");
         return FNKV_ERR_ARG;
     }
+#ifdef FNKV_TIMING
+    {
+        uint64_t * tb = fnkv::timing_buffer();
+        (void)hipMemcpyToSymbolAsync(HIP_SYMBOL(fnkv::g_datc_ts), &tb, sizeof(tb), 0, hipMemcpyHostToDevice,
+                                     static_cast<hipStream_t>(stream));
+    }
+#endif
     hipLaunchKernelGGL(fnkv::datc_prepare_kernel, dim3(static_cast<uint32_t>(rows)), dim3(64 * (fnkv::kHeads + 1)), 0,
                        static_cast<hipStream_t>(stream), *a, rows);
     if (hipGetLastError() != hipSuccess) {
