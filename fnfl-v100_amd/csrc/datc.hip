@@ -473,10 +473,6 @@ template <bool SP> __global__ __launch_bounds__(256) void datc_fold_kernel(fnkv_
     __shared__ float w_of[kGrid];
     __shared__ float wred[2][4];
     __shared__ float accs[8][32];
-    const datc_shape s = datc_shape_of<SP>(a);
-    if (!s.valid) {
-        return;
-    }
     const int32_t h = static_cast<int32_t>(blockIdx.x) / 8, r = static_cast<int32_t>(blockIdx.x) % 8;
     const int32_t t = static_cast<int32_t>(threadIdx.x), wave = t / 64;
 #ifdef FNKV_TIMING
@@ -486,15 +482,22 @@ template <bool SP> __global__ __launch_bounds__(256) void datc_fold_kernel(fnkv_
     const int32_t grp = t / 32, dl = t % 32;
     const int32_t dd = h * kD + 32 * r + dl;
     const float * part = reinterpret_cast<const float *>(a.part);
+    // every partial's values are loaded before the depth word is known; those past the active workgroups (stale,
+    // possibly not finite) are dropped by selection, never weighted
     float ov[kPer];
 #pragma unroll
     for (int32_t i = 0; i < kPer; ++i) {
-        const int32_t c = grp + 8 * i;
-        ov[i] = c < s.active ? part[static_cast<int64_t>(c) * kPartFloats + dd] : 0.0f;
+        ov[i] = part[static_cast<int64_t>(grp + 8 * i) * kPartFloats + dd];
     }
-    const float m_t = t < s.active ? part[static_cast<int64_t>(t) * kPartFloats + kHeads * kD + h] : -INFINITY;
-    const float l_t = t < s.active ? part[static_cast<int64_t>(t) * kPartFloats + kHeads * kD + kHeads + h] : 0.0f;
+    const float m_raw = part[static_cast<int64_t>(t) * kPartFloats + kHeads * kD + h];
+    const float l_raw = part[static_cast<int64_t>(t) * kPartFloats + kHeads * kD + kHeads + h];
     const float gate = t < 32 ? a.qfull[h * kQS + kD + 32 * r + dl] : 0.0f;
+    const datc_shape s = datc_shape_of<SP>(a);
+    if (!s.valid) {
+        return;
+    }
+    const float m_t = t < s.active ? m_raw : -INFINITY;
+    const float l_t = t < s.active ? l_raw : 0.0f;
     float mx = m_t;
 #pragma unroll
     for (int32_t o = 32; o > 0; o >>= 1) {
@@ -520,7 +523,7 @@ template <bool SP> __global__ __launch_bounds__(256) void datc_fold_kernel(fnkv_
     float acc = 0.0f;
 #pragma unroll
     for (int32_t i = 0; i < kPer; ++i) {
-        acc = __builtin_fmaf(ov[i], w_of[grp + 8 * i], acc);
+        acc = grp + 8 * i < s.active ? __builtin_fmaf(ov[i], w_of[grp + 8 * i], acc) : acc;
     }
     accs[grp][dl] = acc;
     __syncthreads();
