@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libfnkv.so")
-SOURCES = ["pool.hip", "append.hip", "decode.hip", "prefill.hip", "sparse.hip", "datc.hip"]
+SOURCES = ["pool.hip", "append.hip", "decode.hip", "prefill.hip", "sparse.hip", "datc.hip", "qsa.hip"]
 ARCH = os.environ.get("FNKV_ARCH", "gfx950")
 
 COMMON = [

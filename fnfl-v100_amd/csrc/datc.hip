@@ -26,6 +26,7 @@
 #include "../../include/fnkv.h"
 #include "common.h"
 #include "mfma.h"
+#include "rope.h"
 
 #include <hip/hip_runtime.h>
 
@@ -39,8 +40,6 @@ namespace {
 constexpr int32_t kHeads = FNKV_DATC_HEADS;
 constexpr int32_t kD = 256;
 constexpr int32_t kQS = FNKV_DATC_QSTRIDE;
-constexpr int32_t kNRot = 64;           // rotated dimensions (fn/kernels/qsa/qsa.h n_rot)
-constexpr float kRmsEps = 1e-6f;        // fn/model/shapes.h:35 rms_eps
 constexpr int32_t kGrid = 256;          // attention workgroups
 constexpr int32_t kWaves = 4;
 constexpr int32_t kTile = 32;           // cells a wave's step
@@ -75,61 +74,6 @@ namespace {
 #endif
 
 // ---- prepare ----
-
-// The F32 rms norm and IMROPE of one 256-wide row (pinned by the reference as build_norm LLM_NORM_RMS, then
-// ggml_rope_multi with GGML_ROPE_TYPE_IMROPE; fn/kernels/qsa/attend.cu:151-198, imrope.cuh:14-20). A lane holds dims
-// 4 lane .. 4 lane + 3. Rotation pair i (< 32) is dims i and i + 32; its angle is its plane's position times
-// theta_scale^i as the F32 product chain, the plane picked by the sector rule (sections 11, 11, 10, 0).
-__device__ __forceinline__ void norm_rope(float (&y)[4], const float * src, const float * w, const int32_t * pos,
-                                          int32_t stride, int32_t col, float ts, int32_t lane) {
-    const float4 x = reinterpret_cast<const float4 *>(src)[lane];
-    float ss = x.x * x.x;
-    ss = __builtin_fmaf(x.y, x.y, ss);
-    ss = __builtin_fmaf(x.z, x.z, ss);
-    ss = __builtin_fmaf(x.w, x.w, ss);
-#pragma unroll
-    for (int32_t o = 32; o > 0; o >>= 1) {
-        ss += __shfl_xor(ss, o, 64);
-    }
-    const float r = 1.0f / sqrtf(ss * (1.0f / kD) + kRmsEps);
-    const float4 g = reinterpret_cast<const float4 *>(w)[lane];
-    y[0] = x.x * r * g.x;
-    y[1] = x.y * r * g.y;
-    y[2] = x.z * r * g.z;
-    y[3] = x.w * r * g.w;
-    // lane i < 32 forms pair i's angle
-    const int32_t sector = lane & 31;
-    const int32_t plane = sector % 3 == 1 && sector < 33   ? 1
-                          : sector % 3 == 2 && sector < 30 ? 2
-                          : sector % 3 == 0 && sector < 33 ? 0
-                                                           : 3;
-    float theta = static_cast<float>(pos[plane * stride + col]);
-#pragma unroll
-    for (int32_t i = 0; i < kNRot / 2 - 1; ++i) {
-        theta = i < sector ? theta * ts : theta;
-    }
-    float s = 0.0f, c = 0.0f;
-    sincosf(theta, &s, &c);
-    // dims 0..31 sit in lanes 0..7, their partners 32..63 in lanes 8..15
-#pragma unroll
-    for (int32_t e = 0; e < 4; ++e) {
-        const int32_t pair = 4 * (lane & 7) + e;
-        const float ce = __shfl(c, pair, 64);
-        const float se = __shfl(s, pair, 64);
-        const float other = __shfl_xor(y[e], 8, 64);
-        if (lane < 8) {
-            y[e] = y[e] * ce - other * se;
-        } else if (lane < 16) {
-            y[e] = other * se + y[e] * ce;
-        }
-    }
-}
-
-__device__ __forceinline__ uint2 pack4_f16(const float (&x)[4], float scale) {
-    half2v a{static_cast<_Float16>(x[0] * scale), static_cast<_Float16>(x[1] * scale)};
-    half2v b{static_cast<_Float16>(x[2] * scale), static_cast<_Float16>(x[3] * scale)};
-    return make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
-}
 
 __global__ __launch_bounds__(64 * (kHeads + 1)) void datc_prepare_kernel(fnkv_datc_prepare_args a, int32_t rows) {
     const int32_t wave = static_cast<int32_t>(threadIdx.x) / 64, lane = static_cast<int32_t>(threadIdx.x) % 64;
@@ -465,9 +409,8 @@ template <bool SP> __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend
 }
 
 // the fold of (head h, values 32 r .. 32 r + 31): the active partials in workgroup order, the gate, the F32 output and
-// its activation-format run (fn/kernels/act/act_warp.cuh:12-20's rule: amax, d = amax / 127, id = 127 / amax,
-// q = round-to-even of x id clamped to +-127 (NaN: 0), s = d * sum q). Thread t takes partials t / 32 + 8 i of value
-// t % 32 and issues all its loads before the reductions that weigh them.
+// its activation-format run (act_run). Thread t takes partials t / 32 + 8 i of value t % 32 and issues all its loads
+// before the reductions that weigh them.
 template <bool SP> __global__ __launch_bounds__(256) void datc_fold_kernel(fnkv_datc_attend_args a) {
     constexpr int32_t kPer = kGrid / 8;
     __shared__ float w_of[kGrid];
@@ -534,24 +477,14 @@ template <bool SP> __global__ __launch_bounds__(256) void datc_fold_kernel(fnkv_
                     ((accs[4][dl] + accs[5][dl]) + (accs[6][dl] + accs[7][dl]));
     const float y = A / L * (1.0f / (1.0f + expf(-gate)));
     a.out[dd] = y;
-    float amax = fabsf(y);
-#pragma unroll
-    for (int32_t o = 16; o > 0; o >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    }
-    const float dsc = amax / 127.0f;
-    const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
-    const float e = y * id;
-    const int32_t q = e != e ? 0 : static_cast<int32_t>(fminf(fmaxf(__builtin_rintf(e), -127.0f), 127.0f));
-    int32_t sum = q;
-#pragma unroll
-    for (int32_t o = 16; o > 0; o >>= 1) {
-        sum += __shfl_xor(sum, o, 64);
-    }
-    a.codes[dd] = static_cast<int8_t>(q);
+    const float yv[1] = {y};
+    int8_t qv[1];
+    float ds[2];
+    act_run<1, 32>(yv, qv, ds);
+    a.codes[dd] = qv[0];
     if (dl == 0) {
-        a.scales[2 * (h * 8 + r)] = dsc;
-        a.scales[2 * (h * 8 + r) + 1] = dsc * static_cast<float>(sum);
+        a.scales[2 * (h * 8 + r)] = ds[0];
+        a.scales[2 * (h * 8 + r) + 1] = ds[1];
     }
     DATC_STAMP(256 + blockIdx.x, 1);
 }

@@ -27,6 +27,7 @@
 #include "mfma.h"
 #include "q8_0.h"
 #include "decode_common.h"
+#include "rope.h"
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -830,7 +831,30 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
             Ls = __builtin_fmaf(sL[i], w, Ls);
         }
         const int32_t t = r / a.G, h = kvh * a.G + r % a.G;
-        uint16_t * o = a.out + ((int64_t(s) * a.T + t) * a.hq + h) * kHeadDim + chunk * 32 + tid * 4;
+        const int64_t row = (int64_t(s) * a.T + t) * a.hq + h;
+        if (a.out_f32 != nullptr) {
+            // the gate, the F32 output and its activation run (the run's 32 values are lanes 0..7's)
+            const float * gr = a.gate + row * a.gate_stride + chunk * 32 + tid * 4;
+            float y[4];
+#pragma unroll
+            for (int32_t e = 0; e < 4; ++e) {
+                y[e] = As[e] / Ls * (1.0f / (1.0f + expf(-gr[e])));
+            }
+            *reinterpret_cast<float4 *>(a.out_f32 + row * kHeadDim + chunk * 32 + tid * 4) =
+                make_float4(y[0], y[1], y[2], y[3]);
+            int8_t q[4];
+            float ds[2];
+            act_run<4, 8>(y, q, ds);
+            *reinterpret_cast<uint32_t *>(a.codes + row * kHeadDim + chunk * 32 + tid * 4) =
+                uint32_t(uint8_t(q[0])) | (uint32_t(uint8_t(q[1])) << 8) | (uint32_t(uint8_t(q[2])) << 16) |
+                (uint32_t(uint8_t(q[3])) << 24);
+            if (tid == 0) {
+                a.act_scales[(row * 8 + chunk) * 2] = ds[0];
+                a.act_scales[(row * 8 + chunk) * 2 + 1] = ds[1];
+            }
+            return;
+        }
+        uint16_t * o = a.out + row * kHeadDim + chunk * 32 + tid * 4;
         const float inv = 1.0f / Ls;
         uint2 pk;
         pk.x = uint32_t(__half_as_ushort(__float2half_rn(As[0] * inv))) |

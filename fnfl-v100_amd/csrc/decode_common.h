@@ -356,12 +356,32 @@ struct merge_args {
     int32_t split0[FNKV_MAX_SEQS + 1];
     const int32_t * sel_n;
     int32_t sel_split;
+    // the gated form (fn/kernels/qsa/attend.cu:619-655's finish): with out_f32 set, row (t, h)'s value d is written as
+    // o / (1 + exp(-gate[(t hq + h) gate_stride + d])) in F32 [T][hq][256] with its int8 activation format (codes
+    // [T][hq 256], act_scales [T][hq 8][2]) instead of the fp16 out
+    const float * gate = nullptr;
+    int32_t gate_stride = 0;
+    float * out_f32 = nullptr;
+    int8_t * codes = nullptr;
+    float * act_scales = nullptr;
 };
 
 class kv_pool;
 // host: the merge launch, and the sparse instantiation of the decode kernels (decode.hip)
 void launch_merge(const merge_args & m, hipStream_t st);
 void launch_decode_sparse(const kv_pool & p, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st);
+// host: a sparse launch over the pool (sparse.hip), optionally with the gated merge (merge_args' gated form)
+struct sparse_gate {
+    const float * gate;
+    int32_t stride;
+    float * out_f32;
+    int8_t * codes;
+    float * scales;
+};
+int sparse_launch(const kv_pool * p, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq, float scale,
+                  const void * q, const void * body, const void * offsets, const void * k_new, const void * v_new,
+                  int32_t new_dtype, void * out, const sparse_gate * gate, void * ws, int64_t ws_bytes,
+                  hipStream_t st, const char * who);
 
 __device__ __forceinline__ int32_t seq_of(const dec_args & a, int32_t split) {
     int32_t s = 0;

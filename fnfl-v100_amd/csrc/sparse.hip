@@ -53,55 +53,46 @@ sparse_plan plan_sparse(const kv_pool & p, int64_t depth, int32_t T, int32_t R) 
     return pl;
 }
 
-} // namespace fnkv
 
-using fnkv::set_error;
-
-extern "C" {
-
-int64_t fnkv_sparse_workspace_bytes(const fnkv_pool * pool, int64_t depth, int32_t T, int32_t hq) {
-    const fnkv::kv_pool * p = fnkv::pool_of(pool);
-    if (p == nullptr || T <= 0 || T > fnkv::kSelMaxRows || depth < 0 || hq <= 0 || hq % p->h_kv() != 0) {
-        return -1;
-    }
-    return fnkv::plan_sparse(*p, depth, T, (hq / p->h_kv()) * T).bytes;
-}
-
-int fnkv_attn_sparse(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq,
-                     float scale, const void * q, const void * body, const void * offsets, const void * k_new,
-                     const void * v_new, int32_t new_dtype, void * out, void * ws, int64_t ws_bytes, void * stream) {
-    const fnkv::kv_pool * p = fnkv::pool_of(pool);
-    if (p == nullptr || slot < 0 || slot >= p->pages().n_slots() || T <= 0 || T > fnkv::kSelMaxRows || depth < 0 ||
+// The sparse launch (validation, the decode kernels' sparse instantiation, the merge); `gate` set: the merge writes
+// the gated F32 output and its activation format instead of the fp16 out. Returns a status; nothing is enqueued
+// unless it is FNKV_OK.
+int sparse_launch(const kv_pool * p, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq, float scale,
+                  const void * q, const void * body, const void * offsets, const void * k_new, const void * v_new,
+                  int32_t new_dtype, void * out, const sparse_gate * gate, void * ws, int64_t ws_bytes,
+                  hipStream_t st, const char * who) {
+    const std::string name(who);
+    if (p == nullptr || slot < 0 || slot >= p->pages().n_slots() || T <= 0 || T > kSelMaxRows || depth < 0 ||
         layer < 0 || layer >= p->layers() || hq <= 0 || hq % p->h_kv() != 0 || q == nullptr || body == nullptr ||
-        offsets == nullptr || out == nullptr || ws == nullptr || !(scale > 0.0f) || !std::isfinite(scale) ||
-        ((k_new == nullptr) != (v_new == nullptr)) || (new_dtype != FNKV_F16 && new_dtype != FNKV_F32)) {
-        set_error("fnkv_attn_sparse: argument outside the contract");
+        offsets == nullptr || (out == nullptr && gate == nullptr) || ws == nullptr || !(scale > 0.0f) ||
+        !std::isfinite(scale) || ((k_new == nullptr) != (v_new == nullptr)) ||
+        (new_dtype != FNKV_F16 && new_dtype != FNKV_F32)) {
+        set_error(name + ": argument outside the contract");
         return FNKV_ERR_ARG;
     }
     const int32_t G = hq / p->h_kv();
     const int32_t R = G * T;
     const int64_t ctx = depth + T;
-    if (R > FNKV_MAX_ROWS || ctx > fnkv::kSelMaxCells || ctx > p->mapped_cells(slot)) {
-        set_error("fnkv_attn_sparse: G * T = " + std::to_string(R) + " (at most " + std::to_string(FNKV_MAX_ROWS) +
+    if (R > FNKV_MAX_ROWS || ctx > kSelMaxCells || ctx > p->mapped_cells(slot)) {
+        set_error(name + ": G * T = " + std::to_string(R) + " (at most " + std::to_string(FNKV_MAX_ROWS) +
                   ") or cells " + std::to_string(ctx) + " outside the slot's mapped cells (at most " +
-                  std::to_string(fnkv::kSelMaxCells) + ")");
+                  std::to_string(kSelMaxCells) + ")");
         return FNKV_ERR_ARG;
     }
     if ((reinterpret_cast<uintptr_t>(q) & 15) != 0 || (reinterpret_cast<uintptr_t>(out) & 15) != 0 ||
         (reinterpret_cast<uintptr_t>(ws) & 15) != 0 || (reinterpret_cast<uintptr_t>(body) & 3) != 0 ||
         (reinterpret_cast<uintptr_t>(offsets) & 3) != 0) {
-        set_error("fnkv_attn_sparse: q, out and ws must be 16-byte aligned, body and offsets 4-byte aligned");
+        set_error(name + ": q, out and ws must be 16-byte aligned, body and offsets 4-byte aligned");
         return FNKV_ERR_ARG;
     }
-    const fnkv::sparse_plan pl = fnkv::plan_sparse(*p, depth, T, R);
+    const sparse_plan pl = plan_sparse(*p, depth, T, R);
     if (ws_bytes < pl.bytes) {
-        set_error("fnkv_attn_sparse: workspace too small (fnkv_sparse_workspace_bytes)");
+        set_error(name + ": workspace too small");
         return FNKV_ERR_ARG;
     }
     uint8_t * w = static_cast<uint8_t *>(ws);
-    hipStream_t st = static_cast<hipStream_t>(stream);
 
-    fnkv::dec_args a;
+    dec_args a;
     a.pv = p->view();
     a.q = static_cast<const uint16_t *>(q);
     a.k_new = k_new; // written by the workgroups that read them (split 0 when no row selects them)
@@ -129,11 +120,11 @@ int fnkv_attn_sparse(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_
     a.sel_n = reinterpret_cast<int32_t *>(w);
     a.sel_split = pl.per_split;
 #ifdef FNKV_TIMING
-    a.ts = fnkv::timing_buffer();
+    a.ts = timing_buffer();
 #endif
-    fnkv::launch_decode_sparse(*p, (R + 15) / 16, dim3(static_cast<uint32_t>(pl.n_splits),
-                                                        static_cast<uint32_t>(p->h_kv())), a, st);
-    fnkv::merge_args m;
+    launch_decode_sparse(*p, (R + 15) / 16, dim3(static_cast<uint32_t>(pl.n_splits), static_cast<uint32_t>(p->h_kv())),
+                         a, st);
+    merge_args m;
     m.po = a.po;
     m.pml = a.pml;
     m.out = static_cast<uint16_t *>(out);
@@ -148,12 +139,41 @@ int fnkv_attn_sparse(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_
     }
     m.sel_n = a.sel_n;
     m.sel_split = pl.per_split;
-    fnkv::launch_merge(m, st);
+    if (gate != nullptr) {
+        m.gate = gate->gate;
+        m.gate_stride = gate->stride;
+        m.out_f32 = gate->out_f32;
+        m.codes = gate->codes;
+        m.act_scales = gate->scales;
+    }
+    launch_merge(m, st);
     if (hipGetLastError() != hipSuccess) {
-        set_error("fnkv_attn_sparse: launch failed");
+        set_error(name + ": launch failed");
         return FNKV_ERR_HIP;
     }
     return FNKV_OK;
+}
+
+} // namespace fnkv
+
+using fnkv::set_error;
+
+extern "C" {
+
+int64_t fnkv_sparse_workspace_bytes(const fnkv_pool * pool, int64_t depth, int32_t T, int32_t hq) {
+    const fnkv::kv_pool * p = fnkv::pool_of(pool);
+    if (p == nullptr || T <= 0 || T > fnkv::kSelMaxRows || depth < 0 || hq <= 0 || hq % p->h_kv() != 0) {
+        return -1;
+    }
+    return fnkv::plan_sparse(*p, depth, T, (hq / p->h_kv()) * T).bytes;
+}
+
+int fnkv_attn_sparse(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq,
+                     float scale, const void * q, const void * body, const void * offsets, const void * k_new,
+                     const void * v_new, int32_t new_dtype, void * out, void * ws, int64_t ws_bytes, void * stream) {
+    return fnkv::sparse_launch(fnkv::pool_of(pool), slot, depth, T, layer, hq, scale, q, body, offsets, k_new, v_new,
+                               new_dtype, out, nullptr, ws, ws_bytes, static_cast<hipStream_t>(stream),
+                               "fnkv_attn_sparse");
 }
 
 } // extern "C"

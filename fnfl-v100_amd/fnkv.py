@@ -23,7 +23,7 @@ EXPORTS = [
     "fnkv_export_q8_0", "fnkv_decode_workspace_bytes", "fnkv_attn_decode", "fnkv_prefill_workspace_bytes",
     "fnkv_attn_prefill", "fnkv_pool_create_fmt", "fnkv_pool_format", "fnkv_export_kv8",
     "fnkv_sparse_workspace_bytes", "fnkv_attn_sparse", "fnkv_rope_theta_scale", "fnkv_datc_part_bytes",
-    "fnkv_datc_prepare", "fnkv_datc_attend",
+    "fnkv_datc_prepare", "fnkv_datc_attend", "fnkv_qsa_workspace_bytes", "fnkv_qsa_attend",
 ]
 DATC_HEADS = 12
 DATC_QSTRIDE = 512
@@ -118,6 +118,11 @@ def lib():
         L.fnkv_prefill_workspace_bytes.argtypes = [P, I64, I32, I32]
         L.fnkv_attn_prefill.restype = ctypes.c_int
         L.fnkv_attn_prefill.argtypes = [P, I32, I32, I64, I32, I32, ctypes.c_float, P, P, P, I64, P]
+        L.fnkv_qsa_workspace_bytes.restype = I64
+        L.fnkv_qsa_workspace_bytes.argtypes = [P, I64, I32, I32]
+        L.fnkv_qsa_attend.restype = ctypes.c_int
+        L.fnkv_qsa_attend.argtypes = [P, I32, I64, I32, I32, I32, P, P, P, P, P, P, ctypes.c_float, P, P, P, P, P, P,
+                                      P, P, I64, P]
         L.fnkv_rope_theta_scale.restype = ctypes.c_float
         L.fnkv_rope_theta_scale.argtypes = []
         L.fnkv_datc_part_bytes.restype = I64
@@ -293,6 +298,23 @@ class Pool:
                                             P(body.data_ptr()), P(offsets.data_ptr()), kp, vp, dt,
                                             P(out.data_ptr()), P(ws.data_ptr()), ws.numel() * ws.element_size(),
                                             _stream(stream)))
+
+    def qsa_ws_bytes(self, depth, T, hq):
+        return lib().fnkv_qsa_workspace_bytes(self.h, depth, T, hq)
+
+    def qsa_attend(self, slot, depth, layer, qfull, kv_k, kv_v, q_norm, k_norm, pos, body, offsets, out, codes,
+                   scales, q_f32=None, k_f32=None, theta_scale=None, ws=None, stream=None):
+        """attn::attend over the pool: qfull F32 [T][hq][512], kv_k / kv_v F32 [T][h_kv][256], pos int32 [4][T],
+        body / offsets as for sparse(); out F32 [T][hq][256], codes int8 [T][hq * 256], scales F32 [T][hq * 8][2]."""
+        import torch
+        T, hq = qfull.shape[0], qfull.shape[1]
+        if ws is None:
+            ws = torch.empty(max(16, self.qsa_ws_bytes(depth, T, hq)), dtype=torch.uint8, device=qfull.device)
+        ts = rope_theta_scale() if theta_scale is None else theta_scale
+        return check(lib().fnkv_qsa_attend(self.h, slot, depth, T, layer, hq, _p(qfull), _p(kv_k), _p(kv_v),
+                                           _p(q_norm), _p(k_norm), _p(pos), ts, _p(body), _p(offsets), _p(out),
+                                           _p(codes), _p(scales), _p(q_f32), _p(k_f32), _p(ws),
+                                           ws.numel() * ws.element_size(), _stream(stream)))
 
     def prefill_ws_bytes(self, ctx, rows, hq):
         return lib().fnkv_prefill_workspace_bytes(self.h, ctx, rows, hq)

@@ -162,6 +162,28 @@ int fnkv_attn_sparse(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_
                      float scale, const void * q, const void * body, const void * offsets, const void * k_new,
                      const void * v_new, int32_t new_dtype, void * out, void * ws, int64_t ws_bytes, void * stream);
 
+/* ---- the reference's decode attention with its prepare and gate (fn/kernels/qsa/attend.h:57-141 attn::attend) ---- */
+
+/* The workspace of fnkv_qsa_attend at this depth (bytes; no zeroing needed); -1 outside the contract. */
+int64_t fnkv_qsa_workspace_bytes(const fnkv_pool * pool, int64_t depth, int32_t T, int32_t hq);
+
+/* attn::attend (attend.h:97-141, args :57-91) over the pool, for T (1..5) rows of the sequence in `slot`, row t at
+ * position depth + t: each row's query heads and its new cell's k get the F32 RMS norm (eps 1e-6) and IMROPE
+ * (attend.cu:151-198; positions pos, device I32 [4][T], plane p of row t at pos[p T + t]; theta_scale
+ * fnkv_rope_theta_scale()), the new cells' K (normed, roped) and V are written into the pool at depth .. depth + T - 1
+ * in its format, each row attends over its selection body (as fnkv_attn_sparse; scores q . k / 16 with q as fp16),
+ * and each (row, head) is finished with its gate: out = o / (1 + exp(-gate)) in F32 with its int8 activation format.
+ * qfull: F32 [T][hq][512] (each head's q, then its gate); kv_k, kv_v: F32 [T][h_kv][256]; q_norm, k_norm: F32 [256];
+ * out: F32 [T][hq][256]; codes: int8 [T][hq 256]; scales: F32 [T][hq 8][2]; q_f32, k_f32 (optional): the F32 q
+ * [T][hq][256] and k [T][h_kv][256] after the norm and rope. Launches in stream order: the prepare, then per group
+ * of rows with (hq / h_kv) x rows <= FNKV_MAX_ROWS the attention and the gated merge (the reference's card, 12 query
+ * heads on one KV head, runs 5 rows as 4 + 1). */
+int fnkv_qsa_attend(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq,
+                    const float * qfull, const float * kv_k, const float * kv_v, const float * q_norm,
+                    const float * k_norm, const int32_t * pos, float theta_scale, const void * body,
+                    const void * offsets, float * out, int8_t * codes, float * scales, float * q_f32, float * k_f32,
+                    void * ws, int64_t ws_bytes, void * stream);
+
 /* ---- chunked-prefill attention (fn/kernels/qsa/qsa_prompt.h:106-124 qsp_attend) ---- */
 
 /* the workspace a prefill launch of this shape uses (bytes; 0: none; -1: a shape outside the contract) */
