@@ -48,6 +48,12 @@ CONFIGS = {
                           "(random, rows disjoint: the reference's QA2 shape), 12 layers"),
     "qsa1": dict(depth=196608 - 1, T=1, layers=12, sparse=True,
                  workload="qsa1: sparse (QSA) attention, 1 row at 196,608 cells over 512 blocks + tail, 12 layers"),
+    "qa2b3": dict(depth=196608 - 3, T=3, layers=12, attend=True,
+                  workload="qa2b3: attn::attend over the Q8_0 pool at the reference's QA2 shape: 12 query heads on one "
+                           "KV head, 3 rows at 196,608 cells, each over its own 512 blocks + tail, prepare (norm, IMROPE) "
+                           "and gate included, 12 layers"),
+    "qa2b1": dict(depth=196608 - 1, T=1, layers=12, attend=True,
+                  workload="qa2b1: the same with 1 row"),
     "datc": dict(cells=196608, datc=True,
                  workload="datc: DA-TC draft step row (prepare with q, dense attention, gate) at 196,608 cells of F16 "
                           "K/V, 12 query heads, the reference's deepest draft-bench point"),
@@ -72,9 +78,9 @@ def algorithmic_bytes(ctxs, T):
     return kv_read + qo + append
 
 
-def make_pool(torch, fnkv, cases, ctxs, T, layers, seed):
+def make_pool(torch, fnkv, cases, ctxs, T, layers, seed, h_kv=HKV):
     n_pages = sum(-(-c // 256) for c in ctxs) + 16
-    pool = fnkv.Pool(len(ctxs) + 1, n_pages, layers, HKV)
+    pool = fnkv.Pool(len(ctxs) + 1, n_pages, layers, h_kv)
     slots = list(range(len(ctxs)))
     cases.scatter_ensure(pool, slots, ctxs, seed, churn=0.2)
     g = torch.Generator(device="cuda")
@@ -83,7 +89,7 @@ def make_pool(torch, fnkv, cases, ctxs, T, layers, seed):
         for s, c in zip(slots, ctxs):
             kv = []
             for _ in range(2):
-                x = torch.randn((c, HKV, D), generator=g, device="cuda", dtype=torch.float32)
+                x = torch.randn((c, h_kv, D), generator=g, device="cuda", dtype=torch.float32)
                 ch = torch.randperm(D, generator=g, device="cuda")[:4]
                 x[:, :, ch] *= 8.0
                 kv.append(x.half())
@@ -423,6 +429,118 @@ def run_sparse(args, cfg):
     pool.close()
 
 
+def run_attend(args, cfg):
+    """fnkv_qsa_attend (attn::attend, fn/kernels/qsa/attend.h:57-141) at the reference's QA2 shape: one step = for
+    each of the 12 layers one call that prepares the rows' q and k (RMS norm, IMROPE), writes the new cells, attends
+    each row over its selection and gates the output (F32 + int8 activation format), captured in a HIP graph. The
+    reference measured its BF16 kernel for this shape at 29.2 us (B = 3) and 22.5 us (B = 1) warm on a V100
+    (attend.h:47-48)."""
+    import numpy as np
+    import torch
+
+    import cases
+    import fnkv
+    import oracle as O
+
+    depth, T, layers = cfg["depth"], cfg["T"], cfg["layers"]
+    hq, h_kv = 12, 1
+    ctx = depth + T
+    torch.cuda.set_device(0)
+    pool, slots = make_pool(torch, fnkv, cases, [ctx], T, layers, args.seed, h_kv=h_kv)
+    bodies, cells = [], []
+    for layer in range(layers):
+        w, o, c = O.qsa_body(depth, T, args.seed + layer)
+        bodies.append((torch.from_numpy(w.view(np.int32)).cuda(), torch.from_numpy(o).cuda()))
+        cells.append(c)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(args.seed + 7)
+    qfull = torch.empty((layers, T, hq, 512), device="cuda").uniform_(-3.0, 3.0, generator=g)
+    kv = torch.empty((layers, 2, T, h_kv, D), device="cuda").uniform_(-2.0, 2.0, generator=g)
+    norms = torch.empty((2, D), device="cuda").uniform_(0.3, 1.8, generator=g)
+    pos = torch.arange(depth, ctx, dtype=torch.int32, device="cuda").repeat(4, 1).contiguous()
+    out = torch.empty((layers, T, hq, D), device="cuda")
+    codes = torch.empty((layers, T, hq * D), dtype=torch.int8, device="cuda")
+    scales = torch.empty((layers, T, hq * 8, 2), device="cuda")
+    ws = torch.empty(pool.qsa_ws_bytes(depth, T, hq), dtype=torch.uint8, device="cuda")
+
+    def step():
+        for layer in range(layers):
+            pool.qsa_attend(0, depth, layer, qfull[layer], kv[layer, 0], kv[layer, 1], norms[0], norms[1], pos,
+                            bodies[layer][0], bodies[layer][1], out[layer], codes[layer], scales[layer], ws=ws)
+
+    step()
+    torch.cuda.synchronize()
+    graph = None
+    if not args.no_graph:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+    run = graph.replay if graph is not None else step
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        run()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = ev0.elapsed_time(ev1) / 1e3
+    assert torch.isfinite(out).all().item(), "non-finite attention output"
+    cell_bytes = h_kv * 2 * (D + 2 * (D // 32))  # K and V of the one KV head: 544 B a cell
+    sel = sum(sum(c.size for c in cl) for cl in cells) / layers
+    bytes_layer = int(sel * cell_bytes + T * hq * 512 * 4 + T * h_kv * D * 4 * 2 + T * hq * D * (4 + 1)
+                      + T * hq * 8 * 8 + T * cell_bytes)
+    launch_s = gpu_s / (args.steps * layers)
+    achieved = bytes_layer / launch_s / 1e9
+    tiles = len(np.unique(np.concatenate([c // 32 for c in cells[0]])))
+    line = {
+        "metric": "attn::attend over the Q8_0 pool at the reference's QA2 shape: tokens/s and us an attend call",
+        "value": round(T * args.steps / wall, 3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0 KV (int8 codes + fp16 scales), fp16 q operand, fp32 prepare / softmax / accumulate / out",
+        "data": "synthetic (seeded N(0,1) K/V with 4 of 256 channels x8; uniform q / k / v / gates / norms; random "
+                "selections)",
+        "config": {"workload": cfg["workload"], "cells": ctx, "rows": T, "layers": layers, "q_heads": hq,
+                   "kv_heads": h_kv, "head_dim": D, "selected_cells_per_layer": int(sel),
+                   "tiles_read_per_layer": tiles, "hip_graph": graph is not None},
+        "roofline": {
+            "kernel": "fnkv_qsa_attend call (qsa_prepare_kernel + decode kernel (sparse) + merge_kernel (gated)), "
+                      "a layer",
+            "bound": "hbm",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "traffic_note": f"whole 17,408 B tiles are read: {tiles} a layer for {int(sel)} selected cells",
+            "bytes_per_launch": bytes_layer,
+            "launch_us": round(launch_s * 1e6, 3),
+            "reference_v100_us": 29.2 if T == 3 else 22.5 if T == 1 else None,
+        },
+    }
+    print(json.dumps(line), flush=True)
+    pool.close()
+
+
 def run_datc(args, cfg):
     """DA-TC's draft step row (fn/kernels/draft/draft.h:47-83): one step = fnkv_datc_prepare (the row's 12 query heads
     and its new cell's K / V) then fnkv_datc_attend (the attention over every cell, the fold, the gate), one HIP graph
@@ -593,6 +711,9 @@ def main():
         return
     if CONFIGS[args.config].get("datc"):
         run_datc(args, CONFIGS[args.config])
+        return
+    if CONFIGS[args.config].get("attend"):
+        run_attend(args, CONFIGS[args.config])
         return
 
     traffic, traffic_detail = None, "skipped (--no-traffic)"

@@ -361,7 +361,8 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
 // the buffers are fixed registers. The Q operands stay in registers at NT = 2 and sit once in LDS at NT = 3. The
 // groups of the second half run half an iteration behind the first (see the loop), so the two waves sharing a SIMD
 // are in different phases.
-template <int NT> struct rows_shape {
+// (two groups a workgroup at NT = 2, two workgroups a CU, measured slower on cfg1: 47.4 against 42.7 us a layer)
+template <int NT, bool SP = false> struct rows_shape {
     static constexpr int GR = NT == 2 ? 4 : 2;                      // tile groups a workgroup
     static constexpr int WAVES = NT * GR;
     static constexpr int SK = NT == 2 ? 3 : 6;                      // K ring slots a group
@@ -379,8 +380,8 @@ template <int NT> struct rows_shape {
 };
 
 template <int NT, bool SP>
-__global__ __launch_bounds__(64 * rows_shape<NT>::WAVES, 1) void decode_rows_kernel(dec_args a) {
-    using SH = rows_shape<NT>;
+__global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_rows_kernel(dec_args a) {
+    using SH = rows_shape<NT, SP>;
     constexpr int GR = SH::GR, WAVES = SH::WAVES, SK = SH::SK, NBM = SH::NBM, CK = SH::CK;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
@@ -866,18 +867,23 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
 }
 
 // LDS of a decode launch: the groups' tile buffers, or the merge's (m, l) and partial rows, whichever is larger
-int32_t decode_lds(int32_t nt) {
+template <int NT, bool SP> int32_t rows_lds() {
+    using SH = rows_shape<NT, SP>;
+    const int32_t ring = SH::GR * SH::GROUP_LDS + SH::Q_LDS;
+    const int32_t merge = SH::GR * NT * 16 * 2 * 4 + SH::GR * NT * 16 * (kHeadDim + 4) * 4;
+    return SP ? std::max(std::max(ring + kSelSlice, merge), kSelLds) : std::max(ring, merge);
+}
+int32_t decode_lds(int32_t nt, bool sp) {
     if (nt == 1) {
         constexpr int32_t waves = dec_shape<1>::WAVES;
         const int32_t tiles = dec_shape<1>::GR * kGroupLds;
         const int32_t merge = waves * 16 * 2 * 4 + waves * 16 * (kHeadDim + 4) * 4;
-        return std::max(std::max(tiles + kSelSlice, merge), kSelLds);
+        return sp ? std::max(std::max(tiles + kSelSlice, merge), kSelLds) : std::max(tiles, merge);
     }
-    const int32_t gr = nt == 2 ? rows_shape<2>::GR : rows_shape<3>::GR;
-    const int32_t ring = gr * (nt == 2 ? rows_shape<2>::GROUP_LDS : rows_shape<3>::GROUP_LDS) +
-                         (nt == 2 ? rows_shape<2>::Q_LDS : rows_shape<3>::Q_LDS);
-    const int32_t merge = gr * nt * 16 * 2 * 4 + gr * nt * 16 * (kHeadDim + 4) * 4;
-    return std::max(std::max(ring + kSelSlice, merge), kSelLds);
+    if (nt == 2) {
+        return sp ? rows_lds<2, true>() : rows_lds<2, false>();
+    }
+    return sp ? rows_lds<3, true>() : rows_lds<3, false>();
 }
 
 int32_t device_cus(int32_t device) {
@@ -957,21 +963,23 @@ template <bool SP> void launch_decode(const kv_pool & p, int32_t NT, dim3 grid, 
         (void)hipGetDevice(&cur);
         (void)hipSetDevice(dev);
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<1, SP>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(1));
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(1, SP));
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<2, SP>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(2));
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(2, SP));
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<3, SP>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3));
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3, SP));
         (void)hipGetLastError();
         (void)hipSetDevice(cur);
         attr_set[dev] = true;
     }
     if (NT == 1) {
-        hipLaunchKernelGGL((decode_kernel<1, SP>), grid, dim3(64 * dec_shape<1>::WAVES), decode_lds(1), st, a);
+        hipLaunchKernelGGL((decode_kernel<1, SP>), grid, dim3(64 * dec_shape<1>::WAVES), decode_lds(1, SP), st, a);
     } else if (NT == 2) {
-        hipLaunchKernelGGL((decode_rows_kernel<2, SP>), grid, dim3(64 * rows_shape<2>::WAVES), decode_lds(2), st, a);
+        hipLaunchKernelGGL((decode_rows_kernel<2, SP>), grid, dim3(64 * rows_shape<2, SP>::WAVES), decode_lds(2, SP),
+                           st, a);
     } else {
-        hipLaunchKernelGGL((decode_rows_kernel<3, SP>), grid, dim3(64 * rows_shape<3>::WAVES), decode_lds(3), st, a);
+        hipLaunchKernelGGL((decode_rows_kernel<3, SP>), grid, dim3(64 * rows_shape<3, SP>::WAVES), decode_lds(3, SP),
+                           st, a);
     }
 }
 
