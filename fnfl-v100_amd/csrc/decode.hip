@@ -151,7 +151,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     if constexpr (SP) {
         append_owned_cells<WAVES>(a, table, kvh, ctx, src.new_mine, wave, lane);
     } else {
-        append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, wave, lane);
+        append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, src.g0, a.strided ? src.stride : 0, wave, lane);
     }
     FNKV_STAMP(1);
     if constexpr (!SP) {
@@ -422,7 +422,7 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
     if constexpr (SP) {
         append_owned_cells<WAVES>(a, table, kvh, ctx, src.new_mine, wave, lane);
     } else {
-        append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, wave, lane);
+        append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, src.g0, a.strided ? src.stride : 0, wave, lane);
     }
     FNKV_STAMP(1);
 
@@ -907,7 +907,7 @@ int32_t device_cus(int32_t device) {
 int32_t choose_split(int32_t n_seq, const int64_t * ctx, int32_t h_kv, int32_t cus) {
     int32_t best = kPageTokens;
     double best_cost = 1e300;
-    for (int32_t st = kPageTokens; st <= 64 * kPageTokens; st *= 2) { // a split's pages fit one wave's lanes
+    for (int32_t st = kPageTokens; st <= 8 * kPageTokens; st *= 2) { // a split's tiles fit one wave's lanes
         int64_t wgs = 0;
         for (int32_t i = 0; i < n_seq; ++i) {
             wgs += (ctx[i] + st - 1) / st;
@@ -925,7 +925,7 @@ int32_t choose_split(int32_t n_seq, const int64_t * ctx, int32_t h_kv, int32_t c
 }
 
 struct dec_plan {
-    int32_t split_tokens = 0, total = 0;
+    int32_t split_tokens = 0, total = 0, strided = 0;
     int32_t split0[FNKV_MAX_SEQS + 1] = {0};
     int64_t po_bytes = 0, pml_bytes = 0;
 };
@@ -933,16 +933,23 @@ struct dec_plan {
 dec_plan plan_decode(const kv_pool & p, int32_t n_seq, const int64_t * ctx, int32_t R) {
     dec_plan pl;
     pl.split_tokens = choose_split(n_seq, ctx, p.h_kv(), device_cus(p.device()));
-    // tuning knob: FNKV_SPLIT_TOKENS (a multiple of 256, at most 16,384) overrides the chosen split size
+    // tuning knob: FNKV_SPLIT_TOKENS (a multiple of 256, at most 2,048) overrides the chosen split size
     if (const char * e = std::getenv("FNKV_SPLIT_TOKENS")) {
         const int32_t v = std::atoi(e);
-        if (v >= kPageTokens && v <= 64 * kPageTokens && v % kPageTokens == 0) {
+        if (v >= kPageTokens && v <= 8 * kPageTokens && v % kPageTokens == 0) {
             pl.split_tokens = v;
         }
     }
     pl.split0[0] = 0;
     for (int32_t i = 0; i < n_seq; ++i) {
         pl.split0[i + 1] = pl.split0[i] + static_cast<int32_t>((ctx[i] + pl.split_tokens - 1) / pl.split_tokens);
+    }
+    // one row tile (R <= 16): the splits of a sequence stride over its tiles, so at any moment the workgroups read
+    // one window of the sequence together (cfg2 T = 1: 56.5 against 57.7 us); the row kernels keep contiguous splits
+    // (T = 3 unchanged, T = 5 5% slower strided). FNKV_STRIDED=0 / 1 overrides, for measurement.
+    pl.strided = R <= 16 ? 1 : 0;
+    if (const char * e = std::getenv("FNKV_STRIDED")) {
+        pl.strided = std::atoi(e) != 0;
     }
     pl.total = pl.split0[n_seq];
     pl.po_bytes = int64_t(pl.total) * p.h_kv() * R * kHeadDim * 4;
@@ -1062,6 +1069,7 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
     a.R = R;
     a.n_seq = n_seq;
     a.split_tokens = pl.split_tokens;
+    a.strided = pl.strided;
     a.sel_body = nullptr;
     a.sel_n = nullptr;
     a.sel_split = 0;

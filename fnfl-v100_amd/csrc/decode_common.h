@@ -29,6 +29,9 @@ struct dec_args {
     float * pml;        // [total_splits][h_kv][R][2] partial (m, l), base-2 domain
     float c2;           // scale * log2(e)
     int32_t layer, T, G, hq, R, n_seq, split_tokens;
+    // dense: 1 when a sequence's n splits stride over its tiles (split j takes tiles j, j + n, ...; at most 64 a
+    // split), 0 when split j takes the cells j split_tokens .. + split_tokens - 1
+    int32_t strided;
     int32_t slot[FNKV_MAX_SEQS];
     int64_t ctx[FNKV_MAX_SEQS];
     int32_t split0[FNKV_MAX_SEQS + 1]; // first split of each sequence; split0[n_seq] = total
@@ -269,11 +272,14 @@ __device__ void sparse_build(const dec_args & a, uint8_t * smem, uint2 * slice, 
 // of the split's logical page i. Sparse: entries e0 .. e0 + n_tiles - 1 of the selection's tile list, kept in LDS
 // (slice: past the ring) and, with LANES, also in lanes (lane i: entry i); lane i holds entry i's physical page.
 // Tile ti of the walk is then a lane read (without LANES, plus one LDS read) either way.
+__device__ __forceinline__ int32_t seq_of(const dec_args & a, int32_t split);
+
 template <bool SP, bool LANES = true> struct split_src {
     int32_t n_tiles = 0;
     int32_t page_lane = 0;
     int32_t new_mine = 0; // sparse: the new cells (bit t: cell ctx - T + t) this workgroup writes
-    int64_t begin = 0;
+    int64_t begin = 0;   // sparse: unused; dense: walk tile i is the sequence's tile g0 + stride i
+    int32_t g0 = 0, stride = 1;
     const uint2 * slice = nullptr;
     uint32_t ent_x = 0, ent_y = 0; // sparse with LANES: lane i holds entry i (register reads instead of LDS reads)
 
@@ -293,10 +299,21 @@ template <bool SP, bool LANES = true> struct split_src {
                 }
             }
         } else {
-            begin = b;
-            n_tiles = static_cast<int32_t>((e - b + kTileTokens - 1) / kTileTokens);
-            const int32_t n_pages = static_cast<int32_t>((e - b + kPageTokens - 1) / kPageTokens);
-            page_lane = lane < n_pages ? table[(b >> 8) + lane] : 0;
+            // at most 64 walk tiles (splits of at most 2,048 cells), lane i holding walk tile i's page: contiguous,
+            // the split's own cells; strided, split j of the sequence's n takes its tiles j, j + n, ...
+            if (a.strided) {
+                const int32_t s = seq_of(a, split);
+                const int32_t j = split - a.split0[s], n = a.split0[s + 1] - a.split0[s];
+                const int32_t tiles = static_cast<int32_t>((a.ctx[s] + kTileTokens - 1) / kTileTokens);
+                g0 = j;
+                stride = n;
+                n_tiles = tiles > j ? (tiles - j + n - 1) / n : 0;
+            } else {
+                g0 = static_cast<int32_t>(b / kTileTokens);
+                stride = 1;
+                n_tiles = static_cast<int32_t>((e - b + kTileTokens - 1) / kTileTokens);
+            }
+            page_lane = lane < n_tiles ? table[(g0 + stride * lane) >> 3] : 0;
         }
     }
     __device__ __forceinline__ uint2 entry(int32_t ti) const {
@@ -316,8 +333,8 @@ template <bool SP, bool LANES = true> struct split_src {
             const int32_t t8 = static_cast<int32_t>(entry(ti).x & 7u);
             return int64_t(phys) * pv.page_stride + int64_t(t8) * kTileBytes;
         } else {
-            const int32_t phys = __builtin_amdgcn_readlane(page_lane, ti >> 3);
-            return int64_t(phys) * pv.page_stride + int64_t(ti & 7) * kTileBytes;
+            const int32_t phys = __builtin_amdgcn_readlane(page_lane, ti);
+            return int64_t(phys) * pv.page_stride + int64_t((g0 + stride * ti) & 7) * kTileBytes;
         }
     }
     // the first cell of walk tile ti
@@ -325,7 +342,7 @@ template <bool SP, bool LANES = true> struct split_src {
         if constexpr (SP) {
             return int64_t(entry(ti).x & 0xffffu) * kTileTokens;
         } else {
-            return begin + int64_t(ti) * kTileTokens;
+            return int64_t(g0 + stride * ti) * kTileTokens;
         }
     }
     // the visibility bits of tile_softmax for this lane (query row of step token t_row, lane group qg)
@@ -425,20 +442,21 @@ __device__ __forceinline__ void append_owned_cells(const dec_args & a, const int
 
 template <int WAVES>
 __device__ __forceinline__ void append_new_cells(const dec_args & a, const int32_t * table, int32_t s, int32_t kvh,
-                                                 int64_t ctx, int64_t begin, int64_t end, int32_t wave,
-                                                 int32_t lane) {
+                                                 int64_t ctx, int64_t begin, int64_t end, int32_t sj, int32_t sn,
+                                                 int32_t wave, int32_t lane) {
     if (a.k_new == nullptr) {
         return;
     }
     const pool_view & pv = a.pv;
     const int64_t first_new = ctx - a.T;
-    const int64_t p0 = begin > first_new ? begin : first_new;
-    const int32_t nrow = static_cast<int32_t>(end - p0);
-    if (nrow <= 0) {
-        return;
-    }
-    for (int32_t job = wave; job < 2 * nrow; job += WAVES) {
-        const int64_t pos = p0 + (job >> 1);
+    // a new cell is written by the workgroup whose walk holds its tile: the split of its cell range, or (strided,
+    // sn splits) split tile % sn
+    for (int32_t job = wave; job < 2 * a.T; job += WAVES) {
+        const int64_t pos = first_new + (job >> 1);
+        const bool mine = sn != 0 ? static_cast<int32_t>((pos >> 5) % sn) == sj : (pos >= begin && pos < end);
+        if (!mine) {
+            continue;
+        }
         const int32_t kv = job & 1;
         const int64_t src = ((int64_t(s) * a.T + (pos - first_new)) * pv.h_kv + kvh) * kHeadDim;
         float x[4];

@@ -108,6 +108,7 @@ int sparse_launch(const kv_pool * p, int32_t slot, int64_t depth, int32_t T, int
     a.R = R;
     a.n_seq = 1;
     a.split_tokens = 0;
+    a.strided = 0;
     for (int32_t i = 0; i < FNKV_MAX_SEQS; ++i) {
         a.slot[i] = slot;
         a.ctx[i] = ctx;

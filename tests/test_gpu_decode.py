@@ -206,3 +206,34 @@ def test_first_launch_matches_reruns(T):
             assert np.isfinite(outs[0].view(np.float16).astype(np.float32)).all()
         finally:
             pool.close()
+
+
+@pytest.mark.parametrize("strided", ["0", "1"])
+@pytest.mark.parametrize("T", [1, 3])
+def test_split_walks_contiguous_and_strided(T, strided, monkeypatch):
+    # a sequence's splits take either their own cell ranges or every n-th tile (the launch's choice, forced here):
+    # both partitions give the same attention within the tolerance, the fused append of the new cells included
+    monkeypatch.setenv("FNKV_STRIDED", strided)
+    monkeypatch.setenv("FNKV_SPLIT_TOKENS", "512")
+    ctxs = [40, 3000, 9000 + 17, 20000 + 5]
+    st = Setup(ctxs, seed=70 + T, churn=0.3)
+    q16 = cases.queries(71 + T, (len(ctxs), T, HQ, 256))
+    got = st.run(q16, T)
+    assert st.check(q16, got, T) <= TOL
+    rng = np.random.default_rng([T, 72])
+    kn = rng.standard_normal((len(ctxs), T, HKV, 256), dtype=np.float32).astype(np.float16)
+    vn = rng.standard_normal((len(ctxs), T, HKV, 256), dtype=np.float32).astype(np.float16)
+    q = torch.from_numpy(q16).cuda()
+    out = torch.empty_like(q)
+    ws = torch.empty(st.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    st.pool.decode(st.slots, ctxs, T, 0, q, out, ws, k_new=torch.from_numpy(kn).cuda(),
+                   v_new=torch.from_numpy(vn).cuda())
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for i, (s, c) in enumerate(zip(st.slots, ctxs)):
+        k16, v16 = cases.kv_rows((70 + T) * 100 + s, c, HKV, 0)  # the rows Setup appended
+        k16, v16 = k16.copy(), v16.copy()
+        k16[c - T:], v16[c - T:] = kn[i], vn[i]
+        (_, _, kf), (_, _, vf) = cases.decoded(O, k16, v16)
+        assert cases.out_err(got[i], O.attn_f64(q16[i].view(np.uint16), kf, vf, c)) <= TOL
+
