@@ -114,7 +114,8 @@ template <int NT> __device__ __forceinline__ void group_sync() {
 }
 
 template <int NT, bool SP>
-__global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(dec_args a) {
+__global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(dec_args a_in) {
+    const dec_args a = SP ? sparse_row_view(a_in) : a_in;
     constexpr int GR = dec_shape<NT>::GR;
     constexpr int WAVES = dec_shape<NT>::WAVES;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -125,7 +126,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     const int32_t j = lane & 15, qg = lane >> 4;
     const int32_t split = static_cast<int32_t>(blockIdx.x);
     const int32_t kvh = static_cast<int32_t>(blockIdx.y);
-    const int32_t s = seq_of(a, split);
+    const int32_t s = SP ? 0 : seq_of(a, split); // a sparse launch is one sequence (constant: no scratch copy of a)
     const int32_t sp = split - a.split0[s];
     const int64_t ctx = a.ctx[s];
     const int64_t begin = int64_t(sp) * a.split_tokens;
@@ -380,7 +381,8 @@ template <int NT, bool SP = false> struct rows_shape {
 };
 
 template <int NT, bool SP>
-__global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_rows_kernel(dec_args a) {
+__global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_rows_kernel(dec_args a_in) {
+    const dec_args a = SP ? sparse_row_view(a_in) : a_in;
     using SH = rows_shape<NT, SP>;
     constexpr int GR = SH::GR, WAVES = SH::WAVES, SK = SH::SK, NBM = SH::NBM, CK = SH::CK;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -391,7 +393,7 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
     const int32_t j = lane & 15, qg = lane >> 4;
     const int32_t split = static_cast<int32_t>(blockIdx.x);
     const int32_t kvh = static_cast<int32_t>(blockIdx.y);
-    const int32_t s = seq_of(a, split);
+    const int32_t s = SP ? 0 : seq_of(a, split); // a sparse launch is one sequence (constant: no scratch copy of a)
     const int32_t sp = split - a.split0[s];
     const int64_t ctx = a.ctx[s];
     const int64_t begin = int64_t(sp) * a.split_tokens;
@@ -793,8 +795,8 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
     const int32_t s0 = a.split0[s];
     int32_t n = a.split0[s + 1] - s0;
     if (a.sel_n != nullptr) { // a sparse launch: only the splits that hold selected tiles ran
-        const int32_t S = sparse_split_size(*a.sel_n, n);
-        const int32_t used = (*a.sel_n + S - 1) / S;
+        const int32_t S = sparse_split_size(a.sel_n[s], n);
+        const int32_t used = (a.sel_n[s] + S - 1) / S;
         n = used < n ? used : n;
     }
     float m = kNegInf, l = 0.0f;

@@ -274,6 +274,37 @@ __device__ void sparse_build(const dec_args & a, uint8_t * smem, uint2 * slice, 
 // Tile ti of the walk is then a lane read (without LANES, plus one LDS read) either way.
 __device__ __forceinline__ int32_t seq_of(const dec_args & a, int32_t split);
 
+// A sparse launch runs each of its T rows as its own set of splits (blockIdx.z = row): this is the launch as row z
+// sees it, one step token at position depth + z with its G query rows, its selection body (the words after the
+// earlier rows', qsa.h:77-81), its list length slot and its region of the partials ([row][split][head][G] rows). With
+// several rows the new cells are in the pool before the launch (a row may read an earlier row's new cell); one row
+// writes its own from k_new, by the split that reads its tile.
+__device__ __forceinline__ dec_args sparse_row_view(const dec_args & in) {
+    dec_args a = in;
+    const int32_t z = static_cast<int32_t>(blockIdx.z);
+    const int64_t depth = in.ctx[0] - in.T;
+    int64_t words = 0;
+    for (int32_t t = 0; t < z; ++t) {
+        const int64_t q = depth + t;
+        const int64_t n_vis = (q + 1) / 4;
+        words += 2 + (n_vis < 512 ? n_vis : 512) + (q + 1) % 4;
+    }
+    const int64_t rows_all = int64_t(gridDim.x) * gridDim.y * in.G; // a row's partial rows
+    a.T = 1;
+    a.R = in.G;
+    a.ctx[0] = depth + z + 1;
+    a.q = in.q + int64_t(z) * in.hq * 256;
+    a.sel_body = in.sel_body + words;
+    a.sel_n = in.sel_n + z;
+    a.po = in.po + int64_t(z) * rows_all * 256;
+    a.pml = in.pml + int64_t(z) * rows_all * 2;
+    if (in.T != 1) {
+        a.k_new = nullptr;
+        a.v_new = nullptr;
+    }
+    return a;
+}
+
 template <bool SP, bool LANES = true> struct split_src {
     int32_t n_tiles = 0;
     int32_t page_lane = 0;
@@ -371,7 +402,7 @@ struct merge_args {
     uint16_t * out; // fp16 [n_seq][T][hq][256]
     int32_t T, G, hq, R, h_kv, n_seq;
     int32_t split0[FNKV_MAX_SEQS + 1];
-    const int32_t * sel_n;
+    const int32_t * sel_n; // sparse: each sequence's (row's) selection list length
     int32_t sel_split;
     // the gated form (fn/kernels/qsa/attend.cu:619-655's finish): with out_f32 set, row (t, h)'s value d is written as
     // o / (1 + exp(-gate[(t hq + h) gate_stride + d])) in F32 [T][hq][256] with its int8 activation format (codes
@@ -395,7 +426,7 @@ struct sparse_gate {
     int8_t * codes;
     float * scales;
 };
-int sparse_launch(const kv_pool * p, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq, float scale,
+int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq, float scale,
                   const void * q, const void * body, const void * offsets, const void * k_new, const void * v_new,
                   int32_t new_dtype, void * out, const sparse_gate * gate, void * ws, int64_t ws_bytes,
                   hipStream_t st, const char * who);

@@ -5,8 +5,8 @@
 // sparse.hip), and finishes each (row, head) with the sigmoid gate into F32 and FNFL's int8 activation format
 // (attend.cu:619-655, act_warp.cuh:12-37), all in stream order:
 //   1. qsa_prepare_kernel: a wave a (row, query head) or (row, KV head): q as fp16 (the attention's operand; the exact
-//      1/16 is applied as the score scale), k as F32 for the new-cell quantizer;
-//   2. the sparse decode launch, its new cells from that F32 k and the caller's F32 v;
+//      1/16 is applied as the score scale); the new cell's K (the normed, roped k) and V quantized into the pool;
+//   2. the sparse decode launch (each row its own splits);
 //   3. the merge with the gated epilogue.
 // Differences from the reference's kernel: the query operand is fp16 (the reference keeps q in F32; the attention is
 // held to the same 2e-3 bound as every other launch here), depth is a host value, and the cache is the paged pool.
@@ -27,15 +27,19 @@ namespace {
 constexpr int32_t kQStride = 512; // qfull: [q | gate] a head (attend.h:54)
 
 struct qsa_prep_args {
+    pool_view pv;
+    const int32_t * table; // the slot's page table
+    int32_t layer;
+    int64_t depth;
     const float * qfull;
     const float * kv_k;
+    const float * kv_v;
     const float * q_norm;
     const float * k_norm;
     const int32_t * pos;
     float theta_scale;
     int32_t T, hq, h_kv;
     uint16_t * q16;  // [T][hq][256]
-    float * k_rope;  // [T][h_kv][256]
     float * q_f32;   // optional [T][hq][256]
     float * k_f32;   // optional [T][h_kv][256]
 };
@@ -53,39 +57,22 @@ __global__ __launch_bounds__(64) void qsa_prepare_kernel(qsa_prep_args a) {
         reinterpret_cast<uint2 *>(a.q16 + o)[lane] = pack4_f16(y, 1.0f);
         return;
     }
+    // the row's new cell: K (normed, roped) and V in the pool's format at depth + t
     const int32_t kvh = r - a.hq;
     norm_rope(y, a.kv_k + (t * a.h_kv + kvh) * 256, a.k_norm, a.pos, a.T, t, a.theta_scale, lane);
     const int32_t o = (t * a.h_kv + kvh) * 256;
-    reinterpret_cast<float4 *>(a.k_rope + o)[lane] = make_float4(y[0], y[1], y[2], y[3]);
     if (a.k_f32 != nullptr) {
         reinterpret_cast<float4 *>(a.k_f32 + o)[lane] = make_float4(y[0], y[1], y[2], y[3]);
     }
+    const int64_t pos = a.depth + t;
+    uint8_t * tile = tile_of(a.pv, a.table, a.layer, kvh, pos);
+    quantize_store_fmt(y, lane, tile, static_cast<int32_t>(pos & 31), 0, a.pv.format);
+    float v[4];
+    load4<true>(a.kv_v + o, lane, v);
+    quantize_store_fmt(v, lane, tile, static_cast<int32_t>(pos & 31), 1, a.pv.format);
 }
 
 int64_t up16(int64_t x) { return (x + 15) & ~int64_t(15); }
-
-// rows a launch takes: G * rows <= FNKV_MAX_ROWS (the reference's card, 12 heads on one KV head, serves 5 rows as 4 + 1)
-int32_t rows_per_launch(int32_t G) { return G >= FNKV_MAX_ROWS ? 1 : FNKV_MAX_ROWS / G; }
-
-// words of row t's body (qsa.h:77-81): 2 + K + tail for the row at position q = depth + t
-int64_t body_words(int64_t q) {
-    const int64_t n_vis = (q + 1) / 4;
-    return 2 + (n_vis < 512 ? n_vis : 512) + (q + 1 - 4 * n_vis);
-}
-
-// the sparse workspace the largest of the row launches needs
-int64_t sparse_ws_max(const fnkv_pool * pool, int64_t depth, int32_t T, int32_t hq, int32_t G) {
-    const int32_t per = rows_per_launch(G);
-    int64_t need = 0;
-    for (int32_t c0 = 0; c0 < T; c0 += per) {
-        const int64_t b = fnkv_sparse_workspace_bytes(pool, depth + c0, T - c0 < per ? T - c0 : per, hq);
-        if (b < 0) {
-            return -1;
-        }
-        need = b > need ? b : need;
-    }
-    return need;
-}
 
 bool aligned16(const void * p) { return p != nullptr && (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -97,15 +84,11 @@ using fnkv::set_error;
 extern "C" {
 
 int64_t fnkv_qsa_workspace_bytes(const fnkv_pool * pool, int64_t depth, int32_t T, int32_t hq) {
-    const fnkv::kv_pool * p = fnkv::pool_of(pool);
-    if (p == nullptr || T <= 0 || T > FNKV_DATC_MAX_ROWS || hq <= 0 || hq % p->h_kv() != 0) {
-        return -1;
-    }
-    const int64_t sp = fnkv::sparse_ws_max(pool, depth, T, hq, hq / p->h_kv());
+    const int64_t sp = fnkv_sparse_workspace_bytes(pool, depth, T, hq);
     if (sp < 0) {
         return -1;
     }
-    return fnkv::up16(sp) + fnkv::up16(int64_t(T) * hq * 256 * 2) + int64_t(T) * p->h_kv() * 256 * 4;
+    return fnkv::up16(sp) + int64_t(T) * hq * 256 * 2;
 }
 
 int fnkv_qsa_attend(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq,
@@ -129,15 +112,12 @@ int fnkv_qsa_attend(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t
         return FNKV_ERR_ARG;
     }
     const int32_t G = hq / p->h_kv();
-    const int64_t sp = fnkv::up16(fnkv::sparse_ws_max(pool, depth, T, hq, G));
+    const int64_t sp = fnkv::up16(fnkv_sparse_workspace_bytes(pool, depth, T, hq));
     uint8_t * w = static_cast<uint8_t *>(ws);
     uint16_t * q16 = reinterpret_cast<uint16_t *>(w + sp);
-    float * k_rope = reinterpret_cast<float *>(w + sp + fnkv::up16(int64_t(T) * hq * 256 * 2));
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // every check of the sparse launches is made here too, before the prepare is enqueued: a refusal enqueues nothing
+    // every check of the sparse launch is made here too, before the prepare is enqueued: a refusal enqueues nothing
     fnkv::sparse_gate gate = {qfull + 256, 512, out, codes, scales};
-    fnkv::qsa_prep_args pa = {qfull, kv_k, q_norm, k_norm, pos, theta_scale, T, hq, p->h_kv(), q16, k_rope, q_f32,
-                              k_f32};
     if (T <= 0 || T > fnkv::kSelMaxRows || depth < 0 || layer < 0 || layer >= p->layers() || slot < 0 ||
         slot >= p->pages().n_slots() || depth + T > p->mapped_cells(slot) || depth + T > fnkv::kSelMaxCells ||
         G > FNKV_MAX_ROWS || body == nullptr ||
@@ -146,28 +126,13 @@ int fnkv_qsa_attend(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t
         set_error("fnkv_qsa_attend: rows, heads, layer or cells outside the contract");
         return FNKV_ERR_ARG;
     }
+    const fnkv::pool_view pv = p->view();
+    fnkv::qsa_prep_args pa = {pv, pv.table + int64_t(slot) * pv.table_stride, layer, depth, qfull, kv_k, kv_v, q_norm,
+                              k_norm, pos, theta_scale, T, hq, p->h_kv(), q16, q_f32, k_f32};
     hipLaunchKernelGGL(fnkv::qsa_prepare_kernel, dim3(static_cast<uint32_t>(T), static_cast<uint32_t>(hq + p->h_kv())),
                        dim3(64), 0, st, pa);
-    // rows in launches of at most FNKV_MAX_ROWS query rows a KV head, in order: a later launch's rows see the earlier
-    // rows' new cells (stream order), each row's body starts where the previous rows' words end
-    const int32_t per = fnkv::rows_per_launch(G);
-    const uint32_t * bw = static_cast<const uint32_t *>(body);
-    for (int32_t c0 = 0; c0 < T; c0 += per) {
-        const int32_t tc = T - c0 < per ? T - c0 : per;
-        const int64_t hk = int64_t(p->h_kv()) * 256;
-        fnkv::sparse_gate gc = {gate.gate + int64_t(c0) * hq * 512, 512, out + int64_t(c0) * hq * 256,
-                                codes + int64_t(c0) * hq * 256, scales + int64_t(c0) * hq * 16};
-        const int rc = fnkv::sparse_launch(p, slot, depth + c0, tc, layer, hq, 1.0f / 16.0f,
-                                           q16 + int64_t(c0) * hq * 256, bw, offsets, k_rope + c0 * hk,
-                                           kv_v + c0 * hk, FNKV_F32, nullptr, &gc, ws, sp, st, "fnkv_qsa_attend");
-        if (rc != FNKV_OK) {
-            return rc;
-        }
-        for (int32_t t = c0; t < c0 + tc; ++t) {
-            bw += fnkv::body_words(depth + t);
-        }
-    }
-    return FNKV_OK;
+    return fnkv::sparse_launch(pool, slot, depth, T, layer, hq, 1.0f / 16.0f, q16, body, offsets, nullptr, nullptr,
+                               FNKV_F32, nullptr, &gate, ws, sp, st, "fnkv_qsa_attend");
 }
 
 } // extern "C"

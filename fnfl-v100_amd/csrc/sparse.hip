@@ -34,33 +34,34 @@ namespace fnkv {
 uint64_t * timing_buffer();
 #endif
 
-// The launch shape of a sparse step: the list's largest length, the entries a split takes, the splits.
+// The launch shape of a sparse step: each of the T rows runs as its own n_splits splits (a row's list: at most its
+// 513 tiles), the entries a split takes, the partials of every row.
 struct sparse_plan {
     int32_t n_max = 0, per_split = 0, n_splits = 0;
     int64_t po_off = 0, pml_off = 0, bytes = 0;
 };
-sparse_plan plan_sparse(const kv_pool & p, int64_t depth, int32_t T, int32_t R) {
+sparse_plan plan_sparse(const kv_pool & p, int64_t depth, int32_t T, int32_t G) {
     sparse_plan pl;
     const int32_t n_tiles = static_cast<int32_t>((depth + T + kTileTokens - 1) / kTileTokens);
-    pl.n_max = std::min(n_tiles, T * (kSelTopBlocks + 1)); // each row: its blocks' tiles and its tail's
-    const int32_t want = std::max(1, device_cus(p.device()) / p.h_kv());
+    pl.n_max = std::min(n_tiles, kSelTopBlocks + 1); // a row's blocks' tiles and its tail's
+    const int32_t want = std::max(1, device_cus(p.device()) / (p.h_kv() * T));
     pl.per_split = std::min(64, std::max(1, (pl.n_max + want - 1) / want));
     pl.n_splits = (pl.n_max + pl.per_split - 1) / pl.per_split;
     auto up16 = [](int64_t x) { return (x + 15) & ~int64_t(15); };
-    pl.po_off = 16; // the list's length first
-    pl.pml_off = up16(pl.po_off + int64_t(pl.n_splits) * p.h_kv() * R * kHeadDim * 4);
-    pl.bytes = up16(pl.pml_off + int64_t(pl.n_splits) * p.h_kv() * R * 2 * 4);
+    pl.po_off = up16(int64_t(T) * 4); // each row's list length first
+    pl.pml_off = up16(pl.po_off + int64_t(T) * pl.n_splits * p.h_kv() * G * kHeadDim * 4);
+    pl.bytes = up16(pl.pml_off + int64_t(T) * pl.n_splits * p.h_kv() * G * 2 * 4);
     return pl;
 }
-
 
 // The sparse launch (validation, the decode kernels' sparse instantiation, the merge); `gate` set: the merge writes
 // the gated F32 output and its activation format instead of the fp16 out. Returns a status; nothing is enqueued
 // unless it is FNKV_OK.
-int sparse_launch(const kv_pool * p, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq, float scale,
+int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq, float scale,
                   const void * q, const void * body, const void * offsets, const void * k_new, const void * v_new,
                   int32_t new_dtype, void * out, const sparse_gate * gate, void * ws, int64_t ws_bytes,
                   hipStream_t st, const char * who) {
+    const kv_pool * p = pool_of(pool);
     const std::string name(who);
     if (p == nullptr || slot < 0 || slot >= p->pages().n_slots() || T <= 0 || T > kSelMaxRows || depth < 0 ||
         layer < 0 || layer >= p->layers() || hq <= 0 || hq % p->h_kv() != 0 || q == nullptr || body == nullptr ||
@@ -71,10 +72,9 @@ int sparse_launch(const kv_pool * p, int32_t slot, int64_t depth, int32_t T, int
         return FNKV_ERR_ARG;
     }
     const int32_t G = hq / p->h_kv();
-    const int32_t R = G * T;
     const int64_t ctx = depth + T;
-    if (R > FNKV_MAX_ROWS || ctx > kSelMaxCells || ctx > p->mapped_cells(slot)) {
-        set_error(name + ": G * T = " + std::to_string(R) + " (at most " + std::to_string(FNKV_MAX_ROWS) +
+    if (G > FNKV_MAX_ROWS || ctx > kSelMaxCells || ctx > p->mapped_cells(slot)) {
+        set_error(name + ": G = " + std::to_string(G) + " (at most " + std::to_string(FNKV_MAX_ROWS) +
                   ") or cells " + std::to_string(ctx) + " outside the slot's mapped cells (at most " +
                   std::to_string(kSelMaxCells) + ")");
         return FNKV_ERR_ARG;
@@ -85,18 +85,27 @@ int sparse_launch(const kv_pool * p, int32_t slot, int64_t depth, int32_t T, int
         set_error(name + ": q, out and ws must be 16-byte aligned, body and offsets 4-byte aligned");
         return FNKV_ERR_ARG;
     }
-    const sparse_plan pl = plan_sparse(*p, depth, T, R);
+    const sparse_plan pl = plan_sparse(*p, depth, T, G);
     if (ws_bytes < pl.bytes) {
         set_error(name + ": workspace too small");
         return FNKV_ERR_ARG;
     }
     uint8_t * w = static_cast<uint8_t *>(ws);
 
+    // several rows: their new cells first (a row may read an earlier row's new cell; the rows run side by side); one
+    // row: the launch writes it, by the split that reads its tile
+    if (k_new != nullptr && T > 1) {
+        const int rc = fnkv_q8_append(const_cast<fnkv_pool *>(pool), slot, layer, depth, T, k_new, v_new, new_dtype,
+                                      st);
+        if (rc != FNKV_OK) {
+            return rc;
+        }
+    }
     dec_args a;
     a.pv = p->view();
     a.q = static_cast<const uint16_t *>(q);
-    a.k_new = k_new; // written by the workgroups that read them (split 0 when no row selects them)
-    a.v_new = v_new;
+    a.k_new = T == 1 ? k_new : nullptr;
+    a.v_new = T == 1 ? v_new : nullptr;
     a.new_f32 = new_dtype == FNKV_F32 ? 1 : 0;
     a.po = reinterpret_cast<float *>(w + pl.po_off);
     a.pml = reinterpret_cast<float *>(w + pl.pml_off);
@@ -105,7 +114,7 @@ int sparse_launch(const kv_pool * p, int32_t slot, int64_t depth, int32_t T, int
     a.T = T;
     a.G = G;
     a.hq = hq;
-    a.R = R;
+    a.R = G * T; // each row's view takes G of them
     a.n_seq = 1;
     a.split_tokens = 0;
     a.strided = 0;
@@ -123,20 +132,23 @@ int sparse_launch(const kv_pool * p, int32_t slot, int64_t depth, int32_t T, int
 #ifdef FNKV_TIMING
     a.ts = timing_buffer();
 #endif
-    launch_decode_sparse(*p, (R + 15) / 16, dim3(static_cast<uint32_t>(pl.n_splits), static_cast<uint32_t>(p->h_kv())),
+    launch_decode_sparse(*p, (G + 15) / 16,
+                         dim3(static_cast<uint32_t>(pl.n_splits), static_cast<uint32_t>(p->h_kv()),
+                              static_cast<uint32_t>(T)),
                          a, st);
     merge_args m;
     m.po = a.po;
     m.pml = a.pml;
     m.out = static_cast<uint16_t *>(out);
-    m.T = T;
+    // the rows fold as sequences of one step token each ([row][split] partials, row r's out at row r)
+    m.T = 1;
     m.G = G;
     m.hq = hq;
-    m.R = R;
+    m.R = G;
     m.h_kv = p->h_kv();
-    m.n_seq = 1;
+    m.n_seq = T;
     for (int32_t i = 0; i <= FNKV_MAX_SEQS; ++i) {
-        m.split0[i] = a.split0[i];
+        m.split0[i] = (i < T ? i : T) * pl.n_splits;
     }
     m.sel_n = a.sel_n;
     m.sel_split = pl.per_split;
@@ -166,13 +178,13 @@ int64_t fnkv_sparse_workspace_bytes(const fnkv_pool * pool, int64_t depth, int32
     if (p == nullptr || T <= 0 || T > fnkv::kSelMaxRows || depth < 0 || hq <= 0 || hq % p->h_kv() != 0) {
         return -1;
     }
-    return fnkv::plan_sparse(*p, depth, T, (hq / p->h_kv()) * T).bytes;
+    return fnkv::plan_sparse(*p, depth, T, hq / p->h_kv()).bytes;
 }
 
 int fnkv_attn_sparse(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq,
                      float scale, const void * q, const void * body, const void * offsets, const void * k_new,
                      const void * v_new, int32_t new_dtype, void * out, void * ws, int64_t ws_bytes, void * stream) {
-    return fnkv::sparse_launch(fnkv::pool_of(pool), slot, depth, T, layer, hq, scale, q, body, offsets, k_new, v_new,
+    return fnkv::sparse_launch(pool, slot, depth, T, layer, hq, scale, q, body, offsets, k_new, v_new,
                                new_dtype, out, nullptr, ws, ws_bytes, static_cast<hipStream_t>(stream),
                                "fnkv_attn_sparse");
 }

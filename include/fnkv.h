@@ -157,7 +157,8 @@ int64_t fnkv_sparse_workspace_bytes(const fnkv_pool * pool, int64_t depth, int32
  * outside the row's whole blocks are ignored. k_new / v_new (optional, [T][h_kv][256] of new_dtype): the rows' own
  * cells, written at depth .. depth + T - 1 before any row reads (a row's selection need not include them). q, out:
  * fp16 [T][hq][256]; scores q.k * scale, softmax and accumulation in fp32, over the pool's codes exactly as the dense
- * launch. depth + T <= 262,176 and mapped. */
+ * launch. depth + T <= 262,176 and mapped; hq / h_kv <= FNKV_MAX_ROWS (each row runs as its own splits, side by side,
+ * after the new cells are written). */
 int fnkv_attn_sparse(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq,
                      float scale, const void * q, const void * body, const void * offsets, const void * k_new,
                      const void * v_new, int32_t new_dtype, void * out, void * ws, int64_t ws_bytes, void * stream);
@@ -175,9 +176,8 @@ int64_t fnkv_qsa_workspace_bytes(const fnkv_pool * pool, int64_t depth, int32_t 
  * and each (row, head) is finished with its gate: out = o / (1 + exp(-gate)) in F32 with its int8 activation format.
  * qfull: F32 [T][hq][512] (each head's q, then its gate); kv_k, kv_v: F32 [T][h_kv][256]; q_norm, k_norm: F32 [256];
  * out: F32 [T][hq][256]; codes: int8 [T][hq 256]; scales: F32 [T][hq 8][2]; q_f32, k_f32 (optional): the F32 q
- * [T][hq][256] and k [T][h_kv][256] after the norm and rope. Launches in stream order: the prepare, then per group
- * of rows with (hq / h_kv) x rows <= FNKV_MAX_ROWS the attention and the gated merge (the reference's card, 12 query
- * heads on one KV head, runs 5 rows as 4 + 1). */
+ * [T][hq][256] and k [T][h_kv][256] after the norm and rope. Three launches in stream order: the prepare (which
+ * writes the new cells), the attention (each row its own splits), the gated merge. hq / h_kv <= FNKV_MAX_ROWS. */
 int fnkv_qsa_attend(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq,
                     const float * qfull, const float * kv_k, const float * kv_v, const float * q_norm,
                     const float * k_norm, const int32_t * pos, float theta_scale, const void * body,
