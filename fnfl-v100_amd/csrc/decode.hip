@@ -116,6 +116,9 @@ template <int NT> __device__ __forceinline__ void group_sync() {
 template <int NT, bool SP>
 __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(dec_args a_in) {
     const dec_args a = SP ? sparse_row_view(a_in) : a_in;
+    if constexpr (SP) {
+        FNKV_STAMP(8); // the wave stamps (8..) are not taken in sparse launches
+    }
     constexpr int GR = dec_shape<NT>::GR;
     constexpr int WAVES = dec_shape<NT>::WAVES;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
