@@ -574,8 +574,15 @@ def run_datc(args, cfg):
     scales = torch.empty(NHd * HDd // 16, dtype=torch.float32, device="cuda")
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
 
+    fused = not args.datc_two_call
+
     def step(i):
         kc, vc = caches[i][0], caches[i][1]
+        if fused:
+            fnkv.datc_step(kv_k=kv[0], kv_v=kv[1], k_norm=norms[1], n_before=ints[0:1], pos=pos, stride=ints[1:2],
+                           k_cache=kc, v_cache=vc, err=err, qfull=qfull, q_norm=norms[0], q16=q16, part=part,
+                           out=out, codes=codes, scales=scales)
+            return
         fnkv.datc_prepare(1, kv_k=kv[0], kv_v=kv[1], k_norm=norms[1], n_before=ints[0:1], pos=pos, stride=ints[1:2],
                           k_cache=kc, v_cache=vc, err=err, qfull=qfull, q_norm=norms[0], q16=q16)
         fnkv.datc_attend(q16=q16, qfull=qfull, k_cache=kc, v_cache=vc, n_before=ints[0:1], part=part, out=out,
@@ -627,7 +634,7 @@ def run_datc(args, cfg):
     bytes_step = (n * HDd * 2 * 2  # K and V of every cell
                   + NHd * 512 * 4 + 2 * HDd * 4 + 2 * HDd * 4 + 4 * 4  # prepare: qfull, k / v, norms, positions
                   + NHd * HDd * 2 + 2 * HDd * 2  # q16 and the new cell written
-                  + NHd * HDd * 2 + NHd * HDd * 4  # attend: q16 and the gates read
+                  + (0 if fused else NHd * HDd * 2) + NHd * HDd * 4  # attend: q16 (two calls) and the gates read
                   + NHd * HDd * 4 + NHd * HDd + NHd * HDd // 16 * 4)  # out, codes, scales written
     achieved = bytes_step / step_s / 1e9
     line = {
@@ -645,10 +652,12 @@ def run_datc(args, cfg):
         "data": "synthetic (seeded N(0,1) F16 caches, uniform q / k / v / gates / norms)",
         "config": {"workload": cfg["workload"], "cells": n, "q_heads": NHd, "head_dim": HDd,
                    "cache_copies_rotated": copies, "rotated_mb": round(copies * copy_bytes / 1e6),
-                   "steps_per_graph": copies, "hip_graph": not args.no_graph},
+                   "steps_per_graph": copies, "hip_graph": not args.no_graph,
+                   "entry": "fnkv_datc_step" if fused else "fnkv_datc_prepare + fnkv_datc_attend"},
         "roofline": {
-            "kernel": "fnkv_datc_prepare + fnkv_datc_attend (datc_prepare_kernel, datc_attend_kernel, "
-                      "datc_fold_kernel), a step",
+            "kernel": ("fnkv_datc_step (datc_attend_kernel, datc_fold_kernel with the prepare folded in)" if fused
+                       else "fnkv_datc_prepare + fnkv_datc_attend (datc_prepare_kernel, datc_attend_kernel, "
+                            "datc_fold_kernel)") + ", a step",
             "bound": "hbm",
             "achieved": round(achieved, 3),
             "peak": PEAK_HBM_GBS,
@@ -696,6 +705,8 @@ def main():
     ap.add_argument("--T", type=int, default=None, help="override the config's query tokens a sequence")
     ap.add_argument("--ctxs", default=None, help="override the config's contexts (comma-separated cells)")
     ap.add_argument("--no-append", action="store_true", help="attend only (the step's cells appended beforehand)")
+    ap.add_argument("--datc-two-call", action="store_true",
+                    help="DA-TC: time fnkv_datc_prepare then fnkv_datc_attend instead of fnkv_datc_step")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes (traffic: null)")
     ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()

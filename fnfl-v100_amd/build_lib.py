@@ -34,7 +34,7 @@ def hipcc():
 # attention kernels run two waves a SIMD and keep their matrix-core accumulators in ordinary registers (VGPR form)
 VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 EXTRA = {"append.hip": ["-ffp-contract=off"], "decode.hip": VGPR_MFMA, "prefill.hip": VGPR_MFMA,
-         "sparse.hip": ["-ffp-contract=off"]}
+         "sparse.hip": ["-ffp-contract=off"], "qsa.hip": ["-ffp-contract=off"]}
 
 
 def _compile(src):

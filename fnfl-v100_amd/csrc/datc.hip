@@ -49,7 +49,8 @@ constexpr int32_t kVBuf = (kTile / 2) * kVPair;           // a tile's V rows: 17
 constexpr int32_t kOStride = kD + 4;                      // floats a head's row of a wave's O in LDS (wave fold)
 constexpr int32_t kFoldLds = kWaves * kHeads * kOStride * 4; // the waves' O, over the V buffers at the end
 constexpr int32_t kMlLds = kFoldLds > 2 * kWaves * kVBuf ? kFoldLds : 2 * kWaves * kVBuf; // waves' m, l: past both
-constexpr int32_t kAttendLds = kMlLds + 2 * kWaves * 16 * 4;
+constexpr int32_t kQLds = kMlLds + 2 * kWaves * 16 * 4;      // the fused step's q16 [12][256]
+constexpr int32_t kAttendLds = kQLds + kHeads * kD * 2;
 constexpr int32_t kSelRatio = 4, kSelBlocks = 512;
 constexpr uint32_t kOob = 0x80000000u;                    // a buffer offset past every cache: reads as zero
 constexpr int32_t kEmptyTile = 1 << 30;                   // a tile base past every row: an empty step
@@ -74,6 +75,12 @@ namespace {
 #endif
 
 // ---- prepare ----
+
+// the prepare's refusal: a row's cell outside the caches, or rows past the round's
+__device__ __forceinline__ bool prepare_refused(const fnkv_datc_prepare_args & a, int32_t rows) {
+    const int32_t nb = *a.n_before, stride = *a.stride;
+    return nb < 0 || static_cast<int64_t>(nb) + a.row0 + rows > a.max_cells || a.row0 + rows > stride;
+}
 
 __global__ __launch_bounds__(64 * (kHeads + 1)) void datc_prepare_kernel(fnkv_datc_prepare_args a, int32_t rows) {
     const int32_t wave = static_cast<int32_t>(threadIdx.x) / 64, lane = static_cast<int32_t>(threadIdx.x) % 64;
@@ -289,11 +296,69 @@ __device__ __forceinline__ void tile_step(const fnkv_datc_attend_args & a, const
     }
 }
 
-template <bool SP> __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend_kernel(fnkv_datc_attend_args a) {
+// FUSED: the wave's three heads' inputs and the lane's position are loaded before the first tile's loads (the loads
+// return in order: issued after them, they would wait for the whole tile), then the tile is issued (unconditionally: a
+// wave without tiles issues the empty tile, zeros and no memory traffic, so the waits for the q inputs count past the
+// tile's loads instead of draining them at a branch join), then the heads are formed into LDS while it is in flight.
+// The V buffer and the q rows are distinct LDS regions (restrict), so the q writes need not wait for the V copies.
+template <bool SP>
+__device__ __forceinline__ void fused_first_tile(const fnkv_datc_attend_args & a, const fnkv_datc_prepare_args & pa,
+                                                 const datc_shape & s, rsrc_t rk, rsrc_t rv, int32_t base, k_tile & kt,
+                                                 uint8_t * __restrict__ vbuf, uint16_t * __restrict__ ql,
+                                                 half8 (&qb)[8], int32_t b, int32_t wave, int32_t lane) {
+    constexpr int32_t kPer = kHeads / kWaves;
+    float4 xq[kPer];
+#pragma unroll
+    for (int32_t i = 0; i < kPer; ++i) {
+        xq[i] = reinterpret_cast<const float4 *>(pa.qfull + (kPer * wave + i) * kQS)[lane];
+    }
+    const float4 gq = reinterpret_cast<const float4 *>(pa.q_norm)[lane];
+    const int32_t pq = rope_pos(pa.pos, *pa.stride, pa.row0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_tile<SP>(a, s, rk, rv, base, kt, vbuf, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    float sn, cs;
+    rope_angle(sn, cs, pq, pa.theta_scale, lane);
+#pragma unroll
+    for (int32_t i = 0; i < kPer; ++i) {
+        const int32_t h = kPer * wave + i;
+        float y[4];
+        norm_rope_apply(y, xq[i], gq, sn, cs, lane);
+        const uint2 q4 = pack4_f16(y, 1.0f / 16.0f);
+        reinterpret_cast<uint2 *>(ql + h * kD)[lane] = q4;
+        if (b == 0) {
+            reinterpret_cast<uint2 *>(pa.q16 + h * kD)[lane] = q4;
+            if (pa.q_f32 != nullptr) {
+                reinterpret_cast<float4 *>(pa.q_f32 + h * kD)[lane] = make_float4(y[0], y[1], y[2], y[3]);
+            }
+        }
+    }
+    // the workgroup's q rows complete in LDS; the barrier waits for the LDS writes only (a __syncthreads would also
+    // drain the tile's copies into LDS)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    const int32_t h = lane % 16, g = lane / 16;
+#pragma unroll
+    for (int32_t j = 0; j < 8; ++j) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (h < kHeads) {
+            v = *reinterpret_cast<const u32x4 *>(ql + h * kD + 32 * j + 8 * g);
+        }
+        qb[j] = __builtin_bit_cast(half8, v);
+    }
+}
+
+// FUSED (the draft step, fnkv_datc_step): the prepare of the one row folded in. Every workgroup forms the row's q
+// itself (wave w heads 3 w .. 3 w + 2, under its first tile's loads) into LDS; workgroup 0 also writes q16 (and q_f32);
+// the wave whose walk holds the row's cell writes its K and V (and k_f32) before issuing any load. The attention and
+// its partials are then those of the prepare and attend launches in turn, bit for bit.
+template <bool SP, bool FUSED>
+__global__ __launch_bounds__(64 * kWaves, 1) void datc_attend_kernel(fnkv_datc_attend_args a,
+                                                                     fnkv_datc_prepare_args pa) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int32_t wave = static_cast<int32_t>(threadIdx.x) / 64, lane = static_cast<int32_t>(threadIdx.x) % 64;
     const datc_shape s = datc_shape_of<SP>(a);
-    if (!s.valid) {
+    if (!s.valid || (FUSED && prepare_refused(pa, 1))) {
         if (blockIdx.x == 0 && threadIdx.x == 0) {
             atomicOr(a.err, FNKV_DEV_ERR_DRAFT_DEPTH);
         }
@@ -316,10 +381,35 @@ template <bool SP> __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend
     const rsrc_t rv = make_rsrc(a.v_cache, static_cast<int32_t>(cache_bytes));
     uint8_t * vb0 = smem + wave * 2 * kVBuf;
     uint8_t * vb1 = vb0 + kVBuf;
+    auto tile_base = [&](int32_t k) { return k < cnt ? (first + per * k) * kTile : kEmptyTile; };
+    if constexpr (FUSED) {
+        // the row's cell: written by the wave whose walk holds its tile (its last), before any of that wave's loads
+        const int32_t cell_l = s.n - 1; // the row's own cell is the last logical cell (dense and SP2)
+        if (cnt > 0 && (cell_l / kTile - first) % per == 0 && cell_l / kTile >= first) {
+            const int32_t nb = *pa.n_before;
+            float y[4];
+            norm_rope(y, pa.kv_k, pa.k_norm, pa.pos, *pa.stride, pa.row0, pa.theta_scale, lane);
+            if (pa.k_f32 != nullptr) {
+                reinterpret_cast<float4 *>(pa.k_f32)[lane] = make_float4(y[0], y[1], y[2], y[3]);
+            }
+            const int64_t at = (static_cast<int64_t>(nb) + pa.row0) * kD;
+            reinterpret_cast<uint2 *>(pa.k_cache + at)[lane] = pack4_f16(y, 1.0f);
+            const float4 v4 = reinterpret_cast<const float4 *>(pa.kv_v)[lane];
+            const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+            reinterpret_cast<uint2 *>(pa.v_cache + at)[lane] = pack4_f16(v, 1.0f);
+            // the stores complete (into L2: the vector L1 writes through, and no wave of this CU has read the tile in
+            // this launch) before this wave, the only one that reads the tile, issues its loads
+            __threadfence_block();
+        }
+    }
     // q16 as the B operand: lane l holds head l % 16's dims 32 j + 8 (l / 16) .. + 7 (heads 12..15 zero); loaded
-    // before the first tile
+    // before the first tile (FUSED: formed after the first tile's loads are issued)
     half8 qb[8];
-    {
+    k_tile ka, kb;
+    if constexpr (FUSED) {
+        fused_first_tile<SP>(a, pa, s, rk, rv, tile_base(0), ka, vb0, reinterpret_cast<uint16_t *>(smem + kQLds), qb,
+                             b, wave, lane);
+    } else {
         const int32_t h = lane % 16, g = lane / 16;
 #pragma unroll
         for (int32_t j = 0; j < 8; ++j) {
@@ -334,7 +424,6 @@ template <bool SP> __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend
     // pair may take an empty tile: cells beyond the row, zeros, no memory traffic) and the loop runs whole pairs, so a
     // step waits for exactly the loads issued before the last 32; an odd last tile is a step of its own that issues
     // nothing
-    auto tile_base = [&](int32_t k) { return k < cnt ? (first + per * k) * kTile : kEmptyTile; };
     float m_run = -INFINITY, l_run = 0.0f;
     floatx4 o[16];
 #pragma unroll
@@ -342,8 +431,9 @@ template <bool SP> __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend
         o[db] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
     if (cnt > 0) {
-        k_tile ka, kb;
-        issue_tile<SP>(a, s, rk, rv, tile_base(0), ka, vb0, lane);
+        if constexpr (!FUSED) {
+            issue_tile<SP>(a, s, rk, rv, tile_base(0), ka, vb0, lane);
+        }
         int32_t k = 0;
         for (; k + 1 < cnt; k += 2) {
             tile_step<SP, true>(a, s, rk, rv, ka, kb, vb0, vb1, tile_base(k), tile_base(k + 1), qb, m_run, l_run, o,
@@ -354,8 +444,8 @@ template <bool SP> __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend
         if (k < cnt) {
             tile_step<SP, false>(a, s, rk, rv, ka, kb, vb0, vb1, tile_base(k), 0, qb, m_run, l_run, o, lane);
         }
-        wait_vmcnt<0>(); // the last (empty) copies land before the fold below reuses the buffers
     }
+    wait_vmcnt<0>(); // the last (empty) copies land before the fold below reuses the buffers
     DATC_STAMP(b, 2);
     // fold the waves: M, the waves' weights, then O summed in wave order
     float * ml = reinterpret_cast<float *>(smem + kMlLds); // a wave still in its last step owns its V buffer
@@ -411,7 +501,8 @@ template <bool SP> __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend
 // the fold of (head h, values 32 r .. 32 r + 31): the active partials in workgroup order, the gate, the F32 output and
 // its activation-format run (act_run). Thread t takes partials t / 32 + 8 i of value t % 32 and issues all its loads
 // before the reductions that weigh them.
-template <bool SP> __global__ __launch_bounds__(256) void datc_fold_kernel(fnkv_datc_attend_args a) {
+template <bool SP, bool FUSED>
+__global__ __launch_bounds__(256) void datc_fold_kernel(fnkv_datc_attend_args a, fnkv_datc_prepare_args pa) {
     constexpr int32_t kPer = kGrid / 8;
     __shared__ float w_of[kGrid];
     __shared__ float wred[2][4];
@@ -436,7 +527,7 @@ template <bool SP> __global__ __launch_bounds__(256) void datc_fold_kernel(fnkv_
     const float l_raw = part[static_cast<int64_t>(t) * kPartFloats + kHeads * kD + kHeads + h];
     const float gate = t < 32 ? a.qfull[h * kQS + kD + 32 * r + dl] : 0.0f;
     const datc_shape s = datc_shape_of<SP>(a);
-    if (!s.valid) {
+    if (!s.valid || (FUSED && prepare_refused(pa, 1))) {
         return;
     }
     const float m_t = t < s.active ? m_raw : -INFINITY;
@@ -536,40 +627,74 @@ int fnkv_datc_prepare(int32_t rows, const fnkv_datc_prepare_args * a, void * str
     return FNKV_OK;
 }
 
-int fnkv_datc_attend(const fnkv_datc_attend_args * a, void * stream) {
-    using fnkv::aligned;
+} // extern "C"
+
+namespace fnkv {
+namespace {
+
+bool attend_args_ok(const fnkv_datc_attend_args * a) {
     // the caches are addressed by 32-bit buffer offsets: at most 4,194,303 cells (2 GiB a cache)
-    if (a == nullptr || a->row0 < 0 || a->row0 >= (a->body != nullptr ? FNKV_DATC_MAX_SPARSE_ROW : FNKV_DATC_MAX_ROWS) ||
-        a->max_cells < 1 || a->max_cells >= (1 << 22) || !aligned(a->q16, 16) || !aligned(a->qfull, 16) ||
-        !aligned(a->k_cache, 16) || !aligned(a->v_cache, 16) || a->n_before == nullptr || !aligned(a->part, 16) ||
-        !aligned(a->out, 16) || a->codes == nullptr || !aligned(a->scales, 8) || a->err == nullptr ||
-        (a->body != nullptr && !aligned(a->body, 4))) {
-        set_error("fnkv_datc_attend: argument outside the contract");
-        return FNKV_ERR_ARG;
-    }
+    return a != nullptr && a->row0 >= 0 &&
+           a->row0 < (a->body != nullptr ? FNKV_DATC_MAX_SPARSE_ROW : FNKV_DATC_MAX_ROWS) && a->max_cells >= 1 &&
+           a->max_cells < (1 << 22) && aligned(a->qfull, 16) && aligned(a->k_cache, 16) && aligned(a->v_cache, 16) &&
+           a->n_before != nullptr && aligned(a->part, 16) && aligned(a->out, 16) && a->codes != nullptr &&
+           aligned(a->scales, 8) && a->err != nullptr && (a->body == nullptr || aligned(a->body, 4));
+}
+
+template <bool FUSED>
+int launch_attend(const fnkv_datc_attend_args & a, const fnkv_datc_prepare_args & pa, hipStream_t st) {
     static bool attr_set[64] = {false};
     int dev = 0;
     (void)hipGetDevice(&dev);
     if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::datc_attend_kernel<false>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::kAttendLds);
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::datc_attend_kernel<true>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::kAttendLds);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(datc_attend_kernel<false, FUSED>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kAttendLds);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(datc_attend_kernel<true, FUSED>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kAttendLds);
         (void)hipGetLastError();
         attr_set[dev] = true;
     }
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (a->body != nullptr) {
-        hipLaunchKernelGGL(fnkv::datc_attend_kernel<true>, dim3(fnkv::kGrid), dim3(64 * fnkv::kWaves),
-                           fnkv::kAttendLds, st, *a);
-        hipLaunchKernelGGL(fnkv::datc_fold_kernel<true>, dim3(fnkv::kHeads * 8), dim3(256), 0, st, *a);
+    if (a.body != nullptr) {
+        hipLaunchKernelGGL((datc_attend_kernel<true, FUSED>), dim3(kGrid), dim3(64 * kWaves), kAttendLds, st, a, pa);
+        hipLaunchKernelGGL((datc_fold_kernel<true, FUSED>), dim3(kHeads * 8), dim3(256), 0, st, a, pa);
     } else {
-        hipLaunchKernelGGL(fnkv::datc_attend_kernel<false>, dim3(fnkv::kGrid), dim3(64 * fnkv::kWaves),
-                           fnkv::kAttendLds, st, *a);
-        hipLaunchKernelGGL(fnkv::datc_fold_kernel<false>, dim3(fnkv::kHeads * 8), dim3(256), 0, st, *a);
+        hipLaunchKernelGGL((datc_attend_kernel<false, FUSED>), dim3(kGrid), dim3(64 * kWaves), kAttendLds, st, a, pa);
+        hipLaunchKernelGGL((datc_fold_kernel<false, FUSED>), dim3(kHeads * 8), dim3(256), 0, st, a, pa);
     }
-    if (hipGetLastError() != hipSuccess) {
+    return hipGetLastError() == hipSuccess ? FNKV_OK : FNKV_ERR_HIP;
+}
+
+} // namespace
+} // namespace fnkv
+
+extern "C" {
+
+int fnkv_datc_attend(const fnkv_datc_attend_args * a, void * stream) {
+    if (!fnkv::attend_args_ok(a) || !fnkv::aligned(a->q16, 16)) {
+        set_error("fnkv_datc_attend: argument outside the contract");
+        return FNKV_ERR_ARG;
+    }
+    const fnkv_datc_prepare_args none = {};
+    if (fnkv::launch_attend<false>(*a, none, static_cast<hipStream_t>(stream)) != FNKV_OK) {
         set_error("fnkv_datc_attend: launch failed");
+        return FNKV_ERR_HIP;
+    }
+    return FNKV_OK;
+}
+
+int fnkv_datc_step(const fnkv_datc_prepare_args * p, const fnkv_datc_attend_args * a, void * stream) {
+    using fnkv::aligned;
+    if (p == nullptr || !fnkv::attend_args_ok(a) || p->qfull == nullptr || p->row0 != a->row0 ||
+        p->k_cache != a->k_cache || p->v_cache != a->v_cache || p->n_before != a->n_before ||
+        p->max_cells != a->max_cells || !aligned(p->qfull, 16) || !aligned(p->kv_k, 16) || !aligned(p->kv_v, 16) ||
+        !aligned(p->q_norm, 16) || !aligned(p->k_norm, 16) || p->pos == nullptr || p->stride == nullptr ||
+        !aligned(p->q16, 16) || (p->q_f32 != nullptr && !aligned(p->q_f32, 16)) ||
+        (p->k_f32 != nullptr && !aligned(p->k_f32, 16)) || !std::isfinite(p->theta_scale)) {
+        set_error("fnkv_datc_step: argument outside the contract");
+        return FNKV_ERR_ARG;
+    }
+    if (fnkv::launch_attend<true>(*a, *p, static_cast<hipStream_t>(stream)) != FNKV_OK) {
+        set_error("fnkv_datc_step: launch failed");
         return FNKV_ERR_HIP;
     }
     return FNKV_OK;

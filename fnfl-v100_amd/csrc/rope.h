@@ -18,9 +18,35 @@ constexpr float kRmsEps = 1e-6f; // fn/model/shapes.h:35 rms_eps
 // ggml_rope_multi with GGML_ROPE_TYPE_IMROPE; fn/kernels/qsa/attend.cu:151-198, imrope.cuh:14-20). A lane holds dims
 // 4 lane .. 4 lane + 3. Rotation pair i (< 32) is dims i and i + 32; its angle is its plane's position times
 // theta_scale^i as the F32 product chain, the plane picked by the sector rule (sections 11, 11, 10, 0).
-__device__ __forceinline__ void norm_rope(float (&y)[4], const float * src, const float * w, const int32_t * pos,
-                                          int32_t stride, int32_t col, float ts, int32_t lane) {
-    const float4 x = reinterpret_cast<const float4 *>(src)[lane];
+// Split in three for callers that issue the loads early: rope_pos (the lane's plane position), rope_angle (the lane's
+// pair angle as sin / cos, shared by every row at one position), norm_rope_apply (the norm and rotation of a loaded row).
+__device__ __forceinline__ int32_t rope_plane(int32_t lane) {
+    const int32_t sector = lane & 31;
+    return sector % 3 == 1 && sector < 33   ? 1
+           : sector % 3 == 2 && sector < 30 ? 2
+           : sector % 3 == 0 && sector < 33 ? 0
+                                            : 3;
+}
+
+__device__ __forceinline__ int32_t rope_pos(const int32_t * pos, int32_t stride, int32_t col, int32_t lane) {
+    return pos[rope_plane(lane) * stride + col];
+}
+
+// lane i < 32 forms pair i's angle
+__device__ __forceinline__ void rope_angle(float & s, float & c, int32_t p, float ts, int32_t lane) {
+    const int32_t sector = lane & 31;
+    float theta = static_cast<float>(p);
+#pragma unroll
+    for (int32_t i = 0; i < kNRot / 2 - 1; ++i) {
+        theta = i < sector ? theta * ts : theta;
+    }
+    s = 0.0f;
+    c = 0.0f;
+    sincosf(theta, &s, &c);
+}
+
+__device__ __forceinline__ void norm_rope_apply(float (&y)[4], const float4 x, const float4 g, float s, float c,
+                                                int32_t lane) {
     float ss = x.x * x.x;
     ss = __builtin_fmaf(x.y, x.y, ss);
     ss = __builtin_fmaf(x.z, x.z, ss);
@@ -30,24 +56,10 @@ __device__ __forceinline__ void norm_rope(float (&y)[4], const float * src, cons
         ss += __shfl_xor(ss, o, 64);
     }
     const float r = 1.0f / sqrtf(ss * (1.0f / 256.0f) + kRmsEps);
-    const float4 g = reinterpret_cast<const float4 *>(w)[lane];
     y[0] = x.x * r * g.x;
     y[1] = x.y * r * g.y;
     y[2] = x.z * r * g.z;
     y[3] = x.w * r * g.w;
-    // lane i < 32 forms pair i's angle
-    const int32_t sector = lane & 31;
-    const int32_t plane = sector % 3 == 1 && sector < 33   ? 1
-                          : sector % 3 == 2 && sector < 30 ? 2
-                          : sector % 3 == 0 && sector < 33 ? 0
-                                                           : 3;
-    float theta = static_cast<float>(pos[plane * stride + col]);
-#pragma unroll
-    for (int32_t i = 0; i < kNRot / 2 - 1; ++i) {
-        theta = i < sector ? theta * ts : theta;
-    }
-    float s = 0.0f, c = 0.0f;
-    sincosf(theta, &s, &c);
     // dims 0..31 sit in lanes 0..7, their partners 32..63 in lanes 8..15
 #pragma unroll
     for (int32_t e = 0; e < 4; ++e) {
@@ -61,6 +73,15 @@ __device__ __forceinline__ void norm_rope(float (&y)[4], const float * src, cons
             y[e] = other * se + y[e] * ce;
         }
     }
+}
+
+__device__ __forceinline__ void norm_rope(float (&y)[4], const float * src, const float * w, const int32_t * pos,
+                                          int32_t stride, int32_t col, float ts, int32_t lane) {
+    const float4 x = reinterpret_cast<const float4 *>(src)[lane];
+    const float4 g = reinterpret_cast<const float4 *>(w)[lane];
+    float s, c;
+    rope_angle(s, c, rope_pos(pos, stride, col, lane), ts, lane);
+    norm_rope_apply(y, x, g, s, c, lane);
 }
 
 __device__ __forceinline__ uint2 pack4_f16(const float (&x)[4], float scale) {

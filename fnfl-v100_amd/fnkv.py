@@ -23,7 +23,7 @@ EXPORTS = [
     "fnkv_export_q8_0", "fnkv_decode_workspace_bytes", "fnkv_attn_decode", "fnkv_prefill_workspace_bytes",
     "fnkv_attn_prefill", "fnkv_pool_create_fmt", "fnkv_pool_format", "fnkv_export_kv8",
     "fnkv_sparse_workspace_bytes", "fnkv_attn_sparse", "fnkv_rope_theta_scale", "fnkv_datc_part_bytes",
-    "fnkv_datc_prepare", "fnkv_datc_attend", "fnkv_qsa_workspace_bytes", "fnkv_qsa_attend",
+    "fnkv_datc_prepare", "fnkv_datc_attend", "fnkv_datc_step", "fnkv_qsa_workspace_bytes", "fnkv_qsa_attend",
 ]
 DATC_HEADS = 12
 DATC_QSTRIDE = 512
@@ -131,6 +131,8 @@ def lib():
         L.fnkv_datc_prepare.argtypes = [I32, ctypes.POINTER(DatcPrepareArgs), P]
         L.fnkv_datc_attend.restype = ctypes.c_int
         L.fnkv_datc_attend.argtypes = [ctypes.POINTER(DatcAttendArgs), P]
+        L.fnkv_datc_step.restype = ctypes.c_int
+        L.fnkv_datc_step.argtypes = [ctypes.POINTER(DatcPrepareArgs), ctypes.POINTER(DatcAttendArgs), P]
         _lib = L
     return _lib
 
@@ -363,3 +365,14 @@ def datc_attend(*, q16, qfull, k_cache, v_cache, n_before, part, out, codes, sca
                        k_cache.shape[0] if max_cells is None else max_cells, _p(part), _p(out), _p(codes),
                        _p(scales), _p(err), _p(body))
     return check(lib().fnkv_datc_attend(ctypes.byref(a), _stream(stream)))
+
+
+def datc_step(*, kv_k, kv_v, k_norm, q_norm, qfull, n_before, pos, stride, k_cache, v_cache, q16, part, out, codes,
+              scales, err, row0=0, q_f32=None, k_f32=None, body=None, theta_scale=None, stream=None):
+    """fnkv_datc_step: the prepare of row row0 (q from qfull's row [12][512]) and its attention in one call."""
+    p = DatcPrepareArgs(_p(qfull), _p(kv_k), _p(kv_v), _p(q_norm), _p(k_norm), _p(n_before), _p(pos), _p(stride),
+                        row0, rope_theta_scale() if theta_scale is None else theta_scale, _p(k_cache), _p(v_cache),
+                        k_cache.shape[0], _p(q16), _p(q_f32), _p(k_f32), _p(err))
+    a = DatcAttendArgs(None, _p(qfull), _p(k_cache), _p(v_cache), _p(n_before), row0, k_cache.shape[0], _p(part),
+                       _p(out), _p(codes), _p(scales), _p(err), _p(body))
+    return check(lib().fnkv_datc_step(ctypes.byref(p), ctypes.byref(a), _stream(stream)))

@@ -269,6 +269,14 @@ int fnkv_datc_prepare(int32_t rows, const fnkv_datc_prepare_args * a, void * str
 /* datc_attend (draft.h:244, datc.cu:582-604): two launches (the split attention, then the fold with the gate) */
 int fnkv_datc_attend(const fnkv_datc_attend_args * a, void * stream);
 
+/* The draft step row as one call: datc_prepare(1, p) then datc_attend(a) in stream order (draft.h:47-78, the
+ * contract and its publication by the kernel boundary), in two launches instead of three: the attention forms the
+ * row's q itself and its one reading wave writes the row's K / V before reading them. Outputs (q16, q_f32, k_f32, the
+ * caches' new cell, out, codes, scales) bitwise those of the two calls. p and a name the same caches, depth word,
+ * max_cells and row0; a->q16 is not read. A refusal of either (the row's cell at or past max_cells, row0 past *stride,
+ * a body not made at this depth) sets FNKV_DEV_ERR_DRAFT_DEPTH and writes nothing. */
+int fnkv_datc_step(const fnkv_datc_prepare_args * p, const fnkv_datc_attend_args * a, void * stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -264,3 +264,90 @@ def test_host_refusals(card):
         fnkv.datc_attend(row0=4, body=body, **att)
     with pytest.raises(fnkv.FnkvError):  # 32-bit cache offsets
         fnkv.datc_attend(max_cells=1 << 22, **att)
+
+
+def run_step(c, n_before, row0, stride, inp, fused):
+    """The step row: fnkv_datc_step, or prepare then attend (the reference's sequence)."""
+    d = c["dev"]
+    nb = torch.tensor([n_before], dtype=torch.int32, device="cuda")
+    st = torch.tensor([stride], dtype=torch.int32, device="cuda")
+    pos = torch.from_numpy(inp["pos"]).cuda()
+    qfull = torch.from_numpy(inp["qfull"]).cuda()
+    kvk = torch.from_numpy(inp["kv_k"]).cuda()
+    kvv = torch.from_numpy(inp["kv_v"]).cuda()
+    body = torch.from_numpy(inp["body"].view(np.int32)).cuda() if inp["body"] is not None else None
+    d["out"].view(torch.int32).fill_(-1)
+    d["q16"].zero_()
+    d["err"].zero_()
+    cell = n_before + row0
+    if cell < CELLS:
+        d["kc"][cell] = 0x7F7F
+        d["vc"][cell] = 0x7F7F
+    common = dict(kv_k=kvk, kv_v=kvv, k_norm=d["kn"], n_before=nb, pos=pos, stride=st, k_cache=d["kc"],
+                  v_cache=d["vc"], err=d["err"], row0=row0, theta_scale=c["ts"])
+    if fused:
+        fnkv.datc_step(q_norm=d["qn"], qfull=qfull, q16=d["q16"], part=d["part"], out=d["out"], codes=d["codes"],
+                       scales=d["scales"], q_f32=d["qf32"], k_f32=d["kf32"], body=body, **common)
+    else:
+        fnkv.datc_prepare(1, qfull=qfull, q_norm=d["qn"], q16=d["q16"], q_f32=d["qf32"], k_f32=d["kf32"], **common)
+        fnkv.datc_attend(q16=d["q16"], qfull=qfull, k_cache=d["kc"], v_cache=d["vc"], n_before=nb, part=d["part"],
+                         out=d["out"], codes=d["codes"], scales=d["scales"], err=d["err"], row0=row0, body=body)
+    torch.cuda.synchronize()
+    o = {"err": int(d["err"].item()) & 0xFFFFFFFF}
+    for k in ("out", "codes", "scales", "q16", "qf32", "kf32"):
+        o[k] = d[k].cpu().numpy().copy()
+    o["q16"] = o["q16"][:1]
+    o["qf32"] = o["qf32"][:1]
+    o["kf32"] = o["kf32"][:1]
+    if cell < CELLS:
+        o["k_new"] = d["kc"][cell].cpu().numpy().copy()
+        o["v_new"] = d["vc"][cell].cpu().numpy().copy()
+    return o
+
+
+@pytest.mark.parametrize("n_before,row0,sparse", [(0, 0, False), (63, 1, False), (4095, 0, False),
+                                                   (58580, 2, False), (196607, 0, False), (7, 1, True),
+                                                   (9217, 3, True), (131070, 2, True)])
+def test_fused_step_matches_prepare_then_attend(card, n_before, row0, sparse):
+    print(f"datc fused step n_before {n_before} row0 {row0} sparse {sparse}", flush=True)
+    inp = make_inputs(card, n_before, 1, 4, True, sparse, row0)
+    two = run_step(card, n_before, row0, 4, inp, fused=False)
+    one = run_step(card, n_before, row0, 4, inp, fused=True)
+    assert two["err"] == 0 and one["err"] == 0
+    for k in ("out", "codes", "scales", "q16", "qf32", "kf32", "k_new", "v_new"):
+        assert np.array_equal(np.asarray(one[k]).view(np.uint8), np.asarray(two[k]).view(np.uint8)), k
+
+
+def test_fused_step_refusals(card):
+    # the row's cell past the caches, row0 past the round's rows, a body not made at this depth: the error bit, no
+    # output, no cell written
+    for n_before, row0, stride, sparse, bad_k in ((CELLS - 1, 1, 4, False, 0), (100, 2, 2, False, 0),
+                                                  (3000, 1, 4, True, 1)):
+        inp = make_inputs(card, n_before, 1, stride, False, sparse, row0, bad_k=bad_k)
+        o = run_step(card, n_before, row0, stride, inp, fused=True)
+        assert o["err"] == ERR
+        assert np.all(o["out"].view(np.uint32) == 0xFFFFFFFF), "output written"
+        if "k_new" in o:
+            assert np.all(o["k_new"].view(np.uint16) == 0x7F7F), "cell written"
+
+
+def test_fused_step_host_refusals(card):
+    d = card["dev"]
+    nb = torch.zeros(1, dtype=torch.int32, device="cuda")
+    st = torch.ones(1, dtype=torch.int32, device="cuda")
+    pos = torch.zeros((4, 1), dtype=torch.int32, device="cuda")
+    kv = torch.zeros((1, HD), dtype=torch.float32, device="cuda")
+    qfull = torch.zeros((NH, QS), dtype=torch.float32, device="cuda")
+    args = dict(kv_k=kv, kv_v=kv, k_norm=d["kn"], q_norm=d["qn"], n_before=nb, pos=pos, stride=st, k_cache=d["kc"],
+                v_cache=d["vc"], q16=d["q16"], part=d["part"], out=d["out"], codes=d["codes"], scales=d["scales"],
+                err=d["err"])
+    d["out"].view(torch.int32).fill_(-1)
+    with pytest.raises(fnkv.FnkvError):  # no q rows
+        fnkv.datc_step(qfull=None, **args)
+    with pytest.raises(fnkv.FnkvError):  # row0 past the attend's rows
+        fnkv.datc_step(qfull=qfull, row0=5, **args)
+    misaligned = torch.zeros(HD + 1, dtype=torch.float32, device="cuda")[1:]
+    with pytest.raises(fnkv.FnkvError):  # k rows off a 16-byte boundary
+        fnkv.datc_step(qfull=qfull, **{**args, "kv_k": misaligned})
+    torch.cuda.synchronize()
+    assert np.all(d["out"].cpu().numpy().view(np.uint32) == 0xFFFFFFFF), "a refusal enqueued work"
