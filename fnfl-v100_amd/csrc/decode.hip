@@ -40,6 +40,29 @@
 
 namespace fnkv {
 
+// The one-row sparse launch's new cell when the launch prepares its row (fused_prep): K = the F32 RMS norm and IMROPE
+// of kv_k (and k_f32 when asked), V = kv_v, each in the pool's format, by the workgroup that reads the cell's tile.
+template <int WAVES>
+__device__ __forceinline__ void append_owned_cell_fused(const dec_args & a, const int32_t * table, int32_t kvh,
+                                                        int64_t ctx, int32_t mine, int32_t wave, int32_t lane) {
+    if ((mine & 1) != 0 && wave < 2) {
+        const pool_view & pv = a.pv;
+        const int64_t pos = ctx - 1;
+        float x[4];
+        if (wave == 0) {
+            norm_rope(x, a.fp.kv_k + kvh * kHeadDim, a.fp.k_norm, a.fp.pos, 1, 0, a.fp.theta_scale, lane);
+            if (a.fp.k_f32 != nullptr) {
+                reinterpret_cast<float4 *>(a.fp.k_f32 + kvh * kHeadDim)[lane] = make_float4(x[0], x[1], x[2], x[3]);
+            }
+        } else {
+            load4<true>(a.fp.kv_v + kvh * kHeadDim, lane, x);
+        }
+        quantize_store_fmt(x, lane, tile_of(pv, table, a.layer, kvh, pos), static_cast<int32_t>(pos & 31), wave,
+                           pv.format);
+    }
+    __syncthreads();
+}
+
 // A tile group is NT waves sharing one tile stream, wave r of the group computing row tile r (query rows 16 r ..
 // 16 r + 15); a workgroup holds GR groups (8 waves for NT = 1 and 2, 6 for NT = 3: two waves a SIMD).
 template <int NT> struct dec_shape {
@@ -141,8 +164,22 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     // latency each but overlapped, not three in a row.
     half8 qop[kBlocks];
     int64_t lim;
+    float4 xq[2], gq;
+    int32_t pq = 0;
     if constexpr (SP) { // the Q rows' latency hidden behind the selection's build
-        load_q_operands(a, s, kvh, rt, j, qg, qop, lim);
+        if (a.fp.qfull != nullptr) {
+            // forming the rows: wave w takes the KV head's query heads w and w + 8; their inputs load now
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int32_t h = wave + 8 * i;
+                xq[i] = h < a.G ? reinterpret_cast<const float4 *>(a.fp.qfull + (kvh * a.G + h) * 512)[lane]
+                                : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            gq = reinterpret_cast<const float4 *>(a.fp.q_norm)[lane];
+            pq = rope_pos(a.fp.pos, 1, 0, lane);
+        } else {
+            load_q_operands(a, s, kvh, rt, j, qg, qop, lim);
+        }
     }
     split_src<SP> src;
     src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * kGroupLds);
@@ -153,7 +190,39 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     FNKV_STAMP(0);
 
     if constexpr (SP) {
-        append_owned_cells<WAVES>(a, table, kvh, ctx, src.new_mine, wave, lane);
+        if (a.fp.qfull != nullptr) {
+            // the KV head's query rows as fp16 in LDS (after the tile buffers and the selection slice), then each
+            // lane's operands from there; split 0 also writes the F32 rows
+            uint16_t * ql = reinterpret_cast<uint16_t *>(smem + GR * kGroupLds + kSelSlice);
+            float sn, cs;
+            rope_angle(sn, cs, pq, a.fp.theta_scale, lane);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int32_t h = wave + 8 * i;
+                if (h < a.G) {
+                    float y[4];
+                    norm_rope_apply(y, xq[i], gq, sn, cs, lane);
+                    reinterpret_cast<uint2 *>(ql + h * kHeadDim)[lane] = pack4_f16(y, 1.0f);
+                    if (split == 0 && a.fp.q_f32 != nullptr) {
+                        reinterpret_cast<float4 *>(a.fp.q_f32 + (kvh * a.G + h) * kHeadDim)[lane] =
+                            make_float4(y[0], y[1], y[2], y[3]);
+                    }
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int b = 0; b < kBlocks; ++b) {
+                u32x4 v = {0, 0, 0, 0};
+                if (j < a.G) {
+                    v = *reinterpret_cast<const u32x4 *>(ql + j * kHeadDim + b * kQK + 8 * qg);
+                }
+                qop[b] = __builtin_bit_cast(half8, v);
+            }
+            lim = ctx - 1;
+            append_owned_cell_fused<WAVES>(a, table, kvh, ctx, src.new_mine, wave, lane);
+        } else {
+            append_owned_cells<WAVES>(a, table, kvh, ctx, src.new_mine, wave, lane);
+        }
     } else {
         append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, src.g0, a.strided ? src.stride : 0, wave, lane);
     }
@@ -883,7 +952,7 @@ int32_t decode_lds(int32_t nt, bool sp) {
         constexpr int32_t waves = dec_shape<1>::WAVES;
         const int32_t tiles = dec_shape<1>::GR * kGroupLds;
         const int32_t merge = waves * 16 * 2 * 4 + waves * 16 * (kHeadDim + 4) * 4;
-        return sp ? std::max(std::max(tiles + kSelSlice, merge), kSelLds) : std::max(tiles, merge);
+        return sp ? std::max(std::max(tiles + kSelSlice + kFusedQLds, merge), kSelLds) : std::max(tiles, merge);
     }
     if (nt == 2) {
         return sp ? rows_lds<2, true>() : rows_lds<2, false>();

@@ -19,6 +19,21 @@ constexpr int32_t kCodeBytes = 16384;  // a tile's K and V codes
 constexpr int32_t kScaleBytes = 1024;  // a tile's K and V scales
 constexpr int32_t kGroupLds = kCodeBytes + 2 * kScaleBytes;
 
+// A one-row sparse launch that prepares its own row (fnkv_qsa_attend at T = 1): the attend's inputs. Each workgroup
+// forms its KV head's query rows (F32 RMS norm and IMROPE, fp16) while its selection builds, and the workgroup that
+// reads the new cell's tile writes the cell's K (normed, roped) and V in the pool's format.
+struct fused_prep {
+    const float * qfull = nullptr; // [hq][512]: each head's q, then its gate; null: the launch reads q
+    const float * kv_k = nullptr;  // [h_kv][256]
+    const float * kv_v = nullptr;  // [h_kv][256]
+    const float * q_norm = nullptr;
+    const float * k_norm = nullptr;
+    const int32_t * pos = nullptr; // [4][1]
+    float theta_scale = 0.0f;
+    float * q_f32 = nullptr; // optional [hq][256]
+    float * k_f32 = nullptr; // optional [h_kv][256]
+};
+
 struct dec_args {
     pool_view pv;
     const uint16_t * q; // fp16 [n_seq][T][hq][256]
@@ -41,6 +56,7 @@ struct dec_args {
     const uint32_t * sel_body;
     int32_t * sel_n;
     int32_t sel_split;
+    fused_prep fp;
 #ifdef FNKV_TIMING
     uint64_t * ts; // per workgroup: 16 real-time stamps (instrumented builds only)
 #endif
@@ -429,7 +445,9 @@ struct sparse_gate {
 int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq, float scale,
                   const void * q, const void * body, const void * offsets, const void * k_new, const void * v_new,
                   int32_t new_dtype, void * out, const sparse_gate * gate, void * ws, int64_t ws_bytes,
-                  hipStream_t st, const char * who);
+                  hipStream_t st, const char * who, const fused_prep * fp = nullptr);
+// LDS of the one-row sparse launch's formed query rows (after the tile buffers and the selection slice)
+constexpr int32_t kFusedQLds = 16 * kHeadDim * 2;
 
 __device__ __forceinline__ int32_t seq_of(const dec_args & a, int32_t split) {
     int32_t s = 0;

@@ -19,6 +19,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 #include <string>
 
 namespace fnkv {
@@ -125,6 +126,23 @@ int fnkv_qsa_attend(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t
         (reinterpret_cast<uintptr_t>(offsets) & 3) != 0) {
         set_error("fnkv_qsa_attend: rows, heads, layer or cells outside the contract");
         return FNKV_ERR_ARG;
+    }
+    // one row of at most 16 query heads a KV head: the sparse launch prepares the row itself (one launch fewer);
+    // FNKV_QSA_TWO_KERNELS=1 keeps the separate prepare launch, for comparison
+    const char * two = std::getenv("FNKV_QSA_TWO_KERNELS");
+    if (T == 1 && G <= 16 && (two == nullptr || std::atoi(two) == 0)) {
+        fnkv::fused_prep fp;
+        fp.qfull = qfull;
+        fp.kv_k = kv_k;
+        fp.kv_v = kv_v;
+        fp.q_norm = q_norm;
+        fp.k_norm = k_norm;
+        fp.pos = pos;
+        fp.theta_scale = theta_scale;
+        fp.q_f32 = q_f32;
+        fp.k_f32 = k_f32;
+        return fnkv::sparse_launch(pool, slot, depth, T, layer, hq, 1.0f / 16.0f, q16, body, offsets, kv_k, kv_v,
+                                   FNKV_F32, nullptr, &gate, ws, sp, st, "fnkv_qsa_attend", &fp);
     }
     const fnkv::pool_view pv = p->view();
     fnkv::qsa_prep_args pa = {pv, pv.table + int64_t(slot) * pv.table_stride, layer, depth, qfull, kv_k, kv_v, q_norm,

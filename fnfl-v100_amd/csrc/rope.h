@@ -33,7 +33,10 @@ __device__ __forceinline__ int32_t rope_pos(const int32_t * pos, int32_t stride,
 }
 
 // lane i < 32 forms pair i's angle
+// The arithmetic is as written in every file that includes this (no contraction of a * b + c into one rounding, whatever
+// the file's flags), so every launch that prepares a row computes the same bits.
 __device__ __forceinline__ void rope_angle(float & s, float & c, int32_t p, float ts, int32_t lane) {
+#pragma clang fp contract(off)
     const int32_t sector = lane & 31;
     float theta = static_cast<float>(p);
 #pragma unroll
@@ -47,6 +50,7 @@ __device__ __forceinline__ void rope_angle(float & s, float & c, int32_t p, floa
 
 __device__ __forceinline__ void norm_rope_apply(float (&y)[4], const float4 x, const float4 g, float s, float c,
                                                 int32_t lane) {
+#pragma clang fp contract(off)
     float ss = x.x * x.x;
     ss = __builtin_fmaf(x.y, x.y, ss);
     ss = __builtin_fmaf(x.z, x.z, ss);

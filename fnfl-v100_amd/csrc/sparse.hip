@@ -26,6 +26,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <string>
 
 namespace fnkv {
@@ -44,7 +45,10 @@ sparse_plan plan_sparse(const kv_pool & p, int64_t depth, int32_t T, int32_t G) 
     sparse_plan pl;
     const int32_t n_tiles = static_cast<int32_t>((depth + T + kTileTokens - 1) / kTileTokens);
     pl.n_max = std::min(n_tiles, kSelTopBlocks + 1); // a row's blocks' tiles and its tail's
-    const int32_t want = std::max(1, device_cus(p.device()) / (p.h_kv() * T));
+    int32_t want = std::max(1, device_cus(p.device()) / (p.h_kv() * T));
+    if (const char * e = std::getenv("FNKV_SPARSE_WANT")) { // splits a row and head, for measurement
+        want = std::max(1, std::atoi(e));
+    }
     pl.per_split = std::min(64, std::max(1, (pl.n_max + want - 1) / want));
     pl.n_splits = (pl.n_max + pl.per_split - 1) / pl.per_split;
     auto up16 = [](int64_t x) { return (x + 15) & ~int64_t(15); };
@@ -60,7 +64,7 @@ sparse_plan plan_sparse(const kv_pool & p, int64_t depth, int32_t T, int32_t G) 
 int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq, float scale,
                   const void * q, const void * body, const void * offsets, const void * k_new, const void * v_new,
                   int32_t new_dtype, void * out, const sparse_gate * gate, void * ws, int64_t ws_bytes,
-                  hipStream_t st, const char * who) {
+                  hipStream_t st, const char * who, const fused_prep * fp) {
     const kv_pool * p = pool_of(pool);
     const std::string name(who);
     if (p == nullptr || slot < 0 || slot >= p->pages().n_slots() || T <= 0 || T > kSelMaxRows || depth < 0 ||
@@ -129,6 +133,13 @@ int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T
     a.sel_body = static_cast<const uint32_t *>(body);
     a.sel_n = reinterpret_cast<int32_t *>(w);
     a.sel_split = pl.per_split;
+    if (fp != nullptr) {
+        if (T != 1 || G > 16) {
+            set_error(name + ": a launch that prepares its row takes one row of at most 16 query heads a KV head");
+            return FNKV_ERR_ARG;
+        }
+        a.fp = *fp;
+    }
 #ifdef FNKV_TIMING
     a.ts = timing_buffer();
 #endif
