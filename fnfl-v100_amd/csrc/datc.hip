@@ -217,16 +217,21 @@ __device__ __forceinline__ u32x2 lds_read_tr4(const uint8_t * p) {
 // V in vbuf), the scores, the online softmax (m, l of head lane % 16), O^T rescaled and accumulated. The two LDS
 // buffers are distinct restrict pointers here, which tells the compiler that the reads of vbuf do not depend on the
 // copies into vnext: it then waits for this tile's copies only, not for the next tile's.
-template <bool SP, bool NEXT>
+// STEP: kIssueNext (issue the next tile, then wait for this one), kNextIssued (the next tile is already in flight:
+// wait for this one), kLast (no next tile: wait for everything)
+constexpr int kIssueNext = 0, kNextIssued = 1, kLast = 2;
+template <bool SP, int STEP>
 __device__ __forceinline__ void tile_step(const fnkv_datc_attend_args & a, const datc_shape & s, rsrc_t rk, rsrc_t rv,
                                           const k_tile & kt, k_tile & kn, const uint8_t * __restrict__ vbuf,
                                           uint8_t * __restrict__ vnext, int32_t base, int32_t next_base,
                                           const half8 (&qb)[8], float & m_run, float & l_run, floatx4 (&o)[16],
                                           int32_t lane) {
     // the next tile's loads go out before anything of this step (the scheduler may not sink them below the scores)
-    if constexpr (NEXT) {
+    if constexpr (STEP == kIssueNext) {
         issue_tile<SP>(a, s, rk, rv, next_base, kn, vnext, lane);
         __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<32>();
+    } else if constexpr (STEP == kNextIssued) {
         wait_vmcnt<32>();
     } else {
         wait_vmcnt<0>();
@@ -301,10 +306,11 @@ __device__ __forceinline__ void tile_step(const fnkv_datc_attend_args & a, const
 // wave without tiles issues the empty tile, zeros and no memory traffic, so the waits for the q inputs count past the
 // tile's loads instead of draining them at a branch join), then the heads are formed into LDS while it is in flight.
 // The V buffer and the q rows are distinct LDS regions (restrict), so the q writes need not wait for the V copies.
-template <bool SP>
+template <bool SP, bool TWO>
 __device__ __forceinline__ void fused_first_tile(const fnkv_datc_attend_args & a, const fnkv_datc_prepare_args & pa,
-                                                 const datc_shape & s, rsrc_t rk, rsrc_t rv, int32_t base, k_tile & kt,
-                                                 uint8_t * __restrict__ vbuf, uint16_t * __restrict__ ql,
+                                                 const datc_shape & s, rsrc_t rk, rsrc_t rv, int32_t base,
+                                                 int32_t base1, k_tile & kt, k_tile & kt1, uint8_t * __restrict__ vbuf,
+                                                 uint8_t * __restrict__ vbuf1, uint16_t * __restrict__ ql,
                                                  half8 (&qb)[8], int32_t b, int32_t wave, int32_t lane) {
     constexpr int32_t kPer = kHeads / kWaves;
     float4 xq[kPer];
@@ -316,6 +322,9 @@ __device__ __forceinline__ void fused_first_tile(const fnkv_datc_attend_args & a
     const int32_t pq = rope_pos(pa.pos, *pa.stride, pa.row0, lane);
     __builtin_amdgcn_sched_barrier(0);
     issue_tile<SP>(a, s, rk, rv, base, kt, vbuf, lane);
+    if constexpr (TWO) {
+        issue_tile<SP>(a, s, rk, rv, base1, kt1, vbuf1, lane);
+    }
     __builtin_amdgcn_sched_barrier(0);
     float sn, cs;
     rope_angle(sn, cs, pq, pa.theta_scale, lane);
@@ -406,9 +415,42 @@ __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend_kernel(fnkv_datc_a
     // before the first tile (FUSED: formed after the first tile's loads are issued)
     half8 qb[8];
     k_tile ka, kb;
+    // one tile in flight while the other is computed; in the loop every step issues its 32 loads (the wave's last
+    // pair may take an empty tile: cells beyond the row, zeros, no memory traffic) and the loop runs whole pairs, so a
+    // step waits for exactly the loads issued before the last 32; an odd last tile is a step of its own that issues
+    // nothing
+    float m_run = -INFINITY, l_run = 0.0f;
+    floatx4 o[16];
+#pragma unroll
+    for (int32_t db = 0; db < 16; ++db) {
+        o[db] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
     if constexpr (FUSED) {
-        fused_first_tile<SP>(a, pa, s, rk, rv, tile_base(0), ka, vb0, reinterpret_cast<uint16_t *>(smem + kQLds), qb,
-                             b, wave, lane);
+        // a wave with two tiles or more also issues its second before forming q, then tile 0's step issues nothing
+        // and the walk goes on from tile 1 with the buffers' roles swapped; a wave with one tile (or none: the empty
+        // tile) issues only that (an empty second tile's copies measured slower at shallow depths). Each path runs
+        // to its end on its own, so the compiler's wait counts never merge two paths' outstanding loads.
+        if (cnt > 1) {
+            fused_first_tile<SP, true>(a, pa, s, rk, rv, tile_base(0), tile_base(1), ka, kb, vb0, vb1,
+                                       reinterpret_cast<uint16_t *>(smem + kQLds), qb, b, wave, lane);
+            tile_step<SP, kNextIssued>(a, s, rk, rv, ka, kb, vb0, vb1, tile_base(0), 0, qb, m_run, l_run, o, lane);
+            int32_t k = 1;
+            for (; k + 1 < cnt; k += 2) {
+                tile_step<SP, kIssueNext>(a, s, rk, rv, kb, ka, vb1, vb0, tile_base(k), tile_base(k + 1), qb, m_run,
+                                          l_run, o, lane);
+                tile_step<SP, kIssueNext>(a, s, rk, rv, ka, kb, vb0, vb1, tile_base(k + 1), tile_base(k + 2), qb,
+                                          m_run, l_run, o, lane);
+            }
+            if (k < cnt) {
+                tile_step<SP, kLast>(a, s, rk, rv, kb, ka, vb1, vb0, tile_base(k), 0, qb, m_run, l_run, o, lane);
+            }
+        } else {
+            fused_first_tile<SP, false>(a, pa, s, rk, rv, tile_base(0), 0, ka, kb, vb0, vb1,
+                                        reinterpret_cast<uint16_t *>(smem + kQLds), qb, b, wave, lane);
+            if (cnt == 1) {
+                tile_step<SP, kLast>(a, s, rk, rv, ka, kb, vb0, vb1, tile_base(0), 0, qb, m_run, l_run, o, lane);
+            }
+        }
     } else {
         const int32_t h = lane % 16, g = lane / 16;
 #pragma unroll
@@ -420,29 +462,17 @@ __global__ __launch_bounds__(64 * kWaves, 1) void datc_attend_kernel(fnkv_datc_a
             qb[j] = __builtin_bit_cast(half8, v);
         }
     }
-    // one tile in flight while the other is computed; in the loop every step issues its 32 loads (the wave's last
-    // pair may take an empty tile: cells beyond the row, zeros, no memory traffic) and the loop runs whole pairs, so a
-    // step waits for exactly the loads issued before the last 32; an odd last tile is a step of its own that issues
-    // nothing
-    float m_run = -INFINITY, l_run = 0.0f;
-    floatx4 o[16];
-#pragma unroll
-    for (int32_t db = 0; db < 16; ++db) {
-        o[db] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    if (cnt > 0) {
-        if constexpr (!FUSED) {
-            issue_tile<SP>(a, s, rk, rv, tile_base(0), ka, vb0, lane);
-        }
+    if (!FUSED && cnt > 0) {
+        issue_tile<SP>(a, s, rk, rv, tile_base(0), ka, vb0, lane);
         int32_t k = 0;
         for (; k + 1 < cnt; k += 2) {
-            tile_step<SP, true>(a, s, rk, rv, ka, kb, vb0, vb1, tile_base(k), tile_base(k + 1), qb, m_run, l_run, o,
+            tile_step<SP, kIssueNext>(a, s, rk, rv, ka, kb, vb0, vb1, tile_base(k), tile_base(k + 1), qb, m_run, l_run, o,
                                 lane);
-            tile_step<SP, true>(a, s, rk, rv, kb, ka, vb1, vb0, tile_base(k + 1), tile_base(k + 2), qb, m_run, l_run,
+            tile_step<SP, kIssueNext>(a, s, rk, rv, kb, ka, vb1, vb0, tile_base(k + 1), tile_base(k + 2), qb, m_run, l_run,
                                 o, lane);
         }
         if (k < cnt) {
-            tile_step<SP, false>(a, s, rk, rv, ka, kb, vb0, vb1, tile_base(k), 0, qb, m_run, l_run, o, lane);
+            tile_step<SP, kLast>(a, s, rk, rv, ka, kb, vb0, vb1, tile_base(k), 0, qb, m_run, l_run, o, lane);
         }
     }
     wait_vmcnt<0>(); // the last (empty) copies land before the fold below reuses the buffers
