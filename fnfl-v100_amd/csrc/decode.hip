@@ -853,9 +853,9 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
 // independent, so they are in flight together: one memory round trip), then the 32 groups fold in order in LDS
 // (deterministic: the same order for every launch).
 __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
-    __shared__ float sM[32];
-    __shared__ float sL[32];
-    __shared__ floatx4 sA[32][8];
+    __shared__ float sM[4];
+    __shared__ float sL[4];
+    __shared__ floatx4 sA[4][8];
     const int32_t tid = static_cast<int32_t>(threadIdx.x);
     const int32_t c4 = tid & 7, g = tid >> 3;
     const int32_t chunk = static_cast<int32_t>(blockIdx.x) & 7;
@@ -886,24 +886,40 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
         l = __builtin_fmaf(l, f_old, ml.y * f_new);
         m = m_new;
     }
-    sA[g][c4] = A;
-    if (c4 == 0) {
-        sM[g] = m;
-        sL[g] = l;
+    // the 32 groups fold pairwise: the wave's 8 by lane exchange (lanes l, l ^ 8, l ^ 16, l ^ 32 share c4), then the
+    // 4 waves' results in LDS, in wave order
+    auto fold = [](float & m0, float & l0, floatx4 & A0, float m1, float l1, floatx4 A1) {
+        const float mn = fmaxf(m0, m1);
+        const float mu = mn == kNegInf ? 0.0f : mn;
+        const float f0 = __builtin_amdgcn_exp2f(m0 - mu), f1 = __builtin_amdgcn_exp2f(m1 - mu);
+        A0 = A0 * f0 + A1 * f1;
+        l0 = __builtin_fmaf(l0, f0, l1 * f1);
+        m0 = mn;
+    };
+#pragma unroll
+    for (int32_t o = 8; o < 64; o <<= 1) {
+        floatx4 A1;
+#pragma unroll
+        for (int32_t e = 0; e < 4; ++e) {
+            A1[e] = __shfl_xor(A[e], o, 64);
+        }
+        fold(m, l, A, __shfl_xor(m, o, 64), __shfl_xor(l, o, 64), A1);
+    }
+    const int32_t wave = tid >> 6;
+    if ((tid & 63) < 8) {
+        sA[wave][c4] = A;
+        if (c4 == 0) {
+            sM[wave] = m;
+            sL[wave] = l;
+        }
     }
     __syncthreads();
     if (tid < 8) {
-        float M = kNegInf;
-        for (int32_t i = 0; i < 32; ++i) {
-            M = fmaxf(M, sM[i]);
-        }
-        const float M_use = M == kNegInf ? 0.0f : M;
-        floatx4 As = {0.0f, 0.0f, 0.0f, 0.0f};
-        float Ls = 0.0f;
-        for (int32_t i = 0; i < 32; ++i) {
-            const float w = __builtin_amdgcn_exp2f(sM[i] - M_use);
-            As += sA[i][tid] * w;
-            Ls = __builtin_fmaf(sL[i], w, Ls);
+        float Ms = sM[0], Ls = sL[0];
+        floatx4 As = sA[0][tid];
+#pragma unroll
+        for (int32_t w = 1; w < 4; ++w) {
+            fold(Ms, Ls, As, sM[w], sL[w], sA[w][tid]);
         }
         const int32_t t = r / a.G, h = kvh * a.G + r % a.G;
         const int64_t row = (int64_t(s) * a.T + t) * a.hq + h;
