@@ -39,7 +39,7 @@ CONFIGS = {
                  workload="cfg2: 1 seq 262,144 cells, decode T=1, 1 layer, scattered pages"),
     "cfg2v": dict(ctxs=[262144], T=5, layers=1, copies=4,
                   workload="cfg2: 1 seq 262,144 cells, verify T=5, 1 layer, scattered pages"),
-    "cfg0": dict(ctxs=[4096], T=1, layers=1, workload="cfg0: 1 seq 4,096 cells, decode T=1, 1 layer"),
+    "cfg0": dict(ctxs=[4096], T=1, layers=1, copies=64, workload="cfg0: 1 seq 4,096 cells, decode T=1, 1 layer"),
     "cfg3": dict(ctxs=[131072 + 2048], T=2048, layers=1, prefill=True,
                  workload="cfg3: 2,048-token fp16 chunk appended at depth 131,072 and attended causally over 133,120 "
                           "cells (chunked prefill, matrix cores), 1 layer"),
