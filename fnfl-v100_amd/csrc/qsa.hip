@@ -8,6 +8,9 @@
 //      1/16 is applied as the score scale); the new cell's K (the normed, roped k) and V quantized into the pool;
 //   2. the sparse decode launch (each row its own splits);
 //   3. the merge with the gated epilogue.
+// One row of at most 16 query heads a KV head skips step 1: the sparse launch forms its query rows in LDS while its
+// selection builds, and the workgroup that reads the new cell's tile writes the cell (fused_prep, decode.hip), with
+// the same arithmetic (the outputs are bitwise those of the three launches).
 // Differences from the reference's kernel: the query operand is fp16 (the reference keeps q in F32; the attention is
 // held to the same 2e-3 bound as every other launch here), depth is a host value, and the cache is the paged pool.
 #include "../../include/fnkv.h"
