@@ -1,6 +1,7 @@
 """Host-side checks of the C-ABI library, CPU only: it loads, exports every entry point include/fnkv.h declares,
 and its pure host logic (the page rounding and the reclaim choice) gives the reference's known answers
 (fn/runtime/slots_test.cpp:26-84). No GPU call is made here."""
+import ctypes
 import os
 import re
 
@@ -48,3 +49,25 @@ def test_reclaim_victim_known_answers():
 
 def test_page_block_bytes():
     assert fnkv.lib().fnkv_page_block_bytes() == 8 * 17408
+
+
+def test_draft_entries_refuse_missing_arguments_on_the_host():
+    # the DA-TC entries check their arguments before any device call: null structs, or structs with null pointers,
+    # are refused with the contract error and a message (draft.h:47-78: rejected, nothing enqueued)
+    L = fnkv.lib()
+    assert L.fnkv_datc_prepare(1, None, None) == fnkv.ERR_ARG
+    assert L.fnkv_datc_attend(None, None) == fnkv.ERR_ARG
+    assert L.fnkv_datc_step(None, None, None) == fnkv.ERR_ARG
+    assert "fnkv_datc_step" in fnkv.last_error()
+    p = fnkv.DatcPrepareArgs()
+    a = fnkv.DatcAttendArgs()
+    p.row0, a.row0 = 0, 1
+    assert L.fnkv_datc_step(ctypes.byref(p), ctypes.byref(a), None) == fnkv.ERR_ARG
+
+
+def test_rope_theta_scale_is_the_f32_power():
+    # theta_scale = powf(1e7, -2 / 64) (attend.cu:830-832), the F32 rounding of the exact value
+    import numpy as np
+    got = np.float32(fnkv.rope_theta_scale())
+    want = np.float32(10000000.0 ** (-2.0 / 64.0))
+    assert abs(float(got) - float(want)) <= float(np.spacing(want))
