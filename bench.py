@@ -158,7 +158,7 @@ def _counter_means(out_dir):
     return {k: sums[k] / counts[k] for k in sums}
 
 
-def measure_traffic(argv):
+def measure_traffic(argv, kernels=("decode", "merge_kernel")):
     """HBM bytes of one fnkv_attn_decode launch (decode + merge kernels) from two rocprofv3 counter passes over a child
     run of the same workload: FETCH_SIZE, then WRITE_SIZE (KiB a dispatch), each scaled by bytes / reading of the
     same counter for the calibration copy of known size in the same child. Runs before this process touches the GPU.
@@ -180,8 +180,8 @@ def measure_traffic(argv):
         shutil.rmtree(out_dir, ignore_errors=True)
         if r.returncode != 0 or not means:
             return None, f"{counter} pass failed ({r.returncode})"
-        launch = sum(v for k, v in means.items() if "decode" in k and "fnkv" in k)
-        launch += sum(v for k, v in means.items() if "merge_kernel" in k)
+        # the launch's kernels (one dispatch each a launch): the fnkv kernels whose names hold one of `kernels`
+        launch = sum(v for k, v in means.items() if "fnkv" in k and any(n in k for n in kernels))
         copy = [v for k, v in means.items() if "neg" in k.lower()]
         if not copy or copy[0] <= 0 or launch <= 0:
             return None, f"{counter}: kernels not found in the counter output"
@@ -547,6 +547,11 @@ def run_datc(args, cfg):
     a step. Every cell comes from HBM: the steps rotate over copies of the caches totalling over 1 GB (the reference's
     warm bench rotates over 200 MB for the V100's 6 MB L2; MI355X's last-level cache is 256 MB). Algorithmic bytes a
     step: K and V of the cells (1,024 B a cell), the prepare's inputs and outputs, the attend's q16, gates and outputs."""
+    traffic, traffic_detail = None, "skipped (--no-traffic)"
+    if not args.traffic_child and not args.no_traffic:
+        passthrough = [x for x in sys.argv[1:] if x not in ("--no-cpu",)]
+        traffic, traffic_detail = measure_traffic(passthrough, ("datc_attend_kernel", "datc_fold_kernel",
+                                                                "datc_prepare_kernel"))
     import numpy as np
     import torch
 
@@ -591,6 +596,9 @@ def run_datc(args, cfg):
     for i in range(copies):
         step(i)
     torch.cuda.synchronize()
+    if args.traffic_child:
+        traffic_child(args, torch, lambda: step(0))
+        return
     # one graph holds `copies` steps, one on each copy of the caches (the reference's bench times graphs of n_copy
     # steps, fn/kernels/draft/draft_bench.cu:250-292); K steps = ceil(K / copies) replays
     replays = max(1, -(-args.steps // copies))
@@ -663,7 +671,8 @@ def run_datc(args, cfg):
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_detail": traffic_detail,
             "bytes_per_launch": bytes_step,
             "launch_us": round(step_s * 1e6, 3),
             "reference_floor_v100_us": round(1.95 + n * 1024 / 1021.6e3, 2),
