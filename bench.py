@@ -35,6 +35,9 @@ PEAK_HBM_GBS = 8000.0
 CONFIGS = {
     "cfg1": dict(ctxs=[8192, 16384, 32768, 65536], T=3, layers=12,
                  workload="cfg1: 4 seqs 8K/16K/32K/64K, verify T=3, 12 layers, shared Q8_0 pool, permuted pages"),
+    "cfg1kv8": dict(ctxs=[8192, 16384, 32768, 65536], T=3, layers=12, fmt="kv8",
+                    workload="cfg1 on a KV8 pool (FNFL's group-64 8-bit format, fn/quant/kv_q8_ref.cpp): 4 seqs "
+                             "8K/16K/32K/64K, verify T=3, 12 layers, permuted pages"),
     "cfg2": dict(ctxs=[262144], T=1, layers=1, copies=4,
                  workload="cfg2: 1 seq 262,144 cells, decode T=1, 1 layer, scattered pages"),
     "cfg2v": dict(ctxs=[262144], T=5, layers=1, copies=4,
@@ -78,9 +81,9 @@ def algorithmic_bytes(ctxs, T):
     return kv_read + qo + append
 
 
-def make_pool(torch, fnkv, cases, ctxs, T, layers, seed, h_kv=HKV):
+def make_pool(torch, fnkv, cases, ctxs, T, layers, seed, h_kv=HKV, fmt=None):
     n_pages = sum(-(-c // 256) for c in ctxs) + 16
-    pool = fnkv.Pool(len(ctxs) + 1, n_pages, layers, h_kv)
+    pool = fnkv.Pool(len(ctxs) + 1, n_pages, layers, h_kv, **({} if fmt is None else {"fmt": fmt}))
     slots = list(range(len(ctxs)))
     cases.scatter_ensure(pool, slots, ctxs, seed, churn=0.2)
     g = torch.Generator(device="cuda")
@@ -758,7 +761,8 @@ def main():
     # several steps as it is over a many-layer step (cfg1's 12 layers)
     copies = cfg.get("copies", 1) if not args.no_graph else 1
     torch.cuda.set_device(0)
-    pool, slots = make_pool(torch, fnkv, cases, ctxs, T, layers * copies, args.seed)
+    fmt = fnkv.FMT_KV8 if cfg.get("fmt") == "kv8" else None
+    pool, slots = make_pool(torch, fnkv, cases, ctxs, T, layers * copies, args.seed, fmt=fmt)
     g = torch.Generator(device="cuda")
     g.manual_seed(args.seed + 7)
     n = len(ctxs)
@@ -829,10 +833,12 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q8_0 KV (int8 codes + fp16 scales), fp16 Q/O, fp32 accumulate",
+        "dtype": ("kv8 KV (int8 codes + fp16 group-64 scales)" if fmt is not None else
+                  "q8_0 KV (int8 codes + fp16 scales)") + ", fp16 Q/O, fp32 accumulate",
         "data": "synthetic (seeded N(0,1) K/V with 4 of 256 channels x8, N(0,1) Q)",
         "config": {"workload": workload, "contexts": ctxs, "T": T, "layers": layers, "q_heads": HQ,
                    "kv_heads": HKV, "head_dim": D, "page_tokens": 256, "hip_graph": graph is not None,
+                   "pool_format": cfg.get("fmt", "q8_0"),
                    "steps_per_graph": copies, "layers_rotated": layers * copies},
         "gb_s": round(bytes_layer * layers * n_steps / wall / 1e9, 3),
         "roofline": {
