@@ -136,7 +136,9 @@ template <int NT> __device__ __forceinline__ void group_sync() {
     }
 }
 
-template <int NT, bool SP>
+// KV8 (the pool's format is FNFL's group-64 rule): a scale serves two 32-value blocks, so the score MFMAs of a group
+// chain and P x (V scale) is formed once a group.
+template <int NT, bool SP, bool KV8 = false>
 __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(dec_args a_in) {
     const dec_args a = SP ? sparse_row_view(a_in) : a_in;
     if constexpr (SP) {
@@ -288,7 +290,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         const int64_t tok0 = src.tok0(ti);
 
         floatx4 sc[2];
-        tile_scores(kb, sc_tile, [&](int b) { return qop[b]; }, sig, j, qg, lane, sc);
+        tile_scores<KV8>(kb, sc_tile, [&](int b) { return qop[b]; }, sig, j, qg, lane, sc);
 
         // ---- online softmax (base 2); P stays in the registers that feed the PV MFMA ----
         const int64_t lim_rel64 = lim - tok0;
@@ -327,11 +329,13 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
             lv = mfma16(sva, pfh, lv);
             lv = mfma16(sva, pfl, lv);
         }
+        half8 ph, pl;
 #pragma unroll
         for (int ld = 0; ld < 8; ++ld) {
-            const half8 vs = *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + ld * 16);
-            half8 ph, pl;
-            scale_hilo(pf, pfh, vs, ph, pl);
+            if (!KV8 || (ld & 1) == 0) { // KV8: block ld + 1 shares block ld's scale
+                const half8 vs = *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + ld * 16);
+                scale_hilo(pf, pfh, vs, ph, pl);
+            }
             const half8 va0 = widen8_biased(vreg[ld][0], vreg[ld][1]);
             const half8 va1 = widen8_biased(vreg[ld][2], vreg[ld][3]);
             acc[2 * ld] = mfma16(va0, ph, acc[2 * ld]);
@@ -452,7 +456,7 @@ template <int NT, bool SP = false> struct rows_shape {
     static constexpr int WAIT_V = 2 * CK + NBM;
 };
 
-template <int NT, bool SP>
+template <int NT, bool SP, bool KV8 = false>
 __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_rows_kernel(dec_args a_in) {
     const dec_args a = SP ? sparse_row_view(a_in) : a_in;
     using SH = rows_shape<NT, SP>;
@@ -605,7 +609,7 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
         const uint8_t * sc_tile = kb + kCodeBytes / 2 - kKScales; // scale offsets are tile-relative
         const int64_t tok0 = src.tok0(grp + k * GR);
         floatx4 sc[2];
-        tile_scores(kb, sc_tile, qop_lds, sig, j, qg, lane, sc);
+        tile_scores<KV8>(kb, sc_tile, qop_lds, sig, j, qg, lane, sc);
         const int64_t lim_rel64 = lim - tok0;
         const int32_t lim_rel = lim_rel64 > 64 ? 64 : static_cast<int32_t>(lim_rel64 < -1 ? -1 : lim_rel64);
         float pf[8];
@@ -648,16 +652,19 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
             lv[rt] = mfma16(sva, ph[rt], lv[rt]);
             lv[rt] = mfma16(sva, pl[rt], lv[rt]);
         }
+        half8 hi[NT], lo[NT];
 #pragma unroll
         for (int32_t i = 0; i < NBM; ++i) {
             if (i < nb) {
-                const half8 vs = *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + (b0 + i) * 16);
                 const half8 va0 = widen8_biased(vb[i][0], vb[i][1]);
                 const half8 va1 = widen8_biased(vb[i][2], vb[i][3]);
-                half8 hi[NT], lo[NT];
+                // KV8: an odd block shares the scale of the block before it (when this wave holds both)
+                if (!KV8 || ((b0 + i) & 1) == 0 || i == 0) {
+                    const half8 vs = *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + (b0 + i) * 16);
 #pragma unroll
-                for (int32_t rt = 0; rt < NT; ++rt) {
-                    scale_hilo_pk(ph[rt], pl[rt], vs, hi[rt], lo[rt]);
+                    for (int32_t rt = 0; rt < NT; ++rt) {
+                        scale_hilo_pk(ph[rt], pl[rt], vs, hi[rt], lo[rt]);
+                    }
                 }
                 // the hi terms of every row tile, then the lo terms: dependent MFMAs 2 NT apart
 #pragma unroll
@@ -1051,7 +1058,28 @@ void launch_merge(const merge_args & m, hipStream_t st) {
     hipLaunchKernelGGL(merge_kernel, dim3(static_cast<uint32_t>(m.n_seq * m.h_kv * m.R * 8)), dim3(256), 0, st, m);
 }
 
-// the decode kernel for NT row tiles (sparse or dense), its LDS attribute set once per device
+template <bool SP, bool KV8> void set_decode_attrs() {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<1, SP, KV8>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(1, SP));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<2, SP, KV8>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(2, SP));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<3, SP, KV8>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3, SP));
+}
+
+template <bool SP, bool KV8> void launch_decode_fmt(int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
+    if (NT == 1) {
+        hipLaunchKernelGGL((decode_kernel<1, SP, KV8>), grid, dim3(64 * dec_shape<1>::WAVES), decode_lds(1, SP), st, a);
+    } else if (NT == 2) {
+        hipLaunchKernelGGL((decode_rows_kernel<2, SP, KV8>), grid, dim3(64 * rows_shape<2, SP>::WAVES),
+                           decode_lds(2, SP), st, a);
+    } else {
+        hipLaunchKernelGGL((decode_rows_kernel<3, SP, KV8>), grid, dim3(64 * rows_shape<3, SP>::WAVES),
+                           decode_lds(3, SP), st, a);
+    }
+}
+
+// the decode kernel for NT row tiles (sparse or dense) and the pool's format, its LDS attribute set once per device
 template <bool SP> void launch_decode(const kv_pool & p, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
     static bool attr_set[64] = {false};
     const int32_t dev = p.device();
@@ -1059,24 +1087,16 @@ template <bool SP> void launch_decode(const kv_pool & p, int32_t NT, dim3 grid, 
         int32_t cur = 0;
         (void)hipGetDevice(&cur);
         (void)hipSetDevice(dev);
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<1, SP>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(1, SP));
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<2, SP>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(2, SP));
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<3, SP>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3, SP));
+        set_decode_attrs<SP, false>();
+        set_decode_attrs<SP, true>();
         (void)hipGetLastError();
         (void)hipSetDevice(cur);
         attr_set[dev] = true;
     }
-    if (NT == 1) {
-        hipLaunchKernelGGL((decode_kernel<1, SP>), grid, dim3(64 * dec_shape<1>::WAVES), decode_lds(1, SP), st, a);
-    } else if (NT == 2) {
-        hipLaunchKernelGGL((decode_rows_kernel<2, SP>), grid, dim3(64 * rows_shape<2, SP>::WAVES), decode_lds(2, SP),
-                           st, a);
+    if (a.pv.format == kFormatKV8) {
+        launch_decode_fmt<SP, true>(NT, grid, a, st);
     } else {
-        hipLaunchKernelGGL((decode_rows_kernel<3, SP>), grid, dim3(64 * rows_shape<3, SP>::WAVES), decode_lds(3, SP),
-                           st, a);
+        launch_decode_fmt<SP, false>(NT, grid, a, st);
     }
 }
 

@@ -570,7 +570,9 @@ __device__ __forceinline__ half8 q_sums(const half8 (&qop)[kBlocks], int32_t qg)
 // S^T = K Q^T for one 16-token half h of a tile from its K codes (kb) and scales (sc_tile + kKScales ...) in LDS:
 // the returned r-th value is the score of token 16 h + 4 qg + r against this lane's row j, unscaled (q . k).
 // The Q operand of block b comes from qop(b): registers, or LDS where registers are short.
-template <typename QOP>
+// PAIR (KV8 pools): the two blocks of a 64-value group share one scale, so their MFMAs chain into one result and
+// the scale applies once a group.
+template <typename QOP, bool PAIR = false>
 __device__ __forceinline__ floatx4 tile_scores_half(const uint8_t * kb, const uint8_t * sc_tile, const QOP & qop,
                                                     half8 sig, int32_t j, int32_t qg, int32_t lane, int32_t h) {
     const half8 zero8 = {};
@@ -594,14 +596,28 @@ __device__ __forceinline__ floatx4 tile_scores_half(const uint8_t * kb, const ui
             for (int bb = 0; bb < 2; ++bb) {
                 const int b = 2 * ld + bb;
                 const half8 ka = widen8_biased(kw[2 * bb], kw[2 * bb + 1]);
-                t[b - 4 * hb] = mfma16(ka, qop(b), floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+                if constexpr (PAIR) { // group ld = blocks 2 ld, 2 ld + 1 (one 1 KiB chunk)
+                    t[ld - 2 * hb] = mfma16(ka, qop(b), bb == 0 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : t[ld - 2 * hb]);
+                } else {
+                    t[b - 4 * hb] = mfma16(ka, qop(b), floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+                }
             }
         }
+        if constexpr (PAIR) {
 #pragma unroll
-        for (int b = 4 * hb; b < 4 * hb + 4; ++b) {
+            for (int ld = 2 * hb; ld < 2 * hb + 2; ++ld) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                acc_s[r] = __builtin_fmaf(static_cast<float>(ks[r][b]), t[b - 4 * hb][r], acc_s[r]);
+                for (int r = 0; r < 4; ++r) {
+                    acc_s[r] = __builtin_fmaf(static_cast<float>(ks[r][2 * ld]), t[ld - 2 * hb][r], acc_s[r]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int b = 4 * hb; b < 4 * hb + 4; ++b) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    acc_s[r] = __builtin_fmaf(static_cast<float>(ks[r][b]), t[b - 4 * hb][r], acc_s[r]);
+                }
             }
         }
     }
@@ -614,12 +630,12 @@ __device__ __forceinline__ floatx4 tile_scores_half(const uint8_t * kb, const ui
 }
 
 // both halves: sc[h][r] is the score of token 16 h + 4 qg + r against this lane's row j
-template <typename QOP>
+template <bool PAIR = false, typename QOP>
 __device__ __forceinline__ void tile_scores(const uint8_t * kb, const uint8_t * sc_tile, const QOP & qop, half8 sig,
                                             int32_t j, int32_t qg, int32_t lane, floatx4 (&sc)[2]) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        sc[h] = tile_scores_half(kb, sc_tile, qop, sig, j, qg, lane, h);
+        sc[h] = tile_scores_half<QOP, PAIR>(kb, sc_tile, qop, sig, j, qg, lane, h);
         __builtin_amdgcn_sched_barrier(0); // one half's operands live at a time
     }
 }
