@@ -12,7 +12,9 @@ What pins each oracle function (oracle/fnkv_oracle.c):
   or_reclaim_victim    the same file's reclaim answers
   or_attn_f64          closed forms (one visible key returns its V row; q = 0 returns the visible rows' mean; equal
                        keys give the mean), brute force by numpy on tiny inputs, and key-order invariance
-  or_attn_ggml         the fp64 form within 2e-3 (fp32 Q) on a seeded BASELINE-shaped case
+  or_attn_ggml         closed forms (one visible cell returns its V row; q = 0 the visible rows' mean; a dominant
+                       key its V row; the head mapping; causality as a shorter context) and the fp64 form within 2e-3
+                       (fp32 Q) on a seeded BASELINE-shaped case
 DA-TC (oracle.py):
   act_quantize         the reference's act_quantize_ref (fn/quant/act_ref.cpp) outputs, bitwise (golden: seeded rows,
                        exact ties, zero / subnormal / huge / NaN / inf runs)
@@ -209,6 +211,48 @@ def test_attn_ggml_path_within_tolerance():
     got8 = O.attn_ggml(q16, kb, vb, n, q_as_q8=True, threads=4).view(np.float16).astype(np.float64)
     # Q itself quantized to Q8_0 (ggml's vec_dot operand): a documented divergence of ~2.6e-2 here, bounded loosely
     assert np.abs(got8 - ref).max() <= 5e-2
+
+
+def _ggml_case(rng, n, T, hq=4, hkv=2, d=64):
+    x = rng.standard_normal((2, n, hkv, d)).astype(np.float16).astype(np.float32)
+    kq, kd = O.q8_0_quantize(x[0])
+    vq, vd = O.q8_0_quantize(x[1])
+    kb = O.to_block_q8_0(kq, kd).reshape(n, hkv, d // 32, 34)
+    vb = O.to_block_q8_0(vq, vd).reshape(n, hkv, d // 32, 34)
+    return kb, vb, O.q8_0_dequantize(kq, kd), O.q8_0_dequantize(vq, vd)
+
+
+def test_attn_ggml_closed_forms():
+    # the ggml-semantics path pinned where the mathematics fixes the answer (its source is not in the checkout):
+    # one visible cell returns that cell's decoded V row (rounded to fp16); q = 0 weighs the visible rows equally
+    # (their mean); a key far above the others returns its V row; heads map to KV heads by h // (hq / hkv); query t of
+    # T sees cells 0 .. n - T + t (causal)
+    rng = np.random.default_rng(15)
+    hq, hkv, d = 4, 2, 64
+    kb, vb, kdec, vdec = _ggml_case(rng, 9, 1, hq, hkv, d)
+    q16 = rng.standard_normal((1, hq, d)).astype(np.float16).view(np.uint16)
+    got = O.attn_ggml(q16, kb, vb, 1, hkv=hkv).view(np.float16)
+    for h in range(hq):
+        assert np.array_equal(got[0, h], vdec[0, h // 2].astype(np.float16))
+    z = np.zeros_like(q16)
+    got = O.attn_ggml(z, kb, vb, 9, hkv=hkv).view(np.float16).astype(np.float64)
+    for h in range(hq):
+        mean = vdec[:9, h // 2].astype(np.float64).mean(axis=0)
+        assert np.abs(got[0, h] - mean).max() <= np.abs(mean).max() * 2.0 ** -10 + 1e-6
+    # a dominant key: q along key 5 of KV head 0, scaled so its score leads the others by > 30 (weights below e^-30)
+    kd0 = kdec[5, 0].astype(np.float64)
+    qd = (kd0 / np.linalg.norm(kd0) * 200.0).astype(np.float16)
+    qh = np.zeros((1, hq, d), np.float16)
+    qh[0, 0] = qd
+    s = (kdec[:9, 0].astype(np.float64) @ qd.astype(np.float64)) / 16.0
+    assert s[5] - np.delete(s, 5).max() > 30.0
+    got = O.attn_ggml(qh.view(np.uint16), kb, vb, 9, hkv=hkv).view(np.float16)
+    assert np.abs(got[0, 0].astype(np.float64) - vdec[5, 0]).max() <= np.abs(vdec[5, 0]).max() * 2.0 ** -10
+    # causality: with T = 3 queries the first sees 7 of 9 cells, the same as a 7-cell context with one query
+    q3 = rng.standard_normal((3, hq, d)).astype(np.float16).view(np.uint16)
+    a = O.attn_ggml(q3, kb, vb, 9, hkv=hkv).view(np.uint16)
+    b = O.attn_ggml(q3[:1], kb, vb, 7, hkv=hkv).view(np.uint16)
+    assert np.array_equal(a[0], b[0])
 
 
 def test_attn_f64_cells_pinned_by_the_dense_form():
