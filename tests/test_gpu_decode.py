@@ -237,3 +237,14 @@ def test_split_walks_contiguous_and_strided(T, strided, monkeypatch):
         (_, _, kf), (_, _, vf) = cases.decoded(O, k16, v16)
         assert cases.out_err(got[i], O.attn_f64(q16[i].view(np.uint16), kf, vf, c)) <= TOL
 
+
+
+@pytest.mark.parametrize("T", [1, 3, 5])
+def test_eight_sequences_at_split_edges(T):
+    # the most sequences a launch takes (FNKV_MAX_SEQS), their contexts at and around the split sizes the planner
+    # picks (1,024 / 2,048 cells) and the 32-cell tile and 256-cell page edges
+    ctxs = [1024, 2048, 2049, 4096, 6143, 10240, 20481, 40000]
+    st = Setup(ctxs, seed=30 + T, churn=0.25)
+    q16 = cases.queries(40 + T, (len(ctxs), T, HQ, 256))
+    got = st.run(q16, T)
+    assert st.check(q16, got, T) <= TOL
