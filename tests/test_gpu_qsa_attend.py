@@ -215,3 +215,10 @@ def test_one_row_prepared_in_the_sparse_launch(depth, hq, h_kv, fmt, monkeypatch
     two, one = once(True), once(False)
     for a, b in zip(two, one):
         assert np.array_equal(np.asarray(a).view(np.uint8), np.asarray(b).view(np.uint8))
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_many_heads_a_kv_head(T):
+    # 32 query heads on one KV head: the row kernels' sparse instantiation, and at T = 1 the separate prepare launch
+    # (the sparse launch prepares its own row only up to 16 heads a KV head)
+    run_case(4000 - T, T, 32, 1, seed=300 + T, planes=True)

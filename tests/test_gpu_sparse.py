@@ -32,16 +32,18 @@ def _decoded(k16, v16, fmt):
     return kf, vf
 
 
-def sparse_case(depth, T, seed, clustered=False, fmt=fnkv.FMT_Q8_0, body=None, new_cells=True):
+def sparse_case(depth, T, seed, clustered=False, fmt=fnkv.FMT_Q8_0, body=None, new_cells=True, hq=None, hkv=None):
+    hq = HQ if hq is None else hq
+    hkv = HKV if hkv is None else hkv
     ctx = depth + T
-    pool = fnkv.Pool(2, -(-ctx // 256) + 8, 1, HKV, fmt=fmt)
+    pool = fnkv.Pool(2, -(-ctx // 256) + 8, 1, hkv, fmt=fmt)
     cases.scatter_ensure(pool, [0], [ctx], seed, churn=0.3)
-    k16, v16 = cases.kv_rows(seed, ctx, HKV)
+    k16, v16 = cases.kv_rows(seed, ctx, hkv)
     upto = depth if new_cells else ctx
     if upto:
         pool.append(0, 0, 0, torch.from_numpy(k16[:upto]).cuda(), torch.from_numpy(v16[:upto]).cuda())
     words, offs, cells = O.qsa_body(depth, T, seed, clustered) if body is None else body
-    q16 = cases.queries(seed + 1, (T, HQ, D))
+    q16 = cases.queries(seed + 1, (T, hq, D))
     q = torch.from_numpy(q16).cuda()
     out = torch.full_like(q, float("nan"))
     kn = torch.from_numpy(k16[depth:]).cuda() if new_cells else None
@@ -69,6 +71,15 @@ def test_sparse_deep_selection(T, clustered):
     # 512 of ~4,000 whole blocks a row: most tiles hold one selected block, the rows' selections differ
     depth = 16003 - T
     pool, got, ref, _ = sparse_case(depth, T, seed=40 + T + (10 if clustered else 0), clustered=clustered)
+    assert np.isfinite(got).all()
+    assert cases.out_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("hq,T", [(32, 1), (32, 3), (48, 2), (48, 5)])
+def test_sparse_many_heads_a_kv_head(hq, T):
+    # more than 16 query heads on one KV head: each row's heads take two or three 16-row tiles (the row kernels'
+    # sparse instantiation); up to 48 (FNKV_MAX_ROWS)
+    pool, got, ref, _ = sparse_case(3001 - T, T, seed=90 + hq + T, hq=hq, hkv=1)
     assert np.isfinite(got).all()
     assert cases.out_err(got, ref) <= TOL
 
