@@ -416,7 +416,7 @@ int fnkv_attn_prefill(const fnkv_pool * pool, int32_t slot, int32_t layer, int64
     }
     const int32_t G = hq / p->h_kv();
     if (fnkv::kPfRows % G != 0) {
-        set_error("fnkv_attn_prefill: the GQA group must divide 128");
+        set_error("fnkv_attn_prefill: the GQA group must divide 256");
         return FNKV_ERR_ARG;
     }
     if ((reinterpret_cast<uintptr_t>(q) & 15) != 0 || (reinterpret_cast<uintptr_t>(out) & 7) != 0) {

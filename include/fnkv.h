@@ -196,7 +196,8 @@ int64_t fnkv_prefill_workspace_bytes(const fnkv_pool * pool, int64_t ctx, int32_
  * V as its codes against P x V-scale in hi + lo fp16 (the reference's prompt attention rounds its operands to fp16
  * once, qsa_prompt.h:55-58; this keeps ~22 bits a product). q: fp16 [rows][hq][256], out: fp16 [rows][hq][256].
  * ws: fnkv_prefill_workspace_bytes bytes of device memory (no zeroing needed) for the key-split partials when the
- * query rows alone do not fill the device; null (or smaller): one split, no workspace. */
+ * query rows alone do not fill the device; null (or smaller): one split, no workspace. The GQA group hq / h_kv must
+ * divide 256 (a workgroup's query rows). */
 int fnkv_attn_prefill(const fnkv_pool * pool, int32_t slot, int32_t layer, int64_t ctx, int32_t rows, int32_t hq,
                       float scale, const void * q, void * out, void * ws, int64_t ws_bytes, void * stream);
 

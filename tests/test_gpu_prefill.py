@@ -22,16 +22,16 @@ def gpu():
         pytest.skip("no GPU")
 
 
-def prefill_case(depth, rows, seed, check_rows):
+def prefill_case(depth, rows, seed, check_rows, hq=HQ, hkv=HKV):
     ctx = depth + rows
-    pool = fnkv.Pool(2, -(-ctx // 256) + 4, 1, HKV)
+    pool = fnkv.Pool(2, -(-ctx // 256) + 4, 1, hkv)
     cases.scatter_ensure(pool, [0], [ctx], seed, churn=0.3)
-    k16, v16 = cases.kv_rows(seed, ctx, HKV)
+    k16, v16 = cases.kv_rows(seed, ctx, hkv)
     kt, vt = torch.from_numpy(k16).cuda(), torch.from_numpy(v16).cuda()
     if depth:
         pool.append(0, 0, 0, kt[:depth].contiguous(), vt[:depth].contiguous())
     pool.append(0, 0, depth, kt[depth:].contiguous(), vt[depth:].contiguous())  # the chunk
-    q16 = cases.queries(seed, (rows, HQ, 256))
+    q16 = cases.queries(seed, (rows, hq, 256))
     q = torch.from_numpy(q16).cuda()
     out = torch.empty_like(q)
     pool.prefill(0, 0, ctx, q, out)
@@ -47,6 +47,16 @@ def prefill_case(depth, rows, seed, check_rows):
 def test_prefill_small(depth, rows):
     check = list(range(rows))
     _, got, err, _ = prefill_case(depth, rows, seed=depth + rows, check_rows=check)
+    assert np.isfinite(got).all()
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 1), (8, 2), (32, 1)])
+def test_prefill_other_head_groups(hq, hkv):
+    # GQA groups of 16, 4 and 32 query heads a KV head (the workgroup's 256 rows then hold 16, 64 or 8 tokens)
+    depth, rows = 700, 90
+    check = list(range(rows))
+    _, got, err, _ = prefill_case(depth, rows, seed=500 + hq + hkv, check_rows=check, hq=hq, hkv=hkv)
     assert np.isfinite(got).all()
     assert err <= TOL
 
