@@ -15,10 +15,19 @@
 
 namespace fnkv {
 
+// pos_dev set: the first position is the device word *pos_dev, read by the launch; a position outside
+// 0 .. max_cells - rows writes nothing (the launch that reads the rows reports it)
 template <bool F32>
 __global__ __launch_bounds__(256) void append_kernel(pool_view pv, int32_t slot, int32_t layer, int64_t pos0,
                                                      int32_t rows, const void * __restrict__ kin,
-                                                     const void * __restrict__ vin) {
+                                                     const void * __restrict__ vin, const int32_t * pos_dev,
+                                                     int64_t max_cells) {
+    if (pos_dev != nullptr) {
+        pos0 = *pos_dev;
+        if (pos0 < 0 || pos0 + rows > max_cells) {
+            return;
+        }
+    }
     const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
     const int64_t w = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
     const int32_t kv = static_cast<int32_t>(w & 1);
@@ -92,6 +101,20 @@ __global__ __launch_bounds__(256) void export_kv8_kernel(pool_view pv, int32_t s
     }
 }
 
+int append_enqueue(const kv_pool & p, int32_t slot, int32_t layer, int64_t pos0, const int32_t * pos_dev,
+                   int64_t max_cells, int32_t rows, const void * k, const void * v, int32_t dtype, hipStream_t st) {
+    const int64_t waves = int64_t(rows) * p.h_kv() * 2;
+    const uint32_t grid = static_cast<uint32_t>((waves + 3) / 4);
+    if (dtype == FNKV_F32) {
+        hipLaunchKernelGGL(append_kernel<true>, dim3(grid), dim3(256), 0, st, p.view(), slot, layer, pos0, rows, k, v,
+                           pos_dev, max_cells);
+    } else {
+        hipLaunchKernelGGL(append_kernel<false>, dim3(grid), dim3(256), 0, st, p.view(), slot, layer, pos0, rows, k,
+                           v, pos_dev, max_cells);
+    }
+    return hipGetLastError() == hipSuccess ? FNKV_OK : FNKV_ERR_HIP;
+}
+
 } // namespace fnkv
 
 using fnkv::set_error;
@@ -119,17 +142,8 @@ int fnkv_q8_append(fnkv_pool * pool, int32_t slot, int32_t layer, int64_t pos0, 
                   std::to_string(p->mapped_cells(slot)) + ")");
         return FNKV_ERR_ARG;
     }
-    const int64_t waves = int64_t(rows) * p->h_kv() * 2;
-    const uint32_t grid = static_cast<uint32_t>((waves + 3) / 4);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (dtype == FNKV_F32) {
-        hipLaunchKernelGGL(fnkv::append_kernel<true>, dim3(grid), dim3(256), 0, st, p->view(), slot, layer, pos0, rows,
-                           k, v);
-    } else {
-        hipLaunchKernelGGL(fnkv::append_kernel<false>, dim3(grid), dim3(256), 0, st, p->view(), slot, layer, pos0,
-                           rows, k, v);
-    }
-    if (hipGetLastError() != hipSuccess) {
+    if (fnkv::append_enqueue(*p, slot, layer, pos0, nullptr, 0, rows, k, v, dtype,
+                             static_cast<hipStream_t>(stream)) != FNKV_OK) {
         set_error("fnkv_q8_append: launch failed");
         return FNKV_ERR_HIP;
     }

@@ -142,6 +142,9 @@ template <int NT, bool SP, bool KV8 = false>
 __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(dec_args a_in) {
     const dec_args a = SP ? sparse_row_view(a_in) : a_in;
     if constexpr (SP) {
+        if (sparse_refused(a)) {
+            return;
+        }
         FNKV_STAMP(8); // the wave stamps (8..) are not taken in sparse launches
     }
     constexpr int GR = dec_shape<NT>::GR;
@@ -156,7 +159,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     const int32_t kvh = static_cast<int32_t>(blockIdx.y);
     const int32_t s = SP ? 0 : seq_of(a, split); // a sparse launch is one sequence (constant: no scratch copy of a)
     const int32_t sp = split - a.split0[s];
-    const int64_t ctx = a.ctx[s];
+    const int64_t ctx = seq_ctx<SP>(a, s);
     const int64_t begin = int64_t(sp) * a.split_tokens;
     const int64_t end = ctx < begin + a.split_tokens ? ctx : begin + a.split_tokens;
     const pool_view & pv = a.pv;
@@ -180,11 +183,14 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
             gq = reinterpret_cast<const float4 *>(a.fp.q_norm)[lane];
             pq = rope_pos(a.fp.pos, 1, 0, lane);
         } else {
-            load_q_operands(a, s, kvh, rt, j, qg, qop, lim);
+            load_q_operands(a, s, ctx, kvh, rt, j, qg, qop, lim);
         }
     }
     split_src<SP> src;
-    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * kGroupLds);
+    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * kGroupLds, ctx);
+    if (refused<SP>(a, s, ctx, sp, kvh)) {
+        return;
+    }
     const int32_t n_tiles = src.n_tiles;
     if (SP && n_tiles == 0) {
         return; // past the selection's tiles (the merge reads only the splits that hold some)
@@ -230,7 +236,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     }
     FNKV_STAMP(1);
     if constexpr (!SP) {
-        load_q_operands(a, s, kvh, rt, j, qg, qop, lim);
+        load_q_operands(a, s, ctx, kvh, rt, j, qg, qop, lim);
     }
 
     floatx4 acc[16];
@@ -459,6 +465,11 @@ template <int NT, bool SP = false> struct rows_shape {
 template <int NT, bool SP, bool KV8 = false>
 __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_rows_kernel(dec_args a_in) {
     const dec_args a = SP ? sparse_row_view(a_in) : a_in;
+    if constexpr (SP) {
+        if (sparse_refused(a)) {
+            return;
+        }
+    }
     using SH = rows_shape<NT, SP>;
     constexpr int GR = SH::GR, WAVES = SH::WAVES, SK = SH::SK, NBM = SH::NBM, CK = SH::CK;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -471,7 +482,7 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
     const int32_t kvh = static_cast<int32_t>(blockIdx.y);
     const int32_t s = SP ? 0 : seq_of(a, split); // a sparse launch is one sequence (constant: no scratch copy of a)
     const int32_t sp = split - a.split0[s];
-    const int64_t ctx = a.ctx[s];
+    const int64_t ctx = seq_ctx<SP>(a, s);
     const int64_t begin = int64_t(sp) * a.split_tokens;
     const int64_t end = ctx < begin + a.split_tokens ? ctx : begin + a.split_tokens;
     const pool_view & pv = a.pv;
@@ -488,10 +499,14 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
     constexpr bool kQReg = NT == 2;
     half8 qreg[kBlocks];
     if constexpr (SP) { // the Q rows' latency hidden behind the selection's build
-        load_q_operands(a, s, kvh, w, j, qg, qreg, lim);
+        load_q_operands(a, s, ctx, kvh, w, j, qg, qreg, lim);
     }
     split_src<SP, NT == 2> src; // NT = 3 is short of registers: its entries stay in LDS
-    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * SH::GROUP_LDS + SH::Q_LDS);
+    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * SH::GROUP_LDS + SH::Q_LDS,
+                                  ctx);
+    if (refused<SP>(a, s, ctx, sp, kvh)) {
+        return;
+    }
     const int32_t n_tiles = src.n_tiles;
     if (SP && n_tiles == 0) {
         return; // past the selection's tiles (the merge reads only the splits that hold some)
@@ -506,7 +521,7 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
 
     uint8_t * const qlds = smem + GR * SH::GROUP_LDS; // [row tile][block][lane] 16 B
     if constexpr (!SP) {
-        load_q_operands(a, s, kvh, w, j, qg, qreg, lim);
+        load_q_operands(a, s, ctx, kvh, w, j, qg, qreg, lim);
     }
     auto qop_lds = [&](int b) {
         if constexpr (kQReg) {
@@ -873,6 +888,21 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
     const int32_t s = rest / a.h_kv;
     const int32_t s0 = a.split0[s];
     int32_t n = a.split0[s + 1] - s0;
+    if (a.ctx_dev != nullptr) { // a device context: a refused sequence is left as it was; strided splits past
+                                // its tiles held nothing
+        const int64_t c = a.ctx_dev[s];
+        if (c < a.T_dev || c > a.cap[s]) {
+            return;
+        }
+        const int64_t tiles = (c + kTileTokens - 1) / kTileTokens;
+        n = tiles < n ? static_cast<int32_t>(tiles) : n;
+    }
+    if (a.depth_dev != nullptr) {
+        const int64_t d = *a.depth_dev;
+        if (d < 0 || d + a.T_dev > a.cap[0]) {
+            return;
+        }
+    }
     if (a.sel_n != nullptr) { // a sparse launch: only the splits that hold selected tiles ran
         const int32_t S = sparse_split_size(a.sel_n[s], n);
         const int32_t used = (a.sel_n[s] + S - 1) / S;
@@ -1116,6 +1146,119 @@ uint64_t * timing_buffer() { return g_timing; }
 }
 #endif
 
+namespace fnkv {
+
+// The dense decode launch: ctx holds each sequence's context (ctx_dev null) or the host's bound on the device word
+// ctx_dev[i] (then the splits stride over the sequence's tiles, so every depth up to the bound spreads over the same
+// grid, and a context outside T .. bound sets FNKV_DEV_ERR_DEPTH in *err and writes nothing for that sequence).
+int decode_launch(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx,
+                  const int64_t * ctx_dev, uint32_t * err, int32_t T, int32_t layer, int32_t hq, float scale,
+                  const void * q, const void * k_new, const void * v_new, int32_t new_dtype, void * out, void * ws,
+                  int64_t ws_bytes, hipStream_t st, const char * who) {
+    const std::string name(who);
+    const kv_pool * p = pool_of(pool);
+    if (p == nullptr || n_seq <= 0 || n_seq > FNKV_MAX_SEQS || slots == nullptr || ctx == nullptr || T <= 0 ||
+        layer < 0 || layer >= p->layers() || hq <= 0 || hq % p->h_kv() != 0 || q == nullptr || out == nullptr ||
+        ws == nullptr || !(scale > 0.0f) || !std::isfinite(scale) || ((k_new == nullptr) != (v_new == nullptr)) ||
+        (new_dtype != FNKV_F16 && new_dtype != FNKV_F32)) {
+        set_error(name + ": argument outside the contract");
+        return FNKV_ERR_ARG;
+    }
+    const int32_t G = hq / p->h_kv();
+    const int32_t R = G * T;
+    if (R > FNKV_MAX_ROWS) {
+        set_error(name + ": G * T = " + std::to_string(R) + " exceeds " + std::to_string(FNKV_MAX_ROWS));
+        return FNKV_ERR_ARG;
+    }
+    if ((reinterpret_cast<uintptr_t>(q) & 15) != 0 || (reinterpret_cast<uintptr_t>(out) & 15) != 0 ||
+        (reinterpret_cast<uintptr_t>(ws) & 15) != 0) {
+        set_error(name + ": q, out and ws must be 16-byte aligned");
+        return FNKV_ERR_ARG;
+    }
+    for (int32_t i = 0; i < n_seq; ++i) {
+        if (slots[i] < 0 || slots[i] >= p->pages().n_slots() || ctx[i] < T || ctx[i] > p->mapped_cells(slots[i])) {
+            set_error(name + ": sequence " + std::to_string(i) + " (slot " + std::to_string(slots[i]) + ", " +
+                      (ctx_dev != nullptr ? "bound " : "ctx ") + std::to_string(ctx[i]) +
+                      ") outside the slot's mapped cells");
+            return FNKV_ERR_ARG;
+        }
+        // with the new cells written by the launch, two sequences in one slot would write the same cells
+        for (int32_t k = 0; k < i && k_new != nullptr; ++k) {
+            if (slots[k] == slots[i]) {
+                set_error(name + ": slot " + std::to_string(slots[i]) + " appears twice in a launch that appends");
+                return FNKV_ERR_ARG;
+            }
+        }
+    }
+    const dec_plan pl = plan_decode(*p, n_seq, ctx, R);
+    if (ws_bytes < pl.po_bytes + pl.pml_bytes) {
+        set_error(name + ": workspace too small");
+        return FNKV_ERR_ARG;
+    }
+    dec_args a;
+    a.pv = p->view();
+    a.q = static_cast<const uint16_t *>(q);
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.new_f32 = new_dtype == FNKV_F32 ? 1 : 0;
+    a.po = static_cast<float *>(ws);
+    a.pml = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + pl.po_bytes);
+    a.c2 = scale * 1.4426950408889634f;
+    a.layer = layer;
+    a.T = T;
+    a.G = G;
+    a.hq = hq;
+    a.R = R;
+    a.n_seq = n_seq;
+    a.split_tokens = pl.split_tokens;
+    a.strided = ctx_dev != nullptr ? 1 : pl.strided;
+    a.sel_body = nullptr;
+    a.sel_n = nullptr;
+    a.sel_split = 0;
+    a.ctx_dev = ctx_dev;
+    a.err = err;
+    for (int32_t i = 0; i < FNKV_MAX_SEQS; ++i) {
+        a.slot[i] = i < n_seq ? slots[i] : 0;
+        a.ctx[i] = i < n_seq ? ctx[i] : 0;
+    }
+    for (int32_t i = 0; i <= FNKV_MAX_SEQS; ++i) {
+        a.split0[i] = i <= n_seq ? pl.split0[i] : pl.total;
+    }
+#ifdef FNKV_TIMING
+    a.ts = g_timing;
+#endif
+    const dim3 grid(static_cast<uint32_t>(pl.total), static_cast<uint32_t>(p->h_kv()));
+    launch_decode<false>(*p, (R + 15) / 16, grid, a, st);
+    merge_args m;
+    m.po = a.po;
+    m.pml = a.pml;
+    m.out = static_cast<uint16_t *>(out);
+    m.T = T;
+    m.G = G;
+    m.hq = hq;
+    m.R = R;
+    m.h_kv = p->h_kv();
+    m.n_seq = n_seq;
+    m.sel_n = nullptr;
+    m.sel_split = 0;
+    m.ctx_dev = ctx_dev;
+    m.T_dev = T;
+    for (int32_t i = 0; i <= FNKV_MAX_SEQS; ++i) {
+        m.split0[i] = a.split0[i];
+    }
+    for (int32_t i = 0; i < FNKV_MAX_SEQS; ++i) {
+        m.cap[i] = a.ctx[i];
+    }
+    launch_merge(m, st);
+    if (hipGetLastError() != hipSuccess) {
+        set_error(name + ": launch failed");
+        return FNKV_ERR_HIP;
+    }
+    return FNKV_OK;
+}
+
+} // namespace fnkv
+
 extern "C" {
 
 int64_t fnkv_decode_workspace_bytes(const fnkv_pool * pool, int32_t n_seq, const int64_t * ctx, int32_t T, int32_t hq) {
@@ -1132,91 +1275,22 @@ int64_t fnkv_decode_workspace_bytes(const fnkv_pool * pool, int32_t n_seq, const
 int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx, int32_t T,
                      int32_t layer, int32_t hq, float scale, const void * q, const void * k_new, const void * v_new,
                      int32_t new_dtype, void * out, void * ws, int64_t ws_bytes, void * stream) {
-    const fnkv::kv_pool * p = fnkv::pool_of(pool);
-    if (p == nullptr || n_seq <= 0 || n_seq > FNKV_MAX_SEQS || slots == nullptr || ctx == nullptr || T <= 0 ||
-        layer < 0 || layer >= p->layers() || hq <= 0 || hq % p->h_kv() != 0 || q == nullptr || out == nullptr ||
-        ws == nullptr || !(scale > 0.0f) || !std::isfinite(scale) || ((k_new == nullptr) != (v_new == nullptr)) ||
-        (new_dtype != FNKV_F16 && new_dtype != FNKV_F32)) {
-        set_error("fnkv_attn_decode: argument outside the contract");
+    return fnkv::decode_launch(pool, n_seq, slots, ctx, nullptr, nullptr, T, layer, hq, scale, q, k_new, v_new,
+                               new_dtype, out, ws, ws_bytes, static_cast<hipStream_t>(stream), "fnkv_attn_decode");
+}
+
+int fnkv_attn_decode_dev(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx,
+                         const int64_t * max_ctx, int32_t T, int32_t layer, int32_t hq, float scale, const void * q,
+                         const void * k_new, const void * v_new, int32_t new_dtype, void * out, void * ws,
+                         int64_t ws_bytes, uint32_t * err, void * stream) {
+    if (ctx == nullptr || err == nullptr || (reinterpret_cast<uintptr_t>(ctx) & 7) != 0 ||
+        (reinterpret_cast<uintptr_t>(err) & 3) != 0) {
+        fnkv::set_error("fnkv_attn_decode_dev: ctx (8-byte aligned) and err (4-byte aligned) device words required");
         return FNKV_ERR_ARG;
     }
-    const int32_t G = hq / p->h_kv();
-    const int32_t R = G * T;
-    if (R > FNKV_MAX_ROWS) {
-        set_error("fnkv_attn_decode: G * T = " + std::to_string(R) + " exceeds " + std::to_string(FNKV_MAX_ROWS));
-        return FNKV_ERR_ARG;
-    }
-    if ((reinterpret_cast<uintptr_t>(q) & 15) != 0 || (reinterpret_cast<uintptr_t>(out) & 15) != 0 ||
-        (reinterpret_cast<uintptr_t>(ws) & 15) != 0) {
-        set_error("fnkv_attn_decode: q, out and ws must be 16-byte aligned");
-        return FNKV_ERR_ARG;
-    }
-    for (int32_t i = 0; i < n_seq; ++i) {
-        if (slots[i] < 0 || slots[i] >= p->pages().n_slots() || ctx[i] < T || ctx[i] > p->mapped_cells(slots[i])) {
-            set_error("fnkv_attn_decode: sequence " + std::to_string(i) + " (slot " + std::to_string(slots[i]) +
-                      ", ctx " + std::to_string(ctx[i]) + ") outside the slot's mapped cells");
-            return FNKV_ERR_ARG;
-        }
-    }
-    const fnkv::dec_plan pl = fnkv::plan_decode(*p, n_seq, ctx, R);
-    if (ws_bytes < pl.po_bytes + pl.pml_bytes) {
-        set_error("fnkv_attn_decode: workspace too small");
-        return FNKV_ERR_ARG;
-    }
-    fnkv::dec_args a;
-    a.pv = p->view();
-    a.q = static_cast<const uint16_t *>(q);
-    a.k_new = k_new;
-    a.v_new = v_new;
-    a.new_f32 = new_dtype == FNKV_F32 ? 1 : 0;
-    a.po = static_cast<float *>(ws);
-    a.pml = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + pl.po_bytes);
-    a.c2 = scale * 1.4426950408889634f;
-    a.layer = layer;
-    a.T = T;
-    a.G = G;
-    a.hq = hq;
-    a.R = R;
-    a.n_seq = n_seq;
-    a.split_tokens = pl.split_tokens;
-    a.strided = pl.strided;
-    a.sel_body = nullptr;
-    a.sel_n = nullptr;
-    a.sel_split = 0;
-    for (int32_t i = 0; i < FNKV_MAX_SEQS; ++i) {
-        a.slot[i] = i < n_seq ? slots[i] : 0;
-        a.ctx[i] = i < n_seq ? ctx[i] : 0;
-    }
-    for (int32_t i = 0; i <= FNKV_MAX_SEQS; ++i) {
-        a.split0[i] = i <= n_seq ? pl.split0[i] : pl.total;
-    }
-#ifdef FNKV_TIMING
-    a.ts = g_timing;
-#endif
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    const dim3 grid(static_cast<uint32_t>(pl.total), static_cast<uint32_t>(p->h_kv()));
-    fnkv::launch_decode<false>(*p, (R + 15) / 16, grid, a, st);
-    fnkv::merge_args m;
-    m.po = a.po;
-    m.pml = a.pml;
-    m.out = static_cast<uint16_t *>(out);
-    m.T = T;
-    m.G = G;
-    m.hq = hq;
-    m.R = R;
-    m.h_kv = p->h_kv();
-    m.n_seq = n_seq;
-    m.sel_n = nullptr;
-    m.sel_split = 0;
-    for (int32_t i = 0; i <= FNKV_MAX_SEQS; ++i) {
-        m.split0[i] = a.split0[i];
-    }
-    fnkv::launch_merge(m, st);
-    if (hipGetLastError() != hipSuccess) {
-        set_error("fnkv_attn_decode: launch failed");
-        return FNKV_ERR_HIP;
-    }
-    return FNKV_OK;
+    return fnkv::decode_launch(pool, n_seq, slots, max_ctx, ctx, err, T, layer, hq, scale, q, k_new, v_new,
+                               new_dtype, out, ws, ws_bytes, static_cast<hipStream_t>(stream),
+                               "fnkv_attn_decode_dev");
 }
 
 } // extern "C"

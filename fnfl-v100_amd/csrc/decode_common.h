@@ -48,8 +48,14 @@ struct dec_args {
     // split), 0 when split j takes the cells j split_tokens .. + split_tokens - 1
     int32_t strided;
     int32_t slot[FNKV_MAX_SEQS];
+    // each sequence's context; with ctx_dev (dense) or depth_dev (sparse) set, the host's bound on it instead (the
+    // launch's grid and workspace follow from the bound, the work from the device word, so one captured launch
+    // serves every step up to the bound)
     int64_t ctx[FNKV_MAX_SEQS];
     int32_t split0[FNKV_MAX_SEQS + 1]; // first split of each sequence; split0[n_seq] = total
+    const int64_t * ctx_dev = nullptr;   // dense: device contexts [n_seq], read by the launch; null: ctx[] are the contexts
+    const int32_t * depth_dev = nullptr; // sparse: device depth (cells before the rows); ctx[0] bounds depth + T
+    uint32_t * err = nullptr;            // with a device word: FNKV_DEV_ERR_DEPTH for a refused context (nothing written)
     // a sparse launch (one sequence, rows at positions ctx - T ..): the rows' selection bodies (qsa.h layout) and
     // where split 0 of head 0 stores the length of the selection's tile list for the merge (the list's entries are
     // spread over the launched splits: sparse_split_size; sel_split is the host's bound on a split's entries)
@@ -298,7 +304,7 @@ __device__ __forceinline__ int32_t seq_of(const dec_args & a, int32_t split);
 __device__ __forceinline__ dec_args sparse_row_view(const dec_args & in) {
     dec_args a = in;
     const int32_t z = static_cast<int32_t>(blockIdx.z);
-    const int64_t depth = in.ctx[0] - in.T;
+    const int64_t depth = in.depth_dev != nullptr ? int64_t(*in.depth_dev) : in.ctx[0] - in.T;
     int64_t words = 0;
     for (int32_t t = 0; t < z; ++t) {
         const int64_t q = depth + t;
@@ -308,7 +314,9 @@ __device__ __forceinline__ dec_args sparse_row_view(const dec_args & in) {
     const int64_t rows_all = int64_t(gridDim.x) * gridDim.y * in.G; // a row's partial rows
     a.T = 1;
     a.R = in.G;
-    a.ctx[0] = depth + z + 1;
+    // a device depth outside 0 .. the bound (ctx[0] - T): marked by a negative context (sparse_refused)
+    a.ctx[0] = in.depth_dev != nullptr && (depth < 0 || depth + in.T > in.ctx[0]) ? -1 : depth + z + 1;
+    a.depth_dev = nullptr;
     a.q = in.q + int64_t(z) * in.hq * 256;
     a.sel_body = in.sel_body + words;
     a.sel_n = in.sel_n + z;
@@ -330,9 +338,12 @@ template <bool SP, bool LANES = true> struct split_src {
     const uint2 * slice = nullptr;
     uint32_t ent_x = 0, ent_y = 0; // sparse with LANES: lane i holds entry i (register reads instead of LDS reads)
 
+    // ctx: the sequence's context (dense, strided: the page lookups are sized by the bound a.ctx[s], so they need
+    // not wait for a context read from the device)
     template <int32_t THREADS>
     __device__ __forceinline__ void init(const dec_args & a, const int32_t * table, int32_t split, int64_t b,
-                                         int64_t e, int32_t lane, uint8_t * smem, uint8_t * slice_lds) {
+                                         int64_t e, int32_t lane, uint8_t * smem, uint8_t * slice_lds,
+                                         int64_t ctx = 0) {
         if constexpr (SP) {
             uint2 * sl = reinterpret_cast<uint2 *>(slice_lds);
             int32_t tile_l = 0;
@@ -351,10 +362,14 @@ template <bool SP, bool LANES = true> struct split_src {
             if (a.strided) {
                 const int32_t s = seq_of(a, split);
                 const int32_t j = split - a.split0[s], n = a.split0[s + 1] - a.split0[s];
-                const int32_t tiles = static_cast<int32_t>((a.ctx[s] + kTileTokens - 1) / kTileTokens);
+                const int32_t tiles_cap = static_cast<int32_t>((a.ctx[s] + kTileTokens - 1) / kTileTokens);
+                const int32_t cap_n = tiles_cap > j ? (tiles_cap - j + n - 1) / n : 0;
+                page_lane = lane < cap_n ? table[(j + n * lane) >> 3] : 0;
+                const int32_t tiles = static_cast<int32_t>((ctx + kTileTokens - 1) / kTileTokens);
                 g0 = j;
                 stride = n;
                 n_tiles = tiles > j ? (tiles - j + n - 1) / n : 0;
+                return;
             } else {
                 g0 = static_cast<int32_t>(b / kTileTokens);
                 stride = 1;
@@ -404,6 +419,43 @@ template <bool SP, bool LANES = true> struct split_src {
     }
 };
 
+// A dense sequence's context: the host's, or the device word's (ctx_dev). A sparse launch's row view holds its own.
+template <bool SP> __device__ __forceinline__ int64_t seq_ctx(const dec_args & a, int32_t s) {
+    if constexpr (!SP) {
+        if (a.ctx_dev != nullptr) {
+            return a.ctx_dev[s];
+        }
+    }
+    return a.ctx[s];
+}
+
+// A device context outside T .. the host's bound: the sequence's workgroups write nothing (its first workgroup sets
+// the error bit). Uniform across the workgroup.
+template <bool SP>
+__device__ __forceinline__ bool refused(const dec_args & a, int32_t s, int64_t ctx, int32_t sp, int32_t kvh) {
+    if constexpr (!SP) {
+        if (a.ctx_dev != nullptr && (ctx < a.T || ctx > a.ctx[s])) {
+            if (sp == 0 && kvh == 0 && threadIdx.x == 0 && a.err != nullptr) {
+                atomicOr(a.err, FNKV_DEV_ERR_DEPTH);
+            }
+            return true;
+        }
+    }
+    return false;
+}
+
+// A sparse row view refused by its device depth (sparse_row_view): nothing is written; the first workgroup of row 0
+// sets the error bit.
+__device__ __forceinline__ bool sparse_refused(const dec_args & a) {
+    if (a.ctx[0] >= 0) {
+        return false;
+    }
+    if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0 && a.err != nullptr) {
+        atomicOr(a.err, FNKV_DEV_ERR_DEPTH);
+    }
+    return true;
+}
+
 // the step token of this lane's query row (rt * 16 + j); padding rows take the last
 __device__ __forceinline__ int32_t t_of_row(const dec_args & a, int32_t rt, int32_t j) {
     const int32_t row = rt * 16 + j;
@@ -420,6 +472,12 @@ struct merge_args {
     int32_t split0[FNKV_MAX_SEQS + 1];
     const int32_t * sel_n; // sparse: each sequence's (row's) selection list length
     int32_t sel_split;
+    // the launch's device word (dec_args): a refused sequence's (or sparse launch's) outputs are left as they were;
+    // dense strided splits past a shorter context hold nothing
+    const int64_t * ctx_dev = nullptr;
+    const int32_t * depth_dev = nullptr;
+    int64_t cap[FNKV_MAX_SEQS] = {0};
+    int32_t T_dev = 0; // the launch's step tokens (rows of a sparse launch)
     // the gated form (fn/kernels/qsa/attend.cu:619-655's finish): with out_f32 set, row (t, h)'s value d is written as
     // o / (1 + exp(-gate[(t hq + h) gate_stride + d])) in F32 [T][hq][256] with its int8 activation format (codes
     // [T][hq 256], act_scales [T][hq 8][2]) instead of the fp16 out
@@ -442,10 +500,18 @@ struct sparse_gate {
     int8_t * codes;
     float * scales;
 };
+// a launch's depth read from device memory (the reference's depth word, attend.h:108): depth + T <= max_cells or
+// the launch writes nothing and ORs FNKV_DEV_ERR_DEPTH into *err
+struct dev_depth {
+    const int32_t * depth;
+    int64_t max_cells;
+    uint32_t * err;
+};
+// dd set: `depth` is not read; the plan (grid, workspace) follows from dd->max_cells
 int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq, float scale,
                   const void * q, const void * body, const void * offsets, const void * k_new, const void * v_new,
                   int32_t new_dtype, void * out, const sparse_gate * gate, void * ws, int64_t ws_bytes,
-                  hipStream_t st, const char * who, const fused_prep * fp = nullptr);
+                  hipStream_t st, const char * who, const fused_prep * fp = nullptr, const dev_depth * dd = nullptr);
 // LDS of the one-row sparse launch's formed query rows (after the tile buffers and the selection slice)
 constexpr int32_t kFusedQLds = 16 * kHeadDim * 2;
 
@@ -527,12 +593,12 @@ __device__ __forceinline__ void append_new_cells(const dec_args & a, const int32
 // hi + lo fp16 (B: lane (row j, qg) holds sigma_hi for qg 0, sigma_lo for qg 1, else 0), and one FMA a score takes it
 // back out. lim: the row's last visible cell.
 // load_q_operands only issues the loads; q_sums reads them, so a kernel can issue its first tile copies in between.
-__device__ __forceinline__ void load_q_operands(const dec_args & a, int32_t s, int32_t kvh, int32_t rt, int32_t j,
-                                                int32_t qg, half8 (&qop)[kBlocks], int64_t & lim) {
+__device__ __forceinline__ void load_q_operands(const dec_args & a, int32_t s, int64_t ctx, int32_t kvh, int32_t rt,
+                                                int32_t j, int32_t qg, half8 (&qop)[kBlocks], int64_t & lim) {
     const int32_t row = rt * 16 + j;
     const bool real_row = row < a.R;
     const int32_t t_row = real_row ? row / a.G : a.T - 1;
-    lim = a.ctx[s] - a.T + t_row;
+    lim = ctx - a.T + t_row;
     const uint16_t * qrow =
         a.q + ((int64_t(s) * a.T + t_row) * a.hq + int64_t(kvh) * a.G + (real_row ? row % a.G : 0)) * kHeadDim;
 #pragma unroll

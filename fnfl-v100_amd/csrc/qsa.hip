@@ -35,6 +35,8 @@ struct qsa_prep_args {
     const int32_t * table; // the slot's page table
     int32_t layer;
     int64_t depth;
+    const int32_t * depth_dev; // set: the depth is this device word, and depth + T <= max_cells or nothing is written
+    int64_t max_cells;
     const float * qfull;
     const float * kv_k;
     const float * kv_v;
@@ -49,6 +51,12 @@ struct qsa_prep_args {
 };
 
 __global__ __launch_bounds__(64) void qsa_prepare_kernel(qsa_prep_args a) {
+    if (a.depth_dev != nullptr) {
+        a.depth = *a.depth_dev;
+        if (a.depth < 0 || a.depth + a.T > a.max_cells) {
+            return; // the attention's launch reports the refusal
+        }
+    }
     const int32_t t = static_cast<int32_t>(blockIdx.x), r = static_cast<int32_t>(blockIdx.y);
     const int32_t lane = static_cast<int32_t>(threadIdx.x);
     float y[4];
@@ -81,6 +89,80 @@ int64_t up16(int64_t x) { return (x + 15) & ~int64_t(15); }
 bool aligned16(const void * p) { return p != nullptr && (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 } // namespace
+
+// attn::attend over the pool (the three launches, or two for one row of at most 16 query heads a KV head); dd set:
+// the depth is read on the device, `depth` is ignored and the plan is dd->max_cells'
+int qsa_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq,
+               const float * qfull, const float * kv_k, const float * kv_v, const float * q_norm, const float * k_norm,
+               const int32_t * pos, float theta_scale, const void * body, const void * offsets, float * out,
+               int8_t * codes, float * scales, float * q_f32, float * k_f32, void * ws, int64_t ws_bytes,
+               hipStream_t st, const dev_depth * dd, const char * who, bool check_only = false) {
+    const std::string name(who);
+    const kv_pool * p = pool_of(pool);
+    if (dd != nullptr) {
+        if (dd->depth == nullptr || dd->err == nullptr || (reinterpret_cast<uintptr_t>(dd->depth) & 3) != 0 ||
+            (reinterpret_cast<uintptr_t>(dd->err) & 3) != 0 || T <= 0 || dd->max_cells < T) {
+            set_error(name + ": the device depth and error words (4-byte aligned) and max_cells >= rows required");
+            return FNKV_ERR_ARG;
+        }
+        depth = dd->max_cells - T;
+    }
+    const int64_t need = fnkv_qsa_workspace_bytes(pool, depth, T, hq);
+    if (p == nullptr || need < 0 || !aligned16(qfull) || !aligned16(kv_k) || !aligned16(kv_v) || !aligned16(q_norm) ||
+        !aligned16(k_norm) || pos == nullptr || (reinterpret_cast<uintptr_t>(pos) & 3) != 0 || !aligned16(out) ||
+        codes == nullptr || (reinterpret_cast<uintptr_t>(codes) & 3) != 0 || scales == nullptr ||
+        (reinterpret_cast<uintptr_t>(scales) & 7) != 0 || (q_f32 != nullptr && !aligned16(q_f32)) ||
+        (k_f32 != nullptr && !aligned16(k_f32)) || !aligned16(ws) || !std::isfinite(theta_scale)) {
+        set_error(name + ": argument outside the contract");
+        return FNKV_ERR_ARG;
+    }
+    if (ws_bytes < need) {
+        set_error(name + ": workspace too small");
+        return FNKV_ERR_ARG;
+    }
+    const int32_t G = hq / p->h_kv();
+    const int64_t sp = up16(fnkv_sparse_workspace_bytes(pool, depth, T, hq));
+    uint8_t * w = static_cast<uint8_t *>(ws);
+    uint16_t * q16 = reinterpret_cast<uint16_t *>(w + sp);
+    // every check of the sparse launch is made here too, before the prepare is enqueued: a refusal enqueues nothing
+    sparse_gate gate = {qfull + 256, 512, out, codes, scales};
+    if (T <= 0 || T > kSelMaxRows || depth < 0 || layer < 0 || layer >= p->layers() || slot < 0 ||
+        slot >= p->pages().n_slots() || depth + T > p->mapped_cells(slot) || depth + T > kSelMaxCells ||
+        G > FNKV_MAX_ROWS || body == nullptr || offsets == nullptr || (reinterpret_cast<uintptr_t>(body) & 3) != 0 ||
+        (reinterpret_cast<uintptr_t>(offsets) & 3) != 0) {
+        set_error(name + ": rows, heads, layer or cells outside the contract");
+        return FNKV_ERR_ARG;
+    }
+    if (check_only) {
+        return FNKV_OK;
+    }
+    // one row of at most 16 query heads a KV head: the sparse launch prepares the row itself (one launch fewer);
+    // FNKV_QSA_TWO_KERNELS=1 keeps the separate prepare launch, for comparison
+    const char * two = std::getenv("FNKV_QSA_TWO_KERNELS");
+    if (T == 1 && G <= 16 && (two == nullptr || std::atoi(two) == 0)) {
+        fused_prep fp;
+        fp.qfull = qfull;
+        fp.kv_k = kv_k;
+        fp.kv_v = kv_v;
+        fp.q_norm = q_norm;
+        fp.k_norm = k_norm;
+        fp.pos = pos;
+        fp.theta_scale = theta_scale;
+        fp.q_f32 = q_f32;
+        fp.k_f32 = k_f32;
+        return sparse_launch(pool, slot, depth, T, layer, hq, 1.0f / 16.0f, q16, body, offsets, kv_k, kv_v, FNKV_F32,
+                             nullptr, &gate, ws, sp, st, who, &fp, dd);
+    }
+    const pool_view pv = p->view();
+    qsa_prep_args pa = {pv, pv.table + int64_t(slot) * pv.table_stride, layer, depth,
+                        dd != nullptr ? dd->depth : nullptr, dd != nullptr ? dd->max_cells : 0, qfull, kv_k, kv_v,
+                        q_norm, k_norm, pos, theta_scale, T, hq, p->h_kv(), q16, q_f32, k_f32};
+    hipLaunchKernelGGL(qsa_prepare_kernel, dim3(static_cast<uint32_t>(T), static_cast<uint32_t>(hq + p->h_kv())),
+                       dim3(64), 0, st, pa);
+    return sparse_launch(pool, slot, depth, T, layer, hq, 1.0f / 16.0f, q16, body, offsets, nullptr, nullptr, FNKV_F32,
+                         nullptr, &gate, ws, sp, st, who, nullptr, dd);
+}
+
 } // namespace fnkv
 
 using fnkv::set_error;
@@ -100,60 +182,62 @@ int fnkv_qsa_attend(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t
                     const float * k_norm, const int32_t * pos, float theta_scale, const void * body,
                     const void * offsets, float * out, int8_t * codes, float * scales, float * q_f32, float * k_f32,
                     void * ws, int64_t ws_bytes, void * stream) {
-    using fnkv::aligned16;
-    const fnkv::kv_pool * p = fnkv::pool_of(pool);
-    const int64_t need = fnkv_qsa_workspace_bytes(pool, depth, T, hq);
-    if (p == nullptr || need < 0 || !aligned16(qfull) || !aligned16(kv_k) || !aligned16(kv_v) || !aligned16(q_norm) ||
-        !aligned16(k_norm) || pos == nullptr || (reinterpret_cast<uintptr_t>(pos) & 3) != 0 || !aligned16(out) ||
-        codes == nullptr || (reinterpret_cast<uintptr_t>(codes) & 3) != 0 || scales == nullptr ||
-        (reinterpret_cast<uintptr_t>(scales) & 7) != 0 || (q_f32 != nullptr && !aligned16(q_f32)) ||
-        (k_f32 != nullptr && !aligned16(k_f32)) || !aligned16(ws) || !std::isfinite(theta_scale)) {
-        set_error("fnkv_qsa_attend: argument outside the contract");
+    return fnkv::qsa_launch(pool, slot, depth, T, layer, hq, qfull, kv_k, kv_v, q_norm, k_norm, pos, theta_scale, body,
+                            offsets, out, codes, scales, q_f32, k_f32, ws, ws_bytes, static_cast<hipStream_t>(stream),
+                            nullptr, "fnkv_qsa_attend");
+}
+
+int64_t fnkv_attend_workspace_bytes(const fnkv_pool * pool, int32_t max_cells, int32_t rows, int32_t hq) {
+    if (rows <= 0 || max_cells < rows) {
+        return -1;
+    }
+    return fnkv_qsa_workspace_bytes(pool, int64_t(max_cells) - rows, rows, hq);
+}
+
+namespace {
+// one lane's checks and launches
+int attend_one(int32_t rows, const fnkv_attend_args * a, hipStream_t st, const char * who, bool check_only) {
+    if (a == nullptr) {
+        fnkv::set_error(std::string(who) + ": null args");
         return FNKV_ERR_ARG;
     }
-    if (ws_bytes < need) {
-        set_error("fnkv_qsa_attend: workspace too small (fnkv_qsa_workspace_bytes)");
+    const fnkv::dev_depth dd = {a->depth, a->max_cells, a->err};
+    return fnkv::qsa_launch(a->pool, a->slot, 0, rows, a->layer, a->hq, a->qfull, a->kv_k, a->kv_v, a->q_norm,
+                            a->k_norm, a->pos, a->theta_scale, a->body, a->offsets, a->out, a->codes, a->scales,
+                            a->q_f32, a->k_f32, a->ws, a->ws_bytes, st, &dd, who, check_only);
+}
+} // namespace
+
+int fnkv_attend(int32_t rows, const fnkv_attend_args * a, void * stream) {
+    return attend_one(rows, a, static_cast<hipStream_t>(stream), "fnkv_attend", false);
+}
+
+int fnkv_attend_lanes(int32_t lanes, int32_t rows, const fnkv_attend_args * a, void * stream) {
+    if (lanes < 2 || lanes > FNKV_MAX_LANES || a == nullptr) {
+        fnkv::set_error("fnkv_attend_lanes: lanes outside 2 .. " + std::to_string(FNKV_MAX_LANES));
         return FNKV_ERR_ARG;
     }
-    const int32_t G = hq / p->h_kv();
-    const int64_t sp = fnkv::up16(fnkv_sparse_workspace_bytes(pool, depth, T, hq));
-    uint8_t * w = static_cast<uint8_t *>(ws);
-    uint16_t * q16 = reinterpret_cast<uint16_t *>(w + sp);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    // every check of the sparse launch is made here too, before the prepare is enqueued: a refusal enqueues nothing
-    fnkv::sparse_gate gate = {qfull + 256, 512, out, codes, scales};
-    if (T <= 0 || T > fnkv::kSelMaxRows || depth < 0 || layer < 0 || layer >= p->layers() || slot < 0 ||
-        slot >= p->pages().n_slots() || depth + T > p->mapped_cells(slot) || depth + T > fnkv::kSelMaxCells ||
-        G > FNKV_MAX_ROWS || body == nullptr ||
-        offsets == nullptr || (reinterpret_cast<uintptr_t>(body) & 3) != 0 ||
-        (reinterpret_cast<uintptr_t>(offsets) & 3) != 0) {
-        set_error("fnkv_qsa_attend: rows, heads, layer or cells outside the contract");
-        return FNKV_ERR_ARG;
+    // every lane is checked before any is enqueued (the host checks of a lane enqueue nothing): all or nothing
+    for (int32_t u = 0; u < lanes; ++u) {
+        if (attend_one(rows, &a[u], nullptr, "fnkv_attend_lanes", true) != FNKV_OK) {
+            fnkv::set_error("fnkv_attend_lanes: lane " + std::to_string(u) + ": " + fnkv::last_error());
+            return FNKV_ERR_ARG;
+        }
+        for (int32_t v = 0; v < u; ++v) { // lanes are distinct sequences: no two write the same cells
+            if (a[v].pool == a[u].pool && a[v].slot == a[u].slot) {
+                fnkv::set_error("fnkv_attend_lanes: lanes " + std::to_string(v) + " and " + std::to_string(u) +
+                                " name the same slot");
+                return FNKV_ERR_ARG;
+            }
+        }
     }
-    // one row of at most 16 query heads a KV head: the sparse launch prepares the row itself (one launch fewer);
-    // FNKV_QSA_TWO_KERNELS=1 keeps the separate prepare launch, for comparison
-    const char * two = std::getenv("FNKV_QSA_TWO_KERNELS");
-    if (T == 1 && G <= 16 && (two == nullptr || std::atoi(two) == 0)) {
-        fnkv::fused_prep fp;
-        fp.qfull = qfull;
-        fp.kv_k = kv_k;
-        fp.kv_v = kv_v;
-        fp.q_norm = q_norm;
-        fp.k_norm = k_norm;
-        fp.pos = pos;
-        fp.theta_scale = theta_scale;
-        fp.q_f32 = q_f32;
-        fp.k_f32 = k_f32;
-        return fnkv::sparse_launch(pool, slot, depth, T, layer, hq, 1.0f / 16.0f, q16, body, offsets, kv_k, kv_v,
-                                   FNKV_F32, nullptr, &gate, ws, sp, st, "fnkv_qsa_attend", &fp);
+    for (int32_t u = 0; u < lanes; ++u) {
+        const int rc = attend_one(rows, &a[u], static_cast<hipStream_t>(stream), "fnkv_attend_lanes", false);
+        if (rc != FNKV_OK) {
+            return rc;
+        }
     }
-    const fnkv::pool_view pv = p->view();
-    fnkv::qsa_prep_args pa = {pv, pv.table + int64_t(slot) * pv.table_stride, layer, depth, qfull, kv_k, kv_v, q_norm,
-                              k_norm, pos, theta_scale, T, hq, p->h_kv(), q16, q_f32, k_f32};
-    hipLaunchKernelGGL(fnkv::qsa_prepare_kernel, dim3(static_cast<uint32_t>(T), static_cast<uint32_t>(hq + p->h_kv())),
-                       dim3(64), 0, st, pa);
-    return fnkv::sparse_launch(pool, slot, depth, T, layer, hq, 1.0f / 16.0f, q16, body, offsets, nullptr, nullptr,
-                               FNKV_F32, nullptr, &gate, ws, sp, st, "fnkv_qsa_attend");
+    return FNKV_OK;
 }
 
 } // extern "C"

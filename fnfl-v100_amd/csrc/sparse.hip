@@ -64,9 +64,17 @@ sparse_plan plan_sparse(const kv_pool & p, int64_t depth, int32_t T, int32_t G) 
 int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq, float scale,
                   const void * q, const void * body, const void * offsets, const void * k_new, const void * v_new,
                   int32_t new_dtype, void * out, const sparse_gate * gate, void * ws, int64_t ws_bytes,
-                  hipStream_t st, const char * who, const fused_prep * fp) {
+                  hipStream_t st, const char * who, const fused_prep * fp, const dev_depth * dd) {
     const kv_pool * p = pool_of(pool);
     const std::string name(who);
+    if (dd != nullptr) { // the plan is the bound's: the deepest rows' tiles
+        if (dd->depth == nullptr || dd->err == nullptr || (reinterpret_cast<uintptr_t>(dd->depth) & 3) != 0 ||
+            (reinterpret_cast<uintptr_t>(dd->err) & 3) != 0 || dd->max_cells < T) {
+            set_error(name + ": the device depth and error words (4-byte aligned) and max_cells >= rows required");
+            return FNKV_ERR_ARG;
+        }
+        depth = dd->max_cells - T;
+    }
     if (p == nullptr || slot < 0 || slot >= p->pages().n_slots() || T <= 0 || T > kSelMaxRows || depth < 0 ||
         layer < 0 || layer >= p->layers() || hq <= 0 || hq % p->h_kv() != 0 || q == nullptr || body == nullptr ||
         offsets == nullptr || (out == nullptr && gate == nullptr) || ws == nullptr || !(scale > 0.0f) ||
@@ -98,11 +106,15 @@ int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T
 
     // several rows: their new cells first (a row may read an earlier row's new cell; the rows run side by side); one
     // row: the launch writes it, by the split that reads its tile
+    if (fp != nullptr && (T != 1 || G > 16)) {
+        set_error(name + ": a launch that prepares its row takes one row of at most 16 query heads a KV head");
+        return FNKV_ERR_ARG;
+    }
     if (k_new != nullptr && T > 1) {
-        const int rc = fnkv_q8_append(const_cast<fnkv_pool *>(pool), slot, layer, depth, T, k_new, v_new, new_dtype,
-                                      st);
-        if (rc != FNKV_OK) {
-            return rc;
+        if (append_enqueue(*p, slot, layer, depth, dd != nullptr ? dd->depth : nullptr, ctx, T, k_new, v_new,
+                           new_dtype, st) != FNKV_OK) {
+            set_error(name + ": launch failed");
+            return FNKV_ERR_HIP;
         }
     }
     dec_args a;
@@ -134,11 +146,11 @@ int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T
     a.sel_n = reinterpret_cast<int32_t *>(w);
     a.sel_split = pl.per_split;
     if (fp != nullptr) {
-        if (T != 1 || G > 16) {
-            set_error(name + ": a launch that prepares its row takes one row of at most 16 query heads a KV head");
-            return FNKV_ERR_ARG;
-        }
         a.fp = *fp;
+    }
+    if (dd != nullptr) {
+        a.depth_dev = dd->depth;
+        a.err = dd->err;
     }
 #ifdef FNKV_TIMING
     a.ts = timing_buffer();
@@ -163,6 +175,11 @@ int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T
     }
     m.sel_n = a.sel_n;
     m.sel_split = pl.per_split;
+    if (dd != nullptr) {
+        m.depth_dev = dd->depth;
+        m.cap[0] = ctx;
+        m.T_dev = T;
+    }
     if (gate != nullptr) {
         m.gate = gate->gate;
         m.gate_stride = gate->stride;
@@ -198,6 +215,16 @@ int fnkv_attn_sparse(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_
     return fnkv::sparse_launch(pool, slot, depth, T, layer, hq, scale, q, body, offsets, k_new, v_new,
                                new_dtype, out, nullptr, ws, ws_bytes, static_cast<hipStream_t>(stream),
                                "fnkv_attn_sparse");
+}
+
+int fnkv_attn_sparse_dev(const fnkv_pool * pool, int32_t slot, const int32_t * depth, int64_t max_cells, int32_t T,
+                         int32_t layer, int32_t hq, float scale, const void * q, const void * body,
+                         const void * offsets, const void * k_new, const void * v_new, int32_t new_dtype, void * out,
+                         void * ws, int64_t ws_bytes, uint32_t * err, void * stream) {
+    const fnkv::dev_depth dd = {depth, max_cells, err};
+    return fnkv::sparse_launch(pool, slot, 0, T, layer, hq, scale, q, body, offsets, k_new, v_new, new_dtype, out,
+                               nullptr, ws, ws_bytes, static_cast<hipStream_t>(stream), "fnkv_attn_sparse_dev",
+                               nullptr, &dd);
 }
 
 } // extern "C"

@@ -24,7 +24,11 @@ EXPORTS = [
     "fnkv_attn_prefill", "fnkv_pool_create_fmt", "fnkv_pool_format", "fnkv_export_kv8",
     "fnkv_sparse_workspace_bytes", "fnkv_attn_sparse", "fnkv_rope_theta_scale", "fnkv_datc_part_bytes",
     "fnkv_datc_prepare", "fnkv_datc_attend", "fnkv_datc_step", "fnkv_qsa_workspace_bytes", "fnkv_qsa_attend",
+    "fnkv_attn_decode_dev", "fnkv_attn_sparse_dev", "fnkv_attend_workspace_bytes", "fnkv_attend",
+    "fnkv_attend_lanes",
 ]
+DEV_ERR_DEPTH = 2
+MAX_LANES = 4
 DATC_HEADS = 12
 DATC_QSTRIDE = 512
 DEV_ERR_DRAFT_DEPTH = 1 << 24
@@ -51,6 +55,14 @@ class DatcAttendArgs(ctypes.Structure):
     """fnkv_datc_attend_args (include/fnkv.h)"""
     _fields_ = [("q16", P), ("qfull", P), ("k_cache", P), ("v_cache", P), ("n_before", P), ("row0", I32),
                 ("max_cells", I32), ("part", P), ("out", P), ("codes", P), ("scales", P), ("err", P), ("body", P)]
+
+
+class AttendArgs(ctypes.Structure):
+    """fnkv_attend_args (include/fnkv.h)"""
+    _fields_ = [("pool", P), ("slot", I32), ("layer", I32), ("hq", I32), ("qfull", P), ("kv_k", P), ("kv_v", P),
+                ("q_norm", P), ("k_norm", P), ("body", P), ("offsets", P), ("pos", P), ("depth", P),
+                ("max_cells", I32), ("theta_scale", ctypes.c_float), ("out", P), ("codes", P), ("scales", P),
+                ("q_f32", P), ("k_f32", P), ("ws", P), ("ws_bytes", I64), ("err", P)]
 
 
 class FnkvError(RuntimeError):
@@ -123,6 +135,18 @@ def lib():
         L.fnkv_qsa_attend.restype = ctypes.c_int
         L.fnkv_qsa_attend.argtypes = [P, I32, I64, I32, I32, I32, P, P, P, P, P, P, ctypes.c_float, P, P, P, P, P, P,
                                       P, P, I64, P]
+        L.fnkv_attn_decode_dev.restype = ctypes.c_int
+        L.fnkv_attn_decode_dev.argtypes = [P, I32, P, P, P, I32, I32, I32, ctypes.c_float, P, P, P, I32, P, P, I64, P,
+                                           P]
+        L.fnkv_attn_sparse_dev.restype = ctypes.c_int
+        L.fnkv_attn_sparse_dev.argtypes = [P, I32, P, I64, I32, I32, I32, ctypes.c_float, P, P, P, P, P, I32, P, P,
+                                           I64, P, P]
+        L.fnkv_attend_workspace_bytes.restype = I64
+        L.fnkv_attend_workspace_bytes.argtypes = [P, I32, I32, I32]
+        L.fnkv_attend.restype = ctypes.c_int
+        L.fnkv_attend.argtypes = [I32, ctypes.POINTER(AttendArgs), P]
+        L.fnkv_attend_lanes.restype = ctypes.c_int
+        L.fnkv_attend_lanes.argtypes = [I32, I32, ctypes.POINTER(AttendArgs), P]
         L.fnkv_rope_theta_scale.restype = ctypes.c_float
         L.fnkv_rope_theta_scale.argtypes = []
         L.fnkv_datc_part_bytes.restype = I64
@@ -282,6 +306,48 @@ class Pool:
                                             dt, P(out.data_ptr()), P(ws.data_ptr()), ws.numel() * ws.element_size(),
                                             _stream(stream)))
 
+    def decode_dev(self, slots, ctx_dev, max_ctx, T, layer, q, out, ws, err, scale=1.0 / 16.0, k_new=None,
+                   v_new=None, stream=None):
+        """fnkv_attn_decode_dev: ctx_dev an int64 device tensor [n_seq] read by the launch, max_ctx the host bounds
+        (the workspace: decode_ws_bytes(max_ctx, T, hq)), err an int32 device word (caller-cleared)."""
+        import torch
+        sp, k1 = _i32_array(slots)
+        mp, k2 = _i64_array(max_ctx)
+        kp = P(k_new.data_ptr()) if k_new is not None else None
+        vp = P(v_new.data_ptr()) if v_new is not None else None
+        dt = F32 if (k_new is not None and k_new.dtype == torch.float32) else F16
+        return check(lib().fnkv_attn_decode_dev(self.h, len(slots), sp, _p(ctx_dev), mp, T, layer, q.shape[2], scale,
+                                                P(q.data_ptr()), kp, vp, dt, P(out.data_ptr()), P(ws.data_ptr()),
+                                                ws.numel() * ws.element_size(), _p(err), _stream(stream)))
+
+    def sparse_dev(self, slot, depth_dev, max_cells, layer, q, body, offsets, out, ws, err, scale=1.0 / 16.0,
+                   k_new=None, v_new=None, stream=None):
+        """fnkv_attn_sparse_dev: depth_dev an int32 device word, max_cells the host bound on depth + T (the workspace:
+        sparse_ws_bytes(max_cells - T, T, hq))."""
+        import torch
+        T, hq = q.shape[0], q.shape[1]
+        kp = P(k_new.data_ptr()) if k_new is not None else None
+        vp = P(v_new.data_ptr()) if v_new is not None else None
+        dt = F32 if (k_new is not None and k_new.dtype == torch.float32) else F16
+        return check(lib().fnkv_attn_sparse_dev(self.h, slot, _p(depth_dev), max_cells, T, layer, hq, scale,
+                                                P(q.data_ptr()), P(body.data_ptr()), P(offsets.data_ptr()), kp, vp,
+                                                dt, P(out.data_ptr()), P(ws.data_ptr()),
+                                                ws.numel() * ws.element_size(), _p(err), _stream(stream)))
+
+    def attend_ws_bytes(self, max_cells, rows, hq):
+        return lib().fnkv_attend_workspace_bytes(self.h, max_cells, rows, hq)
+
+    def attend_args(self, slot, layer, depth_dev, max_cells, qfull, kv_k, kv_v, q_norm, k_norm, pos, body, offsets,
+                    out, codes, scales, ws, err, q_f32=None, k_f32=None, theta_scale=None):
+        """fnkv_attend_args for this pool (device tensors; depth_dev an int32 device word)."""
+        a = AttendArgs(self.h, slot, layer, qfull.shape[1], _p(qfull), _p(kv_k), _p(kv_v), _p(q_norm), _p(k_norm),
+                       _p(body), _p(offsets), _p(pos), _p(depth_dev), max_cells,
+                       rope_theta_scale() if theta_scale is None else theta_scale, _p(out), _p(codes), _p(scales),
+                       _p(q_f32), _p(k_f32), _p(ws), ws.numel() * ws.element_size(), _p(err))
+        a._keep = (qfull, kv_k, kv_v, q_norm, k_norm, pos, body, offsets, out, codes, scales, ws, err, q_f32, k_f32,
+                   depth_dev)
+        return a
+
     def sparse_ws_bytes(self, depth, T, hq):
         return lib().fnkv_sparse_workspace_bytes(self.h, depth, T, hq)
 
@@ -376,3 +442,14 @@ def datc_step(*, kv_k, kv_v, k_norm, q_norm, qfull, n_before, pos, stride, k_cac
     a = DatcAttendArgs(None, _p(qfull), _p(k_cache), _p(v_cache), _p(n_before), row0, k_cache.shape[0], _p(part),
                        _p(out), _p(codes), _p(scales), _p(err), _p(body))
     return check(lib().fnkv_datc_step(ctypes.byref(p), ctypes.byref(a), _stream(stream)))
+
+
+def attend(rows, args, stream=None):
+    """fnkv_attend (attn::attend with the device depth)"""
+    return check(lib().fnkv_attend(rows, ctypes.byref(args), _stream(stream)))
+
+
+def attend_lanes(rows, args_list, stream=None):
+    """fnkv_attend_lanes over a list of AttendArgs"""
+    arr = (AttendArgs * len(args_list))(*args_list)
+    return check(lib().fnkv_attend_lanes(len(args_list), rows, arr, _stream(stream)))

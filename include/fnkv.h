@@ -144,6 +144,27 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
                      int32_t layer, int32_t hq, float scale, const void * q, const void * k_new, const void * v_new,
                      int32_t new_dtype, void * out, void * ws, int64_t ws_bytes, void * stream);
 
+/* The device error word's refused-depth bit (fn/kernels/qsa/attend.h:91-92, :108-110: "sets the error word (2)"): a
+ * launch that reads its context or depth from device memory and finds it outside its contract writes nothing for the
+ * sequence concerned and ORs this bit into the caller-cleared word. (The reference's bit 1, an acquire timeout, has no
+ * counterpart: no launch here waits on another workgroup.) */
+#define FNKV_DEV_ERR_DEPTH 2u
+
+/* fnkv_attn_decode with each sequence's context read from device memory by the launch, the reference's device depth
+ * (attend.h:108, "read by the launch (TG1)"): ctx[n_seq] (device, int64) is read when the launch runs, so one
+ * captured graph serves every decode step; max_ctx[n_seq] (host) bounds it and fixes the grid and the workspace
+ * (fnkv_decode_workspace_bytes(pool, n_seq, max_ctx, T, hq)), each at most the slot's mapped cells when called. A
+ * sequence whose ctx[i] is below T or above max_ctx[i] is refused on the device: nothing of it is written (neither
+ * its new cells nor its out rows) and FNKV_DEV_ERR_DEPTH is ORed into *err (device, caller-cleared); the other
+ * sequences run. Splits of a sequence take its 32-token tiles in turn (split j of n: tiles j, j + n, ...), so a context
+ * below its bound still spreads over every split. Otherwise as fnkv_attn_decode (whose G * T <= 16 launches split the
+ * same way: for equal contexts and bounds their outputs are bitwise equal). Replaces the depth contract of
+ * fn::qsa::attn::attend (attend.h:97-141). */
+int fnkv_attn_decode_dev(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx,
+                         const int64_t * max_ctx, int32_t T, int32_t layer, int32_t hq, float scale, const void * q,
+                         const void * k_new, const void * v_new, int32_t new_dtype, void * out, void * ws,
+                         int64_t ws_bytes, uint32_t * err, void * stream);
+
 /* ---- sparse (QSA) attention at decode rows (fn/kernels/qsa/attend.h:97-141 attend over a selection body) ---- */
 
 /* The workspace a sparse launch at this depth needs (bytes; no zeroing needed); -1 outside the contract. */
@@ -162,6 +183,16 @@ int64_t fnkv_sparse_workspace_bytes(const fnkv_pool * pool, int64_t depth, int32
 int fnkv_attn_sparse(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq,
                      float scale, const void * q, const void * body, const void * offsets, const void * k_new,
                      const void * v_new, int32_t new_dtype, void * out, void * ws, int64_t ws_bytes, void * stream);
+
+/* fnkv_attn_sparse with the depth read from device memory (attend.h:108): depth (device, int32) is read by the launch;
+ * max_cells (host) bounds depth + T, fixes the plan (workspace: fnkv_sparse_workspace_bytes(pool, max_cells - T, T,
+ * hq)) and must not exceed the slot's mapped cells. A depth with depth + T beyond max_cells (or below 0) writes
+ * nothing — no new cells, no out rows — and ORs FNKV_DEV_ERR_DEPTH into *err (device, caller-cleared). The body's
+ * layout follows the depth read. */
+int fnkv_attn_sparse_dev(const fnkv_pool * pool, int32_t slot, const int32_t * depth, int64_t max_cells, int32_t T,
+                         int32_t layer, int32_t hq, float scale, const void * q, const void * body,
+                         const void * offsets, const void * k_new, const void * v_new, int32_t new_dtype, void * out,
+                         void * ws, int64_t ws_bytes, uint32_t * err, void * stream);
 
 /* ---- the reference's decode attention with its prepare and gate (fn/kernels/qsa/attend.h:57-141 attn::attend) ---- */
 
@@ -185,6 +216,53 @@ int fnkv_qsa_attend(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t
                     const float * k_norm, const int32_t * pos, float theta_scale, const void * body,
                     const void * offsets, float * out, int8_t * codes, float * scales, float * q_f32, float * k_f32,
                     void * ws, int64_t ws_bytes, void * stream);
+
+/* fn::qsa::attn::args (attend.h:57-91) over the pool: the cache pair (k_cache, v_cache, k_scale, v_scale) is the pool's
+ * slot and layer; the workspace is the caller's (no zeroing needed: nothing here carries state between launches) and
+ * the error word is its own field (the reference's ws.error). */
+typedef struct {
+    const fnkv_pool * pool;
+    int32_t slot;
+    int32_t layer;
+    int32_t hq;              /* query heads (the reference's card: 12 on one KV head) */
+    const float * qfull;     /* F32 [rows][hq][512]: each head's q, then its gate */
+    const float * kv_k;      /* F32 [rows][h_kv][256], before the norm */
+    const float * kv_v;      /* F32 [rows][h_kv][256] */
+    const float * q_norm;    /* [256] */
+    const float * k_norm;    /* [256] */
+    const uint32_t * body;   /* the selection body of the rows (qsa.h:77-81 layout) */
+    const int32_t * offsets; /* [rows + 1] its byte offsets */
+    const int32_t * pos;     /* [4][rows] the rope planes of each row */
+    const int32_t * depth;   /* device: cells before the rows, read by the launch (TG1) */
+    int32_t max_cells;       /* host: depth + rows beyond it writes nothing and sets FNKV_DEV_ERR_DEPTH */
+    float theta_scale;       /* fnkv_rope_theta_scale() */
+    float * out;             /* F32 [rows][hq][256], gated */
+    int8_t * codes;          /* [rows][hq 256] the activation format */
+    float * scales;          /* [rows][hq 8][2] */
+    float * q_f32;           /* optional [rows][hq][256]: q after the norm and rope */
+    float * k_f32;           /* optional [rows][h_kv][256]: the new cells' F32 k before quantizing */
+    void * ws;               /* fnkv_attend_workspace_bytes of device memory */
+    int64_t ws_bytes;
+    uint32_t * err;          /* device error word, caller-cleared */
+} fnkv_attend_args;
+
+#define FNKV_MAX_LANES 4 /* lanes of a joint verify round (attend.h:143-151: 2 .. 4) */
+
+/* attn::workspace_bytes (attend.h:85) for launches of `rows` rows up to max_cells; -1 outside the contract */
+int64_t fnkv_attend_workspace_bytes(const fnkv_pool * pool, int32_t max_cells, int32_t rows, int32_t hq);
+
+/* attn::attend (attend.h:97-141): fnkv_qsa_attend's computation with the depth read on the device, so one captured
+ * graph serves every step; max_cells at most the slot's mapped cells and 262,176. A refused depth writes nothing
+ * (no new cells, no outputs) and sets FNKV_DEV_ERR_DEPTH. FNKV_ERR_ARG with nothing enqueued for an argument outside
+ * the contract. */
+int fnkv_attend(int32_t rows, const fnkv_attend_args * a, void * stream);
+
+/* attn::attend_lanes (attend.h:143-151): the joint verify round of `lanes` (2 .. FNKV_MAX_LANES) sequences, lane u
+ * on its own arguments a[u] (distinct slots), every lane's rows the same count. Each lane's launches are fnkv_attend's
+ * on its arguments, enqueued lane after lane, so each lane's outputs and written cells are bitwise its lone call's;
+ * a lane at a refused depth sets its own error word and writes nothing, the others run. Every lane is checked before
+ * anything is enqueued: FNKV_ERR_ARG with nothing enqueued when any lane is outside the contract. */
+int fnkv_attend_lanes(int32_t lanes, int32_t rows, const fnkv_attend_args * a, void * stream);
 
 /* ---- chunked-prefill attention (fn/kernels/qsa/qsa_prompt.h:106-124 qsp_attend) ---- */
 
