@@ -35,6 +35,8 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
+#include <string>
 #include <type_traits>
 #include <vector>
 
@@ -1257,6 +1259,44 @@ int decode_launch(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, 
     return FNKV_OK;
 }
 
+// The no-allocation variant's workspace: the split partials of fnkv_attn_decode_noalloc live in this file-scope
+// device array (each device that runs the library holds its own copy until the process ends). Host code never passes
+// the array's name to a kernel (on the host it is only a stand-in for the symbol): it asks each device once for the
+// array's device address and uses that.
+constexpr int64_t kNoAllocScratchBytes = int64_t(16) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void * g_scratch_ptr[64] = {nullptr};
+} // namespace
+
+// the device address of `scratch` on `device` (the current device while it is looked up), looked up on the first
+// call for that device; null (with the error set) when the lookup fails
+void * scratch_on(int32_t device) {
+    if (device < 0 || device >= 64) {
+        set_error("fnkv_attn_decode_noalloc: device index outside 0 .. 63");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device] == nullptr) {
+        int32_t cur = 0;
+        if (hipGetDevice(&cur) != hipSuccess || hipSetDevice(device) != hipSuccess) {
+            set_error("fnkv_attn_decode_noalloc: cannot make the pool's device current");
+            return nullptr;
+        }
+        void * ptr = nullptr;
+        const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        (void)hipSetDevice(cur);
+        if (rc != hipSuccess || ptr == nullptr) {
+            set_error(std::string("fnkv_attn_decode_noalloc: hipGetSymbolAddress failed: ") + hipGetErrorString(rc));
+            return nullptr;
+        }
+        g_scratch_ptr[device] = ptr;
+    }
+    return g_scratch_ptr[device];
+}
+
 } // namespace fnkv
 
 extern "C" {
@@ -1291,6 +1331,40 @@ int fnkv_attn_decode_dev(const fnkv_pool * pool, int32_t n_seq, const int32_t * 
     return fnkv::decode_launch(pool, n_seq, slots, max_ctx, ctx, err, T, layer, hq, scale, q, k_new, v_new,
                                new_dtype, out, ws, ws_bytes, static_cast<hipStream_t>(stream),
                                "fnkv_attn_decode_dev");
+}
+
+int fnkv_attn_decode_noalloc(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx,
+                             const int64_t * max_ctx, int32_t T, int32_t layer, int32_t hq, float scale,
+                             const void * q, const void * k_new, const void * v_new, int32_t new_dtype, void * out,
+                             uint32_t * err, void * stream) {
+    const fnkv::kv_pool * p = fnkv::pool_of(pool);
+    if (p == nullptr || hq <= 0 || max_ctx == nullptr) {
+        fnkv::set_error("fnkv_attn_decode_noalloc: argument outside the contract");
+        return FNKV_ERR_ARG;
+    }
+    const int64_t need = fnkv_decode_workspace_bytes(pool, n_seq, max_ctx, T, hq);
+    if (need < 0) {
+        fnkv::set_error("fnkv_attn_decode_noalloc: argument outside the contract");
+        return FNKV_ERR_ARG;
+    }
+    if (need > fnkv::kNoAllocScratchBytes) {
+        fnkv::set_error("fnkv_attn_decode_noalloc: the launch needs " + std::to_string(need) +
+                        " bytes of split partials, more than the library's fixed " +
+                        std::to_string(fnkv::kNoAllocScratchBytes) + "-byte scratch (use fnkv_attn_decode_dev)");
+        return FNKV_ERR_ARG;
+    }
+    void * ws = fnkv::scratch_on(p->device());
+    if (ws == nullptr) {
+        return FNKV_ERR_HIP;
+    }
+    if (ctx == nullptr || err == nullptr || (reinterpret_cast<uintptr_t>(ctx) & 7) != 0 ||
+        (reinterpret_cast<uintptr_t>(err) & 3) != 0) {
+        fnkv::set_error("fnkv_attn_decode_noalloc: ctx (8-byte aligned) and err (4-byte aligned) device words required");
+        return FNKV_ERR_ARG;
+    }
+    return fnkv::decode_launch(pool, n_seq, slots, max_ctx, ctx, err, T, layer, hq, scale, q, k_new, v_new, new_dtype,
+                               out, ws, fnkv::kNoAllocScratchBytes, static_cast<hipStream_t>(stream),
+                               "fnkv_attn_decode_noalloc");
 }
 
 } // extern "C"

@@ -25,7 +25,7 @@ EXPORTS = [
     "fnkv_sparse_workspace_bytes", "fnkv_attn_sparse", "fnkv_rope_theta_scale", "fnkv_datc_part_bytes",
     "fnkv_datc_prepare", "fnkv_datc_attend", "fnkv_datc_step", "fnkv_qsa_workspace_bytes", "fnkv_qsa_attend",
     "fnkv_attn_decode_dev", "fnkv_attn_sparse_dev", "fnkv_attend_workspace_bytes", "fnkv_attend",
-    "fnkv_attend_lanes",
+    "fnkv_attend_lanes", "fnkv_attn_decode_noalloc",
 ]
 DEV_ERR_DEPTH = 2
 MAX_LANES = 4
@@ -138,6 +138,8 @@ def lib():
         L.fnkv_attn_decode_dev.restype = ctypes.c_int
         L.fnkv_attn_decode_dev.argtypes = [P, I32, P, P, P, I32, I32, I32, ctypes.c_float, P, P, P, I32, P, P, I64, P,
                                            P]
+        L.fnkv_attn_decode_noalloc.restype = ctypes.c_int
+        L.fnkv_attn_decode_noalloc.argtypes = [P, I32, P, P, P, I32, I32, I32, ctypes.c_float, P, P, P, I32, P, P, P]
         L.fnkv_attn_sparse_dev.restype = ctypes.c_int
         L.fnkv_attn_sparse_dev.argtypes = [P, I32, P, I64, I32, I32, I32, ctypes.c_float, P, P, P, P, P, I32, P, P,
                                            I64, P, P]
@@ -319,6 +321,19 @@ class Pool:
         return check(lib().fnkv_attn_decode_dev(self.h, len(slots), sp, _p(ctx_dev), mp, T, layer, q.shape[2], scale,
                                                 P(q.data_ptr()), kp, vp, dt, P(out.data_ptr()), P(ws.data_ptr()),
                                                 ws.numel() * ws.element_size(), _p(err), _stream(stream)))
+
+    def decode_noalloc(self, slots, ctx_dev, max_ctx, T, layer, q, out, err, scale=1.0 / 16.0, k_new=None,
+                       v_new=None, stream=None):
+        """fnkv_attn_decode_noalloc: decode_dev without a workspace (the library's fixed device scratch)."""
+        import torch
+        sp, k1 = _i32_array(slots)
+        mp, k2 = _i64_array(max_ctx)
+        kp = P(k_new.data_ptr()) if k_new is not None else None
+        vp = P(v_new.data_ptr()) if v_new is not None else None
+        dt = F32 if (k_new is not None and k_new.dtype == torch.float32) else F16
+        return check(lib().fnkv_attn_decode_noalloc(self.h, len(slots), sp, _p(ctx_dev), mp, T, layer, q.shape[2],
+                                                    scale, P(q.data_ptr()), kp, vp, dt, P(out.data_ptr()), _p(err),
+                                                    _stream(stream)))
 
     def sparse_dev(self, slot, depth_dev, max_cells, layer, q, body, offsets, out, ws, err, scale=1.0 / 16.0,
                    k_new=None, v_new=None, stream=None):

@@ -165,6 +165,19 @@ int fnkv_attn_decode_dev(const fnkv_pool * pool, int32_t n_seq, const int32_t * 
                          const void * k_new, const void * v_new, int32_t new_dtype, void * out, void * ws,
                          int64_t ws_bytes, uint32_t * err, void * stream);
 
+/* No counterpart in the reference: fnkv_attn_decode_dev for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Arguments and results as
+ * fnkv_attn_decode_dev's, bitwise, without ws / ws_bytes: the split partials live in a fixed 16 MiB device array of the
+ * library (one a GPU, held until the process ends), and the call allocates nothing. A launch whose partials
+ * (fnkv_decode_workspace_bytes(pool, n_seq, max_ctx, T, hq)) exceed 16 MiB is refused (FNKV_ERR_ARG, nothing
+ * enqueued); cfg-sized launches (4 sequences of 8K-64K at T = 3, or one of 262,144 at T = 5) need 6-11 MiB. Every
+ * call on one GPU shares that array (nothing in it needs to start at zero): calls that overlap on one GPU (other
+ * streams, or other threads) race and must be serialized by the caller. */
+int fnkv_attn_decode_noalloc(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx,
+                             const int64_t * max_ctx, int32_t T, int32_t layer, int32_t hq, float scale,
+                             const void * q, const void * k_new, const void * v_new, int32_t new_dtype, void * out,
+                             uint32_t * err, void * stream);
+
 /* ---- sparse (QSA) attention at decode rows (fn/kernels/qsa/attend.h:97-141 attend over a selection body) ---- */
 
 /* The workspace a sparse launch at this depth needs (bytes; no zeroing needed); -1 outside the contract. */
