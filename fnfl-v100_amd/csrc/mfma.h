@@ -154,8 +154,16 @@ __device__ __forceinline__ u32x4 stream_load16(const void * gptr) {
 // plus scalar and immediate offsets, with no 64-bit address arithmetic in VGPRs. The descriptor is a raw buffer
 // (stride 0) of `bytes` bytes with the 32-bit data format gfx9 raw loads need.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// a pointer every lane of the wave holds, made provably uniform (scalar registers): a descriptor the compiler cannot
+// prove uniform becomes a readfirstlane loop around every load that uses it
+__device__ __forceinline__ const void * uniform_ptr(const void * p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(v)));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(v >> 32)));
+    return reinterpret_cast<const void *>((uint64_t(hi) << 32) | lo);
+}
 __device__ __forceinline__ rsrc_t make_rsrc(const void * base, int32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(uniform_ptr(base)), 0, bytes, 0x00020000);
 }
 // 16 B a lane at base + voff + soff into registers
 __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, int32_t voff, int32_t soff) {
