@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libfnkv.so")
-SOURCES = ["pool.hip", "append.hip", "decode.hip", "prefill.hip", "sparse.hip", "datc.hip", "qsa.hip"]
+SOURCES = ["pool.hip", "append.hip", "decode.hip", "prefill.hip", "sparse.hip", "datc.hip", "qsa.hip", "qsp.hip"]
 ARCH = os.environ.get("FNKV_ARCH", "gfx950")
 
 COMMON = [
@@ -34,7 +34,7 @@ def hipcc():
 # attention kernels run two waves a SIMD and keep their matrix-core accumulators in ordinary registers (VGPR form)
 VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 EXTRA = {"append.hip": ["-ffp-contract=off"], "decode.hip": VGPR_MFMA, "prefill.hip": VGPR_MFMA,
-         "sparse.hip": ["-ffp-contract=off"], "qsa.hip": ["-ffp-contract=off"]}
+         "sparse.hip": ["-ffp-contract=off"], "qsa.hip": ["-ffp-contract=off"], "qsp.hip": ["-ffp-contract=off"]}
 
 
 def _compile(src):

@@ -888,8 +888,8 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
     rest /= a.R;
     const int32_t kvh = rest % a.h_kv;
     const int32_t s = rest / a.h_kv;
-    const int32_t s0 = a.split0[s];
-    int32_t n = a.split0[s + 1] - s0;
+    const int32_t s0 = a.uniform_splits > 0 ? s * a.uniform_splits : a.split0[s];
+    int32_t n = a.uniform_splits > 0 ? a.uniform_splits : a.split0[s + 1] - s0;
     if (a.ctx_dev != nullptr) { // a device context: a refused sequence is left as it was; strided splits past
                                 // its tiles held nothing
         const int64_t c = a.ctx_dev[s];
@@ -962,16 +962,34 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
         }
         const int32_t t = r / a.G, h = kvh * a.G + r % a.G;
         const int64_t row = (int64_t(s) * a.T + t) * a.hq + h;
-        if (a.out_f32 != nullptr) {
-            // the gate, the F32 output and its activation run (the run's 32 values are lanes 0..7's)
+        if (a.gate != nullptr) {
+            // the gate, the F32 output and its activation run (the run's 32 values are lanes 0..7's), or the prompt
+            // path's fp16 output
             const float * gr = a.gate + row * a.gate_stride + chunk * 32 + tid * 4;
             float y[4];
 #pragma unroll
             for (int32_t e = 0; e < 4; ++e) {
                 y[e] = As[e] / Ls * (1.0f / (1.0f + expf(-gr[e])));
             }
-            *reinterpret_cast<float4 *>(a.out_f32 + row * kHeadDim + chunk * 32 + tid * 4) =
-                make_float4(y[0], y[1], y[2], y[3]);
+            if (a.out_f32 != nullptr) {
+                *reinterpret_cast<float4 *>(a.out_f32 + row * kHeadDim + chunk * 32 + tid * 4) =
+                    make_float4(y[0], y[1], y[2], y[3]);
+            }
+            if (a.out16 != nullptr) {
+                bool bad = false;
+                uint16_t hb[4];
+#pragma unroll
+                for (int32_t e = 0; e < 4; ++e) {
+                    bad = bad || !(fabsf(y[e]) <= 65504.0f);
+                    hb[e] = __half_as_ushort(__float2half_rn(y[e]));
+                }
+                *reinterpret_cast<uint2 *>(a.out16 + row * kHeadDim + chunk * 32 + tid * 4) =
+                    make_uint2(uint32_t(hb[0]) | (uint32_t(hb[1]) << 16), uint32_t(hb[2]) | (uint32_t(hb[3]) << 16));
+                if (bad && a.err != nullptr) {
+                    atomicOr(a.err, 1u);
+                }
+                return;
+            }
             int8_t q[4];
             float ds[2];
             act_run<4, 8>(y, q, ds);

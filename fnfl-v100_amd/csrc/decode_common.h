@@ -62,6 +62,11 @@ struct dec_args {
     const uint32_t * sel_body;
     int32_t * sel_n;
     int32_t sel_split;
+    // prompt rows (qsp_attend): the bodies sit in slabs of kSlabRows rows (kSlabWords words a slab), row r's at word
+    // offsets[(r / kSlabRows) * (kSlabRows + 1) + r % kSlabRows] / 4 of its slab; the launch's rows are rows
+    // sel_row0 .. of that layout. Null: the rows' bodies are packed in order (qsa.h:77-81)
+    const int32_t * sel_offsets = nullptr;
+    int32_t sel_row0 = 0;
     fused_prep fp;
 #ifdef FNKV_TIMING
     uint64_t * ts; // per workgroup: 16 real-time stamps (instrumented builds only)
@@ -133,6 +138,8 @@ constexpr int32_t kSelMaxTiles = (kSelMaxCells + kTileTokens - 1) / kTileTokens;
 constexpr int32_t kSelTopBlocks = 512;                                            // blocks a row (qsa.h)
 constexpr int32_t kSelMaxRows = 5;
 constexpr int32_t kSelMaxThreads = 512;
+constexpr int32_t kSlabRows = 128;                          // prompt rows a slab (qsa_prompt.h prompt_slab)
+constexpr int64_t kSlabWords = int64_t(kSlabRows) * (2 + kSelTopBlocks + 3); // a slab's bodies (max_row_words each)
 
 // list entries a split takes when n_sel entries go to n_splits splits (at most 64: the host launches enough splits)
 __host__ __device__ inline int32_t sparse_split_size(int32_t n_sel, int32_t n_splits) {
@@ -306,10 +313,15 @@ __device__ __forceinline__ dec_args sparse_row_view(const dec_args & in) {
     const int32_t z = static_cast<int32_t>(blockIdx.z);
     const int64_t depth = in.depth_dev != nullptr ? int64_t(*in.depth_dev) : in.ctx[0] - in.T;
     int64_t words = 0;
-    for (int32_t t = 0; t < z; ++t) {
-        const int64_t q = depth + t;
-        const int64_t n_vis = (q + 1) / 4;
-        words += 2 + (n_vis < 512 ? n_vis : 512) + (q + 1) % 4;
+    if (in.sel_offsets != nullptr) { // a prompt row: its slab, then its offset in the slab
+        const int32_t r = in.sel_row0 + z, slab = r / kSlabRows;
+        words = int64_t(slab) * kSlabWords + in.sel_offsets[slab * (kSlabRows + 1) + r % kSlabRows] / 4;
+    } else {
+        for (int32_t t = 0; t < z; ++t) {
+            const int64_t q = depth + t;
+            const int64_t n_vis = (q + 1) / 4;
+            words += 2 + (n_vis < 512 ? n_vis : 512) + (q + 1) % 4;
+        }
     }
     const int64_t rows_all = int64_t(gridDim.x) * gridDim.y * in.G; // a row's partial rows
     a.T = 1;
@@ -478,6 +490,10 @@ struct merge_args {
     const int32_t * depth_dev = nullptr;
     int64_t cap[FNKV_MAX_SEQS] = {0};
     int32_t T_dev = 0; // the launch's step tokens (rows of a sparse launch)
+    // every sequence (row) holds uniform_splits splits: sequence s's first is s * uniform_splits (0: split0[])
+    int32_t uniform_splits = 0;
+    // the gated form's prompt output (qsp_attend): out16 fp16 [rows][hq][256] of the gated value (out_f32 optional),
+    // bit 0 of *err set for a value that fp16 cannot hold (|x| > 65,504, or NaN); null: the activation format
     // the gated form (fn/kernels/qsa/attend.cu:619-655's finish): with out_f32 set, row (t, h)'s value d is written as
     // o / (1 + exp(-gate[(t hq + h) gate_stride + d])) in F32 [T][hq][256] with its int8 activation format (codes
     // [T][hq 256], act_scales [T][hq 8][2]) instead of the fp16 out
@@ -486,6 +502,8 @@ struct merge_args {
     float * out_f32 = nullptr;
     int8_t * codes = nullptr;
     float * act_scales = nullptr;
+    uint16_t * out16 = nullptr;
+    uint32_t * err = nullptr;
 };
 
 class kv_pool;
@@ -512,6 +530,12 @@ int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T
                   const void * q, const void * body, const void * offsets, const void * k_new, const void * v_new,
                   int32_t new_dtype, void * out, const sparse_gate * gate, void * ws, int64_t ws_bytes,
                   hipStream_t st, const char * who, const fused_prep * fp = nullptr, const dev_depth * dd = nullptr);
+// host: prompt rows over their selection bodies (sparse.hip): the workspace of a chunk of n rows whose last row sees
+// `cells` cells, and the chunk's launches (the sparse kernels, then the gated merge into out16 / out_f32 / err)
+int64_t prompt_ws_bytes(const kv_pool & p, int64_t cells, int32_t n, int32_t G);
+int prompt_launch(const kv_pool & p, int32_t slot, int32_t layer, int32_t pos0, int32_t row0, int32_t n, int32_t hq,
+                  const uint16_t * q16, const uint32_t * body, const int32_t * offsets, const float * gate,
+                  float * out_f32, uint16_t * out16, uint32_t * err, void * ws, hipStream_t st);
 // LDS of the one-row sparse launch's formed query rows (after the tile buffers and the selection slice)
 constexpr int32_t kFusedQLds = 16 * kHeadDim * 2;
 

@@ -195,6 +195,79 @@ int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T
     return FNKV_OK;
 }
 
+// Prompt rows (qsp_attend): rows row0 .. row0 + n - 1 of a prompt half at positions pos0 + row, each over its own
+// selection body (the slab layout), q16 the rows' prepared fp16 queries [n][hq][256], then the gated merge into the
+// F32 (optional) and fp16 outputs. The caller has checked the arguments; ws holds prompt_ws_bytes(pool, cells, n, hq).
+int64_t prompt_ws_bytes(const kv_pool & p, int64_t cells, int32_t n, int32_t G) {
+    return plan_sparse(p, cells - n, n, G).bytes;
+}
+
+int prompt_launch(const kv_pool & p, int32_t slot, int32_t layer, int32_t pos0, int32_t row0, int32_t n, int32_t hq,
+                  const uint16_t * q16, const uint32_t * body, const int32_t * offsets, const float * gate,
+                  float * out_f32, uint16_t * out16, uint32_t * err, void * ws, hipStream_t st) {
+    const int32_t G = hq / p.h_kv();
+    const int64_t last = int64_t(pos0) + row0 + n; // cells the chunk's last row sees
+    const sparse_plan pl = plan_sparse(p, last - n, n, G);
+    uint8_t * w = static_cast<uint8_t *>(ws);
+    dec_args a;
+    a.pv = p.view();
+    a.q = q16;
+    a.k_new = nullptr;
+    a.v_new = nullptr;
+    a.new_f32 = 0;
+    a.po = reinterpret_cast<float *>(w + pl.po_off);
+    a.pml = reinterpret_cast<float *>(w + pl.pml_off);
+    a.c2 = (1.0f / 16.0f) * 1.4426950408889634f;
+    a.layer = layer;
+    a.T = n;
+    a.G = G;
+    a.hq = hq;
+    a.R = G * n;
+    a.n_seq = 1;
+    a.split_tokens = 0;
+    a.strided = 0;
+    for (int32_t i = 0; i < FNKV_MAX_SEQS; ++i) {
+        a.slot[i] = slot;
+        a.ctx[i] = last;
+    }
+    a.split0[0] = 0;
+    for (int32_t i = 1; i <= FNKV_MAX_SEQS; ++i) {
+        a.split0[i] = pl.n_splits;
+    }
+    a.sel_body = body;
+    a.sel_n = reinterpret_cast<int32_t *>(w);
+    a.sel_split = pl.per_split;
+    a.sel_offsets = offsets;
+    a.sel_row0 = row0;
+#ifdef FNKV_TIMING
+    a.ts = timing_buffer();
+#endif
+    launch_decode_sparse(p, (G + 15) / 16,
+                         dim3(static_cast<uint32_t>(pl.n_splits), static_cast<uint32_t>(p.h_kv()),
+                              static_cast<uint32_t>(n)),
+                         a, st);
+    merge_args m;
+    m.po = a.po;
+    m.pml = a.pml;
+    m.out = nullptr;
+    m.T = 1;
+    m.G = G;
+    m.hq = hq;
+    m.R = G;
+    m.h_kv = p.h_kv();
+    m.n_seq = n;
+    m.uniform_splits = pl.n_splits;
+    m.sel_n = a.sel_n;
+    m.sel_split = pl.per_split;
+    m.gate = gate;
+    m.gate_stride = 512;
+    m.out_f32 = out_f32;
+    m.out16 = out16;
+    m.err = err;
+    launch_merge(m, st);
+    return hipGetLastError() == hipSuccess ? FNKV_OK : FNKV_ERR_HIP;
+}
+
 } // namespace fnkv
 
 using fnkv::set_error;

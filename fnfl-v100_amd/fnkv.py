@@ -25,8 +25,10 @@ EXPORTS = [
     "fnkv_sparse_workspace_bytes", "fnkv_attn_sparse", "fnkv_rope_theta_scale", "fnkv_datc_part_bytes",
     "fnkv_datc_prepare", "fnkv_datc_attend", "fnkv_datc_step", "fnkv_qsa_workspace_bytes", "fnkv_qsa_attend",
     "fnkv_attn_decode_dev", "fnkv_attn_sparse_dev", "fnkv_attend_workspace_bytes", "fnkv_attend",
-    "fnkv_attend_lanes", "fnkv_attn_decode_noalloc",
+    "fnkv_attend_lanes", "fnkv_attn_decode_noalloc", "fnkv_qsp_kv", "fnkv_qsp_workspace_bytes", "fnkv_qsp_attend",
 ]
+QSP_MAX_ROWS = 4096
+SLAB_ROWS, ROW_WORDS = 128, 517
 DEV_ERR_DEPTH = 2
 MAX_LANES = 4
 DATC_HEADS = 12
@@ -63,6 +65,19 @@ class AttendArgs(ctypes.Structure):
                 ("q_norm", P), ("k_norm", P), ("body", P), ("offsets", P), ("pos", P), ("depth", P),
                 ("max_cells", I32), ("theta_scale", ctypes.c_float), ("out", P), ("codes", P), ("scales", P),
                 ("q_f32", P), ("k_f32", P), ("ws", P), ("ws_bytes", I64), ("err", P)]
+
+
+class QspKvArgs(ctypes.Structure):
+    """fnkv_qsp_kv_args (include/fnkv.h)"""
+    _fields_ = [("pool", P), ("slot", I32), ("layer", I32), ("kv_k", P), ("kv_v", P), ("k_norm", P), ("rows", I32),
+                ("pos0", I32), ("rope_off", I32), ("planes", P), ("theta_scale", ctypes.c_float)]
+
+
+class QspAttendArgs(ctypes.Structure):
+    """fnkv_qsp_attend_args (include/fnkv.h)"""
+    _fields_ = [("pool", P), ("slot", I32), ("layer", I32), ("hq", I32), ("qfull", P), ("q_norm", P), ("body", P),
+                ("offsets", P), ("rows", I32), ("pos0", I32), ("out", P), ("out16", P), ("err", P),
+                ("rope_off", I32), ("planes", P), ("theta_scale", ctypes.c_float), ("ws", P), ("ws_bytes", I64)]
 
 
 class FnkvError(RuntimeError):
@@ -149,6 +164,12 @@ def lib():
         L.fnkv_attend.argtypes = [I32, ctypes.POINTER(AttendArgs), P]
         L.fnkv_attend_lanes.restype = ctypes.c_int
         L.fnkv_attend_lanes.argtypes = [I32, I32, ctypes.POINTER(AttendArgs), P]
+        L.fnkv_qsp_kv.restype = ctypes.c_int
+        L.fnkv_qsp_kv.argtypes = [ctypes.POINTER(QspKvArgs), P]
+        L.fnkv_qsp_workspace_bytes.restype = I64
+        L.fnkv_qsp_workspace_bytes.argtypes = [P, I32, I32, I32]
+        L.fnkv_qsp_attend.restype = ctypes.c_int
+        L.fnkv_qsp_attend.argtypes = [ctypes.POINTER(QspAttendArgs), P]
         L.fnkv_rope_theta_scale.restype = ctypes.c_float
         L.fnkv_rope_theta_scale.argtypes = []
         L.fnkv_datc_part_bytes.restype = I64
@@ -362,6 +383,28 @@ class Pool:
         a._keep = (qfull, kv_k, kv_v, q_norm, k_norm, pos, body, offsets, out, codes, scales, ws, err, q_f32, k_f32,
                    depth_dev)
         return a
+
+    def qsp_kv(self, slot, layer, pos0, kv_k, kv_v, k_norm, planes=None, rope_off=0, stream=None):
+        """qsp_kv: kv_k, kv_v F32 [rows][h_kv][256] device tensors, planes int32 [rows][4] or None."""
+        a = QspKvArgs(self.h, slot, layer, _p(kv_k), _p(kv_v), _p(k_norm), kv_k.shape[0], pos0, rope_off,
+                      _p(planes), rope_theta_scale())
+        return check(lib().fnkv_qsp_kv(ctypes.byref(a), _stream(stream)))
+
+    def qsp_ws_bytes(self, pos0, rows, hq):
+        return lib().fnkv_qsp_workspace_bytes(self.h, pos0, rows, hq)
+
+    def qsp_attend(self, slot, layer, pos0, qfull, q_norm, body, offsets, out16, out=None, err=None, planes=None,
+                   rope_off=0, ws=None, stream=None):
+        """qsp_attend: qfull F32 [rows][hq][512], body / offsets the slab layout (int32 device tensors), out16
+        fp16 [rows][hq][256], out F32 (optional), err int32 [1] (optional)."""
+        import torch
+        rows, hq = qfull.shape[0], qfull.shape[1]
+        if ws is None:
+            ws = torch.empty(max(16, self.qsp_ws_bytes(pos0, rows, hq)), dtype=torch.uint8, device=qfull.device)
+        a = QspAttendArgs(self.h, slot, layer, hq, _p(qfull), _p(q_norm), _p(body), _p(offsets), rows, pos0,
+                          _p(out), _p(out16), _p(err), rope_off, _p(planes), rope_theta_scale(), _p(ws),
+                          ws.numel() * ws.element_size())
+        return check(lib().fnkv_qsp_attend(ctypes.byref(a), _stream(stream)))
 
     def sparse_ws_bytes(self, depth, T, hq):
         return lib().fnkv_sparse_workspace_bytes(self.h, depth, T, hq)

@@ -277,6 +277,62 @@ int fnkv_attend(int32_t rows, const fnkv_attend_args * a, void * stream);
  * anything is enqueued: FNKV_ERR_ARG with nothing enqueued when any lane is outside the contract. */
 int fnkv_attend_lanes(int32_t lanes, int32_t rows, const fnkv_attend_args * a, void * stream);
 
+/* ---- the prompt path's own contract: qsp_kv and qsp_attend (fn/kernels/qsa/qsa_prompt.h:90-124) ---- */
+
+#define FNKV_QSP_MAX_ROWS 4096 /* rows a call (qsa_prompt.h prompt_max_rows) */
+
+/* fn::qsa::qsp_kv_args (qsa_prompt.h:90-102) over the pool: the caches are the pool's slot and layer (its format:
+ * Q8_0 or KV8) */
+typedef struct {
+    const fnkv_pool * pool;
+    int32_t slot;
+    int32_t layer;
+    const float * kv_k;     /* F32 [rows][h_kv][256], before the norm */
+    const float * kv_v;     /* F32 [rows][h_kv][256] */
+    const float * k_norm;   /* [256] */
+    int32_t rows, pos0;     /* rows 1 .. FNKV_QSP_MAX_ROWS at cells pos0 .. pos0 + rows - 1 (mapped) */
+    int32_t rope_off;       /* row t's rotary position pos0 + rope_off + t (every plane) when planes is null */
+    const int32_t * planes; /* optional device [rows][4]: row t's rope planes (t, h, w, e) */
+    float theta_scale;      /* fnkv_rope_theta_scale() */
+} fnkv_qsp_kv_args;
+
+/* qsp_kv (qsa_prompt.h:104, qsa_prompt_attn.cu:90-122, 440-454): row t's k = IMROPE(RMS norm(kv_k) k_norm) at its
+ * rope position and v = kv_v, written at cell pos0 + t in the pool's format (the codes bitwise the pool quantizer's of
+ * that F32 k). FNKV_ERR_ARG with nothing enqueued outside the contract. */
+int fnkv_qsp_kv(const fnkv_qsp_kv_args * a, void * stream);
+
+/* fn::qsa::qsp_attend_args (qsa_prompt.h:106-122) over the pool */
+typedef struct {
+    const fnkv_pool * pool;
+    int32_t slot;
+    int32_t layer;
+    int32_t hq;              /* query heads (the reference's card: 12 on one KV head) */
+    const float * qfull;     /* F32 [rows][hq][512]: each head's q, then its gate */
+    const float * q_norm;    /* [256] */
+    const uint32_t * body;   /* the rows' selection bodies, slab layout: slab k (rows 128 k ..) at body + k 128 517 */
+    const int32_t * offsets; /* [slabs][129]: row i of slab k's body at byte offsets[129 k + i] of its slab */
+    int32_t rows, pos0;      /* row t at position pos0 + t (its cells, and every cell it selects, written) */
+    float * out;             /* optional F32 [rows][hq][256] */
+    uint16_t * out16;        /* fp16 [rows][hq][256] */
+    uint32_t * err;          /* optional device word: bit 0 for an output fp16 cannot hold (|x| > 65,504, NaN) */
+    int32_t rope_off;        /* as fnkv_qsp_kv_args */
+    const int32_t * planes;
+    float theta_scale;
+    void * ws;               /* fnkv_qsp_workspace_bytes of device memory (no zeroing needed) */
+    int64_t ws_bytes;
+} fnkv_qsp_attend_args;
+
+/* the workspace of fnkv_qsp_attend for these rows at pos0 (bytes); -1 outside the contract */
+int64_t fnkv_qsp_workspace_bytes(const fnkv_pool * pool, int32_t pos0, int32_t rows, int32_t hq);
+
+/* qsp_attend (qsa_prompt.h:124, qsa_prompt_attn.cu:229-471): each row's query heads q = IMROPE(RMS norm(q) q_norm)
+ * attend over the row's selection body (its blocks' 4 cells each, then its tail) with scores q . k / 16, softmax and
+ * accumulation in F32 over the pool's codes, and out = o / (1 + exp(-gate)) goes to out (F32, optional) and out16
+ * (fp16, nearest even), bit 0 of *err for a value fp16 cannot hold. The reference rounds q / 16 and its K / V to fp16
+ * and holds the result to 2e-2 (its prompt test's bound); here q enters as fp16 and every other product keeps ~22
+ * bits, held to 2e-3. FNKV_ERR_ARG with nothing enqueued outside the contract. */
+int fnkv_qsp_attend(const fnkv_qsp_attend_args * a, void * stream);
+
 /* ---- chunked-prefill attention (fn/kernels/qsa/qsa_prompt.h:106-124 qsp_attend) ---- */
 
 /* the workspace a prefill launch of this shape uses (bytes; 0: none; -1: a shape outside the contract) */
