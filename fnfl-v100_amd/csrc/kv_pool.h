@@ -6,6 +6,8 @@
 
 #include "layout.h"
 
+#include <hip/hip_runtime.h>
+
 #include <cstdint>
 #include <string>
 #include <vector>
@@ -70,6 +72,7 @@ class kv_pool {
   private:
     bool zero_pages(const std::vector<int32_t> & phys, std::string & err);
     bool upload_table(int32_t slot, std::string & err);
+    bool finish(std::string & err);
     void release_all();
 
     int32_t n_slots_ = 0, page_cells_ = 0, layers_ = 0, h_kv_ = 0, device_ = 0, table_stride_ = 0;
@@ -77,6 +80,9 @@ class kv_pool {
     int64_t slot_cells_ = 0, bytes_ = 0;
     uint8_t * base_ = nullptr;
     int32_t * table_dev_ = nullptr;
+    int32_t * stage_dev_ = nullptr;  // ensure's staging: n_pages page ids, then one table row
+    int32_t * stage_host_ = nullptr; // pinned, the same layout
+    hipStream_t stream_ = nullptr;   // the pool's own stream (default priority)
     kv_pages pages_;
     int32_t fail_after_ = -1;
 };

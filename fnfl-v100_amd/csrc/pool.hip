@@ -135,20 +135,34 @@ __global__ void zero_pages_kernel(uint8_t * base, const int32_t * pages, int32_t
 kv_pool::~kv_pool() { release_all(); }
 
 void kv_pool::release_all() {
-    if (base_ != nullptr || table_dev_ != nullptr) {
+    if (base_ != nullptr || table_dev_ != nullptr || stage_dev_ != nullptr || stage_host_ != nullptr ||
+        stream_ != nullptr) {
         int32_t cur = 0;
         hipGetDevice(&cur);
         hipSetDevice(device_);
+        if (stream_ != nullptr) {
+            hipStreamSynchronize(stream_);
+            hipStreamDestroy(stream_);
+        }
         if (base_ != nullptr) {
             hipFree(base_);
         }
         if (table_dev_ != nullptr) {
             hipFree(table_dev_);
         }
+        if (stage_dev_ != nullptr) {
+            hipFree(stage_dev_);
+        }
+        if (stage_host_ != nullptr) {
+            hipHostFree(stage_host_);
+        }
         hipSetDevice(cur);
     }
     base_ = nullptr;
     table_dev_ = nullptr;
+    stage_dev_ = nullptr;
+    stage_host_ = nullptr;
+    stream_ = nullptr;
 }
 
 bool kv_pool::init(int32_t n_slots, int32_t n_pages, int32_t page_cells, int32_t layers, int32_t h_kv,
@@ -192,6 +206,13 @@ bool kv_pool::init(int32_t n_slots, int32_t n_pages, int32_t page_cells, int32_t
     }
     bool ok = hipMalloc(&base_, size_t(bytes_)) == hipSuccess;
     ok = ok && hipMalloc(&table_dev_, sizeof(int32_t) * size_t(n_slots) * size_t(table_stride_)) == hipSuccess;
+    // the staging of ensure/trim, allocated once: the new pages' list (n_pages entries at most) and a page-table row,
+    // pinned on the host and on the device, and the pool's own stream (default priority) that orders their copies
+    // and the zeroing kernel
+    const size_t stage = sizeof(int32_t) * (size_t(n_pages) + size_t(table_stride_));
+    ok = ok && hipMalloc(&stage_dev_, stage) == hipSuccess;
+    ok = ok && hipHostMalloc(reinterpret_cast<void **>(&stage_host_), stage, hipHostMallocDefault) == hipSuccess;
+    ok = ok && hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking) == hipSuccess;
     if (ok) {
         std::vector<int32_t> none(size_t(n_slots) * size_t(table_stride_), -1);
         ok = hipMemcpy(table_dev_, none.data(), none.size() * sizeof(int32_t), hipMemcpyHostToDevice) == hipSuccess;
@@ -207,24 +228,23 @@ bool kv_pool::init(int32_t n_slots, int32_t n_pages, int32_t page_cells, int32_t
     return true;
 }
 
+// The new pages' bytes zeroed on the pool's stream: their list copied through the pinned staging (no allocation,
+// no host wait here; finish() waits)
 bool kv_pool::zero_pages(const std::vector<int32_t> & phys, std::string & err) {
     if (phys.empty()) {
         return true;
     }
-    int32_t * dev = nullptr;
-    bool ok = hipMalloc(&dev, phys.size() * sizeof(int32_t)) == hipSuccess;
-    ok = ok && hipMemcpy(dev, phys.data(), phys.size() * sizeof(int32_t), hipMemcpyHostToDevice) == hipSuccess;
+    std::copy(phys.begin(), phys.end(), stage_host_);
+    bool ok = hipMemcpyAsync(stage_dev_, stage_host_, phys.size() * sizeof(int32_t), hipMemcpyHostToDevice,
+                             stream_) == hipSuccess;
     if (ok) {
         const int64_t page_stride = int64_t(h_kv_) * kPageBlock;
         const int32_t chunks = static_cast<int32_t>((page_stride + 16383) / 16384);
         const int64_t grid = int64_t(layers_) * int64_t(phys.size()) * chunks;
-        hipLaunchKernelGGL(zero_pages_kernel, dim3(static_cast<uint32_t>(grid)), dim3(256), 0, nullptr, base_, dev,
-                           static_cast<int32_t>(phys.size()), int64_t(pages_.n_pages()) * page_stride, page_stride,
-                           chunks);
-        ok = hipGetLastError() == hipSuccess && hipStreamSynchronize(nullptr) == hipSuccess;
-    }
-    if (dev != nullptr) {
-        hipFree(dev);
+        hipLaunchKernelGGL(zero_pages_kernel, dim3(static_cast<uint32_t>(grid)), dim3(256), 0, stream_, base_,
+                           stage_dev_, static_cast<int32_t>(phys.size()), int64_t(pages_.n_pages()) * page_stride,
+                           page_stride, chunks);
+        ok = hipGetLastError() == hipSuccess;
     }
     if (!ok) {
         err = "KV pool: zeroing new pages failed";
@@ -232,13 +252,26 @@ bool kv_pool::zero_pages(const std::vector<int32_t> & phys, std::string & err) {
     return ok;
 }
 
+// The slot's page-table row (its mapped pages, then -1) written on the pool's stream after the zeroing it follows
 bool kv_pool::upload_table(int32_t slot, std::string & err) {
-    std::vector<int32_t> row(size_t(table_stride_), -1);
+    int32_t * row = stage_host_ + pages_.n_pages();
     const std::vector<int32_t> & t = pages_.table(slot);
-    std::copy(t.begin(), t.end(), row.begin());
-    if (hipMemcpy(table_dev_ + int64_t(slot) * table_stride_, row.data(), row.size() * sizeof(int32_t),
-                  hipMemcpyHostToDevice) != hipSuccess) {
+    std::fill(row, row + table_stride_, -1);
+    std::copy(t.begin(), t.end(), row);
+    if (hipMemcpyAsync(table_dev_ + int64_t(slot) * table_stride_, row, size_t(table_stride_) * sizeof(int32_t),
+                       hipMemcpyHostToDevice, stream_) != hipSuccess) {
         err = "KV pool: page table upload failed";
+        return false;
+    }
+    return true;
+}
+
+// ensure/trim are synchronous, as the reference's are: the pool's stream drained before they return, so work the
+// caller enqueues afterwards on any stream sees the zeroed pages and the new table row
+bool kv_pool::finish(std::string & err) {
+    if (hipStreamSynchronize(stream_) != hipSuccess) {
+        hipGetLastError();
+        err = "KV pool: page setup failed on the device";
         return false;
     }
     return true;
@@ -275,17 +308,20 @@ bool kv_pool::ensure(int32_t slot, int64_t cells, std::string & err, bool * capa
         // TEST ONLY: the transaction fails after readying fail_after_ of its new pages
         std::vector<int32_t> part(taken.begin(), taken.begin() + std::min<size_t>(size_t(fail_after_), taken.size()));
         zero_pages(part, err);
+        finish(err);
         fail_after_ = -1;
         err = "KV pool: page setup (TEST: an injected failure)";
         ok = false;
     } else {
         ok = zero_pages(taken, err) && upload_table(slot, err);
+        ok = finish(err) && ok;
     }
     if (!ok) {
+        std::string e2;
+        finish(e2); // the staging is free again
         std::vector<int32_t> back;
         pages_.give(slot, first, back);
-        std::string e2;
-        upload_table(slot, e2);
+        upload_table(slot, e2) && finish(e2);
     }
     hipSetDevice(cur);
     return ok;
@@ -302,7 +338,7 @@ bool kv_pool::trim(int32_t slot, int64_t keep_cells, std::string & err) {
     int32_t cur = 0;
     hipGetDevice(&cur);
     hipSetDevice(device_);
-    const bool ok = upload_table(slot, err);
+    const bool ok = upload_table(slot, err) && finish(err);
     hipSetDevice(cur);
     return ok;
 }
