@@ -15,6 +15,9 @@
 
 namespace fnkv {
 
+// Waves 0 .. rows * h_kv - 1 write one K row each; the waves after them write V four cells at a time: the quads of
+// aligned positions 4 g .. 4 g + 3 that the rows touch (the four cells' bytes of one value are adjacent in the V
+// layout, so each lane stores a dword a value; a quad the rows cover in part writes only its own cells).
 // pos_dev set: the first position is the device word *pos_dev, read by the launch; a position outside
 // 0 .. max_cells - rows writes nothing (the launch that reads the rows reports it)
 template <bool F32>
@@ -30,23 +33,49 @@ __global__ __launch_bounds__(256) void append_kernel(pool_view pv, int32_t slot,
     }
     const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
     const int64_t w = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    const int32_t kv = static_cast<int32_t>(w & 1);
-    const int64_t rh = w >> 1;
-    const int32_t head = static_cast<int32_t>(rh % pv.h_kv);
-    const int64_t row = rh / pv.h_kv;
-    if (row >= rows) {
+    const int32_t * table = pv.table + int64_t(slot) * pv.table_stride;
+    const int64_t k_waves = int64_t(rows) * pv.h_kv;
+    if (w < k_waves) {
+        const int32_t head = static_cast<int32_t>(w % pv.h_kv);
+        const int64_t row = w / pv.h_kv;
+        const int64_t src = (row * pv.h_kv + head) * kHeadDim;
+        float x[4];
+        if (F32) {
+            load4<true>(static_cast<const float *>(kin) + src, lane, x);
+        } else {
+            load4<false>(static_cast<const uint16_t *>(kin) + src, lane, x);
+        }
+        const int64_t pos = pos0 + row;
+        quantize_store_fmt(x, lane, tile_of(pv, table, layer, head, pos), static_cast<int32_t>(pos & 31), 0,
+                           pv.format);
         return;
     }
-    const int64_t src = (row * pv.h_kv + head) * kHeadDim;
-    float x[4];
-    if (F32) {
-        load4<true>(static_cast<const float *>(kv ? vin : kin) + src, lane, x);
-    } else {
-        load4<false>(static_cast<const uint16_t *>(kv ? vin : kin) + src, lane, x);
+    const int64_t vw = w - k_waves;
+    const int32_t head = static_cast<int32_t>(vw % pv.h_kv);
+    const int64_t quad = (pos0 >> 2) + vw / pv.h_kv;
+    const int64_t p0 = quad * 4;
+    if (p0 >= pos0 + rows) {
+        return; // past the last quad (the grid allows for any alignment of pos0)
     }
-    const int64_t pos = pos0 + row;
-    uint8_t * t = tile_of(pv, pv.table + int64_t(slot) * pv.table_stride, layer, head, pos);
-    quantize_store_fmt(x, lane, t, static_cast<int32_t>(pos & 31), kv, pv.format);
+    uint32_t packed[4] = {0, 0, 0, 0};
+    uint16_t sbits[4] = {0, 0, 0, 0};
+    uint32_t valid = 0;
+#pragma unroll
+    for (int32_t i = 0; i < 4; ++i) {
+        const int64_t row = p0 + i - pos0;
+        if (row >= 0 && row < rows) { // uniform across the wave
+            valid |= 1u << i;
+            const int64_t src = (row * pv.h_kv + head) * kHeadDim;
+            float x[4];
+            if (F32) {
+                load4<true>(static_cast<const float *>(vin) + src, lane, x);
+            } else {
+                load4<false>(static_cast<const uint16_t *>(vin) + src, lane, x);
+            }
+            quantize_fmt(x, pv.format, packed[i], sbits[i]);
+        }
+    }
+    store_v_quad(packed, sbits, valid, lane, tile_of(pv, table, layer, head, p0), static_cast<int32_t>(p0 & 31));
 }
 
 // one wave a cell: its 8 blocks of (layer, head, kv) as 8 x 34 bytes of block_q8_0
@@ -103,7 +132,8 @@ __global__ __launch_bounds__(256) void export_kv8_kernel(pool_view pv, int32_t s
 
 int append_enqueue(const kv_pool & p, int32_t slot, int32_t layer, int64_t pos0, const int32_t * pos_dev,
                    int64_t max_cells, int32_t rows, const void * k, const void * v, int32_t dtype, hipStream_t st) {
-    const int64_t waves = int64_t(rows) * p.h_kv() * 2;
+    // K: a wave a row; V: a wave a quad of aligned cells, rows / 4 + 2 quads at most whatever pos0's alignment
+    const int64_t waves = int64_t(rows) * p.h_kv() + (int64_t(rows) / 4 + 2) * p.h_kv();
     const uint32_t grid = static_cast<uint32_t>((waves + 3) / 4);
     if (dtype == FNKV_F32) {
         hipLaunchKernelGGL(append_kernel<true>, dim3(grid), dim3(256), 0, st, p.view(), slot, layer, pos0, rows, k, v,

@@ -47,9 +47,9 @@ template <bool F32> __device__ __forceinline__ void load4(const void * row, int3
     }
 }
 
-// quantize this wave's row (x: the lane's 4 values) and store it as cell tt of `tile` (kv: 0 K, 1 V)
-__device__ __forceinline__ void quantize_store(const float (&x)[4], int32_t lane, uint8_t * tile, int32_t tt,
-                                               int32_t kv) {
+// Q8_0: this wave's row (x: the lane's 4 values) -> the lane's 4 codes as excess-128 bytes (byte e = value 4 lane + e)
+// and the block's fp16 scale bits (the same in the block's 8 lanes)
+__device__ __forceinline__ void quantize_q8_0(const float (&x)[4], uint32_t & packed, uint16_t & sbits) {
 #pragma clang fp contract(off)
     float amax = fmaxf(fmaxf(__builtin_fabsf(x[0]), __builtin_fabsf(x[1])),
                        fmaxf(__builtin_fabsf(x[2]), __builtin_fabsf(x[3])));
@@ -59,33 +59,16 @@ __device__ __forceinline__ void quantize_store(const float (&x)[4], int32_t lane
     amax = fmaxf(amax, __shfl_xor(amax, 4));
     const float d = __fdiv_rn(amax, 127.0f);
     const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-    uint32_t packed = 0;
-    uint8_t bytes[4];
+    packed = 0;
 #pragma unroll
     for (int32_t e = 0; e < 4; ++e) {
         const float r = round_half_away(x[e] * id);
         // an in-contract input gives |r| <= 127; outside it (an fp32 input whose d underflows to a subnormal, so id
         // is inf) the reference's int8 store of roundf keeps the low byte of x86's 0x80000000 result: code 0
         const int32_t c = __builtin_fabsf(r) < 2147483648.0f ? static_cast<int32_t>(r) : INT32_MIN;
-        bytes[e] = static_cast<uint8_t>((c & 0xff) ^ 0x80); // excess-128 storage
-        packed |= uint32_t(bytes[e]) << (8 * e);
+        packed |= uint32_t((c & 0xff) ^ 0x80) << (8 * e); // excess-128 storage
     }
-    const int32_t d0 = 4 * lane, b = lane >> 3;
-    const uint16_t dh = __half_as_ushort(__float2half_rn(d));
-    if (kv == 0) {
-        *reinterpret_cast<uint32_t *>(tile + k_code_off(tt, d0)) = packed;
-        if ((lane & 7) == 0) {
-            *reinterpret_cast<uint16_t *>(tile + k_scale_off(tt, b)) = dh;
-        }
-    } else {
-#pragma unroll
-        for (int32_t e = 0; e < 4; ++e) {
-            tile[v_code_off(tt, d0 + e)] = bytes[e];
-        }
-        if ((lane & 7) == 0) {
-            *reinterpret_cast<uint16_t *>(tile + v_scale_off(tt, b)) = dh;
-        }
-    }
+    sbits = __half_as_ushort(__float2half_rn(d));
 }
 
 // The KV8 rule, bit for bit FNFL's kv_q8_quantize_group (fn/quant/kv_q8_ref.cpp:72-87; device kv8::quantize8,
@@ -93,8 +76,7 @@ __device__ __forceinline__ void quantize_store(const float (&x)[4], int32_t lane
 // division, round to nearest even), s its exact value; code = 0 when s == 0, else clamp(rint(x / s), -127, 127)
 // (IEEE division, ties to even). The 16 lanes of a group (lanes 16 g .. 16 g + 15) reduce amax; the group's scale is
 // stored at both of its 32-value blocks.
-__device__ __forceinline__ void quantize_store_kv8(const float (&x)[4], int32_t lane, uint8_t * tile, int32_t tt,
-                                                   int32_t kv) {
+__device__ __forceinline__ void quantize_kv8(const float (&x)[4], uint32_t & packed, uint16_t & sbits) {
 #pragma clang fp contract(off)
     float amax = fmaxf(fmaxf(__builtin_fabsf(x[0]), __builtin_fabsf(x[1])),
                        fmaxf(__builtin_fabsf(x[2]), __builtin_fabsf(x[3])));
@@ -104,8 +86,7 @@ __device__ __forceinline__ void quantize_store_kv8(const float (&x)[4], int32_t 
     amax = fmaxf(amax, __shfl_xor(amax, 8));
     const __half h = __float2half_rn(__fdiv_rn(amax, 127.0f));
     const float sv = __half2float(h);
-    uint32_t packed = 0;
-    uint8_t bytes[4];
+    packed = 0;
 #pragma unroll
     for (int32_t e = 0; e < 4; ++e) {
         int32_t c = 0;
@@ -113,35 +94,77 @@ __device__ __forceinline__ void quantize_store_kv8(const float (&x)[4], int32_t 
             const float r = __builtin_rintf(__fdiv_rn(x[e], sv));
             c = r < -127.0f ? -127 : r > 127.0f ? 127 : static_cast<int32_t>(r);
         }
-        bytes[e] = static_cast<uint8_t>((c & 0xff) ^ 0x80);
-        packed |= uint32_t(bytes[e]) << (8 * e);
+        packed |= uint32_t((c & 0xff) ^ 0x80) << (8 * e);
     }
+    sbits = __half_as_ushort(h);
+}
+
+// the pool's rule (format: kFormatQ8_0 or kFormatKV8, uniform across the wave)
+__device__ __forceinline__ void quantize_fmt(const float (&x)[4], int32_t format, uint32_t & packed,
+                                             uint16_t & sbits) {
+    if (format == kFormatKV8) {
+        quantize_kv8(x, packed, sbits);
+    } else {
+        quantize_q8_0(x, packed, sbits);
+    }
+}
+
+// one quantized row as cell tt of `tile` (kv: 0 K, 1 V): K's 4 codes of a lane are adjacent (one dword store); V's sit
+// in 4 rows of the transposed layout (4 byte stores: the append kernel writes V four cells at a time instead)
+__device__ __forceinline__ void store_row(uint32_t packed, uint16_t sbits, int32_t lane, uint8_t * tile, int32_t tt,
+                                          int32_t kv) {
     const int32_t d0 = 4 * lane, b = lane >> 3;
-    const uint16_t sh = __half_as_ushort(h);
     if (kv == 0) {
         *reinterpret_cast<uint32_t *>(tile + k_code_off(tt, d0)) = packed;
         if ((lane & 7) == 0) {
-            *reinterpret_cast<uint16_t *>(tile + k_scale_off(tt, b)) = sh;
+            *reinterpret_cast<uint16_t *>(tile + k_scale_off(tt, b)) = sbits;
         }
     } else {
 #pragma unroll
         for (int32_t e = 0; e < 4; ++e) {
-            tile[v_code_off(tt, d0 + e)] = bytes[e];
+            tile[v_code_off(tt, d0 + e)] = static_cast<uint8_t>(packed >> (8 * e));
         }
         if ((lane & 7) == 0) {
-            *reinterpret_cast<uint16_t *>(tile + v_scale_off(tt, b)) = sh;
+            *reinterpret_cast<uint16_t *>(tile + v_scale_off(tt, b)) = sbits;
         }
     }
 }
 
-// the pool's rule (format: kFormatQ8_0 or kFormatKV8, uniform across the wave)
+// V rows of the four cells tt0 .. tt0 + 3 (tt0 a multiple of 4) of `tile`, those with bit i of `valid` set: the four
+// cells' bytes of one value are adjacent in the V layout (slots s .. s + 3 of one 16-byte row), so a lane writes one
+// dword a value, and the block's four scales are adjacent too (one 8-byte store); a partial quad writes its bytes one
+// by one (other launches' cells of the quad are left as they are)
+__device__ __forceinline__ void store_v_quad(const uint32_t (&packed)[4], const uint16_t (&sbits)[4], uint32_t valid,
+                                             int32_t lane, uint8_t * tile, int32_t tt0) {
+    const int32_t d0 = 4 * lane, b = lane >> 3;
+    if (valid == 0xfu) {
+#pragma unroll
+        for (int32_t e = 0; e < 4; ++e) {
+            const uint32_t w = ((packed[0] >> (8 * e)) & 0xffu) | (((packed[1] >> (8 * e)) & 0xffu) << 8) |
+                               (((packed[2] >> (8 * e)) & 0xffu) << 16) | (((packed[3] >> (8 * e)) & 0xffu) << 24);
+            *reinterpret_cast<uint32_t *>(tile + v_code_off(tt0, d0 + e)) = w;
+        }
+        if ((lane & 7) == 0) {
+            *reinterpret_cast<uint2 *>(tile + v_scale_off(tt0, b)) =
+                make_uint2(uint32_t(sbits[0]) | (uint32_t(sbits[1]) << 16), uint32_t(sbits[2]) | (uint32_t(sbits[3]) << 16));
+        }
+    } else {
+#pragma unroll
+        for (int32_t i = 0; i < 4; ++i) {
+            if ((valid >> i) & 1u) {
+                store_row(packed[i], sbits[i], lane, tile, tt0 + i, 1);
+            }
+        }
+    }
+}
+
+// quantize this wave's row (x: the lane's 4 values) by the pool's rule and store it as cell tt of `tile`
 __device__ __forceinline__ void quantize_store_fmt(const float (&x)[4], int32_t lane, uint8_t * tile, int32_t tt,
                                                    int32_t kv, int32_t format) {
-    if (format == kFormatKV8) {
-        quantize_store_kv8(x, lane, tile, tt, kv);
-    } else {
-        quantize_store(x, lane, tile, tt, kv);
-    }
+    uint32_t packed;
+    uint16_t sbits;
+    quantize_fmt(x, format, packed, sbits);
+    store_row(packed, sbits, lane, tile, tt, kv);
 }
 
 } // namespace fnkv
