@@ -32,6 +32,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 namespace fnkv {
@@ -673,16 +674,17 @@ bool attend_args_ok(const fnkv_datc_attend_args * a) {
 
 template <bool FUSED>
 int launch_attend(const fnkv_datc_attend_args & a, const fnkv_datc_prepare_args & pa, hipStream_t st) {
-    static bool attr_set[64] = {false};
+    static std::once_flag attr_once[64]; // once per device; a racing first caller waits for it
     int dev = 0;
     (void)hipGetDevice(&dev);
-    if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(datc_attend_kernel<false, FUSED>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, kAttendLds);
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(datc_attend_kernel<true, FUSED>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, kAttendLds);
-        (void)hipGetLastError();
-        attr_set[dev] = true;
+    if (dev >= 0 && dev < 64) {
+        std::call_once(attr_once[dev], []() {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(datc_attend_kernel<false, FUSED>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kAttendLds);
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(datc_attend_kernel<true, FUSED>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kAttendLds);
+            (void)hipGetLastError();
+        });
     }
     if (a.body != nullptr) {
         hipLaunchKernelGGL((datc_attend_kernel<true, FUSED>), dim3(kGrid), dim3(64 * kWaves), kAttendLds, st, a, pa);

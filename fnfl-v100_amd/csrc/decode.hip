@@ -33,6 +33,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <mutex>
@@ -622,6 +623,9 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
         if (grp + k * GR >= n_tiles) {
             return;
         }
+#ifdef FNKV_QK_PRIO
+        __builtin_amdgcn_s_setprio(FNKV_QK_PRIO);
+#endif
         const uint8_t * kb = kslot(k % SK);
         const uint8_t * sc_tile = kb + kCodeBytes / 2 - kKScales; // scale offsets are tile-relative
         const int64_t tok0 = src.tok0(grp + k * GR);
@@ -640,6 +644,9 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
         if (qg == 0) {
             aslot(par, w)[j] = alpha;
         }
+#ifdef FNKV_QK_PRIO
+        __builtin_amdgcn_s_setprio(0);
+#endif
     };
     // O^T += V^T P^T of tile k over this wave's value blocks, for every row tile, from the exchange buffers of
     // parity PAR and the V codes in vb
@@ -1034,19 +1041,20 @@ int32_t decode_lds(int32_t nt, bool sp) {
 }
 
 int32_t device_cus(int32_t device) {
-    static int32_t cache[64] = {0};
+    // threads racing on the first query each store the same count
+    static std::atomic<int32_t> cache[64];
     if (device < 0 || device >= 64) {
         return 256;
     }
-    if (cache[device] == 0) {
-        int32_t n = 0;
+    int32_t n = cache[device].load(std::memory_order_relaxed);
+    if (n == 0) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0) {
-            hipGetLastError();
+            (void)hipGetLastError();
             n = 256;
         }
-        cache[device] = n;
+        cache[device].store(n, std::memory_order_relaxed);
     }
-    return cache[device];
+    return n;
 }
 
 // the split size (tokens, a multiple of the page) for these contexts: the fewest rounds of one workgroup a CU times
@@ -1131,17 +1139,19 @@ template <bool SP, bool KV8> void launch_decode_fmt(int32_t NT, dim3 grid, const
 
 // the decode kernel for NT row tiles (sparse or dense) and the pool's format, its LDS attribute set once per device
 template <bool SP> void launch_decode(const kv_pool & p, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
-    static bool attr_set[64] = {false};
+    // once per device, before any launch of it returns: a thread arriving while another sets the attributes waits
+    static std::once_flag attr_once[64];
     const int32_t dev = p.device();
-    if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-        int32_t cur = 0;
-        (void)hipGetDevice(&cur);
-        (void)hipSetDevice(dev);
-        set_decode_attrs<SP, false>();
-        set_decode_attrs<SP, true>();
-        (void)hipGetLastError();
-        (void)hipSetDevice(cur);
-        attr_set[dev] = true;
+    if (dev >= 0 && dev < 64) {
+        std::call_once(attr_once[dev], [dev]() {
+            int32_t cur = 0;
+            (void)hipGetDevice(&cur);
+            (void)hipSetDevice(dev);
+            set_decode_attrs<SP, false>();
+            set_decode_attrs<SP, true>();
+            (void)hipGetLastError();
+            (void)hipSetDevice(cur);
+        });
     }
     if (a.pv.format == kFormatKV8) {
         launch_decode_fmt<SP, true>(NT, grid, a, st);

@@ -726,7 +726,9 @@ __device__ __forceinline__ void tile_scores(const uint8_t * kb, const uint8_t * 
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         sc[h] = tile_scores_half<QOP, PAIR>(kb, sc_tile, qop, sig, j, qg, lane, h);
+#ifndef FNKV_NO_HALF_SB
         __builtin_amdgcn_sched_barrier(0); // one half's operands live at a time
+#endif
     }
 }
 

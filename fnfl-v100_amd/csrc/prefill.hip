@@ -29,6 +29,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 namespace fnkv {
 
@@ -444,17 +445,18 @@ int fnkv_attn_prefill(const fnkv_pool * pool, int32_t slot, int32_t layer, int64
     a.split_tiles = pl.split_tiles;
     a.po = static_cast<float *>(ws);
     a.pml = a.po == nullptr ? nullptr : a.po + int64_t(pl.n_split) * p->h_kv() * pl.rows_pad * fnkv::kHeadDim;
-    static bool attr_set[64] = {false};
+    static std::once_flag attr_once[64]; // once per device; a racing first caller waits for it
     const int32_t dev = p->device();
-    if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-        int32_t cur = 0;
-        hipGetDevice(&cur);
-        hipSetDevice(dev);
-        hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::prefill_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::kPfLds);
-        hipGetLastError();
-        hipSetDevice(cur);
-        attr_set[dev] = true;
+    if (dev >= 0 && dev < 64) {
+        std::call_once(attr_once[dev], [dev]() {
+            int32_t cur = 0;
+            (void)hipGetDevice(&cur);
+            (void)hipSetDevice(dev);
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(fnkv::prefill_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, fnkv::kPfLds);
+            (void)hipGetLastError();
+            (void)hipSetDevice(cur);
+        });
     }
     const dim3 grid(static_cast<uint32_t>(pl.row_blocks), static_cast<uint32_t>(p->h_kv()),
                     static_cast<uint32_t>(pl.n_split));
