@@ -241,10 +241,30 @@ def test_split_walks_contiguous_and_strided(T, strided, monkeypatch):
 
 @pytest.mark.parametrize("T", [1, 3, 5])
 def test_eight_sequences_at_split_edges(T):
-    # the most sequences a launch takes (FNKV_MAX_SEQS), their contexts at and around the split sizes the planner
+    # eight sequences, their contexts at and around the split sizes the planner
     # picks (1,024 / 2,048 cells) and the 32-cell tile and 256-cell page edges
     ctxs = [1024, 2048, 2049, 4096, 6143, 10240, 20481, 40000]
     st = Setup(ctxs, seed=30 + T, churn=0.25)
     q16 = cases.queries(40 + T, (len(ctxs), T, HQ, 256))
     got = st.run(q16, T)
     assert st.check(q16, got, T) <= TOL
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_sixteen_sequences_the_launch_maximum(T):
+    # FNKV_MAX_SEQS = 16 sequences in one launch (the split table's last entries, the merge's sequence index past 8),
+    # contexts ragged around tile, page and split edges, pages interleaved with churn
+    ctxs = [33, 255, 257, 1000, 1024, 1025, 2047, 2048, 3000, 4096, 5121, 6143, 7777, 8192, 9000, 12289]
+    st = Setup(ctxs, seed=60 + T, churn=0.25)
+    q16 = cases.queries(70 + T, (len(ctxs), T, HQ, 256))
+    got = st.run(q16, T)
+    assert st.check(q16, got, T) <= TOL
+
+
+def test_seventeen_sequences_refused():
+    st = Setup([64] * 17, seed=5)
+    q = torch.zeros((17, 1, HQ, 256), dtype=torch.float16, device="cuda")
+    out = torch.zeros_like(q)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    with pytest.raises(fnkv.FnkvError):
+        st.pool.decode(st.slots, st.ctxs, 1, 0, q, out, ws)
