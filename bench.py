@@ -57,6 +57,10 @@ CONFIGS = {
                            "and gate included, 12 layers"),
     "qa2b1": dict(depth=196608 - 1, T=1, layers=12, attend=True,
                   workload="qa2b1: the same with 1 row"),
+    "cfg4": dict(layers=12, T=5, chunk=4096, mixed=True,
+                 workload="cfg4: mixed 8-sequence pool step with page churn: 3 finished sequences free their pages, 2 "
+                          "sequences append and attend a 4,096-token chunk, 6 verify T=5 at contexts U[1K, 196K], 12 "
+                          "layers"),
     "datc": dict(cells=196608, datc=True,
                  workload="datc: DA-TC draft step row (prepare with q, dense attention, gate) at 196,608 cells of F16 "
                           "K/V, 12 query heads, the reference's deepest draft-bench point"),
@@ -101,36 +105,91 @@ def make_pool(torch, fnkv, cases, ctxs, T, layers, seed, h_kv=HKV, fmt=None):
     return pool, slots
 
 
-def cpu_baseline(ctxs, T, layers, seed, threads):
-    """The oracle's ggml-semantics CPU flash attention (fp32 Q) on one layer of the workload (all sequences),
-    scaled to tokens/s of the whole step; returns the dict for the JSON line."""
+def host_info():
+    """The host the CPU baseline runs on: logical CPUs (nproc), the CPUs this process may run on, the model name, and
+    the thread count used: every CPU the process may use, capped by OMP_NUM_THREADS where the environment sets one (the
+    GPU box sets it to its per-GPU CPU share)."""
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(affinity, int(cap)) if cap.isdigit() and int(cap) > 0 else affinity
+    return {"nproc": os.cpu_count(), "affinity_cpus": affinity, "cpu_model": model, "threads": threads,
+            "thread_cap": f"OMP_NUM_THREADS={cap}" if cap else None}
+
+
+def _best_of(fn, reps=5):
+    fn()  # warmup (threads, caches)
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, time.perf_counter() - t0)
+    return best
+
+
+def _cpu_case(O, cases, seed, ctx, T, threads, q_seed=None):
+    """ggml-semantics CPU flash attention (Q as Q8_0 with an integer dot, as ggml-cpu runs Q8_0 K; V widened to F32)
+    of T query rows over ctx cells of one layer: best-of-5 seconds after a warmup."""
     import numpy as np
 
+    k16, v16 = cases.kv_rows(seed, ctx, HKV)
+    (kq, kd, _), (vq, vd, _) = cases.decoded(O, k16, v16)
+    kb, vb = O.to_block_q8_0(kq, kd), O.to_block_q8_0(vq, vd)
+    del k16, v16, kq, vq
+    q16 = cases.queries(seed if q_seed is None else q_seed, (T, HQ, D)).view(np.uint16)
+    return kb, vb, _best_of(lambda: O.attn_ggml(q16, kb, vb, ctx, q_as_q8=True, threads=threads))
+
+
+def cpu_baseline(ctxs, T, layers, seed, extra=True):
+    """The CPU path timed beside the GPU: the oracle's ggml-semantics flash attention over Q8_0 K/V (Q as Q8_0, integer
+    K dot, F32 V accumulate: ggml-cpu's path for Q8_0 caches), multithreaded over (query row, head), on one of the
+    layers of the workload (all sequences at full context), best-of-5 after a warmup, scaled to tokens/s of the whole
+    step. With `extra`, cfg0 (4,096 cells, T = 1) and cfg2 (262,144 cells, T = 1 and T = 5) are timed the same way.
+    Returns the dict for the JSON line."""
     import cases
     import oracle as O
 
+    info = host_info()
+    threads = info["threads"]
     t_layer = 0.0
     for i, c in enumerate(ctxs):
-        k16, v16 = cases.kv_rows(seed + i, c, HKV)
-        (kq, kd, _), (vq, vd, _) = cases.decoded(O, k16, v16)
-        kb, vb = O.to_block_q8_0(kq, kd), O.to_block_q8_0(vq, vd)
-        q16 = cases.queries(seed + i, (T, HQ, D)).view(np.uint16)
-        O.attn_ggml(q16, kb, vb, min(c, 2048), threads=threads)  # warm the threads and caches
-        t0 = time.perf_counter()
-        O.attn_ggml(q16, kb, vb, c, threads=threads)
-        t_layer += time.perf_counter() - t0
+        t_layer += _cpu_case(O, cases, seed + i, c, T, threads)[2]
     tokens = len(ctxs) * T
     tok_s = tokens / (t_layer * layers)
-    return {
+    out = {
         "value": round(tok_s, 3),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"1 of {layers} layers, all {len(ctxs)} sequences at full context, T={T}, fp32-Q ggml-semantics "
-                  f"flash attention over Q8_0 K/V (oracle/fnkv_oracle.c or_attn_ggml), {threads} threads; "
-                  f"layer time {t_layer * 1e3:.1f} ms x {layers} layers",
+        "sample": f"1 of {layers} layers, all {len(ctxs)} sequences at full context, T={T}, ggml-semantics flash "
+                  f"attention over Q8_0 K/V (Q as Q8_0, integer K dot, F32 V; oracle/fnkv_oracle.c or_attn_ggml), "
+                  f"{threads} threads, best of 5 after a warmup; layer time {t_layer * 1e3:.1f} ms x {layers} layers",
         "gb_s": round(algorithmic_bytes(ctxs, T) / t_layer / 1e9, 3),
+        "host": info,
     }
+    if extra:
+        timings = {}
+        _, _, s0 = _cpu_case(O, cases, seed + 100, 4096, 1, threads)
+        timings["cfg0"] = {"ctx": 4096, "T": 1, "seconds": round(s0, 6), "tokens_s": round(1 / s0, 3),
+                           "gb_s": round(algorithmic_bytes([4096], 1) / s0 / 1e9, 3)}
+        kb, vb, s1 = _cpu_case(O, cases, seed + 200, 262144, 1, threads)
+        timings["cfg2_T1"] = {"ctx": 262144, "T": 1, "seconds": round(s1, 6), "tokens_s": round(1 / s1, 3),
+                              "gb_s": round(algorithmic_bytes([262144], 1) / s1 / 1e9, 3)}
+        import numpy as np
+        q16 = cases.queries(seed + 201, (5, HQ, D)).view(np.uint16)
+        s5 = _best_of(lambda: O.attn_ggml(q16, kb, vb, 262144, q_as_q8=True, threads=threads))
+        timings["cfg2_T5"] = {"ctx": 262144, "T": 5, "seconds": round(s5, 6), "tokens_s": round(5 / s5, 3),
+                              "gb_s": round(algorithmic_bytes([262144], 5) / s5 / 1e9, 3)}
+        out["configs"] = timings
+    return out
 
 
 COPY_BYTES = 1 << 30  # the calibration copy: 1 GiB read, 1 GiB written
@@ -290,7 +349,7 @@ def run_prefill(args, cfg):
     }
     if not args.no_cpu:
         import oracle as O
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host_info()["threads"]
         sample = 16
         (kq, kd, _), (vq, vd, _) = cases.decoded(O, kv[0].cpu().numpy(), kv[1].cpu().numpy())
         kb, vb = O.to_block_q8_0(kq, kd), O.to_block_q8_0(vq, vd)
@@ -410,7 +469,7 @@ def run_sparse(args, cfg):
         },
     }
     if not args.no_cpu:
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host_info()["threads"]
         k16, v16 = cases.kv_rows(args.seed, ctx, HKV)
         q16 = cases.queries(args.seed, (T, HQ, D)).view(np.uint16)
         t_layer = 0.0
@@ -683,7 +742,7 @@ def run_datc(args, cfg):
     }
     if not args.no_cpu:
         from threadpoolctl import threadpool_limits
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host_info()["threads"]
         kh = caches[0][0].cpu().numpy().view(np.uint16)
         vh = caches[0][1].cpu().numpy().view(np.uint16)
         qh = q16[0].cpu().numpy().view(np.uint16)
@@ -705,6 +764,217 @@ def run_datc(args, cfg):
     print(json.dumps(line), flush=True)
 
 
+def run_mixed(args, cfg):
+    """a mixed 8-sequence pool step with page churn. Beforehand three finished sequences take
+    interleaved pages and free them (holes in the free list), then the eight sequences grow page by page in a seeded
+    random order (a fragmented page table). A step = for each of the 12 layers: two sequences each append a 4,096-token
+    fp16 chunk (fnkv_q8_append) and attend it causally over their whole context (fnkv_attn_prefill), then one
+    fnkv_attn_decode launch runs the six other sequences' T = 5 verify (their new cells appended by the launch). The
+    step is one HIP graph; the prefill half and the decode half are also captured and timed on their own, giving the
+    prefill's matrix-core rate (algorithmic flops) and the decode's HBM rate (algorithmic bytes)."""
+    import numpy as np
+    import torch
+
+    import cases
+    import fnkv
+
+    layers, T, chunk = cfg["layers"], cfg["T"], cfg["chunk"]
+    rng = np.random.default_rng([args.seed, 4])
+    pf_slots, vf_slots = [0, 1], [2, 3, 4, 5, 6, 7]
+    pf_depth = [int(rng.integers(1024, 196 * 1024 + 1)) for _ in pf_slots]
+    vf_ctx = [int(rng.integers(1024, 196 * 1024 + 1)) for _ in vf_slots]
+    ctx_of = dict(zip(pf_slots, [d + chunk for d in pf_depth]))
+    ctx_of.update(zip(vf_slots, vf_ctx))
+    finished = {5: int(rng.integers(64, 256)), 6: int(rng.integers(64, 256)), 7: int(rng.integers(64, 256))}
+    n_pages = sum(-(-c // 256) for c in ctx_of.values()) + 32
+    torch.cuda.set_device(0)
+    pool = fnkv.Pool(9, n_pages, layers, HKV)
+    have = {s: 0 for s in finished}
+    while any(have[s] < finished[s] for s in finished):
+        s = int(rng.choice([x for x in finished if have[x] < finished[x]]))
+        have[s] += 1
+        assert pool.ensure(s, have[s] * 256)[0] == 0
+    for s in finished:
+        assert pool.trim(s, 0) == 0
+    order = pf_slots + vf_slots
+    cases.scatter_ensure(pool, order, [ctx_of[s] for s in order], args.seed)
+    g = torch.Generator(device="cuda")
+    chunks = {}
+    for layer in range(layers):
+        g.manual_seed(args.seed * 1000 + layer)
+        for s in order:
+            c = ctx_of[s]
+            kv = []
+            for _ in range(2):
+                x = torch.randn((c, HKV, D), generator=g, device="cuda", dtype=torch.float32)
+                ch = torch.randperm(D, generator=g, device="cuda")[:4]
+                x[:, :, ch] *= 8.0
+                kv.append(x.half())
+            upto = c - chunk if s in pf_slots else c - T
+            pool.append(s, layer, 0, kv[0][:upto].contiguous(), kv[1][:upto].contiguous())
+            if s in pf_slots:
+                chunks[(s, layer)] = (kv[0][upto:].contiguous(), kv[1][upto:].contiguous())
+            del kv
+    torch.cuda.synchronize()
+    g.manual_seed(args.seed + 7)
+    qp = {(s, l): torch.randn((chunk, HQ, D), generator=g, device="cuda").half() for s in pf_slots
+          for l in range(layers)}
+    outp = {k: torch.empty_like(v) for k, v in qp.items()}
+    wsp = {}
+    for s in pf_slots:
+        n = pool.prefill_ws_bytes(ctx_of[s], chunk, HQ)
+        wsp[s] = torch.empty(max(n, 16), dtype=torch.uint8, device="cuda") if n > 0 else False
+    nv = len(vf_slots)
+    qv = torch.randn((layers, nv, T, HQ, D), generator=g, device="cuda").half()
+    kn = torch.randn((layers, nv, T, HKV, D), generator=g, device="cuda").half()
+    vn = torch.randn((layers, nv, T, HKV, D), generator=g, device="cuda").half()
+    outv = torch.empty_like(qv)
+    ctxs = [ctx_of[s] for s in vf_slots]
+    wsv = torch.empty(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+
+    def prefill_half(layer):
+        for s in pf_slots:
+            kc, vc = chunks[(s, layer)]
+            pool.append(s, layer, ctx_of[s] - chunk, kc, vc)
+            pool.prefill(s, layer, ctx_of[s], qp[(s, layer)], outp[(s, layer)], ws=wsp[s])
+
+    def decode_half(layer):
+        pool.decode(vf_slots, ctxs, T, layer, qv[layer], outv[layer], wsv, k_new=kn[layer], v_new=vn[layer])
+
+    def whole():
+        for layer in range(layers):
+            prefill_half(layer)
+            decode_half(layer)
+
+    def pre_only():
+        for layer in range(layers):
+            prefill_half(layer)
+
+    def dec_only():
+        for layer in range(layers):
+            decode_half(layer)
+
+    whole()
+    torch.cuda.synchronize()
+
+    def capture(fn):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            fn()
+        torch.cuda.synchronize()
+        return gr
+
+    def timed(gr, steps, warmup):
+        for _ in range(warmup):
+            gr.replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        for _ in range(steps):
+            gr.replay()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, ev0.elapsed_time(ev1) / 1e3
+
+    steps, warm = max(1, args.steps), max(1, args.warmup)
+    g_whole = capture(whole)
+    wall, gpu_whole = timed(g_whole, steps, warm)
+    del g_whole
+    g_dec = capture(dec_only)
+    _, gpu_dec = timed(g_dec, max(steps, 20), warm)
+    gpu_dec /= max(steps, 20)
+    del g_dec
+    g_pre = capture(pre_only)
+    _, gpu_pre = timed(g_pre, steps, warm)
+    gpu_pre /= steps
+    del g_pre
+    assert torch.isfinite(outv.float()).all().item(), "non-finite verify output"
+    assert all(torch.isfinite(o.float()).all().item() for o in outp.values()), "non-finite prefill output"
+
+    tokens = (len(pf_slots) * chunk + nv * T) * steps
+    flops = layers * sum(prefill_flops(ctx_of[s], chunk) for s in pf_slots)
+    dec_bytes = layers * algorithmic_bytes(ctxs, T)
+    pre_tflops = flops / gpu_pre / 1e12
+    dec_gbs = dec_bytes / gpu_dec / 1e9
+    line = {
+        "metric": "decode-attn tokens/s + achieved HBM GB/s over Q8_0 paged KV, 64K-262K ctx",
+        "value": round(tokens / wall, 3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": round(wall / steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0 KV (int8 codes + fp16 scales), fp16 Q/O, fp32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V with 4 of 256 channels x8, N(0,1) Q)",
+        "config": {"workload": cfg["workload"], "prefill_depths": pf_depth, "chunk": chunk,
+                   "verify_contexts": vf_ctx, "T": T, "layers": layers, "q_heads": HQ, "kv_heads": HKV,
+                   "head_dim": D, "page_tokens": 256, "finished_pages_freed": sum(finished.values()),
+                   "hip_graph": True},
+        "step_us": round(gpu_whole / steps * 1e6, 3),
+        "roofline": {
+            "kernel": "prefill half (fnkv_q8_append + fnkv_attn_prefill of both chunks), per step",
+            "bound": "mfma",
+            "achieved": round(pre_tflops, 3),
+            "peak": PEAK_MFMA_F16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(pre_tflops / PEAK_MFMA_F16_TFLOPS, 4),
+            "traffic": None,
+            "flops_per_step": flops,
+            "prefill_us_per_step": round(gpu_pre * 1e6, 3),
+        },
+        "decode_part": {
+            "kernel": "fnkv_attn_decode launch over the six verify sequences (T = 5), 12 a step",
+            "bound": "hbm",
+            "achieved": round(dec_gbs, 3),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(dec_gbs / PEAK_HBM_GBS, 4),
+            "bytes_per_step": dec_bytes,
+            "launch_us": round(gpu_dec / layers * 1e6, 3),
+        },
+    }
+    pool.close()
+    if not args.no_cpu:
+        import oracle as O
+        info = host_info()
+        threads = info["threads"]
+        # decode half: one layer, the six verify sequences; prefill half: the last 16 rows of one chunk, scaled by
+        # visible pairs to both chunks
+        t_dec = 0.0
+        for i, c in enumerate(vf_ctx):
+            t_dec += _cpu_case(O, cases, args.seed + i, c, T, threads)[2]
+        s0 = pf_slots[0]
+        c0 = ctx_of[s0]
+        kb, vb, _ = _cpu_case(O, cases, args.seed + 50, c0, 1, threads)
+        sample = 16
+        q16 = cases.queries(args.seed + 51, (sample, HQ, D)).view(np.uint16)
+        t_s = _best_of(lambda: O.attn_ggml(q16, kb, vb, c0, q_as_q8=True, threads=threads), reps=3)
+        sample_flops = 4 * D * HQ * sum(c0 - sample + t + 1 for t in range(sample))
+        t_pre = t_s * (flops / layers) / sample_flops
+        cpu_step = layers * (t_dec + t_pre)
+        line["cpu_baseline"] = {
+            "value": round((len(pf_slots) * chunk + nv * T) / cpu_step, 3), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"one layer's six verify sequences (T={T}, best of 5) and the last {sample} rows of one chunk "
+                      f"(best of 3, scaled by visible pairs to both chunks), ggml-semantics flash attention (Q as "
+                      f"Q8_0; oracle/fnkv_oracle.c or_attn_ggml), {threads} threads, x {layers} layers",
+            "host": info,
+        }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -720,6 +990,7 @@ def main():
     ap.add_argument("--datc-two-call", action="store_true",
                     help="DA-TC: time fnkv_datc_prepare then fnkv_datc_attend instead of fnkv_datc_step")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes (traffic: null)")
+    ap.add_argument("--no-extra", action="store_true", help="cfg1: skip the cfg2 / cfg2v launches timed beside it")
     ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -734,6 +1005,9 @@ def main():
         return
     if CONFIGS[args.config].get("datc"):
         run_datc(args, CONFIGS[args.config])
+        return
+    if CONFIGS[args.config].get("mixed"):
+        run_mixed(args, CONFIGS[args.config])
         return
     if CONFIGS[args.config].get("attend"):
         run_attend(args, CONFIGS[args.config])
@@ -755,13 +1029,69 @@ def main():
         T = args.T
     if args.ctxs is not None:
         ctxs = [int(c) for c in args.ctxs.split(",")]
-    workload = cfg["workload"] if (args.T is None and args.ctxs is None) else f"custom: contexts {ctxs}, T={T}, {layers} layers"
-    # a single-layer step is one short launch pair: the graph then holds `copies` steps, each over its own layer of the
-    # pool (over 1 GB of caches in all, beyond the 256 MB last-level cache), so one replay's idle gap is spread over
-    # several steps as it is over a many-layer step (cfg1's 12 layers)
-    copies = cfg.get("copies", 1) if not args.no_graph else 1
+    custom = args.T is not None or args.ctxs is not None
+    workload = cfg["workload"] if not custom else f"custom: contexts {ctxs}, T={T}, {layers} layers"
     torch.cuda.set_device(0)
     fmt = fnkv.FMT_KV8 if cfg.get("fmt") == "kv8" else None
+    r = time_decode(args, torch, fnkv, cases, ctxs, T, layers, cfg.get("copies", 1), fmt, args.steps, args.warmup)
+    if r is None:  # the counter pass's child
+        return
+    line = {
+        "metric": "decode-attn tokens/s + achieved HBM GB/s over Q8_0 paged KV, 64K-262K ctx",
+        "value": r["tokens_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": r["n_steps"],
+        "warmup": r["warmup"],
+        "ms_per_step": r["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": ("kv8 KV (int8 codes + fp16 group-64 scales)" if fmt is not None else
+                  "q8_0 KV (int8 codes + fp16 scales)") + ", fp16 Q/O, fp32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V with 4 of 256 channels x8, N(0,1) Q)",
+        "config": {"workload": workload, "contexts": ctxs, "T": T, "layers": layers, "q_heads": HQ,
+                   "kv_heads": HKV, "head_dim": D, "page_tokens": 256, "hip_graph": r["graph"],
+                   "pool_format": cfg.get("fmt", "q8_0"),
+                   "steps_per_graph": r["copies"], "layers_rotated": layers * r["copies"]},
+        "gb_s": r["gb_s"],
+        "roofline": {
+            "kernel": "fnkv_attn_decode launch (decode_kernel + merge_kernel), per layer",
+            "bound": "hbm",
+            "achieved": r["achieved"],
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": r["frac"],
+            "traffic": traffic,
+            "traffic_detail": traffic_detail,
+            "bytes_per_launch": r["bytes_per_launch"],
+            "launch_us": r["launch_us"],
+        },
+    }
+    # the default run also times BASELINE config 2 (262,144 cells, decode T = 1 and verify T = 5), the metric's
+    # deep-context end, on the same box: the same launch, figures per launch
+    if args.config == "cfg1" and not custom and not args.no_extra:
+        also = {}
+        for name in ("cfg2", "cfg2v"):
+            c2 = CONFIGS[name]
+            x = time_decode(args, torch, fnkv, cases, c2["ctxs"], c2["T"], c2["layers"], c2["copies"], None, 8, 4)
+            also[name] = {"workload": c2["workload"], "launch_us": x["launch_us"], "achieved_gb_s": x["achieved"],
+                          "frac": x["frac"], "tokens_s": x["tokens_s"], "bytes_per_launch": x["bytes_per_launch"],
+                          "steps": x["n_steps"]}
+        line["configs_also"] = also
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(ctxs, T, layers, args.seed, extra=args.config == "cfg1" and not custom)
+    print(json.dumps(line), flush=True)
+
+
+def time_decode(args, torch, fnkv, cases, ctxs, T, layers, copies, fmt, steps, warmup):
+    """One fnkv_attn_decode launch a layer over `layers` layers (each appending its T new cells per sequence and
+    attending over the whole context), captured in a HIP graph of `copies` steps over separate layers of the pool (a
+    single-layer step is one short launch pair: the graph then holds several steps, each over its own layer, over 1 GB
+    of caches in all, beyond the 256 MB last-level cache, so one replay's idle gap is spread over several steps as it
+    is over cfg1's 12 layers); W replays untimed, then the timed ones between HIP events on the graph's stream.
+    Returns the figures, or None in a counter pass's child (which only runs the launches)."""
+    copies = copies if not args.no_graph else 1
     pool, slots = make_pool(torch, fnkv, cases, ctxs, T, layers * copies, args.seed, fmt=fmt)
     g = torch.Generator(device="cuda")
     g.manual_seed(args.seed + 7)
@@ -782,7 +1112,7 @@ def main():
     if args.traffic_child:
         traffic_child(args, torch, step)
         pool.close()
-        return
+        return None
     graph = None
     if not args.no_graph:
         s = torch.cuda.Stream()
@@ -797,8 +1127,8 @@ def main():
         torch.cuda.synchronize()
     run = graph.replay if graph is not None else step
 
-    replays = max(1, -(-args.steps // copies))
-    warm = max(1, -(-args.warmup // copies))
+    replays = max(1, -(-steps // copies))
+    warm = max(1, -(-warmup // copies))
     n_steps = replays * copies
     for _ in range(warm):
         run()
@@ -816,49 +1146,17 @@ def main():
     wall = time.perf_counter() - t0
     gpu_s = ev0.elapsed_time(ev1) / 1e3
     assert torch.isfinite(out.float()).all().item(), "non-finite attention output"
+    del graph
+    pool.close()
 
-    ms_per_step = wall / n_steps * 1e3
-    tokens = n * T * n_steps
     bytes_layer = algorithmic_bytes(ctxs, T)
     launch_s = gpu_s / (n_steps * layers)  # one layer's attention launch (decode_kernel + merge_kernel)
     achieved = bytes_layer / launch_s / 1e9
-    line = {
-        "metric": "decode-attn tokens/s + achieved HBM GB/s over Q8_0 paged KV, 64K-262K ctx",
-        "value": round(tokens / wall, 3),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": n_steps,
-        "warmup": warm * copies,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": ("kv8 KV (int8 codes + fp16 group-64 scales)" if fmt is not None else
-                  "q8_0 KV (int8 codes + fp16 scales)") + ", fp16 Q/O, fp32 accumulate",
-        "data": "synthetic (seeded N(0,1) K/V with 4 of 256 channels x8, N(0,1) Q)",
-        "config": {"workload": workload, "contexts": ctxs, "T": T, "layers": layers, "q_heads": HQ,
-                   "kv_heads": HKV, "head_dim": D, "page_tokens": 256, "hip_graph": graph is not None,
-                   "pool_format": cfg.get("fmt", "q8_0"),
-                   "steps_per_graph": copies, "layers_rotated": layers * copies},
-        "gb_s": round(bytes_layer * layers * n_steps / wall / 1e9, 3),
-        "roofline": {
-            "kernel": "fnkv_attn_decode launch (decode_kernel + merge_kernel), per layer",
-            "bound": "hbm",
-            "achieved": round(achieved, 3),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": traffic,
-            "traffic_detail": traffic_detail,
-            "bytes_per_launch": bytes_layer,
-            "launch_us": round(launch_s * 1e6, 3),
-        },
-    }
-    if not args.no_cpu:
-        threads = max(1, min(16, os.cpu_count() or 1))
-        line["cpu_baseline"] = cpu_baseline(ctxs, T, layers, args.seed, threads)
-    print(json.dumps(line), flush=True)
-    pool.close()
+    return {"tokens_s": round(n * T * n_steps / wall, 3), "n_steps": n_steps, "warmup": warm * copies,
+            "ms_per_step": round(wall / n_steps * 1e3, 4), "graph": not args.no_graph, "copies": copies,
+            "gb_s": round(bytes_layer * layers * n_steps / wall / 1e9, 3), "achieved": round(achieved, 3),
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "bytes_per_launch": bytes_layer,
+            "launch_us": round(launch_s * 1e6, 3)}
 
 
 if __name__ == "__main__":
