@@ -770,13 +770,11 @@ __device__ __forceinline__ void tile_softmax(const floatx4 (&sc)[2], int32_t lim
     const float m_new = move ? mx : m_run;
     const float m_use = m_new == kNegInf ? 0.0f : m_new;
     alpha = move ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
-    float lsum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         pf[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(raw[i], c2, -m_use));
-        lsum += pf[i];
     }
-    l_run = __builtin_fmaf(l_run, alpha, lsum);
+    l_run = __builtin_fmaf(l_run, alpha, sum8(pf));
     m_run = m_new;
 }
 

@@ -39,23 +39,37 @@ __device__ __forceinline__ half8 widen8(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(half8, r);
 }
 
+// x - fp16 value h as one mixed-precision FMA (v_fma_mix_f32 reading the fp16 operand in place: half `HI` of the
+// packed pair), exact when h is x truncated to fp16
+template <int HI> __device__ __forceinline__ float sub_f16(float x, uint32_t h2) {
+    float r;
+    if constexpr (HI) {
+        __asm__("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(x));
+    } else {
+        __asm__("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(x));
+    }
+    return r;
+}
+
 // x (8 fp32 values) as hi + lo, both fp16: hi = x rounded toward zero, lo = the remainder rounded toward zero, so
 // hi + lo carries x to about 22 bits (the remainder of a truncation to fp16 is exact in fp32)
 __device__ __forceinline__ void split_hilo(const float (&x)[8], half8 & hi, half8 & lo) {
-    typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
     u32x4 h, l;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const fp16x2 hv = __builtin_amdgcn_cvt_pkrtz(x[2 * i], x[2 * i + 1]);
-        // x - hi as one mixed-precision FMA each (hi read as fp16), exact
-        const float r0 = __builtin_fmaf(static_cast<float>(hv[0]), -1.0f, x[2 * i]);
-        const float r1 = __builtin_fmaf(static_cast<float>(hv[1]), -1.0f, x[2 * i + 1]);
-        const fp16x2 lv = __builtin_amdgcn_cvt_pkrtz(r0, r1);
-        h[i] = __builtin_bit_cast(uint32_t, hv);
-        l[i] = __builtin_bit_cast(uint32_t, lv);
+        const uint32_t hv = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x[2 * i], x[2 * i + 1]));
+        const float r0 = sub_f16<0>(x[2 * i], hv);
+        const float r1 = sub_f16<1>(x[2 * i + 1], hv);
+        h[i] = hv;
+        l[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
     }
     hi = __builtin_bit_cast(half8, h);
     lo = __builtin_bit_cast(half8, l);
+}
+
+// the sum of 8 values as a balanced tree (three dependent adds instead of eight)
+__device__ __forceinline__ float sum8(const float (&x)[8]) {
+    return ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
 }
 
 // 8 codes as the fp16 values 1152 + code (one byte permute per two codes): the operand when the 1152 bias is folded
@@ -97,11 +111,17 @@ __device__ __forceinline__ void scale_hilo_pk(half8 ph, half8 pl, half8 s, half8
 
 // x combined across the wave's four 16-lane rows (lanes l, l ^ 16, l ^ 32, l ^ 48) by two lane swaps on the VALU
 // (v_permlane16_swap, v_permlane32_swap), without the LDS round trip of a shuffle
+// (the max as plain v_max_f32: the lane-swapped values are scores, never NaN, so no canonicalization is needed)
+__device__ __forceinline__ float max_plain(float a, float b) {
+    float r;
+    __asm__("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 __device__ __forceinline__ float rows_max(float x) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    x = max_plain(__uint_as_float(a[0]), __uint_as_float(a[1]));
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    return max_plain(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float rows_sum(float x) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -194,6 +214,36 @@ __device__ __forceinline__ void barrier_keep_loads() {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     __asm__ __volatile__("" ::: "memory");
+}
+
+// Progress flags of a tile group in LDS: the group's waves meet through them instead of the workgroup's s_barrier, so
+// the workgroup's groups run decoupled. A wave publishes a value once its own LDS writes (and the LDS copies it has
+// waited for) are done: lgkmcnt(0) before the flag's store, global loads left in flight. A wave waits for a flag by
+// polling it with s_sleep between reads; a wait longer than `limit` polls gives up and returns false (a bug
+// indicator: every wave of a group reaches every flag value it publishes, so a normal wait is a few thousand cycles).
+__device__ __forceinline__ void flag_publish(int32_t * f, int32_t v) {
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (0 << 8));
+    *reinterpret_cast<volatile int32_t *>(f) = v;
+    __builtin_amdgcn_sched_barrier(0);
+    __asm__ __volatile__("" ::: "memory");
+}
+__device__ __forceinline__ bool flag_wait(const int32_t * f, int32_t v, int32_t limit) {
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    bool ok = true;
+    int32_t n = 0;
+    while (__builtin_amdgcn_readfirstlane(*reinterpret_cast<const volatile int32_t *>(f)) < v) {
+        if (++n > limit) {
+            ok = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __asm__ __volatile__("" ::: "memory");
+    return ok;
 }
 
 } // namespace fnkv
