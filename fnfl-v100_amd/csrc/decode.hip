@@ -463,7 +463,6 @@ template <int NT, bool SP = false> struct rows_shape {
     static constexpr int AX = 2 * NT * 16 * 4;                      // rescale factors: [parity][row tile][row]
     static constexpr int GROUP_LDS = SK * KSLOT + PX + AX;
     static constexpr int Q_LDS = NT == 2 ? 0 : NT * kBlocks * 64 * 16; // Q operands (NT = 3), shared by the groups
-    static constexpr int FLAG_LDS = 64;                                 // the waves' progress flags (decoupled loop)
     // loads a wave has issued after tile k's K chunks when it waits for them (top of iteration k), and after tile
     // k's V codes when it waits for those (before PV of iteration k)
     static constexpr int WAIT_K = NBM + (SK - 2) * (CK + NBM);
@@ -510,8 +509,8 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
         load_q_operands(a, s, ctx, kvh, w, j, qg, qreg, lim);
     }
     split_src<SP, NT == 2> src; // NT = 3 is short of registers: its entries stay in LDS
-    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem,
-                                  smem + GR * SH::GROUP_LDS + SH::Q_LDS + SH::FLAG_LDS, ctx);
+    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * SH::GROUP_LDS + SH::Q_LDS,
+                                  ctx);
     if (refused<SP>(a, s, ctx, sp, kvh)) {
         return;
     }
@@ -618,30 +617,7 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
     // heavy PV of one overlaps the VALU-heavy scores and softmax of the other instead of both doing the same phase.
     // Every wave passes the same barriers: two an iteration, n_iter + 1 iterations.
     const int32_t n_iter = (((n_tiles + GR - 1) / GR) + 1) & ~1;
-#if defined(FNKV_NO_LATE) || defined(FNKV_DECOUPLED)
-    const bool late = false;
-#else
     const bool late = grp >= GR / 2;
-#endif
-#ifdef FNKV_DECOUPLED
-    // the group's waves meet through progress flags (wave w's at flags[w]): 2 k once its share of tile k's K copy has
-    // landed (and its PV of tile k - 1 is done), 2 k + 1 once its P of tile k is in LDS
-    int32_t * const flags = reinterpret_cast<int32_t *>(smem + GR * SH::GROUP_LDS + SH::Q_LDS);
-    if (threadIdx.x < WAVES) {
-        flags[threadIdx.x] = -1;
-    }
-    barrier_keep_loads();
-    bool flags_ok = true;
-    auto group_meet = [&](int32_t v) {
-        flag_publish(flags + wave, v);
-#pragma unroll
-        for (int32_t o = 0; o < NT; ++o) {
-            if (o != w && flags_ok) {
-                flags_ok = flag_wait(flags + grp * NT + o, v, 1 << 22);
-            }
-        }
-    };
-#endif
     const half8 zero8 = {};
     FNKV_PHASE_DECL();
 
@@ -737,20 +713,12 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
         FNKV_PHASE(0 + (k > 0 ? 7 : 0));
         wait_vmcnt<SH::WAIT_K>(); // this wave's chunks of tile k's K copy have landed
         FNKV_PHASE(1);
-#ifdef FNKV_DECOUPLED
-        group_meet(2 * k); // ... every wave's of the group; slot (k - 1) % SK and P buffers of k - 2 are free
-#else
         barrier_keep_loads();     // ... every wave's; slot (k - 1) % SK and P buffers of k - 2 are free
-#endif
         FNKV_PHASE(2);
         issue_k(tile_ptr(k + SK - 1), (k + SK - 1) % SK);
         qk_phase(par_c, k);
         FNKV_PHASE(3);
-#ifdef FNKV_DECOUPLED
-        group_meet(2 * k + 1); // every row tile's P and factors are in LDS
-#else
         barrier_keep_loads(); // every row tile's P and factors are in LDS
-#endif
         FNKV_PHASE(4);
         pv_phase(par_c, k, vb);
         FNKV_PHASE(6);
@@ -821,11 +789,6 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
         late_iteration(std::integral_constant<int32_t, 0>(), n_iter, vbuf1); // PV of the last tile
     }
     wait_vmcnt<0>();
-#ifdef FNKV_DECOUPLED
-    if (!flags_ok && a.err != nullptr && lane == 0) {
-        atomicOr(a.err, FNKV_DEV_ERR_ACQUIRE);
-    }
-#endif
     FNKV_PHASE_STORE();
     FNKV_STAMP(3);
     FNKV_STAMP_WAVE();
@@ -1061,7 +1024,7 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
 // LDS of a decode launch: the groups' tile buffers, or the merge's (m, l) and partial rows, whichever is larger
 template <int NT, bool SP> int32_t rows_lds() {
     using SH = rows_shape<NT, SP>;
-    const int32_t ring = SH::GR * SH::GROUP_LDS + SH::Q_LDS + SH::FLAG_LDS;
+    const int32_t ring = SH::GR * SH::GROUP_LDS + SH::Q_LDS;
     const int32_t merge = SH::GR * NT * 16 * 2 * 4 + SH::GR * NT * 16 * (kHeadDim + 4) * 4;
     return SP ? std::max(std::max(ring + kSelSlice, merge), kSelLds) : std::max(ring, merge);
 }

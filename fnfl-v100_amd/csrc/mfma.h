@@ -216,34 +216,4 @@ __device__ __forceinline__ void barrier_keep_loads() {
     __asm__ __volatile__("" ::: "memory");
 }
 
-// Progress flags of a tile group in LDS: the group's waves meet through them instead of the workgroup's s_barrier, so
-// the workgroup's groups run decoupled. A wave publishes a value once its own LDS writes (and the LDS copies it has
-// waited for) are done: lgkmcnt(0) before the flag's store, global loads left in flight. A wave waits for a flag by
-// polling it with s_sleep between reads; a wait longer than `limit` polls gives up and returns false (a bug
-// indicator: every wave of a group reaches every flag value it publishes, so a normal wait is a few thousand cycles).
-__device__ __forceinline__ void flag_publish(int32_t * f, int32_t v) {
-    __asm__ __volatile__("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (0 << 8));
-    *reinterpret_cast<volatile int32_t *>(f) = v;
-    __builtin_amdgcn_sched_barrier(0);
-    __asm__ __volatile__("" ::: "memory");
-}
-__device__ __forceinline__ bool flag_wait(const int32_t * f, int32_t v, int32_t limit) {
-    __asm__ __volatile__("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    bool ok = true;
-    int32_t n = 0;
-    while (__builtin_amdgcn_readfirstlane(*reinterpret_cast<const volatile int32_t *>(f)) < v) {
-        if (++n > limit) {
-            ok = false;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    __asm__ __volatile__("" ::: "memory");
-    return ok;
-}
-
 } // namespace fnkv

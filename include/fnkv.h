@@ -148,7 +148,6 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
  * launch that reads its context or depth from device memory and finds it outside its contract writes nothing for the
  * sequence concerned and ORs this bit into the caller-cleared word. (The reference's bit 1, an acquire timeout, has no
  * counterpart: no launch here waits on another workgroup.) */
-#define FNKV_DEV_ERR_ACQUIRE 1u /* a wait inside the launch gave up (the reference's acquire-timeout bit) */
 #define FNKV_DEV_ERR_DEPTH 2u
 
 /* fnkv_attn_decode with each sequence's context read from device memory by the launch, the reference's device depth
