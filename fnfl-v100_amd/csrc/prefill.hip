@@ -5,8 +5,8 @@
 // 229-436, made dense and causal, on the pool's codes): S = Q K^T * scale, online softmax, O = P V, fp16 out. The
 // reference rounds its K/V operand to fp16 once (q4_h4, qsa_prompt_attn.cu:195-207) and P to fp16, within a loose
 // 2e-2 bound; here every product carries ~22 bits, so the result meets 2e-3 against fp64 even when a few cells
-// dominate: K goes to the matrix cores exactly as hi + lo fp16 (code x scale has 8 x 11 significant bits), V as its
-// codes (exact in fp16) against P x (the token's V scale) as hi + lo fp16.
+// dominate: K and V go to the matrix cores exactly as hi + lo fp16 (code x scale has 8 x 11 significant bits), P as
+// hi + lo fp16.
 //
 // How (MI355X): matrix-core bound (4 d flops a visible (query, key) pair and head), so K/V tiles are dequantized once
 // a workgroup and shared by all its query rows.
@@ -14,11 +14,15 @@
 //     rows (256 / G query tokens x the G heads of one KV head); each wave owns two 16-row tiles, so each operand
 //     read from LDS feeds two MFMAs. Its waves walk the key tiles (32 tokens) of the workgroup's key split in order;
 //     the splits (blockIdx.z) fill the device when the row blocks alone do not, and a merge kernel folds them.
-//   * Each tile streams HBM -> LDS (16 direct 1 KiB loads of codes split over the waves into a double-buffered
-//     staging slot; the scales chunk into a 4-entry ring), is converted once into fp16 operand planes (K hi, K lo, V
-//     codes; double-buffered: tile k + 1's while tile k is computed); then every wave runs S^T = K Q^T (two
-//     v_mfma_f32_16x16x32_f16 a block, half and row tile) and O^T += V^T (P s_v)^T (two a 16-value tile and row tile).
-//   * The softmax (base 2) runs on the S^T registers as in the decode kernel; P feeds the PV MFMA in place.
+//   * Each tile's codes go from HBM straight into the registers of the wave that converts them (wave w: K chunk w
+//     and V chunk w, a tile ahead), its scales chunk into a small LDS ring; every wave converts its two chunks into
+//     the fp16 operand planes of the tile (K hi, K lo, V hi, V lo: code x scale for both, the V scale per token;
+//     double-buffered: tile k + 1's while tile k is computed); then every wave runs S^T = K Q^T (two
+//     v_mfma_f32_16x16x32_f16 a block, half and row tile) and O^T += V^T P^T (three a 16-value tile and row tile:
+//     V hi P hi, V lo P hi, V hi P lo). Scaling V once a workgroup instead of P once a row tile and block keeps the
+//     per-wave VALU work (which the counters showed issuing mostly apart from the matrix cores) to the softmax.
+//   * The softmax (base 2, the running max moved lazily) runs on the S^T registers as in the decode kernel; P feeds
+//     the PV MFMA in place.
 #include "../../include/fnkv.h"
 #include "common.h"
 #include "layout.h"
@@ -36,12 +40,12 @@ namespace fnkv {
 constexpr int32_t kPfWaves = 8;                      // two a SIMD
 constexpr int32_t kPfNT = 2;                         // 16-row tiles a wave (each plane read serves both)
 constexpr int32_t kPfRows = kPfWaves * kPfNT * 16;   // 256 rows a workgroup
-constexpr int32_t kPfStage = 16 * 1024;              // a tile's K codes, then its V codes
 constexpr int32_t kPfPlane = 16 * 1024;             // one fp16 operand plane of a tile
-constexpr int32_t kPfSet = 3 * kPfPlane;             // a tile's planes: K hi, K lo, V codes
+constexpr int32_t kPfSet = 4 * kPfPlane;             // a tile's planes: K hi, K lo, V hi, V lo
 constexpr int32_t kPfScaleRing = 4;                  // tiles' scale chunks (K then V scales, 1 KiB), a ring
-constexpr int32_t kPfLds = 2 * kPfStage + 2 * kPfSet + kPfScaleRing * 1024; // staging and planes double-buffered
+constexpr int32_t kPfLds = 2 * kPfSet + kPfScaleRing * 1024; // planes double-buffered, the scale ring
 constexpr float kPfNegInf = -__builtin_inff();
+constexpr float kPfLazyLog2 = 6.0f; // the running max moves only past this margin
 
 struct pf_args {
     pool_view pv;
@@ -55,18 +59,12 @@ struct pf_args {
     int32_t n_split, split_tiles; // key tiles split over blockIdx.z: split z takes tiles z * split_tiles ..
 };
 
-// a tile's 16 code chunks of 1 KiB (K, then V) into a staging slot (wave w copies chunks w and w + 8) and its scales
-// chunk into its place in the scale ring (wave 0)
-__device__ __forceinline__ void pf_issue(const uint8_t * tile, uint8_t * stage, uint8_t * scales, int32_t wave,
-                                         int32_t lane) {
-#pragma unroll
-    for (int32_t c = 0; c < 16 / kPfWaves; ++c) {
-        const int32_t ch = wave + c * kPfWaves;
-        lds_load16(tile + ch * 1024 + lane * 16, stage + ch * 1024);
-    }
-    if (wave == 0) {
-        lds_load16(tile + kKScales + lane * 16, scales);
-    }
+// this wave's code chunks of a tile (K chunk w, then V chunk w: 16 B a lane each) into registers
+__device__ __forceinline__ void pf_load_codes(const uint8_t * tile, int32_t wave, int32_t lane, u32x4 (&c)[2]) {
+    __asm__ __volatile__("" ::: "memory"); // younger than every load issued before (the waits count on it)
+    c[0] = stream_load16(tile + kKCodes + wave * 1024 + lane * 16);
+    c[1] = stream_load16(tile + kVCodes + wave * 1024 + lane * 16);
+    keep_issued();
 }
 
 __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
@@ -84,6 +82,30 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
     // this workgroup's key tiles: its split's share of those the block's queries see
     const int32_t ts0 = static_cast<int32_t>(blockIdx.z) * a.split_tiles;
     const int32_t n_tiles = max(0, min(n_tiles_all, ts0 + a.split_tiles) - ts0);
+
+    const pool_view & pv = a.pv;
+    const int32_t * table = pv.table + int64_t(a.slot) * pv.table_stride;
+    const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
+    auto tile_ptr = [&](int32_t li) -> const uint8_t * { // the split's li-th tile (past the last: the last again)
+        li = li < n_tiles ? li : n_tiles - 1;
+        const int64_t tok = int64_t(ts0 + li) * kTileTokens;
+        const int32_t phys = table[tok >> 8];
+        return layer_base + int64_t(phys) * pv.page_stride + int64_t((tok & 255) >> 5) * kTileBytes;
+    };
+    uint8_t * const plane_base = smem;
+    uint8_t * const ring_base = smem + 2 * kPfSet;
+    auto ring = [&](int32_t li) { return ring_base + (li & (kPfScaleRing - 1)) * 1024; };
+    auto issue_ring = [&](int32_t li) { // wave 0: tile li's scales chunk (K then V scales) into its ring slot
+        if (wave == 0) {
+            lds_load16(tile_ptr(li) + kKScales + lane * 16, ring(li));
+        }
+    };
+    u32x4 codes[2];
+    // the first tile's copies before the Q loads (their latencies overlap)
+    if (n_tiles > 0) {
+        issue_ring(0);
+        pf_load_codes(tile_ptr(0), wave, lane, codes);
+    }
 
     // Q operands (B of S^T = K Q^T) of this wave's two row tiles, and each row's causal limit
     half8 qop[kPfNT][kBlocks];
@@ -116,38 +138,21 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
         }
     }
 
-    const pool_view & pv = a.pv;
-    const int32_t * table = pv.table + int64_t(a.slot) * pv.table_stride;
-    const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
-    auto tile_ptr = [&](int32_t li) -> const uint8_t * { // the split's li-th tile
-        const int64_t tok = int64_t(ts0 + li) * kTileTokens;
-        const int32_t phys = table[tok >> 8];
-        return layer_base + int64_t(phys) * pv.page_stride + int64_t((tok & 255) >> 5) * kTileBytes;
-    };
-    uint8_t * const stage_base = smem;
-    uint8_t * const plane_base = smem + 2 * kPfStage;
-    uint8_t * const ring_base = plane_base + 2 * kPfSet;
-    auto ring = [&](int32_t li) { return ring_base + (li & (kPfScaleRing - 1)) * 1024; };
-
-    // tile ti's codes and scales (staging slot ti & 1) -> the fp16 operand planes (set ti & 1): K exactly as hi + lo
-    // (code x scale has 8 x 11 significant bits: hi = fp16(code x scale), lo = the remainder by one fused
-    // multiply-add), V as its codes (exact) with the V scales beside them. Wave w converts K chunk (h, ld) = w and V
-    // chunk ld = w.
+    // this wave's chunks of tile ti (in `codes`) -> the fp16 operand planes of set ti & 1, each exactly as hi + lo
+    // (code x scale has 8 x 11 significant bits: hi = fp16(code x scale), lo = the remainder by one fused multiply-add).
+    // K chunk w covers tokens 16 (w / 4) .. + 15 and blocks 2 (w % 4), 2 (w % 4) + 1 (the lane's row is a token: one
+    // scale a block); V chunk w the MFMA tiles 2 w, 2 w + 1 of block w (the lane's 8 slots are 8 tokens: their 8 V
+    // scales of block w, which the ring holds in slot order)
     auto dequant = [&](int32_t ti) {
-        const uint8_t * st = stage_base + (ti & 1) * kPfStage;
-        const uint8_t * ksc = ring(ti); // K scales [32 tokens][8 blocks]
+        const uint8_t * rg = ring(ti); // K scales [32 tokens][8 blocks], then V scales [4 lane groups][8 blocks][8]
         uint8_t * pl = plane_base + (ti & 1) * kPfSet;
-#pragma unroll
-        for (int32_t c = 0; c < 8 / kPfWaves; ++c) {
-            const int32_t kc = wave + c * kPfWaves; // K chunk: h = kc / 4, ld = kc % 4
-            const int32_t h = kc >> 2, ld = kc & 3;
-            const u32x4 w = *reinterpret_cast<const u32x4 *>(st + kc * 1024 + lane * 16);
-            // this lane's row is token 16 h + j; blocks 2 ld and 2 ld + 1
-            const half2v s2 = *reinterpret_cast<const half2v *>(ksc + (16 * h + j) * 16 + ld * 4);
+        {
+            const int32_t h = wave >> 2, ld = wave & 3;
+            const half2v s2 = *reinterpret_cast<const half2v *>(rg + (16 * h + j) * 16 + ld * 4);
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb) {
                 const int32_t b = 2 * ld + bb;
-                const half8 code = widen8(w[2 * bb], w[2 * bb + 1]);
+                const half8 code = widen8(codes[0][2 * bb], codes[0][2 * bb + 1]);
                 const half8 sv = {s2[bb], s2[bb], s2[bb], s2[bb], s2[bb], s2[bb], s2[bb], s2[bb]};
                 const half8 hi = code * sv;
                 const half8 lo = __builtin_elementwise_fma(code, sv, -hi);
@@ -156,14 +161,16 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
                 *reinterpret_cast<half8 *>(pl + kPfPlane + off) = lo;
             }
         }
-#pragma unroll
-        for (int32_t c = 0; c < 8 / kPfWaves; ++c) {
-            const int32_t vc = wave + c * kPfWaves; // V chunk ld = vc: MFMA tiles m = 2 vc, 2 vc + 1 of block vc
-            const u32x4 w = *reinterpret_cast<const u32x4 *>(st + kVCodes + vc * 1024 + lane * 16);
+        {
+            const half8 vs = *reinterpret_cast<const half8 *>(rg + 512 + qg * 128 + wave * 16);
 #pragma unroll
             for (int mm = 0; mm < 2; ++mm) {
-                const int32_t off = ((2 * vc + mm) * 64 + lane) * 16;
-                *reinterpret_cast<half8 *>(pl + 2 * kPfPlane + off) = widen8(w[2 * mm], w[2 * mm + 1]);
+                const half8 code = widen8(codes[1][2 * mm], codes[1][2 * mm + 1]);
+                const half8 hi = code * vs;
+                const half8 lo = __builtin_elementwise_fma(code, vs, -hi);
+                const int32_t off = ((2 * wave + mm) * 64 + lane) * 16;
+                *reinterpret_cast<half8 *>(pl + 2 * kPfPlane + off) = hi;
+                *reinterpret_cast<half8 *>(pl + 3 * kPfPlane + off) = lo;
             }
         }
     };
@@ -187,6 +194,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
 #pragma unroll
                 for (int nt = 0; nt < kPfNT; ++nt) {
                     sc[nt][h] = mfma16(khi, qop[nt][b], sc[nt][h]);
+                }
+#pragma unroll
+                for (int nt = 0; nt < kPfNT; ++nt) {
                     sc[nt][h] = mfma16(klo, qop[nt][b], sc[nt][h]);
                 }
             }
@@ -194,9 +204,10 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
         half8 ph[kPfNT], plo[kPfNT];
 #pragma unroll
         for (int nt = 0; nt < kPfNT; ++nt) {
+            // this lane's tokens 16 h + r of the tile (r = 4 qg + 0..3) are visible to its row while <= rel
+            const int32_t rel = lim[nt] - ti * kTileTokens - 4 * qg;
             float v[8];
             float mx = kPfNegInf;
-            const int32_t rel = lim[nt] - ti * kTileTokens - 4 * qg; // this lane's tokens 16 h + r visible: <= rel
             if (__all(rel >= 16 + 3)) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
@@ -218,17 +229,16 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
                 }
             }
             mx = rows_max(mx) * a.c2;
-            const float m_new = fmaxf(m_run[nt], mx);
+            const bool move = mx > m_run[nt] + kPfLazyLog2; // m_run = -inf: any visible score moves it
+            const float m_new = move ? mx : m_run[nt];
             const float m_use = m_new == kPfNegInf ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run[nt] - m_use);
-            float lsum = 0.0f;
+            const float alpha = move ? __builtin_amdgcn_exp2f(m_run[nt] - m_use) : 1.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 v[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[i], a.c2, -m_use));
-                lsum += v[i];
             }
             split_hilo(v, ph[nt], plo[nt]);
-            l_run[nt] = __builtin_fmaf(l_run[nt], alpha, lsum);
+            l_run[nt] = __builtin_fmaf(l_run[nt], alpha, sum8(v));
             m_run[nt] = m_new;
             if (__any(alpha != 1.0f)) {
 #pragma unroll
@@ -237,51 +247,57 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
                 }
             }
         }
-        // O^T += V^T (P x s_v)^T, block by block: the V codes exact in fp16, P times the block's V scale (per
-        // token) as hi + lo fp16 (packed-fp16 TwoProduct: the pair carries ~22 bits)
+        // O^T += V^T P^T block by block: V hi P hi, V lo P hi, V hi P lo (the lo x lo term is below 2^-22); one
+        // accumulator's MFMAs are four apart
 #pragma unroll
         for (int b = 0; b < kBlocks; ++b) {
-            // V scales [4 lane groups][8 blocks][8 slots] after the K scales
-            const half8 vs = *reinterpret_cast<const half8 *>(ring(ti) + 512 + qg * 128 + b * 16);
-            const half8 vc0 = *reinterpret_cast<const half8 *>(pl + 2 * kPfPlane + ((2 * b) * 64 + lane) * 16);
-            const half8 vc1 = *reinterpret_cast<const half8 *>(pl + 2 * kPfPlane + ((2 * b + 1) * 64 + lane) * 16);
+            const half8 vh0 = *reinterpret_cast<const half8 *>(pl + 2 * kPfPlane + ((2 * b) * 64 + lane) * 16);
+            const half8 vh1 = *reinterpret_cast<const half8 *>(pl + 2 * kPfPlane + ((2 * b + 1) * 64 + lane) * 16);
+            const half8 vl0 = *reinterpret_cast<const half8 *>(pl + 3 * kPfPlane + ((2 * b) * 64 + lane) * 16);
+            const half8 vl1 = *reinterpret_cast<const half8 *>(pl + 3 * kPfPlane + ((2 * b + 1) * 64 + lane) * 16);
 #pragma unroll
             for (int nt = 0; nt < kPfNT; ++nt) {
-                half8 shi, slo;
-                scale_hilo_pk(ph[nt], plo[nt], vs, shi, slo);
-                acc[nt][2 * b] = mfma16(vc0, shi, acc[nt][2 * b]);
-                acc[nt][2 * b + 1] = mfma16(vc1, shi, acc[nt][2 * b + 1]);
-                acc[nt][2 * b] = mfma16(vc0, slo, acc[nt][2 * b]);
-                acc[nt][2 * b + 1] = mfma16(vc1, slo, acc[nt][2 * b + 1]);
+                acc[nt][2 * b] = mfma16(vh0, ph[nt], acc[nt][2 * b]);
+                acc[nt][2 * b + 1] = mfma16(vh1, ph[nt], acc[nt][2 * b + 1]);
+            }
+#pragma unroll
+            for (int nt = 0; nt < kPfNT; ++nt) {
+                acc[nt][2 * b] = mfma16(vl0, ph[nt], acc[nt][2 * b]);
+                acc[nt][2 * b + 1] = mfma16(vl1, ph[nt], acc[nt][2 * b + 1]);
+            }
+#pragma unroll
+            for (int nt = 0; nt < kPfNT; ++nt) {
+                acc[nt][2 * b] = mfma16(vh0, plo[nt], acc[nt][2 * b]);
+                acc[nt][2 * b + 1] = mfma16(vh1, plo[nt], acc[nt][2 * b + 1]);
             }
             __builtin_amdgcn_sched_barrier(0); // one block's operands live at a time
         }
     };
 
-    // Iteration ti: [tile ti + 1's data has landed; barrier] [copy tile ti + 2's K codes and scales into the staging
-    // slot tile ti used] [dequantize tile ti + 1 into the other plane set, load this wave's V chunk of tile ti + 2]
-    // [compute tile ti]: the VALU-heavy dequantization of the next tile and the matrix-core work on this one are
-    // independent, so one wave's overlaps the other's.
+    // Iteration ti: [tile ti + 1's scales have landed (wave 0 waited); barrier: planes ti complete, planes
+    // (ti + 1) & 1 free] [this wave's codes of tile ti + 1 (loaded during iteration ti - 1) -> planes (ti + 1) & 1]
+    // [tile ti + 2's scales and codes issued] [compute tile ti]. Every iteration issues the same loads (past the last
+    // tile: the last again), so the vmcnt counts are exact: a wave's two code loads, after them nothing; wave 0 issues
+    // the scales copy first.
     if (n_tiles > 0) {
-        pf_issue(tile_ptr(0), stage_base, ring(0), wave, lane);
         wait_vmcnt<0>();
-        __syncthreads();
-        if (n_tiles > 1) {
-            pf_issue(tile_ptr(1), stage_base + kPfStage, ring(1), wave, lane);
-        }
+        __syncthreads(); // tile 0's codes and scales have landed
         dequant(0);
+        issue_ring(1);
+        pf_load_codes(tile_ptr(1), wave, lane, codes);
     }
     for (int32_t ti = 0; ti < n_tiles; ++ti) {
-        wait_vmcnt<0>(); // tile ti + 1's copy (the last loads issued)
-        __syncthreads(); // ... every wave's; planes ti complete; staging slot ti & 1 and planes (ti + 1) & 1 free
-        if (ti + 2 < n_tiles) {
-            pf_issue(tile_ptr(ti + 2), stage_base + (ti & 1) * kPfStage, ring(ti + 2), wave, lane);
+        if (wave == 0) {
+            wait_vmcnt<2>(); // tile ti + 1's scales (its two code loads may be in flight)
         }
-        if (ti + 1 < n_tiles) {
-            dequant(ti + 1);
-        }
+        barrier_keep_loads();
+        wait_vmcnt<0>(); // this wave's codes of tile ti + 1
+        dequant(ti + 1);
+        issue_ring(ti + 2);
+        pf_load_codes(tile_ptr(ti + 2), wave, lane, codes);
         compute(ti);
     }
+    wait_vmcnt<0>();
 
     // ---- one split: normalise and write; several: the unnormalised partial (acc, m, l) for the merge ----
     if (a.n_split > 1) {
