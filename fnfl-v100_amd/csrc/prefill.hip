@@ -37,13 +37,30 @@
 
 namespace fnkv {
 
+#ifdef FNKV_TIMING
+uint64_t * timing_buffer();
+#define PF_T(i)                                                                                                    \
+    do {                                                                                                           \
+        const uint64_t now_ = __builtin_amdgcn_s_memtime();                                                        \
+        if ((i) > 0) {                                                                                             \
+            pf_ph[(i)-1] += now_ - pf_last;                                                                        \
+        }                                                                                                          \
+        pf_last = now_;                                                                                            \
+    } while (0)
+#else
+#define PF_T(i)                                                                                                    \
+    do {                                                                                                           \
+    } while (0)
+#endif
+
 constexpr int32_t kPfWaves = 8;                      // two a SIMD
 constexpr int32_t kPfNT = 2;                         // 16-row tiles a wave (each plane read serves both)
 constexpr int32_t kPfRows = kPfWaves * kPfNT * 16;   // 256 rows a workgroup
 constexpr int32_t kPfPlane = 16 * 1024;             // one fp16 operand plane of a tile
 constexpr int32_t kPfSet = 4 * kPfPlane;             // a tile's planes: K hi, K lo, V hi, V lo
 constexpr int32_t kPfScaleRing = 4;                  // tiles' scale chunks (K then V scales, 1 KiB), a ring
-constexpr int32_t kPfLds = 2 * kPfSet + kPfScaleRing * 1024; // planes double-buffered, the scale ring
+constexpr int32_t kPfPages = 2048;                   // the split's page table entries held in LDS (a split <= 512 K cells)
+constexpr int32_t kPfLds = 2 * kPfSet + kPfScaleRing * 1024 + kPfPages * 4; // planes double-buffered, ring, pages
 constexpr float kPfNegInf = -__builtin_inff();
 constexpr float kPfLazyLog2 = 6.0f; // the running max moves only past this margin
 
@@ -57,6 +74,9 @@ struct pf_args {
     int64_t ctx;        // cells of the sequence (the chunk included)
     int32_t rows, G, hq, layer, slot;
     int32_t n_split, split_tiles; // key tiles split over blockIdx.z: split z takes tiles z * split_tiles ..
+#ifdef FNKV_TIMING
+    uint64_t * ts; // per wave: phase cycle sums (instrumented builds only)
+#endif
 };
 
 // this wave's code chunks of a tile (K chunk w, then V chunk w: 16 B a lane each) into registers
@@ -86,14 +106,23 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
     const pool_view & pv = a.pv;
     const int32_t * table = pv.table + int64_t(a.slot) * pv.table_stride;
     const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
+    uint8_t * const plane_base = smem;
+    uint8_t * const ring_base = smem + 2 * kPfSet;
+    // the split's page table entries, copied into LDS once: a tile's address is then an LDS read, not a memory round
+    // trip on the path to its copy
+    int32_t * const pages = reinterpret_cast<int32_t *>(ring_base + kPfScaleRing * 1024);
+    const int32_t page0 = (ts0 * kTileTokens) >> 8;
+    const int32_t n_pages = n_tiles > 0 ? (((ts0 + n_tiles - 1) * kTileTokens) >> 8) - page0 + 1 : 0;
+    for (int32_t i = static_cast<int32_t>(threadIdx.x); i < n_pages; i += 64 * kPfWaves) {
+        pages[i] = table[page0 + i];
+    }
+    __syncthreads();
     auto tile_ptr = [&](int32_t li) -> const uint8_t * { // the split's li-th tile (past the last: the last again)
         li = li < n_tiles ? li : n_tiles - 1;
         const int64_t tok = int64_t(ts0 + li) * kTileTokens;
-        const int32_t phys = table[tok >> 8];
+        const int32_t phys = __builtin_amdgcn_readfirstlane(pages[(tok >> 8) - page0]);
         return layer_base + int64_t(phys) * pv.page_stride + int64_t((tok & 255) >> 5) * kTileBytes;
     };
-    uint8_t * const plane_base = smem;
-    uint8_t * const ring_base = smem + 2 * kPfSet;
     auto ring = [&](int32_t li) { return ring_base + (li & (kPfScaleRing - 1)) * 1024; };
     auto issue_ring = [&](int32_t li) { // wave 0: tile li's scales chunk (K then V scales) into its ring slot
         if (wave == 0) {
@@ -101,6 +130,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
         }
     };
     u32x4 codes[2];
+#ifdef FNKV_TIMING
+    uint64_t pf_ph[8] = {0, 0, 0, 0, 0, 0, 0, 0}, pf_last = 0;
+#endif
     // the first tile's copies before the Q loads (their latencies overlap)
     if (n_tiles > 0) {
         issue_ring(0);
@@ -201,6 +233,13 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
                 }
             }
         }
+#ifdef FNKV_TIMING
+        {
+            const uint64_t now_ = __builtin_amdgcn_s_memtime();
+            pf_ph[4] += now_ - pf_last;
+            pf_last = now_;
+        }
+#endif
         half8 ph[kPfNT], plo[kPfNT];
 #pragma unroll
         for (int nt = 0; nt < kPfNT; ++nt) {
@@ -247,6 +286,13 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
                 }
             }
         }
+#ifdef FNKV_TIMING
+        {
+            const uint64_t now_ = __builtin_amdgcn_s_memtime();
+            pf_ph[5] += now_ - pf_last;
+            pf_last = now_;
+        }
+#endif
         // O^T += V^T P^T block by block: V hi P hi, V lo P hi, V hi P lo (the lo x lo term is below 2^-22); one
         // accumulator's MFMAs are four apart
 #pragma unroll
@@ -287,17 +333,30 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
         pf_load_codes(tile_ptr(1), wave, lane, codes);
     }
     for (int32_t ti = 0; ti < n_tiles; ++ti) {
+        PF_T(0);
         if (wave == 0) {
             wait_vmcnt<2>(); // tile ti + 1's scales (its two code loads may be in flight)
         }
         barrier_keep_loads();
+        PF_T(1);
         wait_vmcnt<0>(); // this wave's codes of tile ti + 1
+        PF_T(2);
         dequant(ti + 1);
         issue_ring(ti + 2);
         pf_load_codes(tile_ptr(ti + 2), wave, lane, codes);
+        PF_T(3);
         compute(ti);
+        PF_T(4);
     }
     wait_vmcnt<0>();
+#ifdef FNKV_TIMING
+    if (lane == 0 && a.ts != nullptr) {
+        const int64_t wg = (int64_t(blockIdx.z) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        for (int i = 0; i < 8; ++i) {
+            a.ts[(wg * kPfWaves + wave) * 8 + i] = pf_ph[i];
+        }
+    }
+#endif
 
     // ---- one split: normalise and write; several: the unnormalised partial (acc, m, l) for the merge ----
     if (a.n_split > 1) {
@@ -398,6 +457,8 @@ pf_plan plan_prefill(const kv_pool & p, int64_t ctx, int32_t rows, int32_t G) {
     const int32_t cus = device_cus(p.device());
     int32_t ns = (cus + base - 1) / base;
     ns = std::min(ns, std::max(1, max_tiles / 16));
+    // a split's pages fit the kernel's LDS copy of the table
+    ns = std::max(ns, (max_tiles + kPfPages * kTilesPerPage - kTilesPerPage - 1) / (kPfPages * kTilesPerPage - kTilesPerPage));
     ns = std::min(ns, 64);
     pl.n_split = std::max(1, ns);
     pl.split_tiles = (max_tiles + pl.n_split - 1) / pl.n_split;
@@ -459,6 +520,9 @@ int fnkv_attn_prefill(const fnkv_pool * pool, int32_t slot, int32_t layer, int64
     }
     a.n_split = pl.n_split;
     a.split_tiles = pl.split_tiles;
+#ifdef FNKV_TIMING
+    a.ts = fnkv::timing_buffer();
+#endif
     a.po = static_cast<float *>(ws);
     a.pml = a.po == nullptr ? nullptr : a.po + int64_t(pl.n_split) * p->h_kv() * pl.rows_pad * fnkv::kHeadDim;
     static std::once_flag attr_once[64]; // once per device; a racing first caller waits for it

@@ -339,9 +339,9 @@ int fnkv_qsp_attend(const fnkv_qsp_attend_args * a, void * stream);
 int64_t fnkv_prefill_workspace_bytes(const fnkv_pool * pool, int64_t ctx, int32_t rows, int32_t hq);
 
 /* Causal attention of `rows` query tokens (positions ctx - rows .. ctx - 1 of the slot, already appended) over the
- * slot's cells 0 .. ctx - 1 of `layer`, on the matrix cores with fp32 accumulation: K as exact hi + lo fp16 operands,
- * V as its codes against P x V-scale in hi + lo fp16 (the reference's prompt attention rounds its operands to fp16
- * once, qsa_prompt.h:55-58; this keeps ~22 bits a product). q: fp16 [rows][hq][256], out: fp16 [rows][hq][256].
+ * slot's cells 0 .. ctx - 1 of `layer`, on the matrix cores with fp32 accumulation: K and V (code x scale) as exact
+ * hi + lo fp16 operands, P as hi + lo fp16 (the reference's prompt attention rounds its operands to fp16 once,
+ * qsa_prompt.h:55-58; this keeps ~22 bits a product). q: fp16 [rows][hq][256], out: fp16 [rows][hq][256].
  * ws: fnkv_prefill_workspace_bytes bytes of device memory (no zeroing needed) for the key-split partials when the
  * query rows alone do not fill the device; null (or smaller): one split, no workspace. The GQA group hq / h_kv must
  * divide 256 (a workgroup's query rows). */
