@@ -119,6 +119,46 @@ def test_config1_shapes_one_layer():
     assert st.check(q16, got, 3) <= TOL
 
 
+def test_config1_all_twelve_layers():
+    # BASELINE config 1 in full: 4 sequences at 8K / 16K / 32K / 64K, T = 3, all 12 layers of one pool, each layer's
+    # new cells appended by its launch (as the bench's step); every layer's outputs checked against the fp64
+    # attention over that layer's cells as the pool holds them (exported as ggml block_q8_0 and decoded by the oracle)
+    ctxs, T, layers = [8192, 16384, 32768, 65536], 3, 12
+    n_pages = sum(-(-c // 256) for c in ctxs) + 8
+    pool = fnkv.Pool(len(ctxs) + 1, n_pages, layers, HKV)
+    slots = list(range(len(ctxs)))
+    cases.scatter_ensure(pool, slots, ctxs, 12, churn=0.2)
+    g = torch.Generator(device="cuda")
+    for layer in range(layers):
+        g.manual_seed(1200 + layer)
+        for s_, c in zip(slots, ctxs):
+            k = (torch.randn((c - T, HKV, 256), generator=g, device="cuda") * 1.5).half()
+            v = torch.randn((c - T, HKV, 256), generator=g, device="cuda").half()
+            pool.append(s_, layer, 0, k, v)
+    q16 = cases.queries(13, (layers, len(ctxs), T, HQ, 256))
+    kn = cases.queries(14, (layers, len(ctxs), T, HKV, 256))
+    vn = cases.queries(15, (layers, len(ctxs), T, HKV, 256))
+    q, k_new, v_new = (torch.from_numpy(x).cuda() for x in (q16, kn, vn))
+    out = torch.empty_like(q)
+    ws = torch.empty(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    for layer in range(layers):
+        pool.decode(slots, ctxs, T, layer, q[layer], out[layer], ws, k_new=k_new[layer], v_new=v_new[layer])
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    worst = 0.0
+    for layer in range(layers):
+        for i, (s_, c) in enumerate(zip(slots, ctxs)):
+            kf = np.empty((c, HKV, 256), np.float32)
+            vf = np.empty((c, HKV, 256), np.float32)
+            for h in range(HKV):
+                for kv, dst in ((0, kf), (1, vf)):
+                    qs, d = O.from_block_q8_0(pool.export(s_, layer, h, kv, 0, c).cpu().numpy())
+                    dst[:, h, :] = O.q8_0_dequantize(qs.reshape(c, 256), d.reshape(c, 8))
+            ref = O.attn_f64(q16[layer, i].view(np.uint16), kf, vf, c)
+            worst = max(worst, cases.out_err(got[layer, i], ref))
+    assert worst <= TOL, worst
+
+
 @pytest.mark.parametrize("T", [1, 5])
 def test_config2_deep_context(T):
     # 262,144 cells in scattered pages, decode (T = 1) and a depth-4 verify (T = 5)

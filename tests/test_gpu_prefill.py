@@ -79,10 +79,29 @@ def test_config3_chunk_at_depth_131072():
     # a 2,048-token chunk appended at depth 131,072, causal over 133,120 cells; rows checked:
     # the first, a spread, and the last
     rows = 2048
-    check = [0, 1, 255, 1024, 1777, 2046, 2047]
-    _, got, err, _ = prefill_case(131072, rows, seed=3, check_rows=check)
+    check = sorted(set([0, 1, 255, 1024, 1777, 2046, 2047] + list(range(5, rows, 64))))
+    pool, got, err, (q16, kf, vf, ctx) = prefill_case(131072, rows, seed=3, check_rows=check)
     assert np.isfinite(got).all()
     assert err <= TOL
+    # every one of the 2,048 rows against the decode kernel: rows t - 5 .. t are the last six positions of context
+    # depth + t + 1, a T = 6 verify over the same cells (a different kernel, the same causal rule); both are within
+    # the tolerance of the fp64 attention, so they agree within twice it
+    depth = ctx - rows
+    ws = torch.empty(pool.decode_ws_bytes([ctx], 6, HQ), dtype=torch.uint8, device="cuda")
+    qd = torch.from_numpy(q16).cuda()
+    outs = []
+    ends = list(range(5, rows, 6)) + ([rows - 1] if (rows - 6) % 6 else [])
+    for t in ends:
+        q = qd[t - 5:t + 1].contiguous()[None]
+        out = torch.empty_like(q)
+        pool.decode([0], [depth + t + 1], 6, 0, q, out, ws)
+        outs.append((t, out))
+    torch.cuda.synchronize()
+    worst = 0.0
+    for t, out in outs:
+        d = out.cpu().numpy()[0].astype(np.float64)
+        worst = max(worst, float(np.abs(d - got[t - 5:t + 1].astype(np.float64)).max()))
+    assert worst <= 2 * TOL, worst
 
 
 def test_prefill_key_splits_agree_with_one_split():
