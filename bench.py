@@ -254,10 +254,10 @@ def measure_traffic(argv, kernels=("decode", "merge_kernel")):
     return total, detail
 
 
-def run_prefill(args, cfg):
-    """BASELINE config 3: one step = the chunk's Q8_0 append (fnkv_q8_append) + its causal attention over the whole
-    context (fnkv_attn_prefill), captured in a HIP graph; the roofline is the matrix cores' (algorithmic flops)."""
-    import numpy as np
+def time_prefill(args, cfg, steps, warmup):
+    """BASELINE config 3's step (the chunk's Q8_0 append + its causal attention over the whole context) captured in a
+    HIP graph and replayed: returns (wall seconds, GPU seconds between HIP events, the pool's K/V, q) of `steps`
+    replays after `warmup`."""
     import torch
 
     import cases
@@ -302,7 +302,7 @@ def run_prefill(args, cfg):
             step()
         torch.cuda.synchronize()
     run = graph.replay if graph is not None else step
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         run()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
@@ -310,13 +310,28 @@ def run_prefill(args, cfg):
     ev1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record(stream)
-    for _ in range(args.steps):
+    for _ in range(steps):
         run()
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_s = ev0.elapsed_time(ev1) / 1e3
     assert torch.isfinite(out.float()).all().item(), "non-finite attention output"
+    del graph
+    pool.close()
+    return wall, gpu_s, kv, q
+
+
+def run_prefill(args, cfg):
+    """BASELINE config 3: one step = the chunk's Q8_0 append (fnkv_q8_append) + its causal attention over the whole
+    context (fnkv_attn_prefill), captured in a HIP graph; the roofline is the matrix cores' (algorithmic flops)."""
+    import numpy as np
+
+    import cases
+
+    ctx, rows = cfg["ctxs"][0], cfg["T"]
+    wall, gpu_s, kv, q = time_prefill(args, cfg, args.steps, args.warmup)
+    graph = not args.no_graph
     flops = prefill_flops(ctx, rows)
     step_s = gpu_s / args.steps
     tflops = flops / step_s / 1e12
@@ -334,7 +349,7 @@ def run_prefill(args, cfg):
         "dtype": "q8_0 KV dequantized to fp16 hi + lo, fp16 Q/O, fp32 accumulate",
         "data": "synthetic (seeded N(0,1) K/V with 4 of 256 channels x8, N(0,1) Q)",
         "config": {"workload": cfg["workload"], "context": ctx, "chunk": rows, "q_heads": HQ, "kv_heads": HKV,
-                   "head_dim": D, "page_tokens": 256, "hip_graph": graph is not None},
+                   "head_dim": D, "page_tokens": 256, "hip_graph": graph},
         "roofline": {
             "kernel": "fnkv_q8_append + fnkv_attn_prefill (append_kernel + prefill_kernel + prefill_merge_kernel), per step",
             "bound": "mfma",
@@ -354,21 +369,18 @@ def run_prefill(args, cfg):
         (kq, kd, _), (vq, vd, _) = cases.decoded(O, kv[0].cpu().numpy(), kv[1].cpu().numpy())
         kb, vb = O.to_block_q8_0(kq, kd), O.to_block_q8_0(vq, vd)
         q16 = q[-sample:].cpu().numpy().view(np.uint16)
-        O.attn_ggml(q16[:1], kb, vb, 2048, threads=threads)
-        t1 = time.perf_counter()
-        O.attn_ggml(q16, kb, vb, ctx, threads=threads)
-        dt = time.perf_counter() - t1
+        dt = _best_of(lambda: O.attn_ggml(q16, kb, vb, ctx, q_as_q8=True, threads=threads), reps=3)
         sample_flops = 4 * D * HQ * sum(ctx - sample + t + 1 for t in range(sample))
         cpu_step = dt * flops / sample_flops
         line["cpu_baseline"] = {
             "value": round(rows / cpu_step, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"the chunk's last {sample} of {rows} query rows over the full context, fp32-Q ggml-semantics "
-                      f"flash attention (oracle/fnkv_oracle.c or_attn_ggml), {threads} threads, {dt:.2f} s, scaled "
-                      f"by visible pairs to the chunk",
+            "sample": f"the chunk's last {sample} of {rows} query rows over the full context, ggml-semantics flash "
+                      f"attention (Q as Q8_0; oracle/fnkv_oracle.c or_attn_ggml), {threads} threads, best of 3: "
+                      f"{dt:.2f} s, scaled by visible pairs to the chunk",
+            "host": host_info(),
             "tflops": round(sample_flops / dt / 1e12, 4),
         }
     print(json.dumps(line), flush=True)
-    pool.close()
 
 
 def run_sparse(args, cfg):
@@ -1078,6 +1090,12 @@ def main():
             also[name] = {"workload": c2["workload"], "launch_us": x["launch_us"], "achieved_gb_s": x["achieved"],
                           "frac": x["frac"], "tokens_s": x["tokens_s"], "bytes_per_launch": x["bytes_per_launch"],
                           "steps": x["n_steps"]}
+        c3 = CONFIGS["cfg3"]
+        _, gpu_s, _, _ = time_prefill(args, c3, 3, 1)
+        step_s = gpu_s / 3
+        tf = prefill_flops(c3["ctxs"][0], c3["T"]) / step_s / 1e12
+        also["cfg3"] = {"workload": c3["workload"], "step_us": round(step_s * 1e6, 3), "achieved_tflops": round(tf, 3),
+                        "frac": round(tf / PEAK_MFMA_F16_TFLOPS, 4), "bound": "mfma"}
         line["configs_also"] = also
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(ctxs, T, layers, args.seed, extra=args.config == "cfg1" and not custom)

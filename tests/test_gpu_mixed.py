@@ -3,7 +3,9 @@
 shared pool, every layer. Parity against the oracle's fp64 attention over the decoded cache (max-abs 2e-3) at
 contexts the oracle finishes in seconds; at BASELINE's full contexts (1K..196K) the same step is checked through
 properties that do not need the oracle (finite outputs, the verify launch over six sequences against each sequence
-launched alone, the prefill chunk's last rows against a T = 5 verify of the same cells)."""
+launched alone, the prefill chunk's last rows against a T = 5 verify of the same cells) and, for every verify row and
+a spread of prefill rows, against the fp64 attention over the cells as the pool holds them (exported as ggml
+block_q8_0)."""
 import numpy as np
 import pytest
 
@@ -114,6 +116,18 @@ def test_config4_mixed_step_parity():
     assert np.isfinite(worst) and worst <= TOL, errs
 
 
+def exported_cells(pool, slot, layer, c):
+    """The slot's first c cells of `layer` as the pool holds them (exported as ggml block_q8_0), decoded by the
+    oracle: float32 K, V [c][HKV][256]."""
+    kf = np.empty((c, HKV, D), np.float32)
+    vf = np.empty((c, HKV, D), np.float32)
+    for h in range(HKV):
+        for kv, dst in ((0, kf), (1, vf)):
+            qs, d = O.from_block_q8_0(pool.export(slot, layer, h, kv, 0, c).cpu().numpy())
+            dst[:, h, :] = O.q8_0_dequantize(qs.reshape(c, D), d.reshape(c, D // 32))
+    return kf, vf
+
+
 def test_config4_full_contexts_properties():
     seed, layers, T = 41, 1, 5
     rng = np.random.default_rng([seed, 1])
@@ -131,7 +145,9 @@ def test_config4_full_contexts_properties():
     for s in order:
         x = torch.randn((2, ctx_of[s], HKV, D), generator=g, device="cuda").half()
         pool.append(s, 0, 0, x[0].contiguous(), x[1].contiguous())
-    # the prefill chunks: finite; the chunk's last five rows agree with a T = 5 verify over the same cells
+    # the prefill chunks: finite; the chunk's last five rows agree with a T = 5 verify over the same cells; a spread
+    # of rows against the fp64 attention over the cells as the pool holds them
+    errs = {}
     for s in pf_slots:
         c = ctx_of[s]
         q = torch.randn((CHUNK, HQ, D), generator=g, device="cuda").half()
@@ -144,6 +160,10 @@ def test_config4_full_contexts_properties():
         torch.cuda.synchronize()
         assert torch.isfinite(out.float()).all().item()
         assert (ov[0].float() - out[-5:].float()).abs().max().item() <= 2 * TOL
+        rows = [0, 1, 511, 2047, 3000, CHUNK - 1]
+        kf, vf = exported_cells(pool, s, 0, c)
+        ref = O.attn_f64(q.cpu().numpy().view(np.uint16), kf, vf, c, rows=rows)
+        errs[("prefill", s)] = cases.out_err(out.cpu().numpy()[rows], ref)
     # the six verify steps in one launch against each launched alone
     q = torch.randn((len(vf_slots), T, HQ, D), generator=g, device="cuda").half()
     ctxs = [ctx_of[s] for s in vf_slots]
@@ -152,9 +172,16 @@ def test_config4_full_contexts_properties():
     pool.decode(vf_slots, ctxs, T, 0, q, out, ws)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all().item()
+    got = out.cpu().numpy()
+    q16 = q.cpu().numpy()
     for i, s in enumerate(vf_slots):
         one = torch.empty_like(q[i:i + 1])
         ws1 = torch.empty(pool.decode_ws_bytes([ctxs[i]], T, HQ), dtype=torch.uint8, device="cuda")
         pool.decode([s], [ctxs[i]], T, 0, q[i:i + 1].contiguous(), one, ws1)
         torch.cuda.synchronize()
         assert (one[0].float() - out[i].float()).abs().max().item() <= 2 * TOL
+        kf, vf = exported_cells(pool, s, 0, ctxs[i])
+        ref = O.attn_f64(q16[i].view(np.uint16), kf, vf, ctxs[i])
+        errs[("verify", s)] = cases.out_err(got[i], ref)
+    worst = max(errs.values())
+    assert np.isfinite(worst) and worst <= TOL, errs
