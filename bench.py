@@ -590,7 +590,7 @@ def run_attend(args, cfg):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q8_0 KV (int8 codes + fp16 scales), fp16 q operand, fp32 prepare / softmax / accumulate / out",
+        "dtype": "q8_0 KV (int8 codes + fp16 scales), q as fp16 hi + lo operands, fp32 prepare / softmax / accumulate / out",
         "data": "synthetic (seeded N(0,1) K/V with 4 of 256 channels x8; uniform q / k / v / gates / norms; random "
                 "selections)",
         "config": {"workload": cfg["workload"], "cells": ctx, "rows": T, "layers": layers, "q_heads": hq,

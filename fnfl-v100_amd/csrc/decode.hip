@@ -141,8 +141,11 @@ template <int NT> __device__ __forceinline__ void group_sync() {
 
 // KV8 (the pool's format is FNFL's group-64 rule): a scale serves two 32-value blocks, so the score MFMAs of a group
 // chain and P x (V scale) is formed once a group.
-template <int NT, bool SP, bool KV8 = false>
+// QLO (sparse launches with a.q_lo): the scores take q as fp16 hi + lo, the low parts in LDS after the selection
+// slice ([block][lane] 16 B, the region the one-row launch forms its query rows in).
+template <int NT, bool SP, bool KV8 = false, bool QLO = false>
 __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(dec_args a_in) {
+    static_assert(!QLO || (SP && NT == 1 && dec_shape<NT>::WAVES == kBlocks), "QLO: one row tile, a wave a block");
     const dec_args a = SP ? sparse_row_view(a_in) : a_in;
     if constexpr (SP) {
         if (sparse_refused(a)) {
@@ -189,6 +192,20 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
             load_q_operands(a, s, ctx, kvh, rt, j, qg, qop, lim);
         }
     }
+    // QLO: thread c loads the low part of operand (block c / 64, lane c % 64); stored to LDS after the build
+    u32x4 qlo_ld = {0, 0, 0, 0};
+    if constexpr (QLO) {
+        if (a.fp.qfull == nullptr) {
+            const int32_t L = static_cast<int32_t>(threadIdx.x) & 63, b = static_cast<int32_t>(threadIdx.x) >> 6;
+            const int32_t row = L & 15;
+            if (row < a.R) {
+                const int32_t t_row = row / a.G;
+                qlo_ld = *reinterpret_cast<const u32x4 *>(
+                    a.q_lo + ((int64_t(s) * a.T + t_row) * a.hq + int64_t(kvh) * a.G + row % a.G) * kHeadDim +
+                    b * kQK + 8 * (L >> 4));
+            }
+        }
+    }
     split_src<SP> src;
     src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * kGroupLds, ctx);
     if (refused<SP>(a, s, ctx, sp, kvh)) {
@@ -207,6 +224,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
             uint16_t * ql = reinterpret_cast<uint16_t *>(smem + GR * kGroupLds + kSelSlice);
             float sn, cs;
             rope_angle(sn, cs, pq, a.fp.theta_scale, lane);
+            uint2 lo_pk[2] = {make_uint2(0, 0), make_uint2(0, 0)}; // QLO: fp16(y - hi), heads >= G zero
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int32_t h = wave + 8 * i;
@@ -214,6 +232,14 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
                     float y[4];
                     norm_rope_apply(y, xq[i], gq, sn, cs, lane);
                     reinterpret_cast<uint2 *>(ql + h * kHeadDim)[lane] = pack4_f16(y, 1.0f);
+                    if constexpr (QLO) {
+                        float lo[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            lo[e] = y[e] - static_cast<float>(static_cast<_Float16>(y[e]));
+                        }
+                        lo_pk[i] = pack4_f16(lo, 1.0f);
+                    }
                     if (split == 0 && a.fp.q_f32 != nullptr) {
                         reinterpret_cast<float4 *>(a.fp.q_f32 + (kvh * a.G + h) * kHeadDim)[lane] =
                             make_float4(y[0], y[1], y[2], y[3]);
@@ -229,10 +255,28 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
                 }
                 qop[b] = __builtin_bit_cast(half8, v);
             }
+            if constexpr (QLO) {
+                // the low parts fp16(y - hi) into the same region, as operands: value 4 lane + i of head h is
+                // element 4 (lane & 1) + i of operand (block lane / 8, lane (h, (lane & 7) / 2)); heads >= G zero
+                __syncthreads(); // every operand read above
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int32_t h = wave + 8 * i;
+                    *reinterpret_cast<uint2 *>(smem + GR * kGroupLds + kSelSlice +
+                                               ((lane >> 3) * 64 + ((lane & 7) >> 1) * 16 + h) * 16 + (lane & 1) * 8) =
+                        lo_pk[i];
+                }
+            }
             lim = ctx - 1;
-            append_owned_cell_fused<WAVES>(a, table, kvh, ctx, src.new_mine, wave, lane);
+            append_owned_cell_fused<WAVES>(a, table, kvh, ctx, src.new_mine, wave, lane); // ends with a barrier
         } else {
+            if constexpr (QLO) {
+                *reinterpret_cast<u32x4 *>(smem + GR * kGroupLds + kSelSlice + threadIdx.x * 16) = qlo_ld;
+            }
             append_owned_cells<WAVES>(a, table, kvh, ctx, src.new_mine, wave, lane);
+            if constexpr (QLO) {
+                __syncthreads();
+            }
         }
     } else {
         append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, src.g0, a.strided ? src.stride : 0, wave, lane);
@@ -284,7 +328,12 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         issue_k<NT>(t0p, kbuf(0), sslot(0), rt, lane);
         vload(t0p);
     }
-    const half8 sig = q_sums(qop, qg);
+    const uint8_t * const qlo_base = smem + GR * kGroupLds + kSelSlice;
+    auto qlo_lds = [&](int b) { return *reinterpret_cast<const half8 *>(qlo_base + (b * 64 + lane) * 16); };
+    half8 sig = {}; // QLO: the codes enter exactly, no bias operand
+    if constexpr (!QLO) {
+        sig = q_sums(qop, qg);
+    }
     for (int32_t it = 0; it < n_iter; ++it) {
         const int32_t ti = grp + it * GR;
         const bool have = ti < n_tiles;
@@ -299,7 +348,11 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         const int64_t tok0 = src.tok0(ti);
 
         floatx4 sc[2];
-        tile_scores<KV8>(kb, sc_tile, [&](int b) { return qop[b]; }, sig, j, qg, lane, sc);
+        if constexpr (QLO) {
+            tile_scores<KV8>(kb, sc_tile, [&](int b) { return qop[b]; }, sig, j, qg, lane, sc, qlo_lds);
+        } else {
+            tile_scores<KV8>(kb, sc_tile, [&](int b) { return qop[b]; }, sig, j, qg, lane, sc);
+        }
 
         // ---- online softmax (base 2); P stays in the registers that feed the PV MFMA ----
         const int64_t lim_rel64 = lim - tok0;
@@ -307,7 +360,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         float pf[8];
         {
             float alpha;
-            tile_softmax(sc, lim_rel, a.c2, qg, m_run, l_run, pf, alpha, src.vis(ti, t_row, qg));
+            tile_softmax<QLO>(sc, lim_rel, a.c2, qg, m_run, l_run, pf, alpha, src.vis(ti, t_row, qg));
             if (__any(alpha != 1.0f)) {
 #pragma unroll
                 for (int m = 0; m < 16; ++m) {
@@ -332,7 +385,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
             }
             pfl = to_half8_rtz(r8);
         }
-        {
+        if constexpr (!QLO) { // QLO: the codes enter exactly (the bias would amplify lo's rounding 1152 / |code|-fold)
             // A: lane (block b = j, qg) holds s_v[token(qg, s)][b] for its 8 slots s (zero for b >= 8)
             const half8 sva = j < 8 ? *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + j * 16) : zero8;
             lv = mfma16(sva, pfh, lv);
@@ -343,10 +396,10 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         for (int ld = 0; ld < 8; ++ld) {
             if (!KV8 || (ld & 1) == 0) { // KV8: block ld + 1 shares block ld's scale
                 const half8 vs = *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + ld * 16);
-                scale_hilo(pf, pfh, vs, ph, pl);
+                scale_hilo<QLO>(pf, pfh, vs, ph, pl);
             }
-            const half8 va0 = widen8_biased(vreg[ld][0], vreg[ld][1]);
-            const half8 va1 = widen8_biased(vreg[ld][2], vreg[ld][3]);
+            const half8 va0 = widen8<QLO>(vreg[ld][0], vreg[ld][1]);
+            const half8 va1 = widen8<QLO>(vreg[ld][2], vreg[ld][3]);
             acc[2 * ld] = mfma16(va0, ph, acc[2 * ld]);
             acc[2 * ld + 1] = mfma16(va1, ph, acc[2 * ld + 1]);
             acc[2 * ld] = mfma16(va0, pl, acc[2 * ld]);
@@ -360,7 +413,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     FNKV_STAMP_WAVE();
 
     // the V bias: acc[m] carries 1152 * lv[b = m / 2]; lv[b] of this lane's row sits in lane (j, b / 4), element b % 4
-    {
+    if constexpr (!QLO) {
         float lb[kBlocks];
 #pragma unroll
         for (int b = 0; b < kBlocks; ++b) {
@@ -452,10 +505,10 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
 #define FNKV_QK_PRIO 1
 #endif
 constexpr int16_t kQkPrio = FNKV_QK_PRIO; // wave priority (s_setprio) of the scores + softmax phase
-template <int NT, bool SP = false> struct rows_shape {
+template <int NT, bool SP = false, bool QLO = false> struct rows_shape {
     static constexpr int GR = NT == 2 ? 4 : 2;                      // tile groups a workgroup
     static constexpr int WAVES = NT * GR;
-    static constexpr int SK = NT == 2 ? 3 : 6;                      // K ring slots a group
+    static constexpr int SK = NT == 2 ? 3 : QLO ? 4 : 6;            // K ring slots a group (QLO: room for q's lo)
     static constexpr int NBM = (kBlocks + NT - 1) / NT;             // value blocks a wave (the last may own fewer)
     static constexpr int CK = (9 + NT - 1) / NT;                    // 1 KiB K chunks a wave issues a tile
     static constexpr int KSLOT = kCodeBytes / 2 + kScaleBytes;      // K codes, then the tile's K and V scales
@@ -463,21 +516,23 @@ template <int NT, bool SP = false> struct rows_shape {
     static constexpr int AX = 2 * NT * 16 * 4;                      // rescale factors: [parity][row tile][row]
     static constexpr int GROUP_LDS = SK * KSLOT + PX + AX;
     static constexpr int Q_LDS = NT == 2 ? 0 : NT * kBlocks * 64 * 16; // Q operands (NT = 3), shared by the groups
+    static constexpr int QLO_LDS = QLO ? NT * kBlocks * 64 * 16 : 0;    // q's low parts (QLO), after them
     // loads a wave has issued after tile k's K chunks when it waits for them (top of iteration k), and after tile
     // k's V codes when it waits for those (before PV of iteration k)
     static constexpr int WAIT_K = NBM + (SK - 2) * (CK + NBM);
     static constexpr int WAIT_V = 2 * CK + NBM;
 };
 
-template <int NT, bool SP, bool KV8 = false>
-__global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_rows_kernel(dec_args a_in) {
+template <int NT, bool SP, bool KV8 = false, bool QLO = false>
+__global__ __launch_bounds__((64 * rows_shape<NT, SP, QLO>::WAVES), 1) void decode_rows_kernel(dec_args a_in) {
+    static_assert(!QLO || SP, "QLO: sparse launches");
     const dec_args a = SP ? sparse_row_view(a_in) : a_in;
     if constexpr (SP) {
         if (sparse_refused(a)) {
             return;
         }
     }
-    using SH = rows_shape<NT, SP>;
+    using SH = rows_shape<NT, SP, QLO>;
     constexpr int GR = SH::GR, WAVES = SH::WAVES, SK = SH::SK, NBM = SH::NBM, CK = SH::CK;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
@@ -508,9 +563,26 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
     if constexpr (SP) { // the Q rows' latency hidden behind the selection's build
         load_q_operands(a, s, ctx, kvh, w, j, qg, qreg, lim);
     }
+    // QLO: the workgroup loads q's low parts as operands ([row tile][block][lane] 16 B), chunk c = thread + i WAVES 64
+    constexpr int QLO_PER = QLO ? NT * kBlocks * 64 / (64 * WAVES) : 1;
+    static_assert(!QLO || QLO_PER * 64 * WAVES == NT * kBlocks * 64, "QLO: whole chunks a thread");
+    u32x4 qlo_ld[QLO_PER];
+    if constexpr (QLO) {
+#pragma unroll
+        for (int i = 0; i < QLO_PER; ++i) {
+            const int32_t c = static_cast<int32_t>(threadIdx.x) + i * 64 * WAVES;
+            const int32_t L = c & 63, b = (c >> 6) % kBlocks, row = (c >> 9) * 16 + (L & 15);
+            qlo_ld[i] = u32x4{0, 0, 0, 0};
+            if (row < a.R) {
+                qlo_ld[i] = *reinterpret_cast<const u32x4 *>(
+                    a.q_lo + ((int64_t(s) * a.T + row / a.G) * a.hq + int64_t(kvh) * a.G + row % a.G) * kHeadDim +
+                    b * kQK + 8 * (L >> 4));
+            }
+        }
+    }
     split_src<SP, NT == 2> src; // NT = 3 is short of registers: its entries stay in LDS
-    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * SH::GROUP_LDS + SH::Q_LDS,
-                                  ctx);
+    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem,
+                                  smem + GR * SH::GROUP_LDS + SH::Q_LDS + SH::QLO_LDS, ctx);
     if (refused<SP>(a, s, ctx, sp, kvh)) {
         return;
     }
@@ -527,6 +599,16 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
     FNKV_STAMP(1);
 
     uint8_t * const qlds = smem + GR * SH::GROUP_LDS; // [row tile][block][lane] 16 B
+    uint8_t * const qlo_base = qlds + SH::Q_LDS;        // QLO: the same layout
+    if constexpr (QLO) { // read after the loop's first barrier
+#pragma unroll
+        for (int i = 0; i < QLO_PER; ++i) {
+            *reinterpret_cast<u32x4 *>(qlo_base + (threadIdx.x + i * 64 * WAVES) * 16) = qlo_ld[i];
+        }
+    }
+    auto qlo_lds = [&](int b) {
+        return *reinterpret_cast<const half8 *>(qlo_base + (w * kBlocks + b) * 1024 + lane * 16);
+    };
     if constexpr (!SP) {
         load_q_operands(a, s, ctx, kvh, w, j, qg, qreg, lim);
     }
@@ -633,12 +715,16 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
         const uint8_t * sc_tile = kb + kCodeBytes / 2 - kKScales; // scale offsets are tile-relative
         const int64_t tok0 = src.tok0(grp + k * GR);
         floatx4 sc[2];
-        tile_scores<KV8>(kb, sc_tile, qop_lds, sig, j, qg, lane, sc);
+        if constexpr (QLO) {
+            tile_scores<KV8>(kb, sc_tile, qop_lds, sig, j, qg, lane, sc, qlo_lds);
+        } else {
+            tile_scores<KV8>(kb, sc_tile, qop_lds, sig, j, qg, lane, sc);
+        }
         const int64_t lim_rel64 = lim - tok0;
         const int32_t lim_rel = lim_rel64 > 64 ? 64 : static_cast<int32_t>(lim_rel64 < -1 ? -1 : lim_rel64);
         float pf[8];
         float alpha;
-        tile_softmax(sc, lim_rel, a.c2, qg, m_run, l_run, pf, alpha, src.vis(grp + k * GR, t_row, qg));
+        tile_softmax<QLO>(sc, lim_rel, a.c2, qg, m_run, l_run, pf, alpha, src.vis(grp + k * GR, t_row, qg));
         half8 ph, pl;
         split_hilo(pf, ph, pl);
         u32x4 * px = reinterpret_cast<u32x4 *>(pslot(par, w) + lane * 32);
@@ -674,15 +760,17 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
                 }
                 lv[rt] *= alpha;
             }
-            lv[rt] = mfma16(sva, ph[rt], lv[rt]);
-            lv[rt] = mfma16(sva, pl[rt], lv[rt]);
+            if constexpr (!QLO) { // QLO: the codes enter exactly
+                lv[rt] = mfma16(sva, ph[rt], lv[rt]);
+                lv[rt] = mfma16(sva, pl[rt], lv[rt]);
+            }
         }
         half8 hi[NT], lo[NT];
 #pragma unroll
         for (int32_t i = 0; i < NBM; ++i) {
             if (i < nb) {
-                const half8 va0 = widen8_biased(vb[i][0], vb[i][1]);
-                const half8 va1 = widen8_biased(vb[i][2], vb[i][3]);
+                const half8 va0 = widen8<QLO>(vb[i][0], vb[i][1]);
+                const half8 va1 = widen8<QLO>(vb[i][2], vb[i][3]);
                 // KV8: an odd block shares the scale of the block before it (when this wave holds both)
                 if (!KV8 || ((b0 + i) & 1) == 0 || i == 0) {
                     const half8 vs = *reinterpret_cast<const half8 *>(sc_tile + kVScales + qg * 128 + (b0 + i) * 16);
@@ -741,7 +829,9 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
     // after the prologue's copies are issued: the bias operand from the Q rows, and at NT = 3 the Q operands into
     // LDS (group 0's waves; read after the loop's first barrier)
     auto q_finish = [&]() {
-        sig = q_sums(qreg, qg);
+        if constexpr (!QLO) { // QLO: the codes enter exactly, no bias operand
+            sig = q_sums(qreg, qg);
+        }
         if constexpr (!kQReg) {
             if (grp == 0) {
 #pragma unroll
@@ -794,9 +884,9 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP>::WAVES), 1) void decode_ro
     FNKV_STAMP_WAVE();
 
     // the V bias: acc[rt][i] carries 1152 * lv[rt][b0 + i]; lv[rt][b] of this lane's row sits in lane (j, b / 4),
-    // element b % 4
+    // element b % 4 (QLO: no bias, the codes entered exactly)
 #pragma unroll
-    for (int32_t rt = 0; rt < NT; ++rt) {
+    for (int32_t rt = 0; rt < (QLO ? 0 : NT); ++rt) {
         float lb[kBlocks];
 #pragma unroll
         for (int b = 0; b < kBlocks; ++b) {
@@ -1022,13 +1112,13 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
 }
 
 // LDS of a decode launch: the groups' tile buffers, or the merge's (m, l) and partial rows, whichever is larger
-template <int NT, bool SP> int32_t rows_lds() {
-    using SH = rows_shape<NT, SP>;
-    const int32_t ring = SH::GR * SH::GROUP_LDS + SH::Q_LDS;
+template <int NT, bool SP, bool QLO = false> int32_t rows_lds() {
+    using SH = rows_shape<NT, SP, QLO>;
+    const int32_t ring = SH::GR * SH::GROUP_LDS + SH::Q_LDS + SH::QLO_LDS;
     const int32_t merge = SH::GR * NT * 16 * 2 * 4 + SH::GR * NT * 16 * (kHeadDim + 4) * 4;
     return SP ? std::max(std::max(ring + kSelSlice, merge), kSelLds) : std::max(ring, merge);
 }
-int32_t decode_lds(int32_t nt, bool sp) {
+int32_t decode_lds(int32_t nt, bool sp, bool qlo = false) {
     if (nt == 1) {
         constexpr int32_t waves = dec_shape<1>::WAVES;
         const int32_t tiles = dec_shape<1>::GR * kGroupLds;
@@ -1036,9 +1126,9 @@ int32_t decode_lds(int32_t nt, bool sp) {
         return sp ? std::max(std::max(tiles + kSelSlice + kFusedQLds, merge), kSelLds) : std::max(tiles, merge);
     }
     if (nt == 2) {
-        return sp ? rows_lds<2, true>() : rows_lds<2, false>();
+        return sp ? (qlo ? rows_lds<2, true, true>() : rows_lds<2, true>()) : rows_lds<2, false>();
     }
-    return sp ? rows_lds<3, true>() : rows_lds<3, false>();
+    return sp ? (qlo ? rows_lds<3, true, true>() : rows_lds<3, true>()) : rows_lds<3, false>();
 }
 
 int32_t device_cus(int32_t device) {
@@ -1117,24 +1207,26 @@ void launch_merge(const merge_args & m, hipStream_t st) {
     hipLaunchKernelGGL(merge_kernel, dim3(static_cast<uint32_t>(m.n_seq * m.h_kv * m.R * 8)), dim3(256), 0, st, m);
 }
 
-template <bool SP, bool KV8> void set_decode_attrs() {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<1, SP, KV8>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(1, SP));
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<2, SP, KV8>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(2, SP));
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<3, SP, KV8>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3, SP));
+template <bool SP, bool KV8, bool QLO = false> void set_decode_attrs() {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<1, SP, KV8, QLO>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(1, SP, QLO));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<2, SP, KV8, QLO>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(2, SP, QLO));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<3, SP, KV8, QLO>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3, SP, QLO));
 }
 
-template <bool SP, bool KV8> void launch_decode_fmt(int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
+template <bool SP, bool KV8, bool QLO = false>
+void launch_decode_fmt(int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
     if (NT == 1) {
-        hipLaunchKernelGGL((decode_kernel<1, SP, KV8>), grid, dim3(64 * dec_shape<1>::WAVES), decode_lds(1, SP), st, a);
+        hipLaunchKernelGGL((decode_kernel<1, SP, KV8, QLO>), grid, dim3(64 * dec_shape<1>::WAVES),
+                           decode_lds(1, SP, QLO), st, a);
     } else if (NT == 2) {
-        hipLaunchKernelGGL((decode_rows_kernel<2, SP, KV8>), grid, dim3(64 * rows_shape<2, SP>::WAVES),
-                           decode_lds(2, SP), st, a);
+        hipLaunchKernelGGL((decode_rows_kernel<2, SP, KV8, QLO>), grid, dim3(64 * rows_shape<2, SP, QLO>::WAVES),
+                           decode_lds(2, SP, QLO), st, a);
     } else {
-        hipLaunchKernelGGL((decode_rows_kernel<3, SP, KV8>), grid, dim3(64 * rows_shape<3, SP>::WAVES),
-                           decode_lds(3, SP), st, a);
+        hipLaunchKernelGGL((decode_rows_kernel<3, SP, KV8, QLO>), grid, dim3(64 * rows_shape<3, SP, QLO>::WAVES),
+                           decode_lds(3, SP, QLO), st, a);
     }
 }
 
@@ -1150,9 +1242,23 @@ template <bool SP> void launch_decode(const kv_pool & p, int32_t NT, dim3 grid, 
             (void)hipSetDevice(dev);
             set_decode_attrs<SP, false>();
             set_decode_attrs<SP, true>();
+            if constexpr (SP) {
+                set_decode_attrs<SP, false, true>();
+                set_decode_attrs<SP, true, true>();
+            }
             (void)hipGetLastError();
             (void)hipSetDevice(cur);
         });
+    }
+    if constexpr (SP) {
+        if (a.q_lo != nullptr) {
+            if (a.pv.format == kFormatKV8) {
+                launch_decode_fmt<SP, true, true>(NT, grid, a, st);
+            } else {
+                launch_decode_fmt<SP, false, true>(NT, grid, a, st);
+            }
+            return;
+        }
     }
     if (a.pv.format == kFormatKV8) {
         launch_decode_fmt<SP, true>(NT, grid, a, st);

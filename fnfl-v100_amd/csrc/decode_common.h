@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 namespace fnkv {
 
@@ -68,6 +69,10 @@ struct dec_args {
     const int32_t * sel_offsets = nullptr;
     int32_t sel_row0 = 0;
     fused_prep fp;
+    // a sparse launch whose query is F32: q's fp16 low parts (fp16(q - hi), [T][hq][256], hi in q); the scores then
+    // take q as hi + lo (about 22 significant bits). With fp.qfull set the launch forms both itself and only the
+    // pointer's presence is read.
+    const uint16_t * q_lo = nullptr;
 #ifdef FNKV_TIMING
     uint64_t * ts; // per workgroup: 16 real-time stamps (instrumented builds only)
 #endif
@@ -330,6 +335,9 @@ __device__ __forceinline__ dec_args sparse_row_view(const dec_args & in) {
     a.ctx[0] = in.depth_dev != nullptr && (depth < 0 || depth + in.T > in.ctx[0]) ? -1 : depth + z + 1;
     a.depth_dev = nullptr;
     a.q = in.q + int64_t(z) * in.hq * 256;
+    if (in.q_lo != nullptr) {
+        a.q_lo = in.q_lo + int64_t(z) * in.hq * 256;
+    }
     a.sel_body = in.sel_body + words;
     a.sel_n = in.sel_n + z;
     a.po = in.po + int64_t(z) * rows_all * 256;
@@ -525,11 +533,13 @@ struct dev_depth {
     int64_t max_cells;
     uint32_t * err;
 };
-// dd set: `depth` is not read; the plan (grid, workspace) follows from dd->max_cells
+// dd set: `depth` is not read; the plan (grid, workspace) follows from dd->max_cells. q_lo set: q's fp16 low parts
+// beside q (dec_args::q_lo), 16-byte aligned
 int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq, float scale,
                   const void * q, const void * body, const void * offsets, const void * k_new, const void * v_new,
                   int32_t new_dtype, void * out, const sparse_gate * gate, void * ws, int64_t ws_bytes,
-                  hipStream_t st, const char * who, const fused_prep * fp = nullptr, const dev_depth * dd = nullptr);
+                  hipStream_t st, const char * who, const fused_prep * fp = nullptr, const dev_depth * dd = nullptr,
+                  const uint16_t * q_lo = nullptr);
 // host: prompt rows over their selection bodies (sparse.hip): the workspace of a chunk of n rows whose last row sees
 // `cells` cells, and the chunk's launches (the sparse kernels, then the gated merge into out16 / out_f32 / err)
 int64_t prompt_ws_bytes(const kv_pool & p, int64_t cells, int32_t n, int32_t G);
@@ -635,6 +645,13 @@ __device__ __forceinline__ void load_q_operands(const dec_args & a, int32_t s, i
     }
 }
 
+// The scores' optional second Q operand: none (q is the fp16 operand alone), or q's fp16 low parts, block b's from
+// qlo(b), chained into the same MFMA results as the hi parts (the K codes then enter exactly, without the bias).
+struct no_qlo {
+    __device__ half8 operator()(int) const { return half8{}; }
+};
+template <typename QLOP> constexpr bool has_qlo = !std::is_same<QLOP, no_qlo>::value;
+
 // sig: the row's per-block sums of q (the bias correction's operand), as fp16 hi (qg = 0) and lo (qg = 1) parts
 __device__ __forceinline__ half8 q_sums(const half8 (&qop)[kBlocks], int32_t qg) {
     float sigma[kBlocks];
@@ -662,9 +679,10 @@ __device__ __forceinline__ half8 q_sums(const half8 (&qop)[kBlocks], int32_t qg)
 // The Q operand of block b comes from qop(b): registers, or LDS where registers are short.
 // PAIR (KV8 pools): the two blocks of a 64-value group share one scale, so their MFMAs chain into one result and
 // the scale applies once a group.
-template <typename QOP, bool PAIR = false>
+template <typename QOP, bool PAIR = false, typename QLOP = no_qlo>
 __device__ __forceinline__ floatx4 tile_scores_half(const uint8_t * kb, const uint8_t * sc_tile, const QOP & qop,
-                                                    half8 sig, int32_t j, int32_t qg, int32_t lane, int32_t h) {
+                                                    half8 sig, int32_t j, int32_t qg, int32_t lane, int32_t h,
+                                                    const QLOP & qlo = QLOP()) {
     const half8 zero8 = {};
     // this lane's score rows are tokens 16 h + 4 qg + r; their K scales, all 8 blocks
     half8 ks[4];
@@ -672,9 +690,13 @@ __device__ __forceinline__ floatx4 tile_scores_half(const uint8_t * kb, const ui
     for (int r = 0; r < 4; ++r) {
         ks[r] = *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + 4 * qg + r) * 16);
     }
-    // the bias term: A = this lane's token row of K scales (twice), B = sigma hi / lo
-    const half8 srow = qg < 2 ? *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + j) * 16) : zero8;
-    const floatx4 corr = mfma16(srow, sig, floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+    // the bias term: A = this lane's token row of K scales (twice), B = sigma hi / lo. With q's low parts the codes
+    // enter exactly instead: the bias's partial sums (1152 sum q) would cost the fp32 accumulation ~8 bits
+    floatx4 corr = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (!has_qlo<QLOP>) {
+        const half8 srow = qg < 2 ? *reinterpret_cast<const half8 *>(sc_tile + kKScales + (16 * h + j) * 16) : zero8;
+        corr = mfma16(srow, sig, floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+    }
     floatx4 acc_s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb) { // blocks 4 hb .. 4 hb + 3 (fewer live results)
@@ -685,11 +707,17 @@ __device__ __forceinline__ floatx4 tile_scores_half(const uint8_t * kb, const ui
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb) {
                 const int b = 2 * ld + bb;
-                const half8 ka = widen8_biased(kw[2 * bb], kw[2 * bb + 1]);
+                const half8 ka = widen8<has_qlo<QLOP>>(kw[2 * bb], kw[2 * bb + 1]);
                 if constexpr (PAIR) { // group ld = blocks 2 ld, 2 ld + 1 (one 1 KiB chunk)
                     t[ld - 2 * hb] = mfma16(ka, qop(b), bb == 0 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : t[ld - 2 * hb]);
+                    if constexpr (has_qlo<QLOP>) {
+                        t[ld - 2 * hb] = mfma16(ka, qlo(b), t[ld - 2 * hb]);
+                    }
                 } else {
                     t[b - 4 * hb] = mfma16(ka, qop(b), floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+                    if constexpr (has_qlo<QLOP>) {
+                        t[b - 4 * hb] = mfma16(ka, qlo(b), t[b - 4 * hb]);
+                    }
                 }
             }
         }
@@ -711,6 +739,9 @@ __device__ __forceinline__ floatx4 tile_scores_half(const uint8_t * kb, const ui
             }
         }
     }
+    if constexpr (has_qlo<QLOP>) {
+        return acc_s;
+    }
     floatx4 sc;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -720,12 +751,13 @@ __device__ __forceinline__ floatx4 tile_scores_half(const uint8_t * kb, const ui
 }
 
 // both halves: sc[h][r] is the score of token 16 h + 4 qg + r against this lane's row j
-template <bool PAIR = false, typename QOP>
+template <bool PAIR = false, typename QOP, typename QLOP = no_qlo>
 __device__ __forceinline__ void tile_scores(const uint8_t * kb, const uint8_t * sc_tile, const QOP & qop, half8 sig,
-                                            int32_t j, int32_t qg, int32_t lane, floatx4 (&sc)[2]) {
+                                            int32_t j, int32_t qg, int32_t lane, floatx4 (&sc)[2],
+                                            const QLOP & qlo = QLOP()) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        sc[h] = tile_scores_half<QOP, PAIR>(kb, sc_tile, qop, sig, j, qg, lane, h);
+        sc[h] = tile_scores_half<QOP, PAIR, QLOP>(kb, sc_tile, qop, sig, j, qg, lane, h, qlo);
 #ifndef FNKV_NO_HALF_SB
         __builtin_amdgcn_sched_barrier(0); // one half's operands live at a time
 #endif
@@ -739,6 +771,11 @@ __device__ __forceinline__ void tile_scores(const uint8_t * kb, const uint8_t * 
 // times a V scale (at most 65504 / 127) inside fp16. alpha is the same in the row's four lanes.
 constexpr float kLazyLog2 = 6.0f;
 // vis: bit h set when this lane's 4 cells of half h (one 4-cell block) are in its row's selection (dense: 3).
+// EXACT_MAX (the launches that take q as hi + lo): m_run follows every new max and the weights are 2^(c2 sc - m_run
+// + kLazyLog2), the row's largest exactly 64 (the same bound). The weights, l and the accumulators then carry a
+// common 2^6, which cancels in every fold (l and O scale together); the gain: a weight times a V scale keeps 6 more
+// bits above fp16's subnormal range in its lo part (a weight near 1 times a scale near 2^-6 has lo near 2^-18).
+template <bool EXACT_MAX = false>
 __device__ __forceinline__ void tile_softmax(const floatx4 (&sc)[2], int32_t lim_rel, float c2, int32_t qg,
                                              float & m_run, float & l_run, float (&pf)[8], float & alpha,
                                              uint32_t vis = 3) {
@@ -766,13 +803,14 @@ __device__ __forceinline__ void tile_softmax(const floatx4 (&sc)[2], int32_t lim
         }
     }
     mx = rows_max(mx) * c2;
-    const bool move = mx > m_run + kLazyLog2; // m_run = -inf: any visible score moves it
+    const bool move = mx > m_run + (EXACT_MAX ? 0.0f : kLazyLog2); // m_run = -inf: any visible score moves it
     const float m_new = move ? mx : m_run;
     const float m_use = m_new == kNegInf ? 0.0f : m_new;
     alpha = move ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
+    const float m_pf = EXACT_MAX ? m_use - kLazyLog2 : m_use;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        pf[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(raw[i], c2, -m_use));
+        pf[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(raw[i], c2, -m_pf));
     }
     l_run = __builtin_fmaf(l_run, alpha, sum8(pf));
     m_run = m_new;

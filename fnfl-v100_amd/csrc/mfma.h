@@ -83,12 +83,31 @@ __device__ __forceinline__ half8 widen8_biased(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(half8, r);
 }
 
+// 8 codes as fp16 values: 1152 + code (EXACT false: the bias is folded out elsewhere), or the code itself (the
+// biased integers less 1152, exact)
+template <bool EXACT> __device__ __forceinline__ half8 widen8(uint32_t lo, uint32_t hi) {
+    half8 w = widen8_biased(lo, hi);
+    if constexpr (EXACT) {
+        const _Float16 b = static_cast<_Float16>(1152.0f);
+        w = w - half8{b, b, b, b, b, b, b, b};
+    }
+    return w;
+}
+
 // p (8 fp32 values, and the same rounded toward zero to fp16) times s (8 fp16) as hi + lo fp16: hi = fp16(ph * s)
-// (packed multiply), lo = the fp32 remainder p * s - hi (one fused multiply-add, exact to fp32) rounded toward zero.
-// hi + lo carries p * s to about 2^-19 relative.
+// (packed multiply), lo = the fp32 remainder p * s - hi (one fused multiply-add, exact to fp32) rounded toward zero
+// (RNE: to nearest). hi + lo carries p * s to about 2^-19 relative, and to 2^-24 (2^-25 RNE) absolute where lo is
+// subnormal.
+template <bool RNE = false>
 __device__ __forceinline__ void scale_hilo(const float (&p)[8], half8 ph, half8 s, half8 & hi, half8 & lo) {
-    typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
     hi = ph * s;
+    if constexpr (RNE) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            lo[i] = static_cast<_Float16>(__builtin_fmaf(p[i], static_cast<float>(s[i]), -static_cast<float>(hi[i])));
+        }
+        return;
+    }
     u32x4 l;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -64,7 +64,8 @@ sparse_plan plan_sparse(const kv_pool & p, int64_t depth, int32_t T, int32_t G) 
 int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq, float scale,
                   const void * q, const void * body, const void * offsets, const void * k_new, const void * v_new,
                   int32_t new_dtype, void * out, const sparse_gate * gate, void * ws, int64_t ws_bytes,
-                  hipStream_t st, const char * who, const fused_prep * fp, const dev_depth * dd) {
+                  hipStream_t st, const char * who, const fused_prep * fp, const dev_depth * dd,
+                  const uint16_t * q_lo) {
     const kv_pool * p = pool_of(pool);
     const std::string name(who);
     if (dd != nullptr) { // the plan is the bound's: the deepest rows' tiles
@@ -91,7 +92,7 @@ int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T
                   std::to_string(kSelMaxCells) + ")");
         return FNKV_ERR_ARG;
     }
-    if ((reinterpret_cast<uintptr_t>(q) & 15) != 0 || (reinterpret_cast<uintptr_t>(out) & 15) != 0 ||
+    if ((reinterpret_cast<uintptr_t>(q) & 15) != 0 || (reinterpret_cast<uintptr_t>(q_lo) & 15) != 0 || (reinterpret_cast<uintptr_t>(out) & 15) != 0 ||
         (reinterpret_cast<uintptr_t>(ws) & 15) != 0 || (reinterpret_cast<uintptr_t>(body) & 3) != 0 ||
         (reinterpret_cast<uintptr_t>(offsets) & 3) != 0) {
         set_error(name + ": q, out and ws must be 16-byte aligned, body and offsets 4-byte aligned");
@@ -148,6 +149,7 @@ int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T
     if (fp != nullptr) {
         a.fp = *fp;
     }
+    a.q_lo = q_lo;
     if (dd != nullptr) {
         a.depth_dev = dd->depth;
         a.err = dd->err;

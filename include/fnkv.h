@@ -216,8 +216,9 @@ int64_t fnkv_qsa_workspace_bytes(const fnkv_pool * pool, int64_t depth, int32_t 
  * position depth + t: each row's query heads and its new cell's k get the F32 RMS norm (eps 1e-6) and IMROPE
  * (attend.cu:151-198; positions pos, device I32 [4][T], plane p of row t at pos[p T + t]; theta_scale
  * fnkv_rope_theta_scale()), the new cells' K (normed, roped) and V are written into the pool at depth .. depth + T - 1
- * in its format, each row attends over its selection body (as fnkv_attn_sparse; scores q . k / 16 with q as fp16),
- * and each (row, head) is finished with its gate: out = o / (1 + exp(-gate)) in F32 with its int8 activation format.
+ * in its format, each row attends over its selection body (as fnkv_attn_sparse, but q enters as fp16 hi + lo, about
+ * 22 bits of the F32 q, the codes exactly and P with 6 more bits; scores q . k / 16; within the reference checker's
+ * 1e-5 normalized bound, qa2_test.cpp:58), and each (row, head) is finished with its gate: out = o / (1 + exp(-gate)) in F32 with its int8 activation format.
  * qfull: F32 [T][hq][512] (each head's q, then its gate); kv_k, kv_v: F32 [T][h_kv][256]; q_norm, k_norm: F32 [256];
  * out: F32 [T][hq][256]; codes: int8 [T][hq 256]; scales: F32 [T][hq 8][2]; q_f32, k_f32 (optional): the F32 q
  * [T][hq][256] and k [T][h_kv][256] after the norm and rope. Three launches in stream order: the prepare (which

@@ -230,8 +230,12 @@ def attn_f64(q16, k, v, n_ctx, scale=1.0 / 16.0, rows=None):
 def attn_f64_cells(q16, k, v, cells, scale=1.0 / 16.0):
     """FP64 attention of each query row over its own list of cells (the QSA attention's math, attend.h:16-18:
     softmax_c(q . K[c] * scale) . V[c] over row t's selected cells). q16: uint16 [T][hq][d]; k, v: float32
-    [n][hkv][d] (decoded cache); cells: T int arrays -> float64 [T][hq][d]."""
-    q = np.ascontiguousarray(q16, dtype=np.uint16).view(np.float16).astype(np.float64)
+    [n][hkv][d] (decoded cache); cells: T int arrays -> float64 [T][hq][d]. A float q16 is taken as the query's
+    values themselves (an F32 or FP64 query)."""
+    if np.asarray(q16).dtype.kind == "f":
+        q = np.asarray(q16, np.float64)
+    else:
+        q = np.ascontiguousarray(q16, dtype=np.uint16).view(np.float16).astype(np.float64)
     T, hq, d = q.shape
     hkv = k.shape[1]
     G = hq // hkv

@@ -269,6 +269,9 @@ def test_attn_f64_cells_pinned_by_the_dense_form():
     assert np.allclose(one[:, 0], v[7, 0][None, :]) and np.allclose(one[:, 3], v[7, 1][None, :])
     perm = [rng.permutation(c) for c in cells]
     np.testing.assert_allclose(O.attn_f64_cells(q16, k, v, perm), O.attn_f64(q16, k, v, n), rtol=0, atol=1e-12)
+    # a float query is taken as its values: the fp16 bits' values give the same result
+    q64 = q16.view(np.float16).astype(np.float64)
+    np.testing.assert_array_equal(O.attn_f64_cells(q64, k, v, cells), O.attn_f64_cells(q16, k, v, cells))
 
 
 def test_qsa_body_layout():
