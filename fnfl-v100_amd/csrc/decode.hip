@@ -501,6 +501,8 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
 // groups of the second half run half an iteration behind the first (see the loop), so the two waves sharing a SIMD
 // are in different phases.
 // (two groups a workgroup at NT = 2, two workgroups a CU, measured slower on cfg1: 47.4 against 42.7 us a layer)
+// Dense launches at NT = 3 run decode_kernel<3> instead (each wave its own row tile over all value blocks, V loaded by
+// each wave: cfg2v T = 5 111 against 118 us a layer); sparse ones keep this kernel.
 #ifndef FNKV_QK_PRIO
 #define FNKV_QK_PRIO 1
 #endif
@@ -1128,7 +1130,11 @@ int32_t decode_lds(int32_t nt, bool sp, bool qlo = false) {
     if (nt == 2) {
         return sp ? (qlo ? rows_lds<2, true, true>() : rows_lds<2, true>()) : rows_lds<2, false>();
     }
-    return sp ? (qlo ? rows_lds<3, true, true>() : rows_lds<3, true>()) : rows_lds<3, false>();
+    if (!sp) { // decode_kernel<3>: the groups' tile buffers, or the merge's (m, l) and partial rows
+        constexpr int32_t waves = dec_shape<3>::WAVES;
+        return std::max(dec_shape<3>::GR * kGroupLds, waves * 16 * 2 * 4 + waves * 16 * (kHeadDim + 4) * 4);
+    }
+    return qlo ? rows_lds<3, true, true>() : rows_lds<3, true>();
 }
 
 int32_t device_cus(int32_t device) {
@@ -1212,8 +1218,13 @@ template <bool SP, bool KV8, bool QLO = false> void set_decode_attrs() {
                               hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(1, SP, QLO));
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<2, SP, KV8, QLO>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(2, SP, QLO));
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<3, SP, KV8, QLO>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3, SP, QLO));
+    if constexpr (SP) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<3, SP, KV8, QLO>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3, SP, QLO));
+    } else {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<3, SP, KV8>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3, SP));
+    }
 }
 
 template <bool SP, bool KV8, bool QLO = false>
@@ -1225,8 +1236,13 @@ void launch_decode_fmt(int32_t NT, dim3 grid, const dec_args & a, hipStream_t st
         hipLaunchKernelGGL((decode_rows_kernel<2, SP, KV8, QLO>), grid, dim3(64 * rows_shape<2, SP, QLO>::WAVES),
                            decode_lds(2, SP, QLO), st, a);
     } else {
-        hipLaunchKernelGGL((decode_rows_kernel<3, SP, KV8, QLO>), grid, dim3(64 * rows_shape<3, SP, QLO>::WAVES),
-                           decode_lds(3, SP, QLO), st, a);
+        if constexpr (!SP) { // dense: each wave of a 3-wave group runs its row tile's scores and PV
+            hipLaunchKernelGGL((decode_kernel<3, SP, KV8>), grid, dim3(64 * dec_shape<3>::WAVES), decode_lds(3, SP),
+                               st, a);
+        } else {
+            hipLaunchKernelGGL((decode_rows_kernel<3, SP, KV8, QLO>), grid, dim3(64 * rows_shape<3, SP, QLO>::WAVES),
+                               decode_lds(3, SP, QLO), st, a);
+        }
     }
 }
 
