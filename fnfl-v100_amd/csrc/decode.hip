@@ -43,24 +43,34 @@
 
 namespace fnkv {
 
-// The one-row sparse launch's new cell when the launch prepares its row (fused_prep): K = the F32 RMS norm and IMROPE
-// of kv_k (and k_f32 when asked), V = kv_v, each in the pool's format, by the workgroup that reads the cell's tile.
+// The new cells when the sparse launch prepares its rows (fused_prep): row z's view (ctx = depth + z + 1) writes
+// cell depth + c, for c in `cells` (bit c): K = the F32 RMS norm and IMROPE of kv_k's row c (and k_f32's row c when
+// `own`: the cell is row z's own and this workgroup its owner), V = kv_v's row c, each in the pool's format. Several
+// workgroups may write one cell (every one that reads its tile, so its own loads follow its own stores); they store
+// the same bytes.
 template <int WAVES>
-__device__ __forceinline__ void append_owned_cell_fused(const dec_args & a, const int32_t * table, int32_t kvh,
-                                                        int64_t ctx, int32_t mine, int32_t wave, int32_t lane) {
-    if ((mine & 1) != 0 && wave < 2) {
-        const pool_view & pv = a.pv;
-        const int64_t pos = ctx - 1;
+__device__ __forceinline__ void append_cells_fused(const dec_args & a, const int32_t * table, int32_t kvh,
+                                                   int64_t ctx, uint32_t cells, bool own, int32_t wave, int32_t lane) {
+    const int32_t z = static_cast<int32_t>(blockIdx.z);
+    const int64_t depth = ctx - 1 - z;
+    const pool_view & pv = a.pv;
+    for (int32_t job = wave; job < 2 * (z + 1); job += WAVES) {
+        const int32_t c = job >> 1, kv = job & 1;
+        if (((cells >> c) & 1u) == 0) {
+            continue;
+        }
+        const int64_t pos = depth + c;
+        const int64_t src = (int64_t(c) * pv.h_kv + kvh) * kHeadDim;
         float x[4];
-        if (wave == 0) {
-            norm_rope(x, a.fp.kv_k + kvh * kHeadDim, a.fp.k_norm, a.fp.pos, 1, 0, a.fp.theta_scale, lane);
-            if (a.fp.k_f32 != nullptr) {
-                reinterpret_cast<float4 *>(a.fp.k_f32 + kvh * kHeadDim)[lane] = make_float4(x[0], x[1], x[2], x[3]);
+        if (kv == 0) {
+            norm_rope(x, a.fp.kv_k + src, a.fp.k_norm, a.fp.pos, a.fp.rows, c, a.fp.theta_scale, lane);
+            if (own && c == z && a.fp.k_f32 != nullptr) {
+                reinterpret_cast<float4 *>(a.fp.k_f32 + src)[lane] = make_float4(x[0], x[1], x[2], x[3]);
             }
         } else {
-            load4<true>(a.fp.kv_v + kvh * kHeadDim, lane, x);
+            load4<true>(a.fp.kv_v + src, lane, x);
         }
-        quantize_store_fmt(x, lane, tile_of(pv, table, a.layer, kvh, pos), static_cast<int32_t>(pos & 31), wave,
+        quantize_store_fmt(x, lane, tile_of(pv, table, a.layer, kvh, pos), static_cast<int32_t>(pos & 31), kv,
                            pv.format);
     }
     __syncthreads();
@@ -183,11 +193,12 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int32_t h = wave + 8 * i;
-                xq[i] = h < a.G ? reinterpret_cast<const float4 *>(a.fp.qfull + (kvh * a.G + h) * 512)[lane]
+                xq[i] = h < a.G ? reinterpret_cast<const float4 *>(
+                                      a.fp.qfull + (int64_t(blockIdx.z) * a.hq + kvh * a.G + h) * 512)[lane]
                                 : float4{0.0f, 0.0f, 0.0f, 0.0f};
             }
             gq = reinterpret_cast<const float4 *>(a.fp.q_norm)[lane];
-            pq = rope_pos(a.fp.pos, 1, 0, lane);
+            pq = rope_pos(a.fp.pos, a.fp.rows, static_cast<int32_t>(blockIdx.z), lane);
         } else {
             load_q_operands(a, s, ctx, kvh, rt, j, qg, qop, lim);
         }
@@ -241,7 +252,8 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
                         lo_pk[i] = pack4_f16(lo, 1.0f);
                     }
                     if (split == 0 && a.fp.q_f32 != nullptr) {
-                        reinterpret_cast<float4 *>(a.fp.q_f32 + (kvh * a.G + h) * kHeadDim)[lane] =
+                        reinterpret_cast<float4 *>(
+                            a.fp.q_f32 + (int64_t(blockIdx.z) * a.hq + kvh * a.G + h) * kHeadDim)[lane] =
                             make_float4(y[0], y[1], y[2], y[3]);
                     }
                 }
@@ -268,7 +280,14 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
                 }
             }
             lim = ctx - 1;
-            append_owned_cell_fused<WAVES>(a, table, kvh, ctx, src.new_mine, wave, lane); // ends with a barrier
+            // the row's own cell when this split owns it, and every earlier row's cell whose tile this split reads
+            uint32_t cells = static_cast<uint32_t>(src.new_mine & 1) << blockIdx.z;
+            for (int32_t c = 0; c < static_cast<int32_t>(blockIdx.z); ++c) {
+                const uint32_t tile_c = static_cast<uint32_t>((ctx - 1 - static_cast<int32_t>(blockIdx.z) + c) >> 5);
+                const bool hit = lane < n_tiles && (src.ent_x & 0xffffu) == tile_c;
+                cells |= __any(hit) ? (1u << c) : 0u;
+            }
+            append_cells_fused<WAVES>(a, table, kvh, ctx, cells, (src.new_mine & 1) != 0, wave, lane); // + barrier
         } else {
             if constexpr (QLO) {
                 *reinterpret_cast<u32x4 *>(smem + GR * kGroupLds + kSelSlice + threadIdx.x * 16) = qlo_ld;

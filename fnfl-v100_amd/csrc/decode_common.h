@@ -24,15 +24,17 @@ constexpr int32_t kGroupLds = kCodeBytes + 2 * kScaleBytes;
 // forms its KV head's query rows (F32 RMS norm and IMROPE, fp16) while its selection builds, and the workgroup that
 // reads the new cell's tile writes the cell's K (normed, roped) and V in the pool's format.
 struct fused_prep {
-    const float * qfull = nullptr; // [hq][512]: each head's q, then its gate; null: the launch reads q
-    const float * kv_k = nullptr;  // [h_kv][256]
-    const float * kv_v = nullptr;  // [h_kv][256]
+    const float * qfull = nullptr; // [rows][hq][512]: each head's q, then its gate; null: the launch reads q
+    const float * kv_k = nullptr;  // [rows][h_kv][256]
+    const float * kv_v = nullptr;  // [rows][h_kv][256]
     const float * q_norm = nullptr;
     const float * k_norm = nullptr;
-    const int32_t * pos = nullptr; // [4][1]
+    const int32_t * pos = nullptr; // [4][rows]
     float theta_scale = 0.0f;
-    float * q_f32 = nullptr; // optional [hq][256]
-    float * k_f32 = nullptr; // optional [h_kv][256]
+    float * q_f32 = nullptr; // optional [rows][hq][256]
+    float * k_f32 = nullptr; // optional [rows][h_kv][256]
+    int32_t rows = 1;        // the call's rows: row z (grid.z) is qfull's, pos's column and q_f32's row z; its new
+                             // cell depth + z is kv_k / kv_v / k_f32's row z
 };
 
 struct dec_args {

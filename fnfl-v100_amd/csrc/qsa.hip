@@ -9,9 +9,10 @@
 //      normed, roped k) and V quantized into the pool;
 //   2. the sparse decode launch (each row its own splits);
 //   3. the merge with the gated epilogue.
-// One row of at most 16 query heads a KV head skips step 1: the sparse launch forms its query rows in LDS while its
-// selection builds, and the workgroup that reads the new cell's tile writes the cell (fused_prep, decode.hip), with
-// the same arithmetic (the outputs are bitwise those of the three launches).
+// At most 16 query heads a KV head skip step 1: the sparse launch forms each row's query heads in LDS while the row's
+// selection builds, and every workgroup that reads a new cell's tile writes that cell first (a row's own cell also
+// by its owner when no workgroup reads it; fused_prep, decode.hip). Workgroups that write the same cell store the same
+// bytes, and the arithmetic is the prepare kernel's, so the outputs are bitwise those of the three launches.
 // Differences from the reference's kernel: the query enters the matrix cores as two fp16 parts (the reference keeps q
 // in F32; hi + lo carries it to about 2^-22 relative, and the output meets the reference checker's 1e-5 normalized
 // bound, qa2_test.cpp:58), depth is a host value, and the cache is the paged pool.
@@ -146,10 +147,10 @@ int qsa_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, i
     if (check_only) {
         return FNKV_OK;
     }
-    // one row of at most 16 query heads a KV head: the sparse launch prepares the row itself (one launch fewer);
+    // at most 16 query heads a KV head: the sparse launch prepares its rows itself (one launch fewer);
     // FNKV_QSA_TWO_KERNELS=1 keeps the separate prepare launch, for comparison
     const char * two = std::getenv("FNKV_QSA_TWO_KERNELS");
-    if (T == 1 && G <= 16 && (two == nullptr || std::atoi(two) == 0)) {
+    if (G <= 16 && (two == nullptr || std::atoi(two) == 0)) {
         fused_prep fp;
         fp.qfull = qfull;
         fp.kv_k = kv_k;
@@ -160,6 +161,7 @@ int qsa_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, i
         fp.theta_scale = theta_scale;
         fp.q_f32 = q_f32;
         fp.k_f32 = k_f32;
+        fp.rows = T;
         return sparse_launch(pool, slot, depth, T, layer, hq, 1.0f / 16.0f, q16, body, offsets, kv_k, kv_v, FNKV_F32,
                              nullptr, &gate, ws, sp, st, who, &fp, dd, q16_lo);
     }

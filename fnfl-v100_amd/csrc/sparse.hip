@@ -107,11 +107,11 @@ int sparse_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T
 
     // several rows: their new cells first (a row may read an earlier row's new cell; the rows run side by side); one
     // row: the launch writes it, by the split that reads its tile
-    if (fp != nullptr && (T != 1 || G > 16)) {
-        set_error(name + ": a launch that prepares its row takes one row of at most 16 query heads a KV head");
+    if (fp != nullptr && (G > 16 || fp->rows != T)) {
+        set_error(name + ": a launch that prepares its rows takes at most 16 query heads a KV head");
         return FNKV_ERR_ARG;
     }
-    if (k_new != nullptr && T > 1) {
+    if (k_new != nullptr && T > 1 && fp == nullptr) {
         if (append_enqueue(*p, slot, layer, depth, dd != nullptr ? dd->depth : nullptr, ctx, T, k_new, v_new,
                            new_dtype, st) != FNKV_OK) {
             set_error(name + ": launch failed");

@@ -222,8 +222,8 @@ int64_t fnkv_qsa_workspace_bytes(const fnkv_pool * pool, int64_t depth, int32_t 
  * qfull: F32 [T][hq][512] (each head's q, then its gate); kv_k, kv_v: F32 [T][h_kv][256]; q_norm, k_norm: F32 [256];
  * out: F32 [T][hq][256]; codes: int8 [T][hq 256]; scales: F32 [T][hq 8][2]; q_f32, k_f32 (optional): the F32 q
  * [T][hq][256] and k [T][h_kv][256] after the norm and rope. Three launches in stream order: the prepare (which
- * writes the new cells), the attention (each row its own splits), the gated merge; one row of at most 16 query heads
- * a KV head: two (the attention forms its rows and writes the new cell itself, bitwise the same outputs).
+ * writes the new cells), the attention (each row its own splits), the gated merge; at most 16 query heads a KV head:
+ * two (the attention forms each row's query heads and writes the new cells itself, bitwise the same outputs).
  * hq / h_kv <= FNKV_MAX_ROWS. */
 int fnkv_qsa_attend(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, int32_t layer, int32_t hq,
                     const float * qfull, const float * kv_k, const float * kv_v, const float * q_norm,

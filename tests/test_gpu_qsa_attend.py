@@ -177,36 +177,40 @@ def test_refusals_enqueue_nothing():
     assert torch.count_nonzero(out).item() == 0 and torch.count_nonzero(kv).item() == 0
 
 
-@pytest.mark.parametrize("depth,hq,h_kv,fmt", [(0, 12, 1, fnkv.FMT_Q8_0), (5000, 12, 1, fnkv.FMT_Q8_0),
-                                               (16002, 16, 2, fnkv.FMT_Q8_0), (7001, 12, 1, fnkv.FMT_KV8)])
-def test_one_row_prepared_in_the_sparse_launch(depth, hq, h_kv, fmt, monkeypatch):
-    # one row: the sparse launch forms the query rows and writes the new cell itself; every output (F32 out, codes,
-    # scales, q_f32, k_f32, the new cell in the pool) bitwise that of the separate prepare launch
+@pytest.mark.parametrize("depth,T,hq,h_kv,fmt", [(0, 1, 12, 1, fnkv.FMT_Q8_0), (5000, 1, 12, 1, fnkv.FMT_Q8_0),
+                                                 (16002, 1, 16, 2, fnkv.FMT_Q8_0), (7001, 1, 12, 1, fnkv.FMT_KV8),
+                                                 (0, 3, 12, 1, fnkv.FMT_Q8_0), (29, 5, 12, 1, fnkv.FMT_Q8_0),
+                                                 (196605, 3, 12, 1, fnkv.FMT_Q8_0), (16000, 5, 16, 2, fnkv.FMT_Q8_0),
+                                                 (7001, 4, 12, 1, fnkv.FMT_KV8)])
+def test_rows_prepared_in_the_sparse_launch(depth, T, hq, h_kv, fmt, monkeypatch):
+    # up to 16 query heads a KV head: the sparse launch forms each row's query heads and writes the new cells itself
+    # (every workgroup that reads a new cell's tile writes it first); every output (F32 out, codes, scales, q_f32,
+    # k_f32, the new cells in the pool) bitwise that of the separate prepare launch
     def once(two):
         if two:
             monkeypatch.setenv("FNKV_QSA_TWO_KERNELS", "1")
         else:
             monkeypatch.delenv("FNKV_QSA_TWO_KERNELS", raising=False)
-        rng = np.random.default_rng([depth, 23])
-        ctx = depth + 1
+        rng = np.random.default_rng([depth, T, 23])
+        ctx = depth + T
         pool = fnkv.Pool(2, -(-ctx // 256) + 8, 1, h_kv, fmt=fmt)
         cases.scatter_ensure(pool, [0], [ctx], depth + 3, churn=0.3)
         k16, v16 = cases.kv_rows(depth + 3, ctx, h_kv)
         if depth:
             pool.append(0, 0, 0, torch.from_numpy(k16[:depth]).cuda(), torch.from_numpy(v16[:depth]).cuda())
-        words, offs, _ = O.qsa_body(depth, 1, depth + 5)
+        words, offs, _ = O.qsa_body(depth, T, depth + 5)
         d = {n: torch.from_numpy(x).cuda() for n, x in dict(
-            qfull=rng.uniform(-3.0, 3.0, (1, hq, 512)).astype(np.float32),
-            kv_k=rng.uniform(-2.0, 2.0, (1, h_kv, 256)).astype(np.float32),
-            kv_v=rng.uniform(-1.5, 1.5, (1, h_kv, 256)).astype(np.float32),
+            qfull=rng.uniform(-3.0, 3.0, (T, hq, 512)).astype(np.float32),
+            kv_k=rng.uniform(-2.0, 2.0, (T, h_kv, 256)).astype(np.float32),
+            kv_v=rng.uniform(-1.5, 1.5, (T, h_kv, 256)).astype(np.float32),
             q_norm=rng.uniform(0.3, 1.8, 256).astype(np.float32),
             k_norm=rng.uniform(0.3, 1.8, 256).astype(np.float32),
-            pos=positions(depth, 1, True)).items()}
-        out = torch.full((1, hq, 256), float("nan"), device="cuda")
-        codes = torch.zeros((1, hq * 256), dtype=torch.int8, device="cuda")
-        scales = torch.zeros((1, hq * 8, 2), device="cuda")
-        q_f32 = torch.empty((1, hq, 256), device="cuda")
-        k_f32 = torch.empty((1, h_kv, 256), device="cuda")
+            pos=positions(depth, T, True)).items()}
+        out = torch.full((T, hq, 256), float("nan"), device="cuda")
+        codes = torch.zeros((T, hq * 256), dtype=torch.int8, device="cuda")
+        scales = torch.zeros((T, hq * 8, 2), device="cuda")
+        q_f32 = torch.empty((T, hq, 256), device="cuda")
+        k_f32 = torch.empty((T, h_kv, 256), device="cuda")
         pool.qsa_attend(0, depth, 0, d["qfull"], d["kv_k"], d["kv_v"], d["q_norm"], d["k_norm"], d["pos"],
                         torch.from_numpy(words.view(np.int32)).cuda(), torch.from_numpy(offs).cuda(), out, codes,
                         scales, q_f32=q_f32, k_f32=k_f32)
@@ -214,10 +218,10 @@ def test_one_row_prepared_in_the_sparse_launch(depth, hq, h_kv, fmt, monkeypatch
         for h in range(h_kv):
             for kv in range(2):
                 if fmt == fnkv.FMT_KV8:
-                    c, sc = pool.export_kv8(0, 0, h, kv, depth, 1)
+                    c, sc = pool.export_kv8(0, 0, h, kv, depth, T)
                     cells += [c.cpu().numpy(), sc.cpu().numpy()]
                 else:
-                    cells.append(pool.export(0, 0, h, kv, depth, 1).cpu().numpy())
+                    cells.append(pool.export(0, 0, h, kv, depth, T).cpu().numpy())
         torch.cuda.synchronize()
         res = [out.cpu().numpy(), codes.cpu().numpy(), scales.cpu().numpy(), q_f32.cpu().numpy(),
                k_f32.cpu().numpy()] + cells
