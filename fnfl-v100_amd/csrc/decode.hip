@@ -48,9 +48,12 @@ namespace fnkv {
 // `own`: the cell is row z's own and this workgroup its owner), V = kv_v's row c, each in the pool's format. Several
 // workgroups may write one cell (every one that reads its tile, so its own loads follow its own stores); they store
 // the same bytes.
+// sn, cs: the row's own position's rope angle (cell z's); own_x, own_g: cell z's k row and the k norm (the wave of
+// job 2 z), or its v row (the wave of job 2 z + 1), loaded early
 template <int WAVES>
 __device__ __forceinline__ void append_cells_fused(const dec_args & a, const int32_t * table, int32_t kvh,
-                                                   int64_t ctx, uint32_t cells, bool own, int32_t wave, int32_t lane) {
+                                                   int64_t ctx, uint32_t cells, bool own, float sn, float cs,
+                                                   float4 own_x, float4 own_g, int32_t wave, int32_t lane) {
     const int32_t z = static_cast<int32_t>(blockIdx.z);
     const int64_t depth = ctx - 1 - z;
     const pool_view & pv = a.pv;
@@ -63,10 +66,19 @@ __device__ __forceinline__ void append_cells_fused(const dec_args & a, const int
         const int64_t src = (int64_t(c) * pv.h_kv + kvh) * kHeadDim;
         float x[4];
         if (kv == 0) {
-            norm_rope(x, a.fp.kv_k + src, a.fp.k_norm, a.fp.pos, a.fp.rows, c, a.fp.theta_scale, lane);
+            if (c == z) {
+                norm_rope_apply(x, own_x, own_g, sn, cs, lane);
+            } else {
+                norm_rope(x, a.fp.kv_k + src, a.fp.k_norm, a.fp.pos, a.fp.rows, c, a.fp.theta_scale, lane);
+            }
             if (own && c == z && a.fp.k_f32 != nullptr) {
                 reinterpret_cast<float4 *>(a.fp.k_f32 + src)[lane] = make_float4(x[0], x[1], x[2], x[3]);
             }
+        } else if (c == z) {
+            x[0] = own_x.x;
+            x[1] = own_x.y;
+            x[2] = own_x.z;
+            x[3] = own_x.w;
         } else {
             load4<true>(a.fp.kv_v + src, lane, x);
         }
@@ -186,6 +198,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     half8 qop[kBlocks];
     int64_t lim;
     float4 xq[2], gq;
+    float4 own_x = {0.0f, 0.0f, 0.0f, 0.0f}, own_g = {0.0f, 0.0f, 0.0f, 0.0f}; // a prepared row's own cell
     int32_t pq = 0;
     if constexpr (SP) { // the Q rows' latency hidden behind the selection's build
         if (a.fp.qfull != nullptr) {
@@ -199,6 +212,15 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
             }
             gq = reinterpret_cast<const float4 *>(a.fp.q_norm)[lane];
             pq = rope_pos(a.fp.pos, a.fp.rows, static_cast<int32_t>(blockIdx.z), lane);
+            // the row's own cell's inputs, for the waves that write its K (and the k norm) and its V
+            const int32_t zc = static_cast<int32_t>(blockIdx.z);
+            const int64_t crow = (int64_t(zc) * pv.h_kv + kvh) * kHeadDim;
+            if (wave == (2 * zc) % WAVES) {
+                own_x = reinterpret_cast<const float4 *>(a.fp.kv_k + crow)[lane];
+                own_g = reinterpret_cast<const float4 *>(a.fp.k_norm)[lane];
+            } else if (wave == (2 * zc + 1) % WAVES) {
+                own_x = reinterpret_cast<const float4 *>(a.fp.kv_v + crow)[lane];
+            }
         } else {
             load_q_operands(a, s, ctx, kvh, rt, j, qg, qop, lim);
         }
@@ -218,7 +240,13 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         }
     }
     split_src<SP> src;
-    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * kGroupLds, ctx);
+    // a launch that prepares its row: the row's rope angle while the selection's loads are in flight
+    float sn = 0.0f, cs = 0.0f;
+    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * kGroupLds, ctx, [&] {
+        if (SP && a.fp.qfull != nullptr) {
+            rope_angle(sn, cs, pq, a.fp.theta_scale, lane);
+        }
+    });
     if (refused<SP>(a, s, ctx, sp, kvh)) {
         return;
     }
@@ -233,8 +261,6 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
             // the KV head's query rows as fp16 in LDS (after the tile buffers and the selection slice), then each
             // lane's operands from there; split 0 also writes the F32 rows
             uint16_t * ql = reinterpret_cast<uint16_t *>(smem + GR * kGroupLds + kSelSlice);
-            float sn, cs;
-            rope_angle(sn, cs, pq, a.fp.theta_scale, lane);
             uint2 lo_pk[2] = {make_uint2(0, 0), make_uint2(0, 0)}; // QLO: fp16(y - hi), heads >= G zero
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
@@ -258,7 +284,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
                     }
                 }
             }
-            __syncthreads();
+            barrier_keep_loads(); // the rows are in LDS (the F32 rows' stores need not have landed)
 #pragma unroll
             for (int b = 0; b < kBlocks; ++b) {
                 u32x4 v = {0, 0, 0, 0};
@@ -270,7 +296,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
             if constexpr (QLO) {
                 // the low parts fp16(y - hi) into the same region, as operands: value 4 lane + i of head h is
                 // element 4 (lane & 1) + i of operand (block lane / 8, lane (h, (lane & 7) / 2)); heads >= G zero
-                __syncthreads(); // every operand read above
+                barrier_keep_loads(); // every operand read above
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
                     const int32_t h = wave + 8 * i;
@@ -287,7 +313,8 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
                 const bool hit = lane < n_tiles && (src.ent_x & 0xffffu) == tile_c;
                 cells |= __any(hit) ? (1u << c) : 0u;
             }
-            append_cells_fused<WAVES>(a, table, kvh, ctx, cells, (src.new_mine & 1) != 0, wave, lane); // + barrier
+            append_cells_fused<WAVES>(a, table, kvh, ctx, cells, (src.new_mine & 1) != 0, sn, cs, own_x, own_g,
+                                      wave, lane); // ends with a barrier
         } else {
             if constexpr (QLO) {
                 *reinterpret_cast<u32x4 *>(smem + GR * kGroupLds + kSelSlice + threadIdx.x * 16) = qlo_ld;

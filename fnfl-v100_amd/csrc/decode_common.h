@@ -135,14 +135,13 @@ struct dec_args {
     } while (0)
 #endif
 
-// A sparse launch's selection as the workgroup sees it. Every workgroup rebuilds it in LDS from the bodies (a few
-// KB): row t's 8 block bits of each 32-cell tile (bit 8 t of mlo for t < 4, of mhi for t = 4), a 4-cell block a bit;
-// the tiles any row selected, in ascending order, are the list whose entries the splits take in turn. Rebuilding
-// costs each workgroup one read of the bodies, which replaces the launch (and the memory round trip) that a separate
-// planning kernel would add.
-constexpr int32_t kSelMaxCells = 262144 + 32;                                     // the reference's max_cells
-constexpr int32_t kSelMaxTiles = (kSelMaxCells + kTileTokens - 1) / kTileTokens; // 8,193
-constexpr int32_t kSelTopBlocks = 512;                                            // blocks a row (qsa.h)
+// A sparse launch's selection as the workgroup sees it. Every workgroup rebuilds its row's list in LDS from the row's
+// body (a few KB): the tiles the row selected, in ascending order, each with its 8 block bits (a 4-cell block a bit;
+// the list entry's second word), are the list whose entries the splits take in turn. Rebuilding costs each workgroup
+// one read of the body, which replaces the launch (and the memory round trip) that a separate planning kernel would
+// add.
+constexpr int32_t kSelMaxCells = 262144 + 32; // the reference's max_cells
+constexpr int32_t kSelTopBlocks = 512;        // blocks a row (qsa.h)
 constexpr int32_t kSelMaxRows = 5;
 constexpr int32_t kSelMaxThreads = 512;
 constexpr int32_t kSlabRows = 128;                          // prompt rows a slab (qsa_prompt.h prompt_slab)
@@ -153,138 +152,118 @@ __host__ __device__ inline int32_t sparse_split_size(int32_t n_sel, int32_t n_sp
     const int32_t s = (n_sel + n_splits - 1) / n_splits;
     return s < 1 ? 1 : s;
 }
-constexpr int32_t kSelLds = 2 * kSelMaxTiles * 4 + kSelMaxThreads * 4 + 64; // the build's scratch
+constexpr int32_t kSelLds = (kSelTopBlocks + 1 + kSelMaxThreads / 64 + 1) * 4; // the build's scratch
 constexpr int32_t kSelSlice = 64 * 8; // a split's entries (logical tile | row 4's bits << 16, rows 0-3's bits)
 
-template <int32_t THREADS>
+// hook: the caller's work while the body's loads are in flight (ALU only; run by every thread)
+// The row view's selection (one row at q = ctx - 1): its K = min(n_vis, 512) block IDs (qsa.h:63-66: ascending) that
+// lie in 0 .. n_vis - 1 (others are ignored), then its tail block n_vis when (q + 1) % 4 != 0; the list is the tiles of
+// those blocks in order, each entry (tile | 0, the tile's 8 block bits) with the run of list blocks that share its tile
+// (at most 8, distinct blocks being ascending). Two block-wide scans over at most 513 entries, no per-tile bitmap.
+template <int32_t THREADS, typename HOOK>
 __device__ void sparse_build(const dec_args & a, uint8_t * smem, uint2 * slice, int32_t split, int32_t & n_tiles,
-                             int32_t & tile_l, int32_t & rank_of_new) {
-    static_assert(THREADS <= kSelMaxThreads, "prefix array size");
-    uint32_t * mlo = reinterpret_cast<uint32_t *>(smem);
-    uint32_t * mhi = mlo + kSelMaxTiles;
-    int32_t * base = reinterpret_cast<int32_t *>(mhi + kSelMaxTiles); // [THREADS] each thread's first entry
-    int32_t * total = base + kSelMaxThreads; // [1 + kSelMaxRows]
+                             int32_t & tile_l, int32_t & rank_of_new, const HOOK & hook) {
+    static_assert(THREADS <= kSelMaxThreads && THREADS % 64 == 0, "scratch size");
+    constexpr int32_t PER = (kSelTopBlocks + 1 + THREADS - 1) / THREADS; // consecutive entries a thread
+    constexpr int32_t WAVES = THREADS / 64;
+    int32_t * blk = reinterpret_cast<int32_t *>(smem);   // [kSelTopBlocks + 1] the kept blocks, in order
+    int32_t * wsum = blk + kSelTopBlocks + 1;             // [WAVES] wave totals of a scan
+    int32_t * own = wsum + WAVES;                         // [1] the entry holding the row's own cell's tile
     const int32_t tid = static_cast<int32_t>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
-    const int64_t ctx = a.ctx[0], depth = ctx - a.T;
-    const int32_t n_ctx_tiles = static_cast<int32_t>((ctx + kTileTokens - 1) / kTileTokens);
-    // Row t at position q sees block b whole when 4 b + 3 <= q; its tail (cells 4 n_vis .. q, n_vis = (q + 1) / 4)
-    // is block n_vis up to its own position, which the causal limit cuts. The layout follows from depth and T alone
-    // (qsa.h:77-81): row t's words start after the earlier rows' 2 + K + tail, so nothing past a row is read, and
-    // entries outside the row's whole blocks are ignored.
-    // Each row's block count follows from its position (K = min(n_vis, 512)), so every row's block IDs are read in
-    // one flat loop (one memory round trip, not one a row); the words' K field is not needed.
-    int32_t row_off[kSelMaxRows + 1], row_k[kSelMaxRows];
-    int32_t n_entries = 0;
-    {
-        int32_t off = 0;
+    const int64_t q = a.ctx[0] - 1;
+    const int32_t n_vis = static_cast<int32_t>((q + 1) / 4);
+    const int32_t K = n_vis < kSelTopBlocks ? n_vis : kSelTopBlocks;
+    const bool tail = (q + 1) % 4 != 0;
+    // a block-wide exclusive scan of one count a thread (thread order), and its total
+    auto scan = [&](int32_t x, int32_t & excl, int32_t & total) {
+        int32_t incl = x;
 #pragma unroll
-        for (int32_t t = 0; t < kSelMaxRows; ++t) {
-            const int64_t q = depth + t;
-            const int32_t n_vis = static_cast<int32_t>((q + 1) / 4);
-            const int32_t k_full = t < a.T ? (n_vis < kSelTopBlocks ? n_vis : kSelTopBlocks) : 0;
-            row_off[t] = n_entries;
-            row_k[t] = off; // the row's first block word
-            n_entries += k_full;
-            off += t < a.T ? 2 + k_full + static_cast<int32_t>((q + 1) % 4) : 0;
+        for (int32_t o = 1; o < 64; o <<= 1) {
+            const int32_t y = __shfl_up(incl, o);
+            incl += lane >= o ? y : 0;
         }
-        row_off[kSelMaxRows] = n_entries;
-    }
-    // all of a thread's loads first (at most kPer), then their bits: one memory round trip
-    constexpr int32_t kPer = (kSelMaxRows * kSelTopBlocks + THREADS - 1) / THREADS;
-    int32_t blk[kPer], row[kPer];
+        if (lane == 63) {
+            wsum[wave] = incl;
+        }
+        __syncthreads();
+        int32_t wb = 0, tot = 0;
 #pragma unroll
-    for (int32_t k = 0; k < kPer; ++k) {
-        const int32_t i = tid + k * THREADS;
-        int32_t t = 0, e0 = 0, w0 = row_k[0]; // the entry's row, its first entry and its first block word
-#pragma unroll
-        for (int32_t r = 1; r < kSelMaxRows; ++r) {
-            const bool in = i >= row_off[r];
-            t = in ? r : t;
-            e0 = in ? row_off[r] : e0;
-            w0 = in ? row_k[r] : w0;
+        for (int32_t w = 0; w < WAVES; ++w) {
+            const int32_t v = wsum[w];
+            wb += w < wave ? v : 0;
+            tot += v;
         }
-        row[k] = t;
-        blk[k] = i < n_entries ? static_cast<int32_t>(a.sel_body[w0 + 2 + (i - e0)]) : -1;
-    }
-    // the bitmap zeroed while the loads are in flight
-    for (int32_t i = tid; i < n_ctx_tiles; i += THREADS) {
-        mlo[i] = 0u;
-        mhi[i] = 0u;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int32_t k = 0; k < kPer; ++k) {
-        const int32_t t = row[k], b = blk[k];
-        const int32_t n_vis = static_cast<int32_t>((depth + t + 1) / 4);
-        if (b >= 0 && b < n_vis) {
-            atomicOr(&(t < 4 ? mlo : mhi)[b >> 3], 1u << (8 * (t & 3) + (b & 7)));
-        }
-    }
-    if (tid < a.T) {
-        const int64_t q = depth + tid;
-        const int32_t n_vis = static_cast<int32_t>((q + 1) / 4);
-        if ((q + 1) % 4 != 0) {
-            atomicOr(&(tid < 4 ? mlo : mhi)[n_vis >> 3], 1u << (8 * (tid & 3) + (n_vis & 7)));
-        }
-    }
-    __syncthreads();
-    // the list: thread i scans tiles i * PER .. (i + 1) * PER - 1 (PER odd, so the threads' reads fall in distinct
-    // banks; the tiles' nonzero flags kept as bits of one register); a block-wide exclusive scan of the counts gives
-    // each thread its first entry
-    constexpr int32_t PER = ((kSelMaxTiles + THREADS - 1) / THREADS) | 1;
-    static_assert(PER <= 32, "one bit a tile");
-    const int32_t t0 = tid * PER;
-    uint32_t bits = 0;
+        excl = wb + incl - x;
+        total = tot;
+        __syncthreads(); // wsum is free again
+    };
+    // the row's block IDs (one memory round trip), then the caller's work
+    int32_t b[PER];
 #pragma unroll
     for (int32_t k = 0; k < PER; ++k) {
-        const int32_t i = t0 + k;
-        const uint32_t v = i < n_ctx_tiles ? (mlo[i] | mhi[i]) : 0u;
-        bits |= (v != 0u ? 1u : 0u) << k;
+        const int32_t i = tid * PER + k;
+        b[k] = i < K ? static_cast<int32_t>(a.sel_body[2 + i]) : -1;
     }
-    const int32_t cnt = __builtin_popcount(bits);
-    int32_t incl = cnt;
+    if (tid == 0) {
+        *own = -1;
+    }
+    hook();
+    // the blocks in 0 .. n_vis - 1, compacted in order, then the tail block (past every whole one)
+    int32_t cnt = 0;
 #pragma unroll
-    for (int32_t o = 1; o < 64; o <<= 1) {
-        const int32_t y = __shfl_up(incl, o);
-        incl += lane >= o ? y : 0;
+    for (int32_t k = 0; k < PER; ++k) {
+        cnt += b[k] >= 0 && b[k] < n_vis ? 1 : 0;
     }
-    if (lane == 63) {
-        base[wave] = incl; // wave totals
-    }
-    int32_t * owner = total + 1; // [kSelMaxRows] the split that writes new cell t (0 when no row selects its tile)
-    if (tid < kSelMaxRows) {
-        owner[tid] = 0;
-    }
-    __syncthreads();
-    int32_t wbase = 0, n_sel = 0;
-    for (int32_t w = 0; w < THREADS / 64; ++w) {
-        wbase += w < wave ? base[w] : 0;
-        n_sel += base[w];
-    }
-    const int32_t first = wbase + incl - cnt;
-    // the entries spread over all the launched splits (S each, the last ones short), so every workgroup gets work
-    const int32_t S = sparse_split_size(n_sel, static_cast<int32_t>(gridDim.x));
-    // this split's entries, and the owners of the new cells' tiles
-    const int32_t e0 = split * S;
-    const int32_t tile_new0 = static_cast<int32_t>(depth >> 5), tile_new1 = static_cast<int32_t>((ctx - 1) >> 5);
-    int32_t pos = first;
-    uint32_t rest = bits;
-    while (rest != 0u) {
-        const int32_t k = __builtin_ctz(rest);
-        rest &= rest - 1u;
-        const int32_t i = t0 + k;
-        if (pos >= e0 && pos < e0 + S) {
-            slice[pos - e0] = uint2{static_cast<uint32_t>(i) | ((mhi[i] & 0xffu) << 16), mlo[i]};
+    int32_t first = 0, n_kept = 0;
+    scan(cnt, first, n_kept);
+#pragma unroll
+    for (int32_t k = 0; k < PER; ++k) {
+        if (b[k] >= 0 && b[k] < n_vis) {
+            blk[first++] = b[k];
         }
-        if (i >= tile_new0 && i <= tile_new1) {
+    }
+    if (tid == 0 && tail) {
+        blk[n_kept] = n_vis;
+    }
+    const int32_t n_all = n_kept + (tail ? 1 : 0);
+    __syncthreads();
+    // a tile's first block in the list heads its entry; the entry's bits are its run's blocks
+    int32_t heads = 0;
+    uint32_t bits[PER];
 #pragma unroll
-            for (int32_t t = 0; t < kSelMaxRows; ++t) {
-                if (t < a.T && static_cast<int32_t>((depth + t) >> 5) == i) {
-                    owner[t] = pos / S;
+    for (int32_t k = 0; k < PER; ++k) {
+        const int32_t i = tid * PER + k;
+        bits[k] = 0u;
+        if (i < n_all) {
+            const int32_t v = blk[i];
+            if (i == 0 || (blk[i - 1] >> 3) != (v >> 3)) {
+                uint32_t m = 0u;
+                for (int32_t jj = i; jj < n_all && (blk[jj] >> 3) == (v >> 3); ++jj) {
+                    m |= 1u << (blk[jj] & 7);
                 }
+                bits[k] = m;
+                ++heads;
             }
         }
-        ++pos;
+    }
+    int32_t idx = 0, n_sel = 0;
+    scan(heads, idx, n_sel);
+    // the entries spread over all the launched splits (S each, the last ones short), so every workgroup gets work
+    const int32_t S = sparse_split_size(n_sel, static_cast<int32_t>(gridDim.x));
+    const int32_t e0 = split * S;
+    const int32_t own_tile = static_cast<int32_t>(q >> 5);
+#pragma unroll
+    for (int32_t k = 0; k < PER; ++k) {
+        if (bits[k] != 0u) {
+            const int32_t tile = blk[tid * PER + k] >> 3;
+            if (idx >= e0 && idx < e0 + S) {
+                slice[idx - e0] = uint2{static_cast<uint32_t>(tile), bits[k]};
+            }
+            if (tile == own_tile) {
+                *own = idx;
+            }
+            ++idx;
+        }
     }
     __syncthreads();
     const int32_t left = n_sel - e0;
@@ -295,12 +274,9 @@ __device__ void sparse_build(const dec_args & a, uint8_t * smem, uint2 * slice, 
     if (split == 0 && blockIdx.y == 0 && tid == 0) {
         *a.sel_n = n_sel;
     }
-    int32_t mine = 0; // the new cells this split writes (bit t: cell depth + t)
-#pragma unroll
-    for (int32_t t = 0; t < kSelMaxRows; ++t) {
-        mine |= (t < a.T && owner[t] == split) ? (1 << t) : 0;
-    }
-    rank_of_new = mine;
+    // the row's own cell: written by the split that reads its tile (split 0 when no entry holds it)
+    const int32_t o = *own;
+    rank_of_new = (o >= 0 ? o / S : 0) == split ? 1 : 0;
     __syncthreads(); // the LDS is the ring's from here
 }
 
@@ -313,8 +289,9 @@ __device__ __forceinline__ int32_t seq_of(const dec_args & a, int32_t split);
 // A sparse launch runs each of its T rows as its own set of splits (blockIdx.z = row): this is the launch as row z
 // sees it, one step token at position depth + z with its G query rows, its selection body (the words after the
 // earlier rows', qsa.h:77-81), its list length slot and its region of the partials ([row][split][head][G] rows). With
-// several rows the new cells are in the pool before the launch (a row may read an earlier row's new cell); one row
-// writes its own from k_new, by the split that reads its tile.
+// several rows the new cells are in the pool before the launch (a row may read an earlier row's new cell), or, when
+// the launch prepares its rows (fused_prep), every workgroup that reads a new cell's tile writes the cell first; one
+// row writes its own from k_new, by the split that reads its tile.
 __device__ __forceinline__ dec_args sparse_row_view(const dec_args & in) {
     dec_args a = in;
     const int32_t z = static_cast<int32_t>(blockIdx.z);
@@ -366,10 +343,17 @@ template <bool SP, bool LANES = true> struct split_src {
     __device__ __forceinline__ void init(const dec_args & a, const int32_t * table, int32_t split, int64_t b,
                                          int64_t e, int32_t lane, uint8_t * smem, uint8_t * slice_lds,
                                          int64_t ctx = 0) {
+        init<THREADS>(a, table, split, b, e, lane, smem, slice_lds, ctx, [] {});
+    }
+    // hook (sparse): work overlapped with the selection's loads (sparse_build)
+    template <int32_t THREADS, typename HOOK>
+    __device__ __forceinline__ void init(const dec_args & a, const int32_t * table, int32_t split, int64_t b,
+                                         int64_t e, int32_t lane, uint8_t * smem, uint8_t * slice_lds,
+                                         int64_t ctx, const HOOK & hook) {
         if constexpr (SP) {
             uint2 * sl = reinterpret_cast<uint2 *>(slice_lds);
             int32_t tile_l = 0;
-            sparse_build<THREADS>(a, smem, sl, split, n_tiles, tile_l, new_mine);
+            sparse_build<THREADS>(a, smem, sl, split, n_tiles, tile_l, new_mine, hook);
             slice = sl;
             if (lane < n_tiles) {
                 page_lane = table[tile_l >> 3];
