@@ -9,18 +9,24 @@
 // A = sum acc_j e^(m_j - M), o = A / L.
 //
 // How (MI355X): HBM-bound, so every byte is read once and the math rides the matrix cores.
-//   * A workgroup (4 waves) owns one (sequence, KV head, split of the cells); its waves take the split's 32-token
-//     tiles round-robin. Each tile (17,408 B: K and V codes, K and V scales) streams HBM -> LDS by 17 direct
-//     global_load_lds_dwordx4 (1 KiB each, fully coalesced), double-buffered per wave.
-//   * The tile layout (layout.h) puts each lane's 16 B exactly where v_mfma_f32_16x16x32_f16 wants its operand, so a
-//     ds_read_b128 at lane * 16 feeds the matrix core: codes widen to fp16 exactly (byte permute + packed subtract).
-//   * S^T = K Q^T one Q8_0 block (32 values) per MFMA; the block's fp32 scale folds in with one FMA per score.
-//     The G query heads x T tokens sharing the KV head are the MFMA's 16-wide column side (rows padded to 16 n).
-//   * Online softmax in the base-2 domain on the S^T registers (a column's 4 lanes reduce with two shuffles); P
-//     lands as the B operand of O^T = V^T P^T without moving: each PV MFMA covers 16 values d of one block b, whose V
-//     scale multiplies P in fp32 once per block; the product goes to the matrix core as hi + lo fp16 (two MFMAs),
-//     which keeps it to ~2^-22 relative where a single fp16 operand would err by 2^-11.
-//   * The 4 waves' partials merge in LDS; the workgroup writes (m, l, acc[256]) a row; merge_kernel folds the splits.
+//   * A workgroup of 8 (6 at three row tiles) waves owns one (sequence, KV head, split of the cells). A tile (32
+//     tokens, 17,408 B: K and V codes, K and V scales) arrives as fully coalesced 1 KiB chunks: the K codes and the
+//     scales straight into LDS (global_load_lds / buffer loads to LDS), the V codes into registers.
+//   * The tile layout (layout.h) puts each lane's 16 B exactly where v_mfma_f32_16x16x32_f16 wants its operand: one
+//     byte permute makes two codes the fp16 values 1152 + code (exact), and one MFMA a tile half takes the 1152 bias
+//     back out (against the K scales and the rows' q sums for S, against the V scales and P for O).
+//   * S^T = K Q^T one Q8_0 block (32 values) per MFMA; the block's scale folds in with one FMA per score. The G query
+//     heads x T tokens sharing the KV head are the MFMA's 16-wide column side (rows padded to 16 n).
+//   * Online softmax in the base-2 domain on the S^T registers (a column's 4 lanes reduce with two lane swaps); P
+//     lands as the B operand of O^T = V^T P^T without moving: each PV MFMA covers 16 values of one block, whose V
+//     scale multiplies P once per block; the product goes to the matrix core as hi + lo fp16 (two MFMAs), which
+//     keeps it to ~2^-22 relative where a single fp16 operand would err by 2^-11.
+//   * Row tiles: decode_kernel<1> (up to 16 rows) runs eight independent tile streams, one a wave;
+//     decode_rows_kernel<2> (up to 32) groups two waves on one stream, each computing S and the softmax of its row
+//     tile and PV of half the value blocks for both, P exchanged in LDS; dense launches with up to 48 rows run
+//     decode_kernel<3> (three waves share a stream's K in LDS, each its row tile's S, softmax and PV), sparse ones
+//     decode_rows_kernel<3>.
+//   * The waves' partials merge in LDS; the workgroup writes (m, l, acc[256]) a row; merge_kernel folds the splits.
 #include "../../include/fnkv.h"
 #include "common.h"
 #include "layout.h"
