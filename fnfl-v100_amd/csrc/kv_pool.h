@@ -14,26 +14,29 @@
 
 namespace fnkv {
 
-// physical pages 0 .. n_pages - 1; each slot's logical pages in order; the free list ascending
+// The page book: physical pages 0 .. n_pages - 1, each slot's logical pages in order (its page-table row), and the
+// free pages as a bitset (bit p of word p / 64 set when page p is free), so taking the lowest free pages is a scan of
+// set bits and returning pages is setting them: O(n_pages / 64) a call. The rule the reference's KATs pin is the
+// order: take hands out the lowest free pages in ascending order, give returns a slot's pages last first.
 class kv_pages {
   public:
     void init(int32_t n_slots, int32_t n_pages);
-    int32_t n_slots() const { return static_cast<int32_t>(map_.size()); }
+    int32_t n_slots() const { return static_cast<int32_t>(rows_.size()); }
     int32_t n_pages() const { return n_pages_; }
-    int32_t free_pages() const { return static_cast<int32_t>(free_.size()); }
+    int32_t free_pages() const { return n_free_; }
     int32_t mapped(int32_t slot) const;
     int32_t physical(int32_t slot, int32_t logical) const; // -1 when not mapped
     static int32_t pages_for(int64_t cells, int32_t page_cells, int32_t n_pages);
     // the slot's next want - mapped(slot) pages, lowest free first; false with nothing taken when they do not fit
     bool take(int32_t slot, int32_t want, std::vector<int32_t> & taken);
-    // the slot's logical pages keep .. mapped - 1 back to the free list, last first (out in that order)
+    // the slot's logical pages keep .. mapped - 1 back to the free set, last first (out in that order)
     void give(int32_t slot, int32_t keep, std::vector<int32_t> & out);
-    const std::vector<int32_t> & table(int32_t slot) const { return map_[size_t(slot)]; }
+    const std::vector<int32_t> & table(int32_t slot) const { return rows_[size_t(slot)]; }
 
   private:
-    int32_t n_pages_ = 0;
-    std::vector<std::vector<int32_t>> map_;
-    std::vector<int32_t> free_;
+    int32_t n_pages_ = 0, n_free_ = 0;
+    std::vector<std::vector<int32_t>> rows_; // each slot's physical page a logical page
+    std::vector<uint64_t> free_bits_;
 };
 
 struct kv_slot_view {

@@ -30,22 +30,23 @@ const char * last_error() { return g_err.c_str(); }
 
 void kv_pages::init(int32_t n_slots, int32_t n_pages) {
     n_pages_ = std::max(0, n_pages);
-    map_.assign(size_t(std::max(0, n_slots)), {});
-    free_.resize(size_t(n_pages_));
-    for (int32_t p = 0; p < n_pages_; ++p) {
-        free_[size_t(p)] = p;
+    n_free_ = n_pages_;
+    rows_.assign(size_t(std::max(0, n_slots)), {});
+    free_bits_.assign(size_t((n_pages_ + 63) / 64), ~uint64_t(0));
+    if (n_pages_ % 64 != 0) {
+        free_bits_.back() = (uint64_t(1) << (n_pages_ % 64)) - 1; // pages past the last are never free
     }
 }
 
 int32_t kv_pages::mapped(int32_t slot) const {
-    return (slot < 0 || slot >= n_slots()) ? 0 : static_cast<int32_t>(map_[size_t(slot)].size());
+    return (slot < 0 || slot >= n_slots()) ? 0 : static_cast<int32_t>(rows_[size_t(slot)].size());
 }
 
 int32_t kv_pages::physical(int32_t slot, int32_t logical) const {
     if (logical < 0 || logical >= mapped(slot)) {
         return -1;
     }
-    return map_[size_t(slot)][size_t(logical)];
+    return rows_[size_t(slot)][size_t(logical)];
 }
 
 int32_t kv_pages::pages_for(int64_t cells, int32_t page_cells, int32_t n_pages) {
@@ -65,14 +66,22 @@ bool kv_pages::take(int32_t slot, int32_t want, std::vector<int32_t> & taken) {
     if (need <= 0) {
         return true;
     }
-    if (need > free_pages()) {
+    if (need > n_free_) {
         return false;
     }
-    // the lowest free pages: the free list is ascending, so its first `need`
-    taken.insert(taken.end(), free_.begin(), free_.begin() + need);
-    free_.erase(free_.begin(), free_.begin() + need);
-    std::vector<int32_t> & m = map_[size_t(slot)];
-    m.insert(m.end(), taken.begin(), taken.end());
+    // the lowest `need` set bits, word by word, in ascending order
+    taken.reserve(size_t(need));
+    for (size_t w = 0; w < free_bits_.size() && int32_t(taken.size()) < need; ++w) {
+        uint64_t & word = free_bits_[w];
+        while (word != 0 && int32_t(taken.size()) < need) {
+            const int32_t bit = __builtin_ctzll(word);
+            word &= word - 1;
+            taken.push_back(int32_t(w) * 64 + bit);
+        }
+    }
+    n_free_ -= need;
+    std::vector<int32_t> & row = rows_[size_t(slot)];
+    row.insert(row.end(), taken.begin(), taken.end());
     return true;
 }
 
@@ -81,19 +90,15 @@ void kv_pages::give(int32_t slot, int32_t keep, std::vector<int32_t> & out) {
     if (slot < 0 || slot >= n_slots()) {
         return;
     }
-    std::vector<int32_t> & m = map_[size_t(slot)];
+    std::vector<int32_t> & row = rows_[size_t(slot)];
     const size_t k = size_t(std::max(0, keep));
-    while (m.size() > k) {
-        out.push_back(m.back());
-        m.pop_back();
+    while (row.size() > k) {
+        const int32_t p = row.back();
+        row.pop_back();
+        out.push_back(p);
+        free_bits_[size_t(p) / 64] |= uint64_t(1) << (p % 64);
+        ++n_free_;
     }
-    // merge the returned pages into the ascending free list
-    std::vector<int32_t> back(out);
-    std::sort(back.begin(), back.end());
-    std::vector<int32_t> merged;
-    merged.reserve(free_.size() + back.size());
-    std::merge(free_.begin(), free_.end(), back.begin(), back.end(), std::back_inserter(merged));
-    free_.swap(merged);
 }
 
 int32_t kv_reclaim_victim(const std::vector<kv_slot_view> & s, int32_t for_slot) {
