@@ -1,7 +1,7 @@
 // The page book, the reclaim choice and the pool (host), plus the pool's C-ABI.
 //   kv_pages            follows fn/model/kv_pool.cpp:85-144 (same rules: pages_for rounding capped at the pool;
-//                       take is all-or-nothing, lowest free page first; give pops last-first and keeps the free list
-//                       ascending).
+//                       take is all-or-nothing, lowest free page first; give pops last-first); the free pages are
+//                       a bitset here, so take is a count-trailing-zeros scan and give sets bits.
 //   kv_reclaim_victim   follows kv_pool.cpp:146-158 (strict < on the release order: ties go to the lower slot).
 //   kv_pool             kv_pool.h:63-138 re-designed: one HBM allocation of physical pages plus an int32 page table a
 //                       slot (the kernels gather through it) instead of VMM-mapped virtual ranges; ensure/trim keep
