@@ -1212,12 +1212,13 @@ int32_t device_cus(int32_t device) {
     return n;
 }
 
-// the split size (tokens, a multiple of the page) for these contexts: the fewest rounds of one workgroup a CU times
-// the split, preferring larger splits (fewer partials) on ties
+// the split size (tokens, a multiple of the 32-token tile from one page to eight) for these contexts: the fewest
+// rounds of one workgroup a CU times the split, preferring larger splits (fewer partials) on ties. Tile granularity
+// lets the splits just fill the device (cfg1's 120 K cells on 256 CUs: 254 workgroups of 31 tiles, not 240 of 32).
 int32_t choose_split(int32_t n_seq, const int64_t * ctx, int32_t h_kv, int32_t cus) {
     int32_t best = kPageTokens;
     double best_cost = 1e300;
-    for (int32_t st = kPageTokens; st <= 8 * kPageTokens; st *= 2) { // a split's tiles fit one wave's lanes
+    for (int32_t st = kPageTokens; st <= 8 * kPageTokens; st += kTileTokens) { // a split's tiles fit one wave's lanes
         int64_t wgs = 0;
         for (int32_t i = 0; i < n_seq; ++i) {
             wgs += (ctx[i] + st - 1) / st;
@@ -1243,10 +1244,10 @@ struct dec_plan {
 dec_plan plan_decode(const kv_pool & p, int32_t n_seq, const int64_t * ctx, int32_t R) {
     dec_plan pl;
     pl.split_tokens = choose_split(n_seq, ctx, p.h_kv(), device_cus(p.device()));
-    // tuning knob: FNKV_SPLIT_TOKENS (a multiple of 256, at most 2,048) overrides the chosen split size
+    // tuning knob: FNKV_SPLIT_TOKENS (a multiple of 32 from 256 to 2,048) overrides the chosen split size
     if (const char * e = std::getenv("FNKV_SPLIT_TOKENS")) {
         const int32_t v = std::atoi(e);
-        if (v >= kPageTokens && v <= 8 * kPageTokens && v % kPageTokens == 0) {
+        if (v >= kPageTokens && v <= 8 * kPageTokens && v % kTileTokens == 0) {
             pl.split_tokens = v;
         }
     }

@@ -248,14 +248,17 @@ def test_first_launch_matches_reruns(T):
             pool.close()
 
 
+@pytest.mark.parametrize("split", ["512", "992", "288"])
 @pytest.mark.parametrize("strided", ["0", "1"])
-@pytest.mark.parametrize("T", [1, 3])
-def test_split_walks_contiguous_and_strided(T, strided, monkeypatch):
+@pytest.mark.parametrize("T", [1, 3, 5])
+def test_split_walks_contiguous_and_strided(T, strided, split, monkeypatch):
     # a sequence's splits take either their own cell ranges or every n-th tile (the launch's choice, forced here):
-    # both partitions give the same attention within the tolerance, the fused append of the new cells included
+    # both partitions give the same attention within the tolerance, the fused append of the new cells included; the
+    # split sizes are tile multiples, 992 and 288 not page multiples (split edges inside a page; 2,016 = 7 x 288 is
+    # the edge the second sequence's new cells straddle at T > 1)
     monkeypatch.setenv("FNKV_STRIDED", strided)
-    monkeypatch.setenv("FNKV_SPLIT_TOKENS", "512")
-    ctxs = [40, 3000, 9000 + 17, 20000 + 5]
+    monkeypatch.setenv("FNKV_SPLIT_TOKENS", split)
+    ctxs = [40, 2016 + T // 2, 9000 + 17, 20000 + 5]
     st = Setup(ctxs, seed=70 + T, churn=0.3)
     q16 = cases.queries(71 + T, (len(ctxs), T, HQ, 256))
     got = st.run(q16, T)
