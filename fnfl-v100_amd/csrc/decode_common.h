@@ -152,7 +152,7 @@ __host__ __device__ inline int32_t sparse_split_size(int32_t n_sel, int32_t n_sp
     const int32_t s = (n_sel + n_splits - 1) / n_splits;
     return s < 1 ? 1 : s;
 }
-constexpr int32_t kSelLds = (kSelTopBlocks + 1 + kSelMaxThreads / 64 + 1) * 4; // the build's scratch
+constexpr int32_t kSelLds = (kSelTopBlocks + 1 + kSelMaxThreads / 64 + 1 + 64) * 4; // the build's scratch
 constexpr int32_t kSelSlice = 64 * 8; // a split's entries (logical tile | row 4's bits << 16, rows 0-3's bits)
 
 // hook: the caller's work while the body's loads are in flight (ALU only; run by every thread)
@@ -160,21 +160,28 @@ constexpr int32_t kSelSlice = 64 * 8; // a split's entries (logical tile | row 4
 // lie in 0 .. n_vis - 1 (others are ignored), then its tail block n_vis when (q + 1) % 4 != 0; the list is the tiles of
 // those blocks in order, each entry (tile | 0, the tile's 8 block bits) with the run of list blocks that share its tile
 // (at most 8, distinct blocks being ascending). Two block-wide scans over at most 513 entries, no per-tile bitmap.
+// Each thread keeps the blocks it loaded through the build (compaction keeps their order, so its kept blocks sit at
+// consecutive list positions) and loads their physical pages as soon as the IDs arrive: the page-table round trip
+// runs under the scans instead of after them, and the split's pages come out in page_l (lane i: entry i's page).
 template <int32_t THREADS, typename HOOK>
-__device__ void sparse_build(const dec_args & a, uint8_t * smem, uint2 * slice, int32_t split, int32_t & n_tiles,
-                             int32_t & tile_l, int32_t & rank_of_new, const HOOK & hook) {
+__device__ void sparse_build(const dec_args & a, const int32_t * table, uint8_t * smem, uint2 * slice,
+                             int32_t split, int32_t & n_tiles, int32_t & tile_l, int32_t & page_l,
+                             int32_t & rank_of_new, const HOOK & hook) {
     static_assert(THREADS <= kSelMaxThreads && THREADS % 64 == 0, "scratch size");
-    constexpr int32_t PER = (kSelTopBlocks + 1 + THREADS - 1) / THREADS; // consecutive entries a thread
+    constexpr int32_t PER = (kSelTopBlocks + THREADS - 1) / THREADS; // consecutive IDs a thread
     constexpr int32_t WAVES = THREADS / 64;
     int32_t * blk = reinterpret_cast<int32_t *>(smem);   // [kSelTopBlocks + 1] the kept blocks, in order
     int32_t * wsum = blk + kSelTopBlocks + 1;             // [WAVES] wave totals of a scan
     int32_t * own = wsum + WAVES;                         // [1] the entry holding the row's own cell's tile
+    int32_t * spage = own + 1;                            // [64] the split's entries' physical pages
     const int32_t tid = static_cast<int32_t>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
     const int64_t q = a.ctx[0] - 1;
     const int32_t n_vis = static_cast<int32_t>((q + 1) / 4);
     const int32_t K = n_vis < kSelTopBlocks ? n_vis : kSelTopBlocks;
     const bool tail = (q + 1) % 4 != 0;
-    // a block-wide exclusive scan of one count a thread (thread order), and its total
+    const bool tail_mine = tail && tid == THREADS - 1; // the last thread: the tail comes after every kept block
+    // a block-wide exclusive scan of one count a thread (thread order), and its total; the barriers leave global
+    // loads in flight
     auto scan = [&](int32_t x, int32_t & excl, int32_t & total) {
         int32_t incl = x;
 #pragma unroll
@@ -185,7 +192,7 @@ __device__ void sparse_build(const dec_args & a, uint8_t * smem, uint2 * slice, 
         if (lane == 63) {
             wsum[wave] = incl;
         }
-        __syncthreads();
+        barrier_keep_loads();
         int32_t wb = 0, tot = 0;
 #pragma unroll
         for (int32_t w = 0; w < WAVES; ++w) {
@@ -195,81 +202,96 @@ __device__ void sparse_build(const dec_args & a, uint8_t * smem, uint2 * slice, 
         }
         excl = wb + incl - x;
         total = tot;
-        __syncthreads(); // wsum is free again
+        barrier_keep_loads(); // wsum is free again
     };
-    // the row's block IDs (one memory round trip), then the caller's work
+    // the row's block IDs (one memory round trip), then the caller's work, then the kept blocks' pages
     int32_t b[PER];
 #pragma unroll
     for (int32_t k = 0; k < PER; ++k) {
         const int32_t i = tid * PER + k;
         b[k] = i < K ? static_cast<int32_t>(a.sel_body[2 + i]) : -1;
     }
+    int32_t tail_pg = tail_mine ? table[n_vis >> 6] : 0;
     if (tid == 0) {
         *own = -1;
     }
     hook();
-    // the blocks in 0 .. n_vis - 1, compacted in order, then the tail block (past every whole one)
+    bool keep[PER];
+    int32_t pg[PER];
     int32_t cnt = 0;
 #pragma unroll
     for (int32_t k = 0; k < PER; ++k) {
-        cnt += b[k] >= 0 && b[k] < n_vis ? 1 : 0;
+        keep[k] = b[k] >= 0 && b[k] < n_vis;
+        pg[k] = keep[k] ? table[b[k] >> 6] : 0; // block -> tile (8 blocks) -> page (8 tiles)
+        cnt += keep[k] ? 1 : 0;
     }
+    // the kept blocks, compacted in order, then the tail block (past every whole one)
     int32_t first = 0, n_kept = 0;
     scan(cnt, first, n_kept);
+    int32_t pos[PER];
 #pragma unroll
-    for (int32_t k = 0; k < PER; ++k) {
-        if (b[k] >= 0 && b[k] < n_vis) {
-            blk[first++] = b[k];
+    for (int32_t k = 0, p = first; k < PER; ++k) {
+        pos[k] = p;
+        if (keep[k]) {
+            blk[p++] = b[k];
         }
     }
-    if (tid == 0 && tail) {
+    if (tail_mine) {
         blk[n_kept] = n_vis;
     }
     const int32_t n_all = n_kept + (tail ? 1 : 0);
-    __syncthreads();
+    barrier_keep_loads();
     // a tile's first block in the list heads its entry; the entry's bits are its run's blocks
+    auto head_bits = [&](int32_t i, int32_t v) -> uint32_t {
+        if (i != 0 && (blk[i - 1] >> 3) == (v >> 3)) {
+            return 0u;
+        }
+        uint32_t m = 0u;
+        for (int32_t jj = i; jj < n_all && (blk[jj] >> 3) == (v >> 3); ++jj) {
+            m |= 1u << (blk[jj] & 7);
+        }
+        return m;
+    };
     int32_t heads = 0;
     uint32_t bits[PER];
 #pragma unroll
     for (int32_t k = 0; k < PER; ++k) {
-        const int32_t i = tid * PER + k;
-        bits[k] = 0u;
-        if (i < n_all) {
-            const int32_t v = blk[i];
-            if (i == 0 || (blk[i - 1] >> 3) != (v >> 3)) {
-                uint32_t m = 0u;
-                for (int32_t jj = i; jj < n_all && (blk[jj] >> 3) == (v >> 3); ++jj) {
-                    m |= 1u << (blk[jj] & 7);
-                }
-                bits[k] = m;
-                ++heads;
-            }
-        }
+        bits[k] = keep[k] ? head_bits(pos[k], b[k]) : 0u;
+        heads += bits[k] != 0u ? 1 : 0;
     }
+    const uint32_t tail_bits = tail_mine ? head_bits(n_kept, n_vis) : 0u;
+    heads += tail_bits != 0u ? 1 : 0;
     int32_t idx = 0, n_sel = 0;
     scan(heads, idx, n_sel);
     // the entries spread over all the launched splits (S each, the last ones short), so every workgroup gets work
     const int32_t S = sparse_split_size(n_sel, static_cast<int32_t>(gridDim.x));
     const int32_t e0 = split * S;
     const int32_t own_tile = static_cast<int32_t>(q >> 5);
+    auto put = [&](int32_t tile, uint32_t m, int32_t page) {
+        if (idx >= e0 && idx < e0 + S) {
+            slice[idx - e0] = uint2{static_cast<uint32_t>(tile), m};
+            spage[idx - e0] = page;
+        }
+        if (tile == own_tile) {
+            *own = idx;
+        }
+        ++idx;
+    };
 #pragma unroll
     for (int32_t k = 0; k < PER; ++k) {
         if (bits[k] != 0u) {
-            const int32_t tile = blk[tid * PER + k] >> 3;
-            if (idx >= e0 && idx < e0 + S) {
-                slice[idx - e0] = uint2{static_cast<uint32_t>(tile), bits[k]};
-            }
-            if (tile == own_tile) {
-                *own = idx;
-            }
-            ++idx;
+            put(b[k] >> 3, bits[k], pg[k]);
         }
     }
-    __syncthreads();
+    if (tail_bits != 0u) {
+        put(n_vis >> 3, tail_bits, tail_pg);
+    }
+    barrier_keep_loads();
     const int32_t left = n_sel - e0;
     n_tiles = left < 0 ? 0 : left < S ? left : S;
     if (lane < n_tiles) {
         tile_l = static_cast<int32_t>(slice[lane].x & 0xffffu);
+        page_l = spage[lane];
     }
     if (split == 0 && blockIdx.y == 0 && tid == 0) {
         *a.sel_n = n_sel;
@@ -352,11 +374,11 @@ template <bool SP, bool LANES = true> struct split_src {
                                          int64_t ctx, const HOOK & hook) {
         if constexpr (SP) {
             uint2 * sl = reinterpret_cast<uint2 *>(slice_lds);
-            int32_t tile_l = 0;
-            sparse_build<THREADS>(a, smem, sl, split, n_tiles, tile_l, new_mine, hook);
+            int32_t tile_l = 0, page_l = 0;
+            sparse_build<THREADS>(a, table, smem, sl, split, n_tiles, tile_l, page_l, new_mine, hook);
             slice = sl;
             if (lane < n_tiles) {
-                page_lane = table[tile_l >> 3];
+                page_lane = page_l;
                 if constexpr (LANES) {
                     ent_x = sl[lane].x;
                     ent_y = sl[lane].y;
