@@ -207,8 +207,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
         }
     };
 
-    // tile ti on planes set ti & 1: scores, online softmax, PV
-    auto compute = [&](int32_t ti) {
+    // tile ti on planes set ti & 1: scores, then `between` (the next tile's conversion, its VALU work beside the last
+    // score MFMAs and the softmax's dependent chains), online softmax, PV
+    auto compute = [&](int32_t ti, auto && between) {
         const uint8_t * pl = plane_base + (ti & 1) * kPfSet;
         floatx4 sc[kPfNT][2];
 #pragma unroll
@@ -240,6 +241,7 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
             pf_last = now_;
         }
 #endif
+        between();
         half8 ph[kPfNT], plo[kPfNT];
 #pragma unroll
         for (int nt = 0; nt < kPfNT; ++nt) {
@@ -321,10 +323,10 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
     };
 
     // Iteration ti: [tile ti + 1's scales have landed (wave 0 waited); barrier: planes ti complete, planes
-    // (ti + 1) & 1 free] [this wave's codes of tile ti + 1 (loaded during iteration ti - 1) -> planes (ti + 1) & 1]
-    // [tile ti + 2's scales and codes issued] [compute tile ti]. Every iteration issues the same loads (past the last
-    // tile: the last again), so the vmcnt counts are exact: a wave's two code loads, after them nothing; wave 0 issues
-    // the scales copy first.
+    // (ti + 1) & 1 free] [tile ti's scores] [this wave's codes of tile ti + 1 (loaded during iteration ti - 1) ->
+    // planes (ti + 1) & 1] [tile ti + 2's scales and codes issued] [tile ti's softmax and PV]. Every iteration issues
+    // the same loads (past the last tile: the last again), so the vmcnt counts are exact: a wave's two code loads,
+    // after them nothing; wave 0 issues the scales copy first.
     if (n_tiles > 0) {
         wait_vmcnt<0>();
         __syncthreads(); // tile 0's codes and scales have landed
@@ -339,13 +341,13 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
         }
         barrier_keep_loads();
         PF_T(1);
-        wait_vmcnt<0>(); // this wave's codes of tile ti + 1
         PF_T(2);
-        dequant(ti + 1);
-        issue_ring(ti + 2);
-        pf_load_codes(tile_ptr(ti + 2), wave, lane, codes);
-        PF_T(3);
-        compute(ti);
+        compute(ti, [&] {
+            wait_vmcnt<0>(); // this wave's codes of tile ti + 1
+            dequant(ti + 1);
+            issue_ring(ti + 2);
+            pf_load_codes(tile_ptr(ti + 2), wave, lane, codes);
+        });
         PF_T(4);
     }
     wait_vmcnt<0>();
