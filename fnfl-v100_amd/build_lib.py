@@ -1,4 +1,5 @@
-"""Builds libfnkv.so (the HIP library behind include/fnkv.h) for gfx950, in-tree.
+"""Builds libfnkv.so (the HIP library behind include/fnkv.h) for gfx950, in-tree, and the C++ host harness
+engine_step (host/engine_step.cpp: the reference engine's calling pattern over the C-ABI) linked against it.
 
 hipcc compiles each source to an object (in parallel) and links the shared library next to this file. Every HIP
 source is compiled with packed-fp32 instructions disabled (their hand-written forms are avoided on this target) and
@@ -13,6 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libfnkv.so")
+HARNESS = os.path.join(HERE, "engine_step")
 SOURCES = ["pool.hip", "append.hip", "decode.hip", "prefill.hip", "sparse.hip", "datc.hip", "qsa.hip", "qsp.hip"]
 ARCH = os.environ.get("FNKV_ARCH", "gfx950")
 
@@ -60,8 +62,16 @@ def build(verbose=False):
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    # the host harness: host code only, linked against the library next to it
+    tmp = HARNESS + ".tmp"
+    cmd = [hipcc(), "-O2", "-std=c++17", "-Wall", "-I", os.path.join(HERE, "..", "include"),
+           os.path.join(HERE, "host", "engine_step.cpp"), "-L", HERE, "-lfnkv", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on host/engine_step.cpp:\n{r.stderr}")
+    os.replace(tmp, HARNESS)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {HARNESS}")
     return LIB
 
 
