@@ -58,6 +58,36 @@ def test_book_known_answers_on_the_pool():
     p.close()
 
 
+def test_book_random_churn_across_free_set_words():
+    # seeded ensure / trim churn over 300 pages (the free set spans five 64-page words, and takes and gives cross
+    # word edges) on 6 slots; after every call each slot's page table and the free count equal the oracle book's
+    # (kv_pool.cpp:85-144: take lowest-first and all-or-nothing, give last-first)
+    n_pages, n_slots, pc = 300, 6, 256
+    p = fnkv.Pool(n_slots, n_pages, 1, 2)
+    ref = O.Pages(n_slots, n_pages)
+    rng = np.random.default_rng(20260)
+    fails = 0
+    for op in range(400):
+        slot = int(rng.integers(0, n_slots))
+        if rng.random() < 0.6:
+            want = int(rng.integers(0, 160))
+            code, cap = p.ensure(slot, want * pc)
+            ok, _ = ref.take(slot, want)
+            assert (code == 0) == ok, (op, slot, want)
+            fails += 0 if ok else 1
+            if not ok:
+                assert code == fnkv.ERR_CAPACITY and cap
+        else:
+            keep = int(rng.integers(0, max(1, ref.mapped(slot) + 1)))
+            assert p.trim(slot, keep * pc) == 0
+            ref.give(slot, keep)
+        assert p.free_pages() == ref.free_pages(), op
+        for sl in range(n_slots):
+            assert p.table(sl) == ref.table(sl), (op, sl)
+    assert fails > 10  # the pool ran full often enough to exercise the all-or-nothing rule
+    p.close()
+
+
 def test_injected_failure_leaves_the_slot_unchanged():
     p = fnkv.Pool(2, 8, 2, 2)
     assert p.ensure(0, 2 * 256)[0] == 0
