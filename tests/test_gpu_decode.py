@@ -311,3 +311,37 @@ def test_seventeen_sequences_refused():
     ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
     with pytest.raises(fnkv.FnkvError):
         st.pool.decode(st.slots, st.ctxs, 1, 0, q, out, ws)
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_seeded_random_launches(case):
+    # seeded launch shapes: 1-8 sequences, T 1-6, contexts log-uniform in [T, 40,000] (so split, page and tile edges
+    # fall anywhere under the planner's tile-granular splits), pages interleaved with churn; every other case passes
+    # the step's new cells to the launch, which writes them before reading
+    rng = np.random.default_rng([case, 4242])
+    n_seq = int(rng.integers(1, 9))
+    T = int(rng.integers(1, 7))
+    ctxs = [int(max(T, round(np.exp(rng.uniform(np.log(T + 1), np.log(40000)))))) for _ in range(n_seq)]
+    seed = 300 + case
+    st = Setup(ctxs, seed=seed, churn=0.25)
+    q16 = cases.queries(seed, (n_seq, T, HQ, 256))
+    print(f"case {case}: n_seq {n_seq} T {T} ctxs {ctxs}", flush=True)
+    if case % 2 == 0:
+        got = st.run(q16, T)
+        assert st.check(q16, got, T) <= TOL
+        return
+    kn = rng.standard_normal((n_seq, T, HKV, 256), dtype=np.float32).astype(np.float16)
+    vn = rng.standard_normal((n_seq, T, HKV, 256), dtype=np.float32).astype(np.float16)
+    q = torch.from_numpy(q16).cuda()
+    out = torch.empty_like(q)
+    ws = torch.empty(st.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    st.pool.decode(st.slots, ctxs, T, 0, q, out, ws, k_new=torch.from_numpy(kn).cuda(),
+                   v_new=torch.from_numpy(vn).cuda())
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for i, (s, c) in enumerate(zip(st.slots, ctxs)):
+        k16, v16 = cases.kv_rows(seed * 100 + s, c, HKV, 0)  # the rows Setup appended
+        k16, v16 = k16.copy(), v16.copy()
+        k16[c - T:], v16[c - T:] = kn[i], vn[i]
+        (_, _, kf), (_, _, vf) = cases.decoded(O, k16, v16)
+        assert cases.out_err(got[i], O.attn_f64(q16[i].view(np.uint16), kf, vf, c)) <= TOL, (case, i)
