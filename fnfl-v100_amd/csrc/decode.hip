@@ -392,13 +392,17 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     if constexpr (!QLO) {
         sig = q_sums(qop, qg);
     }
+    FNKV_PHASE_DECL();
     for (int32_t it = 0; it < n_iter; ++it) {
+        FNKV_PHASE(0 + (it > 0 ? 7 : 0));
         const int32_t ti = grp + it * GR;
         const bool have = ti < n_tiles;
         const int32_t tn = ti + GR < last_tile ? ti + GR : last_tile;
         const uint8_t * next_ptr = tile_ptr(tn);
         wait_vmcnt<8>(); // tile k's K half has landed (only its 8 V loads may be younger)
+        FNKV_PHASE(1);
         group_sync<NT>(); // ... for every wave of the group; tile k - 1's slot is no longer read
+        FNKV_PHASE(2);
         issue_k<NT>(next_ptr, kbuf((it + 1) & 1), sslot((it + 1) & 1), rt, lane);
         if (have) {
         const uint8_t * kb = kbuf(it & 1);
@@ -412,6 +416,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
             tile_scores<KV8>(kb, sc_tile, [&](int b) { return qop[b]; }, sig, j, qg, lane, sc);
         }
 
+        FNKV_PHASE(3);
         // ---- online softmax (base 2); P stays in the registers that feed the PV MFMA ----
         const int64_t lim_rel64 = lim - tok0;
         const int32_t lim_rel = lim_rel64 > 64 ? 64 : static_cast<int32_t>(lim_rel64 < -1 ? -1 : lim_rel64);
@@ -428,7 +433,9 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
             }
         }
 
+        FNKV_PHASE(4);
         wait_part_k<NT>(rt); // tile k's V codes (tile k + 1's K copy is younger)
+        FNKV_PHASE(5);
         // ---- O^T += V^T P^T: MFMA tile m covers values 16 m .. 16 m + 15 of block m / 2 ----
         // P times the block's V scale goes to the matrix core as hi + lo fp16 (fp16 alone would leave a 2^-11
         // relative error per term, too coarse when a few large cells dominate). The V codes enter as 1152 + code;
@@ -464,8 +471,10 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
             acc[2 * ld + 1] = mfma16(va1, pl, acc[2 * ld + 1]);
         }
         }
+        FNKV_PHASE(6);
         vload(next_ptr);
     }
+    FNKV_PHASE_STORE();
     wait_vmcnt<0>();
     FNKV_STAMP(3);
     FNKV_STAMP_WAVE();
