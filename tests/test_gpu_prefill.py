@@ -119,3 +119,17 @@ def test_prefill_key_splits_agree_with_one_split():
     ref = O.attn_f64(q16.view(np.uint16), kf, vf, ctx, rows=[0, 150, 299])
     assert cases.out_err(one[[0, 150, 299]], ref) <= TOL
     assert np.abs(one.astype(np.float32) - got.astype(np.float32)).max() <= 2 * TOL
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_prefill_seeded_random_shapes(case):
+    # seeded chunk shapes: depth log-uniform in [0, 20,000], rows in [1, 700], GQA groups of 4, 8 or 16 query heads a
+    # KV head; every row of the chunk checked
+    rng = np.random.default_rng([case, 5151])
+    depth = 0 if case == 0 else int(round(np.exp(rng.uniform(0.0, np.log(20000)))))
+    rows = int(rng.integers(1, 701))
+    hq, hkv = [(8, 2), (16, 2), (16, 1)][case % 3]
+    print(f"case {case}: depth {depth} rows {rows} hq {hq} hkv {hkv}", flush=True)
+    _, got, err, _ = prefill_case(depth, rows, seed=900 + case, check_rows=list(range(rows)), hq=hq, hkv=hkv)
+    assert np.isfinite(got).all()
+    assert err <= TOL, (case, depth, rows, err)
