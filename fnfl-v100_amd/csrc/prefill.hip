@@ -124,11 +124,12 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
         return layer_base + int64_t(phys) * pv.page_stride + int64_t((tok & 255) >> 5) * kTileBytes;
     };
     auto ring = [&](int32_t li) { return ring_base + (li & (kPfScaleRing - 1)) * 1024; };
-    auto issue_ring = [&](int32_t li) { // wave 0: tile li's scales chunk (K then V scales) into its ring slot
+    auto issue_ring_at = [&](int32_t li, const uint8_t * tp) { // wave 0: tile li (at tp)'s scales chunk into its slot
         if (wave == 0) {
-            lds_load16(tile_ptr(li) + kKScales + lane * 16, ring(li));
+            lds_load16(tp + kKScales + lane * 16, ring(li));
         }
     };
+    auto issue_ring = [&](int32_t li) { issue_ring_at(li, tile_ptr(li)); };
     u32x4 codes[2];
 #ifdef FNKV_TIMING
     uint64_t pf_ph[8] = {0, 0, 0, 0, 0, 0, 0, 0}, pf_last = 0;
@@ -342,11 +343,13 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
         barrier_keep_loads();
         PF_T(1);
         PF_T(2);
+        // tile ti + 2's address now: its page-table read (LDS) then waits for nothing else
+        const uint8_t * const tp2 = tile_ptr(ti + 2);
         compute(ti, [&] {
             wait_vmcnt<0>(); // this wave's codes of tile ti + 1
             dequant(ti + 1);
-            issue_ring(ti + 2);
-            pf_load_codes(tile_ptr(ti + 2), wave, lane, codes);
+            issue_ring_at(ti + 2, tp2);
+            pf_load_codes(tp2, wave, lane, codes);
         });
         PF_T(4);
     }
