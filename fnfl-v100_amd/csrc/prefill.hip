@@ -319,7 +319,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
                 acc[nt][2 * b] = mfma16(vh0, plo[nt], acc[nt][2 * b]);
                 acc[nt][2 * b + 1] = mfma16(vh1, plo[nt], acc[nt][2 * b + 1]);
             }
-            __builtin_amdgcn_sched_barrier(0); // one block's operands live at a time
+            if (b & 1) {
+                __builtin_amdgcn_sched_barrier(0); // two blocks' operands live at a time
+            }
         }
     };
 
