@@ -1043,6 +1043,33 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP, QLO>::WAVES), 1) void deco
 // columns x 32 split groups. Group g folds splits g, g + 32, ... in order with a running max (all its loads
 // independent, so they are in flight together: one memory round trip), then the 32 groups fold in order in LDS
 // (deterministic: the same order for every launch).
+// The splits of sequence s that hold partials: its first s0 and count n; false when the launch refused the sequence
+// (its outputs are left as they were)
+__device__ __forceinline__ bool merge_splits(const merge_args & a, int32_t s, int32_t & s0, int32_t & n) {
+    s0 = a.uniform_splits > 0 ? s * a.uniform_splits : a.split0[s];
+    n = a.uniform_splits > 0 ? a.uniform_splits : a.split0[s + 1] - s0;
+    if (a.ctx_dev != nullptr) { // a device context: strided splits past its tiles held nothing
+        const int64_t c = a.ctx_dev[s];
+        if (c < a.T_dev || c > a.cap[s]) {
+            return false;
+        }
+        const int64_t tiles = (c + kTileTokens - 1) / kTileTokens;
+        n = tiles < n ? static_cast<int32_t>(tiles) : n;
+    }
+    if (a.depth_dev != nullptr) {
+        const int64_t d = *a.depth_dev;
+        if (d < 0 || d + a.T_dev > a.cap[0]) {
+            return false;
+        }
+    }
+    if (a.sel_n != nullptr) { // a sparse launch: only the splits that hold selected tiles ran
+        const int32_t S = sparse_split_size(a.sel_n[s], n);
+        const int32_t used = (a.sel_n[s] + S - 1) / S;
+        n = used < n ? used : n;
+    }
+    return true;
+}
+
 __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
     __shared__ float sM[4];
     __shared__ float sL[4];
@@ -1055,27 +1082,9 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
     rest /= a.R;
     const int32_t kvh = rest % a.h_kv;
     const int32_t s = rest / a.h_kv;
-    const int32_t s0 = a.uniform_splits > 0 ? s * a.uniform_splits : a.split0[s];
-    int32_t n = a.uniform_splits > 0 ? a.uniform_splits : a.split0[s + 1] - s0;
-    if (a.ctx_dev != nullptr) { // a device context: a refused sequence is left as it was; strided splits past
-                                // its tiles held nothing
-        const int64_t c = a.ctx_dev[s];
-        if (c < a.T_dev || c > a.cap[s]) {
-            return;
-        }
-        const int64_t tiles = (c + kTileTokens - 1) / kTileTokens;
-        n = tiles < n ? static_cast<int32_t>(tiles) : n;
-    }
-    if (a.depth_dev != nullptr) {
-        const int64_t d = *a.depth_dev;
-        if (d < 0 || d + a.T_dev > a.cap[0]) {
-            return;
-        }
-    }
-    if (a.sel_n != nullptr) { // a sparse launch: only the splits that hold selected tiles ran
-        const int32_t S = sparse_split_size(a.sel_n[s], n);
-        const int32_t used = (a.sel_n[s] + S - 1) / S;
-        n = used < n ? used : n;
+    int32_t s0 = 0, n = 0;
+    if (!merge_splits(a, s, s0, n)) {
+        return;
     }
     float m = kNegInf, l = 0.0f;
     floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1277,7 +1286,83 @@ dec_plan plan_decode(const kv_pool & p, int32_t n_seq, const int64_t * ctx, int3
     return pl;
 }
 
+// The plain fp16 output's fold: one workgroup a whole row (256 values), GRP waves = 64 float4 columns x GRP split
+// groups (one a wave: group g folds splits g, g + GRP, ... with a running max, its loads in flight together), then
+// the waves in order in LDS. An eighth of merge_kernel's workgroups: at these sizes a launch's cost is mostly the
+// dispatch of its workgroups.
+template <int GRP> __global__ __launch_bounds__(64 * GRP) void merge_row_kernel(merge_args a) {
+    __shared__ float sM[GRP];
+    __shared__ float sL[GRP];
+    __shared__ floatx4 sA[GRP][64];
+    const int32_t tid = static_cast<int32_t>(threadIdx.x);
+    const int32_t c4 = tid & 63, g = tid >> 6;
+    int32_t rest = static_cast<int32_t>(blockIdx.x);
+    const int32_t r = rest % a.R;
+    rest /= a.R;
+    const int32_t kvh = rest % a.h_kv;
+    const int32_t s = rest / a.h_kv;
+    int32_t s0 = 0, n = 0;
+    if (!merge_splits(a, s, s0, n)) {
+        return;
+    }
+    float m = kNegInf, l = 0.0f;
+    floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+    for (int32_t i = g; i < n; i += GRP) {
+        const int64_t prow = (int64_t(s0 + i) * a.h_kv + kvh) * a.R + r;
+        const float2 ml = *reinterpret_cast<const float2 *>(a.pml + prow * 2);
+        const floatx4 o = *reinterpret_cast<const floatx4 *>(a.po + prow * kHeadDim + c4 * 4);
+        const float m_new = fmaxf(m, ml.x);
+        const float m_use = m_new == kNegInf ? 0.0f : m_new;
+        const float f_old = __builtin_amdgcn_exp2f(m - m_use);
+        const float f_new = __builtin_amdgcn_exp2f(ml.x - m_use);
+        A = A * f_old + o * f_new;
+        l = __builtin_fmaf(l, f_old, ml.y * f_new);
+        m = m_new;
+    }
+    sA[g][c4] = A;
+    if (c4 == 0) {
+        sM[g] = m;
+        sL[g] = l;
+    }
+    __syncthreads();
+    if (g != 0) {
+        return;
+    }
+    float Ms = sM[0], Ls = sL[0];
+    floatx4 As = sA[0][c4];
+#pragma unroll
+    for (int32_t w = 1; w < GRP; ++w) {
+        const float mn = fmaxf(Ms, sM[w]);
+        const float mu = mn == kNegInf ? 0.0f : mn;
+        const float f0 = __builtin_amdgcn_exp2f(Ms - mu), f1 = __builtin_amdgcn_exp2f(sM[w] - mu);
+        As = As * f0 + sA[w][c4] * f1;
+        Ls = __builtin_fmaf(Ls, f0, sL[w] * f1);
+        Ms = mn;
+    }
+    const int32_t t = r / a.G, h = kvh * a.G + r % a.G;
+    const int64_t row = (int64_t(s) * a.T + t) * a.hq + h;
+    const float inv = 1.0f / Ls;
+    uint2 pk;
+    pk.x = uint32_t(__half_as_ushort(__float2half_rn(As[0] * inv))) |
+           (uint32_t(__half_as_ushort(__float2half_rn(As[1] * inv))) << 16);
+    pk.y = uint32_t(__half_as_ushort(__float2half_rn(As[2] * inv))) |
+           (uint32_t(__half_as_ushort(__float2half_rn(As[3] * inv))) << 16);
+    *reinterpret_cast<uint2 *>(a.out + row * kHeadDim + c4 * 4) = pk;
+}
+
 void launch_merge(const merge_args & m, hipStream_t st) {
+    // the plain fp16 output with at most 96 splits a sequence (cfg1's 67; cfg2's 128 fold faster over more threads):
+    // a workgroup a row; otherwise a workgroup a (row, 32 values)
+    int32_t most = m.uniform_splits;
+    for (int32_t i = 0; m.uniform_splits == 0 && i < m.n_seq; ++i) {
+        most = std::max(most, m.split0[i + 1] - m.split0[i]);
+    }
+    if (m.gate == nullptr && most <= 96) {
+        hipLaunchKernelGGL(merge_row_kernel<8>, dim3(static_cast<uint32_t>(m.n_seq * m.h_kv * m.R)), dim3(512), 0, st,
+                           m);
+        return;
+    }
     hipLaunchKernelGGL(merge_kernel, dim3(static_cast<uint32_t>(m.n_seq * m.h_kv * m.R * 8)), dim3(256), 0, st, m);
 }
 
