@@ -15,7 +15,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libfnkv.so")
 HARNESS = os.path.join(HERE, "engine_step")
-SOURCES = ["pool.hip", "append.hip", "decode.hip", "prefill.hip", "sparse.hip", "datc.hip", "qsa.hip", "qsp.hip"]
+SOURCES = ["pool.hip", "append.hip", "decode.hip", "stream.hip", "prefill.hip", "sparse.hip", "datc.hip", "qsa.hip", "qsp.hip"]
 ARCH = os.environ.get("FNKV_ARCH", "gfx950")
 
 COMMON = [
@@ -35,7 +35,7 @@ def hipcc():
 # per-file flags: the quantizer must not fuse x * id into the rounding test (ggml rounds the product first); the
 # attention kernels run two waves a SIMD and keep their matrix-core accumulators in ordinary registers (VGPR form)
 VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
-EXTRA = {"append.hip": ["-ffp-contract=off"], "decode.hip": VGPR_MFMA, "prefill.hip": VGPR_MFMA,
+EXTRA = {"append.hip": ["-ffp-contract=off"], "decode.hip": VGPR_MFMA, "stream.hip": VGPR_MFMA, "prefill.hip": VGPR_MFMA,
          "sparse.hip": ["-ffp-contract=off"], "qsa.hip": ["-ffp-contract=off"], "qsp.hip": ["-ffp-contract=off"]}
 
 

@@ -14,6 +14,9 @@ namespace fnkv {
 void set_error(const std::string & e);
 const char * last_error();
 const kv_pool * pool_of(const fnkv_pool * p);
+// an integer knob from the environment (dflt when unset), for measurement only; callers keep it in a function-local
+// static so it is read once per process
+int32_t env_int_once(const char * name, int32_t dflt);
 // compute units of a device (cached)
 int32_t device_cus(int32_t device);
 // the append's launch (fnkv_q8_append after its checks); pos_dev set: the first position is that device word, and

@@ -1213,6 +1213,11 @@ int32_t decode_lds(int32_t nt, bool sp, bool qlo = false) {
     return qlo ? rows_lds<3, true, true>() : rows_lds<3, true>();
 }
 
+int32_t env_int_once(const char * name, int32_t dflt) {
+    const char * e = std::getenv(name);
+    return e != nullptr ? std::atoi(e) : dflt;
+}
+
 int32_t device_cus(int32_t device) {
     // threads racing on the first query each store the same count
     static std::atomic<int32_t> cache[64];
@@ -1259,27 +1264,27 @@ struct dec_plan {
     int64_t po_bytes = 0, pml_bytes = 0;
 };
 
+// dense launches of at most two row tiles run the stream kernel (stream.hip), the rest decode_kernel<3>
+bool uses_stream(int32_t R) { return R <= 32; }
+
 dec_plan plan_decode(const kv_pool & p, int32_t n_seq, const int64_t * ctx, int32_t R) {
     dec_plan pl;
-    pl.split_tokens = choose_split(n_seq, ctx, p.h_kv(), device_cus(p.device()));
-    // tuning knob: FNKV_SPLIT_TOKENS (a multiple of 32 from 256 to 2,048) overrides the chosen split size
-    if (const char * e = std::getenv("FNKV_SPLIT_TOKENS")) {
-        const int32_t v = std::atoi(e);
-        if (v >= kPageTokens && v <= 8 * kPageTokens && v % kTileTokens == 0) {
-            pl.split_tokens = v;
-        }
+    const int32_t cus = device_cus(p.device());
+    pl.split_tokens =
+        uses_stream(R) ? choose_split_stream(n_seq, ctx, p.h_kv(), cus) : choose_split(n_seq, ctx, p.h_kv(), cus);
+    // tuning knob for measurement: FNKV_SPLIT_TOKENS (a multiple of 32 from 256 to 2,048), read once per process
+    static const int32_t split_knob = env_int_once("FNKV_SPLIT_TOKENS", 0);
+    if (split_knob >= kPageTokens && split_knob <= 8 * kPageTokens && split_knob % kTileTokens == 0) {
+        pl.split_tokens = split_knob;
     }
     pl.split0[0] = 0;
     for (int32_t i = 0; i < n_seq; ++i) {
         pl.split0[i + 1] = pl.split0[i] + static_cast<int32_t>((ctx[i] + pl.split_tokens - 1) / pl.split_tokens);
     }
     // one row tile (R <= 16): the splits of a sequence stride over its tiles, so at any moment the workgroups read
-    // one window of the sequence together (cfg2 T = 1: 56.5 against 57.7 us); the row kernels keep contiguous splits
-    // (T = 3 unchanged, T = 5 5% slower strided). FNKV_STRIDED=0 / 1 overrides, for measurement.
+    // one window of the sequence together, and host and device contexts split alike (device contexts always stride:
+    // decode_launch); more rows: contiguous splits
     pl.strided = R <= 16 ? 1 : 0;
-    if (const char * e = std::getenv("FNKV_STRIDED")) {
-        pl.strided = std::atoi(e) != 0;
-    }
     pl.total = pl.split0[n_seq];
     pl.po_bytes = int64_t(pl.total) * p.h_kv() * R * kHeadDim * 4;
     pl.pml_bytes = int64_t(pl.total) * p.h_kv() * R * 2 * 4;
@@ -1534,7 +1539,11 @@ int decode_launch(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, 
     a.ts = g_timing;
 #endif
     const dim3 grid(static_cast<uint32_t>(pl.total), static_cast<uint32_t>(p->h_kv()));
-    launch_decode<false>(*p, (R + 15) / 16, grid, a, st);
+    if (uses_stream(R)) {
+        launch_stream(p->device(), (R + 15) / 16, grid, a, st);
+    } else {
+        launch_decode<false>(*p, (R + 15) / 16, grid, a, st);
+    }
     merge_args m;
     m.po = a.po;
     m.pml = a.pml;

@@ -149,8 +149,8 @@ int qsa_launch(const fnkv_pool * pool, int32_t slot, int64_t depth, int32_t T, i
     }
     // at most 16 query heads a KV head: the sparse launch prepares its rows itself (one launch fewer);
     // FNKV_QSA_TWO_KERNELS=1 keeps the separate prepare launch, for comparison
-    const char * two = std::getenv("FNKV_QSA_TWO_KERNELS");
-    if (G <= 16 && (two == nullptr || std::atoi(two) == 0)) {
+    static const int32_t two = env_int_once("FNKV_QSA_TWO_KERNELS", 0);
+    if (G <= 16 && two == 0) {
         fused_prep fp;
         fp.qfull = qfull;
         fp.kv_k = kv_k;

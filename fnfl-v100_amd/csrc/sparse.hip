@@ -46,8 +46,9 @@ sparse_plan plan_sparse(const kv_pool & p, int64_t depth, int32_t T, int32_t G) 
     const int32_t n_tiles = static_cast<int32_t>((depth + T + kTileTokens - 1) / kTileTokens);
     pl.n_max = std::min(n_tiles, kSelTopBlocks + 1); // a row's blocks' tiles and its tail's
     int32_t want = std::max(1, device_cus(p.device()) / (p.h_kv() * T));
-    if (const char * e = std::getenv("FNKV_SPARSE_WANT")) { // splits a row and head, for measurement
-        want = std::max(1, std::atoi(e));
+    static const int32_t want_knob = env_int_once("FNKV_SPARSE_WANT", 0); // splits a row and head, for measurement
+    if (want_knob > 0) {
+        want = want_knob;
     }
     pl.per_split = std::min(64, std::max(1, (pl.n_max + want - 1) / want));
     pl.n_splits = (pl.n_max + pl.per_split - 1) / pl.per_split;

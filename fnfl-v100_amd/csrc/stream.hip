@@ -1,0 +1,485 @@
+// Dense decode / speculative-verify attention over the page pool, one tile stream a wave (the launches with host or
+// device contexts: fnkv_attn_decode, fnkv_attn_decode_dev, fnkv_attn_decode_noalloc; fnkv_attend's dense calls).
+//
+// What it computes is decode.hip's: for query row (t, head h) of a sequence holding ctx cells,
+//   o = sum_c softmax_c(q . k_c * scale) v_c over cells c <= ctx - T + t,
+// with the decoded Q8_0 (or KV8) cells, fp32 scores, softmax statistics and accumulators, and the split-K partials
+// (m, l, acc) folded by the merge as the reference's finish does (fn/kernels/qsa/attend.cu:621-655).
+//
+// How (MI355X): a workgroup of 8 waves (two a SIMD) owns one (sequence, KV head, split of the cells); wave w walks
+// the split's tiles w, w + 8, ... on its own, and computes every query row of the KV head (NT row tiles of 16:
+// G T <= 16 NT) itself, so the loop has no workgroup barrier and no exchange of P, and a SIMD's two waves co-issue
+// one's VALU work with the other's MFMAs:
+//   * a tile goes straight from HBM into the wave's LDS slot (its layout is the tile's): the K half (K codes and K
+//     scales) as soon as the scores have read the previous tile's, the V half (V codes and V scales) as soon as PV
+//     has, so each half's latency hides under the other half's work;
+//   * the K codes are widened once a tile (one byte permute makes two codes the fp16 values 1152 + code) and feed the
+//     S^T = K Q^T MFMA of every row tile (the Q operands sit once in LDS for the workgroup); each block's K scale is
+//     one FMA a score; one MFMA a half takes the 1152 bias back out against the rows' q sums;
+//   * online softmax in base 2 on the S^T registers, which are already the B operand of O^T = V^T P^T; P times the
+//     block's V scale enters the matrix core as fp16 hi + lo (~2^-20 relative); the accumulators O^T (NT x 64
+//     registers) stay in VGPRs (NT <= 2 within a wave's 256);
+//   * one MFMA pair a tile against the V scales (and a row of ones) gives each row's V bias sums and its l;
+//   * after the loop the eight waves fold their (m, l, acc) per row in LDS and the workgroup writes the partial.
+#include "../../include/fnkv.h"
+#include "common.h"
+#include "decode_common.h"
+#include "layout.h"
+#include "mfma.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cstdint>
+#include <mutex>
+
+namespace fnkv {
+
+template <int NT> struct stream_shape {
+    static_assert(NT == 1 || NT == 2, "the accumulators of at most two row tiles fit a wave's registers");
+    static constexpr int WAVES = 8;
+    static constexpr int SLOT = kTileBytes;          // a tile, in its HBM layout
+    static constexpr int RING = WAVES * SLOT;        // 139,264 B
+    static constexpr int QOPS = NT * kBlocks * 1024; // the Q operands: [row tile][block][lane] 16 B
+    static constexpr int OSTRIDE = kHeadDim + 4;     // floats a row of the fold buffer
+    static constexpr int FOLD = WAVES * 16 * OSTRIDE * 4 + WAVES * NT * 16 * 2 * 4;
+    static constexpr int LDS = RING + QOPS > FOLD ? RING + QOPS : FOLD;
+    static_assert(LDS <= 160 * 1024, "LDS");
+    // a half tile is 9 loads: 8 chunks of codes and half of the scales chunk; the wave waits for one half with the
+    // other half's 9 issued after it
+    static constexpr int HALF_LOADS = 9;
+};
+
+// S^T = K Q^T of one tile for NT row tiles from the K codes (kb) and the scales chunk (sc) in LDS: sc_out[rt][h][r]
+// is the score (q . k, unscaled) of token 16 h + 4 qg + r against row 16 rt + j. Each 1 KiB chunk of K codes is
+// widened once and feeds the MFMAs of every row tile.
+template <int NT>
+__device__ __forceinline__ void stream_scores(const uint8_t * kb, const uint8_t * sc, const uint8_t * qs,
+                                              const half8 (&sig)[NT], int32_t j, int32_t qg, int32_t lane,
+                                              floatx4 (&s_out)[NT][2]) {
+    const half8 zero8 = {};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        half8 ks[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            ks[r] = *reinterpret_cast<const half8 *>(sc + (16 * h + 4 * qg + r) * 16);
+        }
+        // the bias term: A = the token row's K scales (lanes qg < 2), B = the row's per-block q sums (hi, lo)
+        const half8 srow = qg < 2 ? *reinterpret_cast<const half8 *>(sc + (16 * h + j) * 16) : zero8;
+        // the scores start from the bias term (-1152 times it) and take each block's term with one FMA a score
+        floatx4 acc_s[NT];
+#pragma unroll
+        for (int rt = 0; rt < NT; ++rt) {
+            acc_s[rt] = mfma16(srow, sig[rt], floatx4{0.0f, 0.0f, 0.0f, 0.0f}) * -1152.0f;
+        }
+#pragma unroll
+        for (int ld = 0; ld < 4; ++ld) { // one 1 KiB chunk: blocks 2 ld, 2 ld + 1
+            const u32x4 kw = *reinterpret_cast<const u32x4 *>(kb + h * 4096 + ld * 1024 + lane * 16);
+            floatx4 t[NT][2];
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) {
+                const int b = 2 * ld + bb;
+                const half8 ka = widen8<false>(kw[2 * bb], kw[2 * bb + 1]);
+#pragma unroll
+                for (int rt = 0; rt < NT; ++rt) {
+                    const half8 qo = *reinterpret_cast<const half8 *>(qs + (rt * kBlocks + b) * 1024 + lane * 16);
+                    t[rt][bb] = mfma16(ka, qo, floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+                }
+            }
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) {
+#pragma unroll
+                for (int rt = 0; rt < NT; ++rt) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        acc_s[rt][r] =
+                            __builtin_fmaf(static_cast<float>(ks[r][2 * ld + bb]), t[rt][bb][r], acc_s[rt][r]);
+                    }
+                }
+            }
+            // pin the chunk's FMAs here (the optimizer would otherwise sink them past the later chunks' MFMAs and
+            // keep every chunk's results live at once)
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt) {
+                __asm__ volatile("" : "+v"(acc_s[rt]));
+            }
+            __builtin_amdgcn_sched_barrier(0); // one chunk's operands live at a time
+        }
+#pragma unroll
+        for (int rt = 0; rt < NT; ++rt) {
+            s_out[rt][h] = acc_s[rt];
+        }
+    }
+}
+
+// Online softmax (base 2) of one row tile's tile scores, tokens past lim_rel masked: the row's reference max moves
+// only when the tile's max exceeds it by more than kLazyLog2 (then alpha = 2^(m_old - m_new), else 1), so a weight
+// stays <= 64 and a weight times a V scale stays inside fp16. l is not kept here: the PV step's MFMA against a row
+// of ones sums the weights.
+__device__ __forceinline__ void stream_softmax(const floatx4 (&sc)[2], int32_t lim_rel, float c2, int32_t qg,
+                                               float & m_run, float (&pf)[8], float & alpha) {
+    float raw[8];
+    float mx = kNegInf;
+    if (__all(lim_rel >= 31)) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                raw[4 * h + r] = sc[h][r];
+                mx = fmaxf(mx, raw[4 * h + r]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float x = 16 * h + 4 * qg + r <= lim_rel ? sc[h][r] : kNegInf;
+                raw[4 * h + r] = x;
+                mx = fmaxf(mx, x);
+            }
+        }
+    }
+    mx = rows_max(mx) * c2;
+    const bool move = mx > m_run + kLazyLog2; // m_run = -inf: any visible score moves it
+    const float m_new = move ? mx : m_run;
+    const float m_use = m_new == kNegInf ? 0.0f : m_new;
+    alpha = move ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        pf[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(raw[i], c2, -m_use));
+    }
+    m_run = m_new;
+}
+
+template <int NT>
+__global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
+    using SH = stream_shape<NT>;
+    constexpr int WAVES = SH::WAVES;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(threadIdx.x) >> 6);
+    const int32_t j = lane & 15, qg = lane >> 4;
+    const int32_t split = static_cast<int32_t>(blockIdx.x);
+    const int32_t kvh = static_cast<int32_t>(blockIdx.y);
+    const int32_t s = seq_of(a, split);
+    const int32_t sp = split - a.split0[s];
+    const int64_t ctx = seq_ctx<false>(a, s);
+    const int64_t begin = int64_t(sp) * a.split_tokens;
+    const int64_t end = ctx < begin + a.split_tokens ? ctx : begin + a.split_tokens;
+    const pool_view & pv = a.pv;
+    const int32_t * table = pv.table + int64_t(a.slot[s]) * pv.table_stride;
+
+    // The Q operands of every row tile go into LDS once (the workgroup's waves share them: wave w loads operands w,
+    // w + 8, ...); their loads are issued first, beside the page-table read
+    uint8_t * const qs = smem + SH::RING;
+    constexpr int PER = NT * kBlocks / WAVES;
+    u32x4 qv[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int32_t c = wave + e * WAVES, rt = c / kBlocks, b = c % kBlocks;
+        const int32_t row = rt * 16 + j;
+        qv[e] = u32x4{0, 0, 0, 0};
+        if (row < a.R) {
+            const int32_t t_row = row / a.G;
+            qv[e] = *reinterpret_cast<const u32x4 *>(
+                a.q + ((int64_t(s) * a.T + t_row) * a.hq + int64_t(kvh) * a.G + row % a.G) * kHeadDim + b * kQK +
+                8 * qg);
+        }
+    }
+    split_src<false> src;
+    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, nullptr, ctx);
+    if (refused<false>(a, s, ctx, sp, kvh)) {
+        return;
+    }
+    // uniform in the workgroup; readfirstlane keeps the walk's arithmetic and the loop control scalar
+    const int32_t n_tiles = __builtin_amdgcn_readfirstlane(src.n_tiles);
+    FNKV_STAMP(0);
+    // the step's new cells are written by the workgroup whose walk holds their tile (append_new_cells); only such a
+    // workgroup waits for its stores before its loads
+    if (a.k_new != nullptr) {
+        bool owns = false;
+        for (int32_t t = 0; t < a.T; ++t) {
+            const int64_t pos = ctx - a.T + t;
+            owns |= a.strided ? static_cast<int32_t>((pos >> 5) % src.stride) == src.g0 : (pos >= begin && pos < end);
+        }
+        if (owns) {
+            append_new_cells<WAVES>(a, table, s, kvh, ctx, begin, end, src.g0, a.strided ? src.stride : 0, wave,
+                                    lane);
+        }
+    }
+
+    // this wave's tiles: walk tiles wave, wave + 8, ...
+    const int32_t n_w = __builtin_amdgcn_readfirstlane(n_tiles > wave ? (n_tiles - wave + WAVES - 1) / WAVES : 0);
+    const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
+    uint8_t * const slot = smem + wave * SH::SLOT;
+    const int32_t lane16 = lane * 16;
+    // iteration i's tile; past the wave's last tile a placeholder (the first tile, every lane reading its first
+    // 16 bytes of each chunk), so every iteration issues the same loads and the waits are fixed counts
+    auto tile_at = [&](int32_t i) -> const uint8_t * {
+        const int32_t ti = i < n_w ? wave + i * WAVES : 0;
+        return layer_base + src.tile_off(pv, n_tiles > 0 ? ti : 0);
+    };
+    // half V = 0: the K codes (chunks 0-7) and the K scales (the scales chunk's lanes 0-31); V = 1: the V codes
+    // (chunks 8-15) and the V scales (its lanes 32-63)
+    auto issue_half = [&](int32_t i, int32_t V) {
+        const rsrc_t r = make_rsrc(tile_at(i), kTileBytes);
+        const int32_t voff = i < n_w ? lane16 : 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            buf_lds16(r, slot + (8 * V + c) * 1024, voff, (8 * V + c) * 1024);
+        }
+        if ((lane >> 5) == V) {
+            buf_lds16(r, slot + kKScales, voff, kKScales);
+        }
+        keep_issued();
+    };
+
+    if (n_w > 0) {
+        issue_half(0, 0);
+        issue_half(0, 1);
+    }
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        *reinterpret_cast<u32x4 *>(qs + (wave + e * WAVES) * 1024 + lane * 16) = qv[e];
+    }
+    barrier_keep_loads(); // the Q operands are in LDS (the tile loads stay in flight)
+    FNKV_STAMP(1);
+    // each lane's bias operands (the rows' per-block q sums) and each row's last visible cell
+    half8 sig[NT];
+    int64_t lim[NT];
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt) {
+        half8 qop[kBlocks];
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) {
+            qop[b] = *reinterpret_cast<const half8 *>(qs + (rt * kBlocks + b) * 1024 + lane * 16);
+        }
+        sig[rt] = q_sums(qop, qg);
+        lim[rt] = ctx - a.T + t_of_row(a, rt, j);
+    }
+    floatx4 acc[NT][kBlocks][2];
+    floatx4 lv[NT]; // lane (row j, qg): rows 4 qg + e of sum_t P s_v[t][b] (b < 8) and sum_t P (row 8)
+    float m_run[NT];
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt) {
+        lv[rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        m_run[rt] = kNegInf;
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) {
+            acc[rt][b][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            acc[rt][b][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    const half8 zero8 = {};
+    const _Float16 one = static_cast<_Float16>(1.0f);
+    const half8 ones8 = {one, one, one, one, one, one, one, one};
+
+    // Iteration i: wait for K(i), scores, issue K(i + 1), softmax, wait for V(i), PV, issue V(i + 1).
+    FNKV_PHASE_DECL();
+    for (int32_t i = 0; i < n_w; ++i) {
+        FNKV_PHASE(0 + (i > 0 ? 7 : 0));
+        wait_vmcnt<SH::HALF_LOADS>(); // K(i) has landed (V(i) may be pending)
+        FNKV_PHASE(1);
+        // the scores and the softmax are the longer dependent chain: their wave issues first on a shared SIMD, so
+        // the two waves of a SIMD alternate phases rather than one running ahead
+        __builtin_amdgcn_s_setprio(1);
+        const uint8_t * kb = slot;
+        const uint8_t * sc = kb + kKScales;
+        floatx4 scv[NT][2];
+        stream_scores<NT>(kb, sc, qs, sig, j, qg, lane, scv);
+        issue_half(i + 1, 0); // the scores' reads of K(i) are done (their values are in registers)
+        FNKV_PHASE(2);
+        const int64_t tok0 = src.tok0(wave + i * WAVES);
+        half8 ph[NT], pl[NT];
+#pragma unroll
+        for (int rt = 0; rt < NT; ++rt) {
+            const int64_t lr = lim[rt] - tok0;
+            const int32_t lim_rel = lr > 64 ? 64 : static_cast<int32_t>(lr < -1 ? -1 : lr);
+            float pf[8];
+            float alpha;
+            stream_softmax(scv[rt], lim_rel, a.c2, qg, m_run[rt], pf, alpha);
+            if (__any(alpha != 1.0f)) {
+#pragma unroll
+                for (int b = 0; b < kBlocks; ++b) {
+                    acc[rt][b][0] *= alpha;
+                    acc[rt][b][1] *= alpha;
+                }
+                lv[rt] *= alpha;
+            }
+            split_hilo(pf, ph[rt], pl[rt]);
+        }
+        FNKV_PHASE(3);
+        __builtin_amdgcn_s_setprio(0);
+        wait_vmcnt<SH::HALF_LOADS>(); // V(i) has landed (K(i + 1) may be pending)
+        FNKV_PHASE(4);
+        // A of the bias MFMAs: lane (block j < 8, qg) holds s_v[token(qg, slot)][j], lanes j = 8 ones (l)
+        const half8 sva = j < 8 ? *reinterpret_cast<const half8 *>(sc + 512 + qg * 128 + j * 16) : j == 8 ? ones8 : zero8;
+#pragma unroll
+        for (int rt = 0; rt < NT; ++rt) {
+            lv[rt] = mfma16(sva, ph[rt], lv[rt]);
+            lv[rt] = mfma16(sva, pl[rt], lv[rt]);
+        }
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) {
+            const u32x4 vw = *reinterpret_cast<const u32x4 *>(kb + kVCodes + b * 1024 + lane * 16);
+            const half8 va0 = widen8<false>(vw[0], vw[1]);
+            const half8 va1 = widen8<false>(vw[2], vw[3]);
+            const half8 vs = *reinterpret_cast<const half8 *>(sc + 512 + qg * 128 + b * 16);
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt) {
+                half8 hi, lo;
+                scale_hilo_pk(ph[rt], pl[rt], vs, hi, lo);
+                acc[rt][b][0] = mfma16(va0, hi, acc[rt][b][0]);
+                acc[rt][b][1] = mfma16(va1, hi, acc[rt][b][1]);
+                acc[rt][b][0] = mfma16(va0, lo, acc[rt][b][0]);
+                acc[rt][b][1] = mfma16(va1, lo, acc[rt][b][1]);
+            }
+            __builtin_amdgcn_sched_barrier(0); // one block's operands live at a time
+        }
+        issue_half(i + 1, 1);
+        FNKV_PHASE(5);
+    }
+    FNKV_PHASE_STORE();
+    wait_vmcnt<0>();
+    FNKV_STAMP_WAVE();
+
+    // the V bias: acc[rt][b] carries 1152 lv[rt][b]; lv[rt][b] of this lane's row sits in lane (j, b / 4), element
+    // b % 4; the row's l in lane (j, 2), element 0
+    float l_row[NT];
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt) {
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) {
+            const float lb = __shfl(lv[rt][b & 3], j + 16 * (b >> 2));
+            acc[rt][b][0] -= 1152.0f * lb;
+            acc[rt][b][1] -= 1152.0f * lb;
+        }
+        l_row[rt] = __shfl(lv[rt][0], j + 32);
+    }
+
+    // ---- fold the four waves per row in LDS (fixed order), write the workgroup's partial ----
+    constexpr int32_t OS = SH::OSTRIDE;
+    __syncthreads(); // the rings are no longer read
+    FNKV_STAMP(2);
+    float * ml = reinterpret_cast<float *>(smem);                               // [wave][NT 16 rows][2]
+    float * ob = reinterpret_cast<float *>(smem + WAVES * NT * 16 * 2 * 4);      // [wave][16 rows][OS]
+    if (qg == 0) {
+#pragma unroll
+        for (int rt = 0; rt < NT; ++rt) {
+            ml[(wave * NT * 16 + rt * 16 + j) * 2 + 0] = m_run[rt];
+            ml[(wave * NT * 16 + rt * 16 + j) * 2 + 1] = l_row[rt];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt) {
+        float M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            M = fmaxf(M, ml[(w * NT * 16 + rt * 16 + j) * 2]);
+        }
+        const float f = __builtin_amdgcn_exp2f(m_run[rt] - (M == kNegInf ? 0.0f : M));
+        if (rt * 16 + j < a.R) { // padding rows are not folded
+#pragma unroll
+            for (int b = 0; b < kBlocks; ++b) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    *reinterpret_cast<floatx4 *>(ob + (wave * 16 + j) * OS + 16 * (2 * b + hh) + 4 * qg) =
+                        acc[rt][b][hh] * f;
+                }
+            }
+        }
+        __syncthreads();
+        // thread -> (row, 8 values): 16 rows x 32 groups
+        {
+            const int32_t t = static_cast<int32_t>(threadIdx.x);
+            const int32_t rrow = t >> 5, c0 = (t & 31) * 8;
+            const int32_t r = rt * 16 + rrow;
+            if (r < a.R) {
+                const int64_t prow = (int64_t(split) * pv.h_kv + kvh) * a.R + r;
+                float * dst = a.po + prow * kHeadDim + c0;
+#pragma unroll
+                for (int c = 0; c < 8; c += 4) {
+                    floatx4 sum = *reinterpret_cast<const floatx4 *>(ob + rrow * OS + c0 + c);
+#pragma unroll
+                    for (int w = 1; w < WAVES; ++w) {
+                        sum += *reinterpret_cast<const floatx4 *>(ob + (w * 16 + rrow) * OS + c0 + c);
+                    }
+                    *reinterpret_cast<floatx4 *>(dst + c) = sum;
+                }
+                if ((t & 31) == 0) {
+                    float Mr = kNegInf;
+#pragma unroll
+                    for (int w = 0; w < WAVES; ++w) {
+                        Mr = fmaxf(Mr, ml[(w * NT * 16 + r) * 2]);
+                    }
+                    const float Mr_use = Mr == kNegInf ? 0.0f : Mr;
+                    float L = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < WAVES; ++w) {
+                        L += ml[(w * NT * 16 + r) * 2 + 1] * __builtin_amdgcn_exp2f(ml[(w * NT * 16 + r) * 2] - Mr_use);
+                    }
+                    a.pml[prow * 2 + 0] = Mr;
+                    a.pml[prow * 2 + 1] = L;
+                }
+            }
+        }
+        __syncthreads(); // ob is rewritten by the next row tile
+    }
+    FNKV_STAMP(4);
+}
+
+// The split size (cells) for these contexts: the fewest rounds of one workgroup a CU times a workgroup's time, which
+// is its waves' longest walk (an eighth of the split's tiles, rounded up) plus a fixed cost (the ramp, the fold of the
+// waves and the partial's write, counted as three tiles); larger splits (fewer partials) win ties.
+int32_t choose_split_stream(int32_t n_seq, const int64_t * ctx, int32_t h_kv, int32_t cus) {
+    int32_t best = kPageTokens;
+    int64_t best_cost = INT64_MAX;
+    for (int32_t st = kPageTokens; st <= 8 * kPageTokens; st += kTileTokens) {
+        int64_t wgs = 0;
+        for (int32_t i = 0; i < n_seq; ++i) {
+            wgs += (ctx[i] + st - 1) / st;
+        }
+        wgs *= h_kv;
+        const int64_t rounds = (wgs + cus - 1) / cus;
+        const int64_t wave_tiles = (st / kTileTokens + stream_shape<1>::WAVES - 1) / stream_shape<1>::WAVES;
+        const int64_t cost = rounds * (wave_tiles + 3);
+        if (cost <= best_cost) {
+            best_cost = cost;
+            best = st;
+        }
+    }
+    return best;
+}
+
+template <int NT> void set_stream_attr() {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(stream_kernel<NT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, stream_shape<NT>::LDS);
+}
+
+// the dense launch's kernel for NT row tiles (1 or 2), its LDS attribute set once per device
+void launch_stream(int32_t device, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
+    static std::once_flag attr_once[64];
+    if (device >= 0 && device < 64) {
+        std::call_once(attr_once[device], [device]() {
+            int32_t cur = 0;
+            (void)hipGetDevice(&cur);
+            (void)hipSetDevice(device);
+            set_stream_attr<1>();
+            set_stream_attr<2>();
+            (void)hipGetLastError();
+            (void)hipSetDevice(cur);
+        });
+    }
+    const dim3 block(64 * stream_shape<1>::WAVES);
+    if (NT == 1) {
+        hipLaunchKernelGGL(stream_kernel<1>, grid, block, stream_shape<1>::LDS, st, a);
+    } else {
+        hipLaunchKernelGGL(stream_kernel<2>, grid, block, stream_shape<2>::LDS, st, a);
+    }
+}
+
+} // namespace fnkv

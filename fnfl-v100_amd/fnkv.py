@@ -8,7 +8,8 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libfnkv.so")
+# FNKV_LIB_PATH: another build of the library (for side-by-side measurement)
+LIB_PATH = os.environ.get("FNKV_LIB_PATH", os.path.join(HERE, "libfnkv.so"))
 
 OK, ERR_ARG, ERR_CAPACITY, ERR_HIP = 0, 1, 2, 3
 F16, F32 = 0, 1
