@@ -842,7 +842,7 @@ def run_mixed(args, cfg):
     vn = torch.randn((layers, nv, T, HKV, D), generator=g, device="cuda").half()
     outv = torch.empty_like(qv)
     ctxs = [ctx_of[s] for s in vf_slots]
-    wsv = torch.empty(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    wsv = torch.zeros(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
 
     def prefill_half(layer):
         for s in pf_slots:
@@ -1118,7 +1118,7 @@ def time_decode(args, torch, fnkv, cases, ctxs, T, layers, copies, fmt, steps, w
     kn = torch.randn((layers * copies, n, T, HKV, D), generator=g, device="cuda").half()
     vn = torch.randn((layers * copies, n, T, HKV, D), generator=g, device="cuda").half()
     out = torch.empty_like(q)
-    ws = torch.empty(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
 
     def step():
         for layer in range(layers * copies):

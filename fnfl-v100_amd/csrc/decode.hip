@@ -1213,6 +1213,22 @@ int32_t decode_lds(int32_t nt, bool sp, bool qlo = false) {
     return qlo ? rows_lds<3, true, true>() : rows_lds<3, true>();
 }
 
+// The split-K fold inside the dense launch (stream.hip) is off by default: measured against the merge kernel on one
+// box it is slower (cfg1 43.8-44.2 against 42.0-43.0 us a launch, cfg2 58.9 against 55.0-55.6 us). FNKV_DECODE_FOLD=1
+// (read once) or fnkv_test_decode_fold turns it on. The bound of its waits (real-time ticks of 10 ns) is 200 us, far
+// past any launch's spread of arrivals; tests lower it to drive the given-up-row path from the host.
+std::atomic<int32_t> g_fold_mode{-1}; // -1: the environment's choice
+std::atomic<int64_t> g_fold_spin{20000};
+bool fold_enabled() {
+    const int32_t m = g_fold_mode.load(std::memory_order_relaxed);
+    if (m >= 0) {
+        return m != 0;
+    }
+    static const int32_t knob = env_int_once("FNKV_DECODE_FOLD", 0);
+    return knob != 0;
+}
+int64_t fold_spin_ticks() { return g_fold_spin.load(std::memory_order_relaxed); }
+
 int32_t env_int_once(const char * name, int32_t dflt) {
     const char * e = std::getenv(name);
     return e != nullptr ? std::atoi(e) : dflt;
@@ -1261,7 +1277,10 @@ int32_t choose_split(int32_t n_seq, const int64_t * ctx, int32_t h_kv, int32_t c
 struct dec_plan {
     int32_t split_tokens = 0, total = 0, strided = 0;
     int32_t split0[FNKV_MAX_SEQS + 1] = {0};
-    int64_t po_bytes = 0, pml_bytes = 0;
+    // the workspace: the fold state (first, at a fixed place: its words persist from launch to launch, zero), then
+    // the partials
+    int64_t fold_bytes = 0, po_bytes = 0, pml_bytes = 0;
+    bool fold = false; // the stream kernel folds the splits itself (no merge launch)
 };
 
 // dense launches of at most two row tiles run the stream kernel (stream.hip), the rest decode_kernel<3>
@@ -1286,8 +1305,12 @@ dec_plan plan_decode(const kv_pool & p, int32_t n_seq, const int64_t * ctx, int3
     // decode_launch); more rows: contiguous splits
     pl.strided = R <= 16 ? 1 : 0;
     pl.total = pl.split0[n_seq];
+    pl.fold_bytes = (int64_t(FNKV_MAX_SEQS) * p.h_kv() * kFoldWords * 4 + 255) & ~int64_t(255);
     pl.po_bytes = int64_t(pl.total) * p.h_kv() * R * kHeadDim * 4;
     pl.pml_bytes = int64_t(pl.total) * p.h_kv() * R * 2 * 4;
+    // the fold waits for the other splits of its pair, so every workgroup of the launch must be resident at once:
+    // one a CU (the stream kernel's LDS)
+    pl.fold = fold_enabled() && uses_stream(R) && int64_t(pl.total) * p.h_kv() <= cus;
     return pl;
 }
 
@@ -1502,7 +1525,7 @@ int decode_launch(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, 
         }
     }
     const dec_plan pl = plan_decode(*p, n_seq, ctx, R);
-    if (ws_bytes < pl.po_bytes + pl.pml_bytes) {
+    if (ws_bytes < pl.fold_bytes + pl.po_bytes + pl.pml_bytes) {
         set_error(name + ": workspace too small");
         return FNKV_ERR_ARG;
     }
@@ -1512,8 +1535,13 @@ int decode_launch(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, 
     a.k_new = k_new;
     a.v_new = v_new;
     a.new_f32 = new_dtype == FNKV_F32 ? 1 : 0;
-    a.po = static_cast<float *>(ws);
-    a.pml = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + pl.po_bytes);
+    a.po = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + pl.fold_bytes);
+    a.pml = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + pl.fold_bytes + pl.po_bytes);
+    if (pl.fold) {
+        a.fold = static_cast<uint32_t *>(ws);
+        a.out = static_cast<uint16_t *>(out);
+        a.fold_spin = fold_spin_ticks();
+    }
     a.c2 = scale * 1.4426950408889634f;
     a.layer = layer;
     a.T = T;
@@ -1543,6 +1571,13 @@ int decode_launch(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, 
         launch_stream(p->device(), (R + 15) / 16, grid, a, st);
     } else {
         launch_decode<false>(*p, (R + 15) / 16, grid, a, st);
+    }
+    if (pl.fold) {
+        if (hipGetLastError() != hipSuccess) {
+            set_error(name + ": launch failed");
+            return FNKV_ERR_HIP;
+        }
+        return FNKV_OK;
     }
     merge_args m;
     m.po = a.po;
@@ -1622,7 +1657,12 @@ int64_t fnkv_decode_workspace_bytes(const fnkv_pool * pool, int32_t n_seq, const
     }
     const int32_t R = (hq / p->h_kv()) * T;
     const fnkv::dec_plan pl = fnkv::plan_decode(*p, n_seq, ctx, R);
-    return pl.po_bytes + pl.pml_bytes + 256;
+    return pl.fold_bytes + pl.po_bytes + pl.pml_bytes + 256;
+}
+
+void fnkv_test_decode_fold(int32_t mode, int64_t spin_ticks) {
+    fnkv::g_fold_mode.store(mode < 0 ? -1 : (mode != 0 ? 1 : 0), std::memory_order_relaxed);
+    fnkv::g_fold_spin.store(spin_ticks < 0 ? 20000 : spin_ticks, std::memory_order_relaxed);
 }
 
 int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx, int32_t T,

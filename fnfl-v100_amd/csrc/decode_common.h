@@ -75,10 +75,21 @@ struct dec_args {
     // take q as hi + lo (about 22 significant bits). With fp.qfull set the launch forms both itself and only the
     // pointer's presence is read.
     const uint16_t * q_lo = nullptr;
+    // the split-K fold inside the launch (stream kernel, grid resident at once): fold state words (kFoldWords a
+    // (sequence, KV head); zeroed before a workspace's first launch, each launch leaves them ready for the next), the
+    // fp16 output, and the bound of every wait
+    // (real-time ticks, 100 MHz). Null: the splits' partials go to the merge kernel.
+    uint32_t * fold = nullptr;
+    uint16_t * out = nullptr;
+    int64_t fold_spin = 0;
 #ifdef FNKV_TIMING
     uint64_t * ts; // per workgroup: 16 real-time stamps (instrumented builds only)
 #endif
 };
+// fold state of a (sequence, KV head): the arrival counter, a spare word, and a state word per row; a launch adds
+// kFoldEpoch to the counter in all (more than any pair's splits)
+constexpr int32_t kFoldWords = 2 + FNKV_MAX_ROWS;
+constexpr uint32_t kFoldEpoch = 1024;
 
 #ifdef FNKV_TIMING
 #define FNKV_STAMP(k)                                                                                                \

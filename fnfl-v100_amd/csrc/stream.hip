@@ -154,6 +154,233 @@ __device__ __forceinline__ void stream_softmax(const floatx4 (&sc)[2], int32_t l
     m_run = m_new;
 }
 
+// ---- the split-K fold inside the launch ----
+//
+// With a.fold set (the launch's grid fits the device at once), the splits of a (sequence, KV head) fold among
+// themselves, as the reference's finish does after its grid barrier (fn/kernels/qsa/attend.cu:621-655): each split
+// writes its partial (m, l, acc) with device-scope stores, waits for them, and adds one to the pair's arrival counter;
+// row r is then folded by the pair's split r mod n (its owner), which polls the counter until all n splits have
+// arrived (M = max m_j, L = sum l_j 2^(m_j - M), o = sum acc_j 2^(m_j - M) / L, in a fixed order) and writes the
+// fp16 output. Every wait is bounded by a.fold_spin (real-time ticks): an owner that times out marks its rows given
+// up, and the last split to arrive (which never waits for arrivals) folds them. The counter is never reset: the last
+// split rounds it up to the next multiple of kFoldEpoch, so a launch's arrivals start at a multiple of it (the
+// workspace's fold region starts zeroed, as the reference's counter: attend.h:89-93) and the quotient numbers the
+// launch; a row's state word holds that number (above two bits: 1 taken by its owner, 2 given up).
+// Fold-state words of a (sequence, KV head): [0] arrivals, [1] unused, [2 + r] row r's state.
+
+__device__ __forceinline__ void store_agent(float * p, floatx4 v) {
+    uint64_t * q = reinterpret_cast<uint64_t *>(p);
+    __hip_atomic_store(q, __builtin_bit_cast(uint64_t, float2{v[0], v[1]}), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 1, __builtin_bit_cast(uint64_t, float2{v[2], v[3]}), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent2(float * p, float x, float y) {
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(p), __builtin_bit_cast(uint64_t, float2{x, y}), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_agent2(const float * p) {
+    return __builtin_bit_cast(float2, __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ uint32_t load_agent(const uint32_t * p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 8 output values of row r (values c0 .. c0 + 7) as fp16, scaled by inv
+__device__ __forceinline__ void store_out8(const dec_args & a, int32_t s, int32_t kvh, int32_t r, int32_t c0,
+                                           const floatx4 (&v)[2], float inv) {
+    const int32_t t = r / a.G, h = kvh * a.G + r % a.G;
+    uint16_t * dst = a.out + ((int64_t(s) * a.T + t) * a.hq + h) * kHeadDim + c0;
+    u32x4 pk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float x0 = v[i >> 1][(2 * i) & 3] * inv, x1 = v[i >> 1][(2 * i + 1) & 3] * inv;
+        pk[i] = uint32_t(__half_as_ushort(__float2half_rn(x0))) | (uint32_t(__half_as_ushort(__float2half_rn(x1))) << 16);
+    }
+    *reinterpret_cast<u32x4 *>(dst) = pk;
+}
+
+__device__ __forceinline__ floatx4 load_agent4(const float * p) {
+    const float2 x = load_agent2(p), y = load_agent2(p + 2);
+    return floatx4{x.x, x.y, y.x, y.y};
+}
+
+// Fold the rows in `mask` (bit k: row sp + k n) of the pair (s, kvh) from the n splits' partials and write them; all
+// 512 threads take part. A row is 4 shares (split i to share i mod 4), a share 64 threads of 4 values each folding
+// its splits in order with a running max; then the 4 shares fold in order in LDS. Two rows a pass. The order of every
+// operation is fixed by the row alone, so any split that folds a row writes the same bits.
+template <int THREADS>
+__device__ void fold_rows(const dec_args & a, int32_t s, int32_t kvh, int32_t sp, int32_t n, uint32_t mask,
+                          uint8_t * smem) {
+    static_assert(THREADS == 512, "8 slots of 64 threads");
+    constexpr int32_t kShares = 4, kBatch = 16;
+    const int32_t tid = static_cast<int32_t>(threadIdx.x);
+    const int32_t slot = tid >> 6, c = tid & 63;
+    const int32_t rr = slot >> 2, g = slot & 3; // the pass's row (0, 1) and this slot's share
+    const int32_t s0 = a.split0[s], h_kv = a.pv.h_kv;
+    floatx4 * part = reinterpret_cast<floatx4 *>(smem); // [slot][64][2]: (m, l, -, -), acc
+    while (mask != 0) {
+        int32_t rows[2] = {-1, -1};
+        for (int32_t m = 0; m < 2 && mask != 0; ++m) {
+            const int32_t k = __builtin_ctz(mask);
+            mask &= mask - 1;
+            rows[m] = sp + k * n;
+        }
+        const int32_t r = rows[rr];
+        if (r >= 0) {
+            float M = kNegInf, L = 0.0f;
+            floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int32_t i0 = g; i0 < n; i0 += kBatch * kShares) {
+                float2 mlv[kBatch];
+                floatx4 v[kBatch];
+#pragma unroll
+                for (int q = 0; q < kBatch; ++q) {
+                    const int32_t i = i0 + q * kShares;
+                    mlv[q] = float2{kNegInf, 0.0f};
+                    v[q] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                    if (i < n) {
+                        const int64_t prow = (int64_t(s0 + i) * h_kv + kvh) * a.R + r;
+                        mlv[q] = load_agent2(a.pml + prow * 2);
+                        v[q] = load_agent4(a.po + prow * kHeadDim + 4 * c);
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < kBatch; ++q) {
+                    const float mn = fmaxf(M, mlv[q].x);
+                    const float mu = mn == kNegInf ? 0.0f : mn;
+                    const float fo = __builtin_amdgcn_exp2f(M - mu), fn = __builtin_amdgcn_exp2f(mlv[q].x - mu);
+                    L = __builtin_fmaf(L, fo, mlv[q].y * fn);
+                    A = A * fo + v[q] * fn;
+                    M = mn;
+                }
+            }
+            part[(slot * 64 + c) * 2 + 0] = floatx4{M, L, 0.0f, 0.0f};
+            part[(slot * 64 + c) * 2 + 1] = A;
+        }
+        __syncthreads();
+        if (g == 0 && r >= 0) { // the row's 4 shares in order
+            float M = kNegInf, L = 0.0f;
+            floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int32_t gg = 0; gg < kShares; ++gg) {
+                const floatx4 ml = part[((rr * 4 + gg) * 64 + c) * 2 + 0];
+                const floatx4 p = part[((rr * 4 + gg) * 64 + c) * 2 + 1];
+                const float mn = fmaxf(M, ml[0]);
+                const float mu = mn == kNegInf ? 0.0f : mn;
+                const float fo = __builtin_amdgcn_exp2f(M - mu), fn = __builtin_amdgcn_exp2f(ml[0] - mu);
+                L = __builtin_fmaf(L, fo, ml[1] * fn);
+                A = A * fo + p * fn;
+                M = mn;
+            }
+            const int32_t t = r / a.G, h = kvh * a.G + r % a.G;
+            const float inv = 1.0f / L;
+            uint2 pk;
+            pk.x = uint32_t(__half_as_ushort(__float2half_rn(A[0] * inv))) |
+                   (uint32_t(__half_as_ushort(__float2half_rn(A[1] * inv))) << 16);
+            pk.y = uint32_t(__half_as_ushort(__float2half_rn(A[2] * inv))) |
+                   (uint32_t(__half_as_ushort(__float2half_rn(A[3] * inv))) << 16);
+            *reinterpret_cast<uint2 *>(a.out + ((int64_t(s) * a.T + t) * a.hq + h) * kHeadDim + 4 * c) = pk;
+        }
+        __syncthreads(); // part is rewritten by the next pass
+    }
+}
+
+// The split's part of the pair's fold (the protocol above); called by every thread after the partial's stores
+template <int THREADS>
+__device__ void fold_splits(const dec_args & a, int32_t s, int32_t kvh, int32_t sp, int32_t n, uint8_t * smem) {
+    const int32_t tid = static_cast<int32_t>(threadIdx.x);
+    uint32_t * st = a.fold + (int64_t(s) * a.pv.h_kv + kvh) * kFoldWords;
+    uint32_t * shared_word = reinterpret_cast<uint32_t *>(smem + 16384); // past fold_rows' LDS
+    const int32_t R = a.R;
+    // this split's rows: sp, sp + n, ... (bit k: row sp + k n)
+    uint32_t own = 0;
+    for (int32_t r = sp, k = 0; r < R; r += n, ++k) {
+        own |= 1u << k;
+    }
+    wait_vmcnt<0>(); // this thread's partial stores are complete (device scope)
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(st, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old % kFoldEpoch == static_cast<uint32_t>(n - 1)) { // the last: round the count up to the next epoch
+            __hip_atomic_fetch_add(st, kFoldEpoch - static_cast<uint32_t>(n), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        shared_word[0] = old;
+    }
+    __syncthreads();
+    const uint32_t old = shared_word[0];
+    const uint32_t base = old - old % kFoldEpoch;
+    const uint32_t tag = (base / kFoldEpoch + 1) << 2; // this launch's row-state tag (the epoch), low bits the state
+    const bool last = old % kFoldEpoch == static_cast<uint32_t>(n - 1);
+    if (!last) {
+        if (own == 0) {
+            return;
+        }
+        // poll (bounded) until every split has arrived; then take the rows, or give them up to the last split
+        if (tid == 0) {
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            bool all = false;
+            for (;;) {
+                if (load_agent(st) - base >= static_cast<uint32_t>(n)) {
+                    all = true;
+                    break;
+                }
+                if (__builtin_amdgcn_s_memrealtime() - t0 > static_cast<uint64_t>(a.fold_spin)) {
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            for (uint32_t m = own; m != 0; m &= m - 1) {
+                __hip_atomic_store(st + 2 + sp + __builtin_ctz(m) * n, tag | (all ? 1u : 2u), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+            shared_word[1] = all ? own : 0u;
+        }
+        __syncthreads();
+        const uint32_t mine = shared_word[1];
+        if (mine != 0) {
+            fold_rows<THREADS>(a, s, kvh, sp, n, mine, smem);
+        }
+        return;
+    }
+    // the last split: its own rows at once; then, polling every other row's state in parallel (lane r of wave 0),
+    // the rows their owners gave up (or, past every owner's bound, never decided) as well
+    fold_rows<THREADS>(a, s, kvh, sp, n, own, smem);
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    const uint64_t patience = 2 * static_cast<uint64_t>(a.fold_spin) + 10000; // past every owner's own bound
+    if (tid < 64) {
+        const int32_t r = tid;
+        const bool mine = r < R && r >= sp && (r - sp) % n == 0;
+        bool take = false;
+        bool pending = r < R && !mine;
+        while (__any(pending)) {
+            if (pending) {
+                const uint32_t w = load_agent(st + 2 + r);
+                if ((w & ~3u) == tag) {
+                    pending = false;
+                    take = (w & 3u) == 2u;
+                }
+            }
+            if (__builtin_amdgcn_s_memrealtime() - t0 > patience) {
+                take = take || pending;
+                pending = false;
+            }
+            if (__any(pending)) {
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        const uint64_t b = __ballot(take);
+        if (tid == 0) {
+            shared_word[1] = static_cast<uint32_t>(b);
+        }
+    }
+    __syncthreads();
+    for (uint32_t m = shared_word[1]; m != 0; m &= m - 1) {
+        const int32_t r = __builtin_ctz(m);
+        fold_rows<THREADS>(a, s, kvh, r % n, n, 1u << (r / n), smem);
+    }
+}
+
 template <int NT>
 __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     using SH = stream_shape<NT>;
@@ -360,12 +587,15 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
         l_row[rt] = __shfl(lv[rt][0], j + 32);
     }
 
-    // ---- fold the four waves per row in LDS (fixed order), write the workgroup's partial ----
+    // ---- fold the eight waves per row in LDS (fixed order), then the workgroup's row: the output itself when the
+    // split is its sequence's only one, else the split's partial (and, with the in-kernel fold, its arrival) ----
     constexpr int32_t OS = SH::OSTRIDE;
-    __syncthreads(); // the rings are no longer read
+    const int32_t n_split = a.split0[s + 1] - a.split0[s];
+    const bool direct = a.fold != nullptr && n_split == 1;
+    __syncthreads(); // the slots are no longer read
     FNKV_STAMP(2);
-    float * ml = reinterpret_cast<float *>(smem);                               // [wave][NT 16 rows][2]
-    float * ob = reinterpret_cast<float *>(smem + WAVES * NT * 16 * 2 * 4);      // [wave][16 rows][OS]
+    float * ml = reinterpret_cast<float *>(smem);                          // [wave][NT 16 rows][2]
+    float * ob = reinterpret_cast<float *>(smem + WAVES * NT * 16 * 2 * 4); // [wave][16 rows][OS]
     if (qg == 0) {
 #pragma unroll
         for (int rt = 0; rt < NT; ++rt) {
@@ -399,35 +629,53 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
             const int32_t rrow = t >> 5, c0 = (t & 31) * 8;
             const int32_t r = rt * 16 + rrow;
             if (r < a.R) {
-                const int64_t prow = (int64_t(split) * pv.h_kv + kvh) * a.R + r;
-                float * dst = a.po + prow * kHeadDim + c0;
+                floatx4 sum[2];
 #pragma unroll
-                for (int c = 0; c < 8; c += 4) {
-                    floatx4 sum = *reinterpret_cast<const floatx4 *>(ob + rrow * OS + c0 + c);
+                for (int c = 0; c < 2; ++c) {
+                    sum[c] = *reinterpret_cast<const floatx4 *>(ob + rrow * OS + c0 + 4 * c);
 #pragma unroll
                     for (int w = 1; w < WAVES; ++w) {
-                        sum += *reinterpret_cast<const floatx4 *>(ob + (w * 16 + rrow) * OS + c0 + c);
+                        sum[c] += *reinterpret_cast<const floatx4 *>(ob + (w * 16 + rrow) * OS + c0 + 4 * c);
                     }
-                    *reinterpret_cast<floatx4 *>(dst + c) = sum;
                 }
-                if ((t & 31) == 0) {
-                    float Mr = kNegInf;
+                float Mr = kNegInf;
 #pragma unroll
-                    for (int w = 0; w < WAVES; ++w) {
-                        Mr = fmaxf(Mr, ml[(w * NT * 16 + r) * 2]);
-                    }
-                    const float Mr_use = Mr == kNegInf ? 0.0f : Mr;
-                    float L = 0.0f;
+                for (int w = 0; w < WAVES; ++w) {
+                    Mr = fmaxf(Mr, ml[(w * NT * 16 + r) * 2]);
+                }
+                const float Mr_use = Mr == kNegInf ? 0.0f : Mr;
+                float L = 0.0f;
 #pragma unroll
-                    for (int w = 0; w < WAVES; ++w) {
-                        L += ml[(w * NT * 16 + r) * 2 + 1] * __builtin_amdgcn_exp2f(ml[(w * NT * 16 + r) * 2] - Mr_use);
+                for (int w = 0; w < WAVES; ++w) {
+                    L += ml[(w * NT * 16 + r) * 2 + 1] * __builtin_amdgcn_exp2f(ml[(w * NT * 16 + r) * 2] - Mr_use);
+                }
+                if (direct) {
+                    store_out8(a, s, kvh, r, c0, sum, 1.0f / L);
+                } else {
+                    const int64_t prow = (int64_t(split) * pv.h_kv + kvh) * a.R + r;
+                    float * dst = a.po + prow * kHeadDim + c0;
+                    if (a.fold != nullptr) { // read by other workgroups in this launch: device-scope stores
+                        store_agent(dst, sum[0]);
+                        store_agent(dst + 4, sum[1]);
+                        if ((t & 31) == 0) {
+                            store_agent2(a.pml + prow * 2, Mr, L);
+                        }
+                    } else {
+                        *reinterpret_cast<floatx4 *>(dst) = sum[0];
+                        *reinterpret_cast<floatx4 *>(dst + 4) = sum[1];
+                        if ((t & 31) == 0) {
+                            a.pml[prow * 2 + 0] = Mr;
+                            a.pml[prow * 2 + 1] = L;
+                        }
                     }
-                    a.pml[prow * 2 + 0] = Mr;
-                    a.pml[prow * 2 + 1] = L;
                 }
             }
         }
         __syncthreads(); // ob is rewritten by the next row tile
+    }
+    FNKV_STAMP(3);
+    if (a.fold != nullptr && !direct) {
+        fold_splits<64 * WAVES>(a, s, kvh, sp, n_split, smem);
     }
     FNKV_STAMP(4);
 }

@@ -27,6 +27,7 @@ EXPORTS = [
     "fnkv_datc_prepare", "fnkv_datc_attend", "fnkv_datc_step", "fnkv_qsa_workspace_bytes", "fnkv_qsa_attend",
     "fnkv_attn_decode_dev", "fnkv_attn_sparse_dev", "fnkv_attend_workspace_bytes", "fnkv_attend",
     "fnkv_attend_lanes", "fnkv_attn_decode_noalloc", "fnkv_qsp_kv", "fnkv_qsp_workspace_bytes", "fnkv_qsp_attend",
+    "fnkv_test_decode_fold",
 ]
 QSP_MAX_ROWS = 4096
 SLAB_ROWS, ROW_WORDS = 128, 517
@@ -134,6 +135,8 @@ def lib():
         L.fnkv_export_q8_0.argtypes = [P, I32, I32, I32, I32, I64, I32, P, P]
         L.fnkv_export_kv8.restype = ctypes.c_int
         L.fnkv_export_kv8.argtypes = [P, I32, I32, I32, I32, I64, I32, P, P, P]
+        L.fnkv_test_decode_fold.restype = None
+        L.fnkv_test_decode_fold.argtypes = [I32, I64]
         L.fnkv_decode_workspace_bytes.restype = I64
         L.fnkv_decode_workspace_bytes.argtypes = [P, I32, P, I32, I32]
         L.fnkv_attn_decode.restype = ctypes.c_int

@@ -211,6 +211,9 @@ int main(int argc, char ** argv) {
     _Float16 *q = nullptr, *kn = nullptr, *vn = nullptr, *out = nullptr, *out_ref = nullptr;
     HIP_CHECK(hipMalloc(&ws, ws_bytes));
     HIP_CHECK(hipMalloc(&ws_twin, ws_host));
+    // the workspaces start zeroed once (their fold counters; every launch leaves them at zero)
+    HIP_CHECK(hipMemset(ws, 0, ws_bytes));
+    HIP_CHECK(hipMemset(ws_twin, 0, ws_host));
     HIP_CHECK(hipMalloc(&ctx_dev, sizeof(int64_t) * n_seq));
     HIP_CHECK(hipMalloc(&err, sizeof(uint32_t)));
     HIP_CHECK(hipMalloc(&q, sizeof(_Float16) * q_elems * kLayers));

@@ -127,8 +127,10 @@ int fnkv_export_kv8(const fnkv_pool * pool, int32_t slot, int32_t layer, int32_t
 
 /* ---- decode / speculative verify attention (fn/kernels/qsa/attend.h:97-151 attend, attend_lanes) ---- */
 
-/* The workspace a decode launch over these sequences needs (bytes; device memory the caller allocates; no zeroing
- * needed). ctx[n_seq] as for fnkv_attn_decode. */
+/* The workspace a decode launch over these sequences needs (bytes; device memory the caller allocates and zeroes
+ * once before its first use: its first bytes hold the counters of the launch's split-K fold, which every launch
+ * leaves ready for the next, as the reference's attend workspace, attend.h:89-93). ctx[n_seq] as for
+ * fnkv_attn_decode. */
 int64_t fnkv_decode_workspace_bytes(const fnkv_pool * pool, int32_t n_seq, const int64_t * ctx, int32_t T, int32_t hq);
 
 /* Dense causal attention of T query tokens of each of n_seq sequences over their pooled Q8_0 K/V of `layer`.
@@ -171,12 +173,19 @@ int fnkv_attn_decode_dev(const fnkv_pool * pool, int32_t n_seq, const int32_t * 
  * library (one a GPU, held until the process ends), and the call allocates nothing. A launch whose partials
  * (fnkv_decode_workspace_bytes(pool, n_seq, max_ctx, T, hq)) exceed 16 MiB is refused (FNKV_ERR_ARG, nothing
  * enqueued); cfg-sized launches (4 sequences of 8K-64K at T = 3, or one of 262,144 at T = 5) need 6-11 MiB. Every
- * call on one GPU shares that array (nothing in it needs to start at zero): calls that overlap on one GPU (other
- * streams, or other threads) race and must be serialized by the caller. */
+ * call on one GPU shares that array (it starts zeroed and every call leaves its fold counters ready for the next): calls that
+ * overlap on one GPU (other streams, or other threads) race and must be serialized by the caller. */
 int fnkv_attn_decode_noalloc(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx,
                              const int64_t * max_ctx, int32_t T, int32_t layer, int32_t hq, float scale,
                              const void * q, const void * k_new, const void * v_new, int32_t new_dtype, void * out,
                              uint32_t * err, void * stream);
+
+/* Test hook, no counterpart in the reference: the dense decode launches' split-K fold inside the launch (mode 1; 0:
+ * the partials go to a second, merge launch, the default; negative: the FNKV_DECODE_FOLD environment variable's
+ * choice) and the bound of its waits (real-time ticks of 10 ns; negative: the default, 20,000). A tiny bound makes the
+ * splits that fold rows give them up to the last split to arrive, which folds them instead (the same outputs,
+ * bitwise), so tests drive that path from the host. Affects launches planned after the call, in every thread. */
+void fnkv_test_decode_fold(int32_t mode, int64_t spin_ticks);
 
 /* ---- sparse (QSA) attention at decode rows (fn/kernels/qsa/attend.h:97-141 attend over a selection body) ---- */
 

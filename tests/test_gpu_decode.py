@@ -45,7 +45,7 @@ class Setup:
         ctxs = self.ctxs if ctxs is None else ctxs
         q = torch.from_numpy(q16).cuda()
         out = torch.empty_like(q)
-        ws = torch.empty(self.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+        ws = torch.zeros(self.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
         self.pool.decode(slots, ctxs, T, layer, q, out, ws)
         torch.cuda.synchronize()
         return out.cpu().numpy()
@@ -102,6 +102,35 @@ def test_bitwise_reruns_and_page_placement_invariance():
     assert a.check(q16, r1, 3) <= TOL
 
 
+def test_fold_fallback_and_reused_workspace_bitwise():
+    """The split-K fold inside the launch (stream.hip: row r of a (sequence, KV head) folded by its split r mod n after
+    every split has arrived) against the merge launch: the same outputs, bitwise. With the wait bound at zero the owners
+    give their rows up to the last split to arrive, which folds them: bitwise the same again. One workspace serves every
+    launch (its fold counters stay consistent)."""
+    ctxs = [30000, 9000, 65536]
+    st = Setup(ctxs, seed=5)
+    q16 = cases.queries(5, (3, 3, HQ, 256))
+    q = torch.from_numpy(q16).cuda()
+    ws = torch.zeros(st.pool.decode_ws_bytes(ctxs, 3, HQ), dtype=torch.uint8, device="cuda")
+    outs = []
+    L = fnkv.lib()
+    for mode, spin in ((0, -1), (1, -1), (1, 0), (1, 0), (1, -1), (0, -1)):
+        L.fnkv_test_decode_fold(mode, spin)
+        try:
+            out = torch.empty_like(q)
+            st.pool.decode(st.slots, ctxs, 3, 0, q, out, ws)
+            torch.cuda.synchronize()
+        finally:
+            L.fnkv_test_decode_fold(-1, -1)
+        outs.append(out.cpu().numpy())
+    diffs = [float(np.abs(outs[0].astype(np.float32) - o.astype(np.float32)).max()) for o in outs[1:]]
+    assert all(np.array_equal(outs[0].view(np.uint16), o.view(np.uint16)) for o in outs[1:]), diffs
+    assert st.check(q16, outs[0], 3) <= TOL
+    # the fold region (the workspace's first bytes): each pair's arrival counter at a whole number of launches
+    words = ws[: 16 * HKV * 50 * 4].view(torch.int32).cpu().numpy().reshape(16 * HKV, 50)
+    assert np.all(words[:, 0] % 1024 == 0) and words[:, 0].max() > 0
+
+
 def test_layers_are_separate():
     st = Setup([1500, 600], seed=4, layers=3)
     q16 = cases.queries(4, (2, 1, HQ, 256))
@@ -140,7 +169,7 @@ def test_config1_all_twelve_layers():
     vn = cases.queries(15, (layers, len(ctxs), T, HKV, 256))
     q, k_new, v_new = (torch.from_numpy(x).cuda() for x in (q16, kn, vn))
     out = torch.empty_like(q)
-    ws = torch.empty(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
     for layer in range(layers):
         pool.decode(slots, ctxs, T, layer, q[layer], out[layer], ws, k_new=k_new[layer], v_new=v_new[layer])
     torch.cuda.synchronize()
@@ -197,7 +226,7 @@ def test_fused_append_matches_separate_append():
     vn = torch.from_numpy(cases.queries(10, (3, T, HKV, 256))).cuda()
     q = torch.from_numpy(q16).cuda()
     oa, ob = torch.empty_like(q), torch.empty_like(q)
-    ws = torch.empty(a.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(a.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
     a.pool.decode(a.slots, ctxs, T, 0, q, oa, ws, k_new=kn, v_new=vn)
     for i, (s, c) in enumerate(zip(b.slots, ctxs)):
         b.pool.append(s, 0, c - T, kn[i].contiguous(), vn[i].contiguous())
@@ -235,7 +264,7 @@ def test_first_launch_matches_reruns(T):
             x = torch.randn((2, ctx, HKV, 256), generator=g, device="cuda").half()
             pool.append(0, 0, 0, x[0].contiguous(), x[1].contiguous())
             q = torch.randn((1, T, HQ, 256), generator=g, device="cuda").half()
-            ws = torch.empty(pool.decode_ws_bytes([ctx], T, HQ), dtype=torch.uint8, device="cuda")
+            ws = torch.zeros(pool.decode_ws_bytes([ctx], T, HQ), dtype=torch.uint8, device="cuda")
             outs = []
             for _ in range(6):
                 out = torch.full_like(q, float("nan"))
@@ -268,7 +297,7 @@ def test_split_walks_contiguous_and_strided(T, strided, split, monkeypatch):
     vn = rng.standard_normal((len(ctxs), T, HKV, 256), dtype=np.float32).astype(np.float16)
     q = torch.from_numpy(q16).cuda()
     out = torch.empty_like(q)
-    ws = torch.empty(st.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(st.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
     st.pool.decode(st.slots, ctxs, T, 0, q, out, ws, k_new=torch.from_numpy(kn).cuda(),
                    v_new=torch.from_numpy(vn).cuda())
     torch.cuda.synchronize()
@@ -334,7 +363,7 @@ def test_seeded_random_launches(case):
     vn = rng.standard_normal((n_seq, T, HKV, 256), dtype=np.float32).astype(np.float16)
     q = torch.from_numpy(q16).cuda()
     out = torch.empty_like(q)
-    ws = torch.empty(st.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(st.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
     st.pool.decode(st.slots, ctxs, T, 0, q, out, ws, k_new=torch.from_numpy(kn).cuda(),
                    v_new=torch.from_numpy(vn).cuda())
     torch.cuda.synchronize()

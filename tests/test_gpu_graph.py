@@ -76,7 +76,7 @@ def test_decode_one_graph_advancing_context(T, ctx0):
     kn = torch.empty((n, T, HKV, D), dtype=torch.float16, device="cuda")
     vn = torch.empty_like(kn)
     out = torch.empty_like(q)
-    ws = torch.empty(L.pool.decode_ws_bytes(L.cap, T, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(L.pool.decode_ws_bytes(L.cap, T, HQ), dtype=torch.uint8, device="cuda")
 
     def launch():
         L.pool.decode_dev(L.slots, ctx_dev, L.cap, T, 0, q, out, ws, err, k_new=kn, v_new=vn)
@@ -127,7 +127,7 @@ def test_decode_dev_matches_host_context_launch():
         k16, v16 = L.kv[s]
         L.pool.append(s, 0, L.ctx0[s] - 1, torch.from_numpy(k16[-1:]).cuda(), torch.from_numpy(v16[-1:]).cuda())
     q = torch.from_numpy(cases.queries(5, (2, 1, HQ, D))).cuda()
-    ws = torch.empty(L.pool.decode_ws_bytes(L.cap, 1, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(L.pool.decode_ws_bytes(L.cap, 1, HQ), dtype=torch.uint8, device="cuda")
     a, b = torch.empty_like(q), torch.empty_like(q)
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
     L.pool.decode(L.slots, L.cap, 1, 0, q, a, ws)
@@ -150,7 +150,7 @@ def test_decode_refused_context_writes_nothing(bad):
     kn = torch.from_numpy(np.stack([L.kv[0][0][:T], L.kv[1][0][ctx[1] - T:ctx[1]]])).cuda()
     vn = torch.from_numpy(np.stack([L.kv[0][1][:T], L.kv[1][1][ctx[1] - T:ctx[1]]])).cuda()
     out = torch.full_like(q, 7.0)
-    ws = torch.empty(L.pool.decode_ws_bytes(cap, T, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(L.pool.decode_ws_bytes(cap, T, HQ), dtype=torch.uint8, device="cuda")
     before = [L.pool.export(0, 0, h, kv, 0, cap[0]).cpu() for h in range(HKV) for kv in range(2)]
     L.pool.decode_dev(L.slots, ctx_dev, cap, T, 0, q, out, ws, err, k_new=kn, v_new=vn)
     torch.cuda.synchronize()
@@ -167,7 +167,7 @@ def test_decode_dev_host_refusals_enqueue_nothing():
     L = DecodeLoop([600], 1, 1, seed=2)
     q = torch.zeros((1, 1, HQ, D), dtype=torch.float16, device="cuda")
     out = torch.full_like(q, 3.0)
-    ws = torch.empty(L.pool.decode_ws_bytes(L.cap, 1, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(L.pool.decode_ws_bytes(L.cap, 1, HQ), dtype=torch.uint8, device="cuda")
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
     ctx_dev = torch.tensor([600], dtype=torch.int64, device="cuda")
     with pytest.raises(fnkv.FnkvError):  # a bound past the slot's mapped cells
@@ -183,7 +183,7 @@ def test_decode_duplicate_slot_with_append_refused():
     q = torch.zeros((2, 1, HQ, D), dtype=torch.float16, device="cuda")
     kn = torch.zeros((2, 1, HKV, D), dtype=torch.float16, device="cuda")
     out = torch.empty_like(q)
-    ws = torch.empty(L.pool.decode_ws_bytes([600, 600], 1, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(L.pool.decode_ws_bytes([600, 600], 1, HQ), dtype=torch.uint8, device="cuda")
     with pytest.raises(fnkv.FnkvError):
         L.pool.decode([0, 0], [600, 600], 1, 0, q, out, ws, k_new=kn, v_new=kn)
     L.pool.decode([0, 0], [600, 600], 1, 0, q, out, ws)  # reading one slot twice is fine

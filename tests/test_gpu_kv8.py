@@ -116,7 +116,7 @@ def test_kv8_decode_and_verify(T):
     q16 = cases.queries(40 + T, (len(ctxs), T, HQ, 256))
     q = torch.from_numpy(q16).cuda()
     out = torch.empty_like(q)
-    ws = torch.empty(st.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(st.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
     st.pool.decode(st.slots, ctxs, T, 0, q, out, ws)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
@@ -134,7 +134,7 @@ def test_kv8_fused_append_bit_exact_and_attention():
     q16 = cases.queries(52, (2, T, HQ, 256))
     q = torch.from_numpy(q16).cuda()
     out = torch.empty_like(q)
-    ws = torch.empty(st.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(st.pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
     st.pool.decode(st.slots, ctxs, T, 0, q, out, ws, k_new=torch.from_numpy(kn).cuda(),
                    v_new=torch.from_numpy(vn).cuda())
     torch.cuda.synchronize()

@@ -98,7 +98,7 @@ def test_config4_mixed_step_parity():
         q = torch.from_numpy(q_v).cuda()
         out = torch.empty_like(q)
         ctxs = [ctx_of[s] for s in vf_slots]
-        ws = torch.empty(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+        ws = torch.zeros(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
         pool.decode(vf_slots, ctxs, T, layer, q, out, ws, k_new=torch.from_numpy(kn).cuda(),
                     v_new=torch.from_numpy(vn).cuda())
         torch.cuda.synchronize()
@@ -155,7 +155,7 @@ def test_config4_full_contexts_properties():
         pool.prefill(s, 0, c, q, out)
         qv = q[None, -5:].contiguous()
         ov = torch.empty_like(qv)
-        ws = torch.empty(pool.decode_ws_bytes([c], 5, HQ), dtype=torch.uint8, device="cuda")
+        ws = torch.zeros(pool.decode_ws_bytes([c], 5, HQ), dtype=torch.uint8, device="cuda")
         pool.decode([s], [c], 5, 0, qv, ov, ws)
         torch.cuda.synchronize()
         assert torch.isfinite(out.float()).all().item()
@@ -168,7 +168,7 @@ def test_config4_full_contexts_properties():
     q = torch.randn((len(vf_slots), T, HQ, D), generator=g, device="cuda").half()
     ctxs = [ctx_of[s] for s in vf_slots]
     out = torch.empty_like(q)
-    ws = torch.empty(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
     pool.decode(vf_slots, ctxs, T, 0, q, out, ws)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all().item()
@@ -176,7 +176,7 @@ def test_config4_full_contexts_properties():
     q16 = q.cpu().numpy()
     for i, s in enumerate(vf_slots):
         one = torch.empty_like(q[i:i + 1])
-        ws1 = torch.empty(pool.decode_ws_bytes([ctxs[i]], T, HQ), dtype=torch.uint8, device="cuda")
+        ws1 = torch.zeros(pool.decode_ws_bytes([ctxs[i]], T, HQ), dtype=torch.uint8, device="cuda")
         pool.decode([s], [ctxs[i]], T, 0, q[i:i + 1].contiguous(), one, ws1)
         torch.cuda.synchronize()
         assert (one[0].float() - out[i].float()).abs().max().item() <= 2 * TOL

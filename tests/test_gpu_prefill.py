@@ -68,7 +68,7 @@ def test_prefill_agrees_with_decode_on_last_rows():
     # the chunk's last 5 rows as a T = 5 verify
     q = torch.from_numpy(np.ascontiguousarray(q16[None, -5:])).cuda()
     out = torch.empty_like(q)
-    ws = torch.empty(pool.decode_ws_bytes([ctx], 5, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(pool.decode_ws_bytes([ctx], 5, HQ), dtype=torch.uint8, device="cuda")
     pool.decode([0], [ctx], 5, 0, q, out, ws)
     torch.cuda.synchronize()
     d = out.cpu().numpy()[0].astype(np.float32)
@@ -87,7 +87,7 @@ def test_config3_chunk_at_depth_131072():
     # depth + t + 1, a T = 6 verify over the same cells (a different kernel, the same causal rule); both are within
     # the tolerance of the fp64 attention, so they agree within twice it
     depth = ctx - rows
-    ws = torch.empty(pool.decode_ws_bytes([ctx], 6, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(pool.decode_ws_bytes([ctx], 6, HQ), dtype=torch.uint8, device="cuda")
     qd = torch.from_numpy(q16).cuda()
     outs = []
     ends = list(range(5, rows, 6)) + ([rows - 1] if (rows - 6) % 6 else [])

@@ -112,7 +112,7 @@ def test_sparse_full_selection_agrees_with_dense():
     # at n_vis <= 512 the selection is the whole causal context: the dense launch over the same pool agrees
     depth, T = 1800, 3
     pool, got, ref, (q, bt, ot) = sparse_case(depth, T, seed=91, new_cells=False)
-    ws = torch.empty(pool.decode_ws_bytes([depth + T], T, HQ), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(pool.decode_ws_bytes([depth + T], T, HQ), dtype=torch.uint8, device="cuda")
     dense = torch.empty_like(q)
     pool.decode([0], [depth + T], T, 0, q[None].contiguous(), dense[None], ws)
     torch.cuda.synchronize()

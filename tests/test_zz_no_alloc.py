@@ -51,7 +51,7 @@ def test_noalloc_matches_decode_dev_twice(first, second):
         err = torch.zeros(2, dtype=torch.int32, device="cuda")
         ref = torch.full_like(q, float("nan"))
         got = torch.full_like(q, float("nan"))
-        ws = torch.empty(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+        ws = torch.zeros(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
         pool.decode_dev(slots, ctx_dev, ctxs, T, 0, q, ref, ws, err[0:1], k_new=kn, v_new=vn)
         ref_cells = cells(pool, slots, ctxs, T)
         # the same launch again through the scratch (it rewrites the same new cells with the same values)
