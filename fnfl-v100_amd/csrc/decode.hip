@@ -256,6 +256,11 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     if (refused<SP>(a, s, ctx, sp, kvh)) {
         return;
     }
+    bool unmapped = false;
+    if constexpr (!SP) {
+        unmapped = src.guard_unmapped(lane);
+        report_unmapped(a, unmapped);
+    }
     const int32_t n_tiles = src.n_tiles;
     if (SP && n_tiles == 0) {
         return; // past the selection's tiles (the merge reads only the splits that hold some)
@@ -549,7 +554,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
                 const int32_t w = g * NT + rtile;
                 L += ml[(w * 16 + rrow) * 2 + 1] * __builtin_amdgcn_exp2f(ml[(w * 16 + rrow) * 2] - Mr_use);
             }
-            a.pml[prow * 2 + 0] = Mr;
+            a.pml[prow * 2 + 0] = unmapped ? __builtin_nanf("") : Mr; // NaN: the merge writes nothing
             a.pml[prow * 2 + 1] = L;
         }
     }
@@ -654,6 +659,11 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP, QLO>::WAVES), 1) void deco
                                   smem + GR * SH::GROUP_LDS + SH::Q_LDS + SH::QLO_LDS, ctx);
     if (refused<SP>(a, s, ctx, sp, kvh)) {
         return;
+    }
+    bool unmapped = false;
+    if constexpr (!SP) {
+        unmapped = src.guard_unmapped(lane);
+        report_unmapped(a, unmapped);
     }
     const int32_t n_tiles = src.n_tiles;
     if (SP && n_tiles == 0) {
@@ -1032,7 +1042,7 @@ __global__ __launch_bounds__((64 * rows_shape<NT, SP, QLO>::WAVES), 1) void deco
             for (int g = 0; g < GR; ++g) {
                 L += ml[(g * kRows + r) * 2 + 1] * __builtin_amdgcn_exp2f(ml[(g * kRows + r) * 2] - Mr_use);
             }
-            a.pml[prow * 2 + 0] = Mr;
+            a.pml[prow * 2 + 0] = unmapped ? __builtin_nanf("") : Mr; // NaN: the merge writes nothing
             a.pml[prow * 2 + 1] = L;
         }
     }
@@ -1087,11 +1097,13 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
         return;
     }
     float m = kNegInf, l = 0.0f;
+    int32_t bad = 0; // a split that saw an unmapped page marked its partial with a NaN max: nothing is written
     floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
     for (int32_t i = g; i < n; i += 32) {
         const int64_t prow = (int64_t(s0 + i) * a.h_kv + kvh) * a.R + r;
         const float2 ml = *reinterpret_cast<const float2 *>(a.pml + prow * 2);
+        bad |= ml.x != ml.x ? 1 : 0;
         const floatx4 o = *reinterpret_cast<const floatx4 *>(a.po + prow * kHeadDim + chunk * 32 + c4 * 4);
         const float m_new = fmaxf(m, ml.x);
         const float m_use = m_new == kNegInf ? 0.0f : m_new;
@@ -1128,7 +1140,9 @@ __global__ __launch_bounds__(256) void merge_kernel(merge_args a) {
             sL[wave] = l;
         }
     }
-    __syncthreads();
+    if (__syncthreads_or(bad)) {
+        return;
+    }
     if (tid < 8) {
         float Ms = sM[0], Ls = sL[0];
         floatx4 As = sA[0][tid];
@@ -1334,11 +1348,13 @@ template <int GRP> __global__ __launch_bounds__(64 * GRP) void merge_row_kernel(
         return;
     }
     float m = kNegInf, l = 0.0f;
+    int32_t bad = 0; // a split that saw an unmapped page marked its partial with a NaN max: nothing is written
     floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
     for (int32_t i = g; i < n; i += GRP) {
         const int64_t prow = (int64_t(s0 + i) * a.h_kv + kvh) * a.R + r;
         const float2 ml = *reinterpret_cast<const float2 *>(a.pml + prow * 2);
+        bad |= ml.x != ml.x ? 1 : 0;
         const floatx4 o = *reinterpret_cast<const floatx4 *>(a.po + prow * kHeadDim + c4 * 4);
         const float m_new = fmaxf(m, ml.x);
         const float m_use = m_new == kNegInf ? 0.0f : m_new;
@@ -1353,7 +1369,9 @@ template <int GRP> __global__ __launch_bounds__(64 * GRP) void merge_row_kernel(
         sM[g] = m;
         sL[g] = l;
     }
-    __syncthreads();
+    if (__syncthreads_or(bad)) {
+        return;
+    }
     if (g != 0) {
         return;
     }

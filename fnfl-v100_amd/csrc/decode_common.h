@@ -417,6 +417,16 @@ template <bool SP, bool LANES = true> struct split_src {
             page_lane = lane < n_tiles ? table[(g0 + stride * lane) >> 3] : 0;
         }
     }
+    // A walk tile whose page is not mapped (page-table entry -1: the slot was trimmed under a captured launch, outside
+    // the contract): its lanes read page 0 instead, so nothing faults, and the workgroup is told (uniform) so that it
+    // writes no output for its sequence (its partials carry a NaN max: the merge writes nothing for such a row).
+    __device__ __forceinline__ bool guard_unmapped(int32_t lane) {
+        const bool neg = lane < n_tiles && page_lane < 0;
+        if (neg) {
+            page_lane = 0;
+        }
+        return __any(neg);
+    }
     __device__ __forceinline__ uint2 entry(int32_t ti) const {
         if constexpr (LANES) {
             return uint2{static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int32_t>(ent_x), ti)),
@@ -481,6 +491,13 @@ __device__ __forceinline__ bool refused(const dec_args & a, int32_t s, int64_t c
         }
     }
     return false;
+}
+
+// A dense walk over an unmapped page (split_src::guard_unmapped): with a device word, FNKV_DEV_ERR_DEPTH is set
+__device__ __forceinline__ void report_unmapped(const dec_args & a, bool unmapped) {
+    if (unmapped && threadIdx.x == 0 && a.err != nullptr) {
+        atomicOr(a.err, FNKV_DEV_ERR_DEPTH);
+    }
 }
 
 // A sparse row view refused by its device depth (sparse_row_view): nothing is written; the first workgroup of row 0
@@ -630,6 +647,9 @@ __device__ __forceinline__ void append_new_cells(const dec_args & a, const int32
             continue;
         }
         const int32_t kv = job & 1;
+        if (table[pos >> 8] < 0) {
+            continue; // an unmapped page (outside the contract): nothing is written
+        }
         const int64_t src = ((int64_t(s) * a.T + (pos - first_new)) * pv.h_kv + kvh) * kHeadDim;
         float x[4];
         if (a.new_f32) {

@@ -187,18 +187,17 @@ __device__ __forceinline__ uint32_t load_agent(const uint32_t * p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// 8 output values of row r (values c0 .. c0 + 7) as fp16, scaled by inv
-__device__ __forceinline__ void store_out8(const dec_args & a, int32_t s, int32_t kvh, int32_t r, int32_t c0,
-                                           const floatx4 (&v)[2], float inv) {
+// 4 output values of row r (values c0 .. c0 + 3) as fp16, scaled by inv
+__device__ __forceinline__ void store_out4(const dec_args & a, int32_t s, int32_t kvh, int32_t r, int32_t c0, floatx4 v,
+                                           float inv) {
     const int32_t t = r / a.G, h = kvh * a.G + r % a.G;
     uint16_t * dst = a.out + ((int64_t(s) * a.T + t) * a.hq + h) * kHeadDim + c0;
-    u32x4 pk;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float x0 = v[i >> 1][(2 * i) & 3] * inv, x1 = v[i >> 1][(2 * i + 1) & 3] * inv;
-        pk[i] = uint32_t(__half_as_ushort(__float2half_rn(x0))) | (uint32_t(__half_as_ushort(__float2half_rn(x1))) << 16);
-    }
-    *reinterpret_cast<u32x4 *>(dst) = pk;
+    uint2 pk;
+    pk.x = uint32_t(__half_as_ushort(__float2half_rn(v[0] * inv))) |
+           (uint32_t(__half_as_ushort(__float2half_rn(v[1] * inv))) << 16);
+    pk.y = uint32_t(__half_as_ushort(__float2half_rn(v[2] * inv))) |
+           (uint32_t(__half_as_ushort(__float2half_rn(v[3] * inv))) << 16);
+    *reinterpret_cast<uint2 *>(dst) = pk;
 }
 
 __device__ __forceinline__ floatx4 load_agent4(const float * p) {
@@ -230,6 +229,7 @@ __device__ void fold_rows(const dec_args & a, int32_t s, int32_t kvh, int32_t sp
         const int32_t r = rows[rr];
         if (r >= 0) {
             float M = kNegInf, L = 0.0f;
+            bool bad_share = false;
             floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
             for (int32_t i0 = g; i0 < n; i0 += kBatch * kShares) {
                 float2 mlv[kBatch];
@@ -247,6 +247,7 @@ __device__ void fold_rows(const dec_args & a, int32_t s, int32_t kvh, int32_t sp
                 }
 #pragma unroll
                 for (int q = 0; q < kBatch; ++q) {
+                    bad_share = bad_share || mlv[q].x != mlv[q].x;
                     const float mn = fmaxf(M, mlv[q].x);
                     const float mu = mn == kNegInf ? 0.0f : mn;
                     const float fo = __builtin_amdgcn_exp2f(M - mu), fn = __builtin_amdgcn_exp2f(mlv[q].x - mu);
@@ -255,15 +256,17 @@ __device__ void fold_rows(const dec_args & a, int32_t s, int32_t kvh, int32_t sp
                     M = mn;
                 }
             }
-            part[(slot * 64 + c) * 2 + 0] = floatx4{M, L, 0.0f, 0.0f};
+            part[(slot * 64 + c) * 2 + 0] = floatx4{M, L, bad_share ? 1.0f : 0.0f, 0.0f};
             part[(slot * 64 + c) * 2 + 1] = A;
         }
         __syncthreads();
         if (g == 0 && r >= 0) { // the row's 4 shares in order
             float M = kNegInf, L = 0.0f;
+            bool bad = false;
             floatx4 A = {0.0f, 0.0f, 0.0f, 0.0f};
             for (int32_t gg = 0; gg < kShares; ++gg) {
                 const floatx4 ml = part[((rr * 4 + gg) * 64 + c) * 2 + 0];
+                bad = bad || ml[2] != 0.0f;
                 const floatx4 p = part[((rr * 4 + gg) * 64 + c) * 2 + 1];
                 const float mn = fmaxf(M, ml[0]);
                 const float mu = mn == kNegInf ? 0.0f : mn;
@@ -273,13 +276,15 @@ __device__ void fold_rows(const dec_args & a, int32_t s, int32_t kvh, int32_t sp
                 M = mn;
             }
             const int32_t t = r / a.G, h = kvh * a.G + r % a.G;
-            const float inv = 1.0f / L;
+            const float inv = bad ? 0.0f : 1.0f / L;
             uint2 pk;
             pk.x = uint32_t(__half_as_ushort(__float2half_rn(A[0] * inv))) |
                    (uint32_t(__half_as_ushort(__float2half_rn(A[1] * inv))) << 16);
             pk.y = uint32_t(__half_as_ushort(__float2half_rn(A[2] * inv))) |
                    (uint32_t(__half_as_ushort(__float2half_rn(A[3] * inv))) << 16);
-            *reinterpret_cast<uint2 *>(a.out + ((int64_t(s) * a.T + t) * a.hq + h) * kHeadDim + 4 * c) = pk;
+            if (!bad) { // a split that saw an unmapped page marks its partial: nothing is written for the row
+                *reinterpret_cast<uint2 *>(a.out + ((int64_t(s) * a.T + t) * a.hq + h) * kHeadDim + 4 * c) = pk;
+            }
         }
         __syncthreads(); // part is rewritten by the next pass
     }
@@ -421,12 +426,14 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     if (refused<false>(a, s, ctx, sp, kvh)) {
         return;
     }
+    const bool unmapped = src.guard_unmapped(lane);
+    report_unmapped(a, unmapped);
     // uniform in the workgroup; readfirstlane keeps the walk's arithmetic and the loop control scalar
     const int32_t n_tiles = __builtin_amdgcn_readfirstlane(src.n_tiles);
     FNKV_STAMP(0);
     // the step's new cells are written by the workgroup whose walk holds their tile (append_new_cells); only such a
     // workgroup waits for its stores before its loads
-    if (a.k_new != nullptr) {
+    if (a.k_new != nullptr && !unmapped) {
         bool owns = false;
         for (int32_t t = 0; t < a.T; ++t) {
             const int64_t pos = ctx - a.T + t;
@@ -623,19 +630,20 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
             }
         }
         __syncthreads();
-        // thread -> (row, 8 values): 16 rows x 32 groups
+        // thread -> (row, values c0 .. c0 + 3 and 128 + c0 .. + 3): 16 rows x 32 groups (a row's 32 threads read
+        // consecutive 16-byte pieces, conflict-free)
         {
             const int32_t t = static_cast<int32_t>(threadIdx.x);
-            const int32_t rrow = t >> 5, c0 = (t & 31) * 8;
+            const int32_t rrow = t >> 5, c0 = (t & 31) * 4;
             const int32_t r = rt * 16 + rrow;
             if (r < a.R) {
                 floatx4 sum[2];
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
-                    sum[c] = *reinterpret_cast<const floatx4 *>(ob + rrow * OS + c0 + 4 * c);
+                    sum[c] = *reinterpret_cast<const floatx4 *>(ob + rrow * OS + c0 + 128 * c);
 #pragma unroll
                     for (int w = 1; w < WAVES; ++w) {
-                        sum[c] += *reinterpret_cast<const floatx4 *>(ob + (w * 16 + rrow) * OS + c0 + 4 * c);
+                        sum[c] += *reinterpret_cast<const floatx4 *>(ob + (w * 16 + rrow) * OS + c0 + 128 * c);
                     }
                 }
                 float Mr = kNegInf;
@@ -649,20 +657,24 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
                 for (int w = 0; w < WAVES; ++w) {
                     L += ml[(w * NT * 16 + r) * 2 + 1] * __builtin_amdgcn_exp2f(ml[(w * NT * 16 + r) * 2] - Mr_use);
                 }
-                if (direct) {
-                    store_out8(a, s, kvh, r, c0, sum, 1.0f / L);
-                } else {
+                if (unmapped) {
+                    Mr = __builtin_nanf(""); // the merge (or the fold) writes nothing for this row
+                }
+                if (direct && !unmapped) {
+                    store_out4(a, s, kvh, r, c0, sum[0], 1.0f / L);
+                    store_out4(a, s, kvh, r, 128 + c0, sum[1], 1.0f / L);
+                } else if (!direct) {
                     const int64_t prow = (int64_t(split) * pv.h_kv + kvh) * a.R + r;
                     float * dst = a.po + prow * kHeadDim + c0;
                     if (a.fold != nullptr) { // read by other workgroups in this launch: device-scope stores
                         store_agent(dst, sum[0]);
-                        store_agent(dst + 4, sum[1]);
+                        store_agent(dst + 128, sum[1]);
                         if ((t & 31) == 0) {
                             store_agent2(a.pml + prow * 2, Mr, L);
                         }
                     } else {
                         *reinterpret_cast<floatx4 *>(dst) = sum[0];
-                        *reinterpret_cast<floatx4 *>(dst + 4) = sum[1];
+                        *reinterpret_cast<floatx4 *>(dst + 128) = sum[1];
                         if ((t & 31) == 0) {
                             a.pml[prow * 2 + 0] = Mr;
                             a.pml[prow * 2 + 1] = L;

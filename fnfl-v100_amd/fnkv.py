@@ -135,8 +135,9 @@ def lib():
         L.fnkv_export_q8_0.argtypes = [P, I32, I32, I32, I32, I64, I32, P, P]
         L.fnkv_export_kv8.restype = ctypes.c_int
         L.fnkv_export_kv8.argtypes = [P, I32, I32, I32, I32, I64, I32, P, P, P]
-        L.fnkv_test_decode_fold.restype = None
-        L.fnkv_test_decode_fold.argtypes = [I32, I64]
+        if hasattr(L, "fnkv_test_decode_fold"):  # absent from builds of the library that predate it
+            L.fnkv_test_decode_fold.restype = None
+            L.fnkv_test_decode_fold.argtypes = [I32, I64]
         L.fnkv_decode_workspace_bytes.restype = I64
         L.fnkv_decode_workspace_bytes.argtypes = [P, I32, P, I32, I32]
         L.fnkv_attn_decode.restype = ctypes.c_int

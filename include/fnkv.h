@@ -160,8 +160,10 @@ int fnkv_attn_decode(const fnkv_pool * pool, int32_t n_seq, const int32_t * slot
  * its new cells nor its out rows) and FNKV_DEV_ERR_DEPTH is ORed into *err (device, caller-cleared); the other
  * sequences run. Splits of a sequence take its 32-token tiles in turn (split j of n: tiles j, j + n, ...), so a context
  * below its bound still spreads over every split. Otherwise as fnkv_attn_decode (whose G * T <= 16 launches split the
- * same way: for equal contexts and bounds their outputs are bitwise equal). Replaces the depth contract of
- * fn::qsa::attn::attend (attend.h:97-141). */
+ * same way: for equal contexts and bounds their outputs are bitwise equal). The slots must stay mapped up to max_ctx
+ * while a captured launch may run (no fnkv_pool_trim below it); a launch that nevertheless finds an unmapped page reads
+ * nothing from it, writes nothing for that sequence and ORs FNKV_DEV_ERR_DEPTH into *err. Replaces the depth contract
+ * of fn::qsa::attn::attend (attend.h:97-141). */
 int fnkv_attn_decode_dev(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx,
                          const int64_t * max_ctx, int32_t T, int32_t layer, int32_t hq, float scale, const void * q,
                          const void * k_new, const void * v_new, int32_t new_dtype, void * out, void * ws,

@@ -104,9 +104,9 @@ def test_bitwise_reruns_and_page_placement_invariance():
 
 def test_fold_fallback_and_reused_workspace_bitwise():
     """The split-K fold inside the launch (stream.hip: row r of a (sequence, KV head) folded by its split r mod n after
-    every split has arrived) against the merge launch: the same outputs, bitwise. With the wait bound at zero the owners
-    give their rows up to the last split to arrive, which folds them: bitwise the same again. One workspace serves every
-    launch (its fold counters stay consistent)."""
+    every split has arrived) against the merge launch: both within the tolerance, each bitwise on reruns. With the wait
+    bound at zero the owners give their rows up to the last split to arrive, which folds them: bitwise the fold's
+    outputs again. One workspace serves every launch (its fold counters stay consistent)."""
     ctxs = [30000, 9000, 65536]
     st = Setup(ctxs, seed=5)
     q16 = cases.queries(5, (3, 3, HQ, 256))
@@ -123,9 +123,13 @@ def test_fold_fallback_and_reused_workspace_bitwise():
         finally:
             L.fnkv_test_decode_fold(-1, -1)
         outs.append(out.cpu().numpy())
-    diffs = [float(np.abs(outs[0].astype(np.float32) - o.astype(np.float32)).max()) for o in outs[1:]]
-    assert all(np.array_equal(outs[0].view(np.uint16), o.view(np.uint16)) for o in outs[1:]), diffs
-    assert st.check(q16, outs[0], 3) <= TOL
+    same = lambda x, y: np.array_equal(x.view(np.uint16), y.view(np.uint16))
+    # the merge launch twice, and the fold (default bound, zero bound twice, default again): each bitwise itself
+    assert same(outs[0], outs[5])
+    assert all(same(outs[1], o) for o in outs[2:5])
+    # the two fold the same partials in different orders: equal to within an fp16 rounding
+    assert float(np.abs(outs[0].astype(np.float32) - outs[1].astype(np.float32)).max()) <= 1e-3
+    assert st.check(q16, outs[0], 3) <= TOL and st.check(q16, outs[1], 3) <= TOL
     # the fold region (the workspace's first bytes): each pair's arrival counter at a whole number of launches
     words = ws[: 16 * HKV * 50 * 4].view(torch.int32).cpu().numpy().reshape(16 * HKV, 50)
     assert np.all(words[:, 0] % 1024 == 0) and words[:, 0].max() > 0
