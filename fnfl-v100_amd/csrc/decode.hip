@@ -1297,14 +1297,14 @@ struct dec_plan {
     bool fold = false; // the stream kernel folds the splits itself (no merge launch)
 };
 
-// dense launches of at most two row tiles run the stream kernel (stream.hip), the rest decode_kernel<3>
-bool uses_stream(int32_t R) { return R <= 32; }
+// dense launches run the stream kernel (stream.hip)
+bool uses_stream(int32_t R) { return R <= 48; }
 
 dec_plan plan_decode(const kv_pool & p, int32_t n_seq, const int64_t * ctx, int32_t R) {
     dec_plan pl;
     const int32_t cus = device_cus(p.device());
     pl.split_tokens =
-        uses_stream(R) ? choose_split_stream(n_seq, ctx, p.h_kv(), cus) : choose_split(n_seq, ctx, p.h_kv(), cus);
+        uses_stream(R) ? choose_split_stream(n_seq, ctx, p.h_kv(), cus, (R + 15) / 16) : choose_split(n_seq, ctx, p.h_kv(), cus);
     // tuning knob for measurement: FNKV_SPLIT_TOKENS (a multiple of 32 from 256 to 2,048), read once per process
     static const int32_t split_knob = env_int_once("FNKV_SPLIT_TOKENS", 0);
     if (split_knob >= kPageTokens && split_knob <= 8 * kPageTokens && split_knob % kTileTokens == 0) {

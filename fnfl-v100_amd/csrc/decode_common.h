@@ -553,10 +553,10 @@ struct merge_args {
 class kv_pool;
 // host: the merge launch, and the sparse instantiation of the decode kernels (decode.hip)
 void launch_merge(const merge_args & m, hipStream_t st);
-// host: the dense launch's one-stream-a-wave kernel for NT = 1 or 2 row tiles (stream.hip)
+// host: the dense launch's one-stream-a-wave kernel for NT = 1 .. 3 row tiles (stream.hip)
 void launch_stream(int32_t device, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st);
-// the split size (cells) of a dense launch run by the stream kernel
-int32_t choose_split_stream(int32_t n_seq, const int64_t * ctx, int32_t h_kv, int32_t cus);
+// the split size (cells) of a dense launch run by the stream kernel with NT row tiles
+int32_t choose_split_stream(int32_t n_seq, const int64_t * ctx, int32_t h_kv, int32_t cus, int32_t NT);
 void launch_decode_sparse(const kv_pool & p, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st);
 // host: a sparse launch over the pool (sparse.hip), optionally with the gated merge (merge_args' gated form)
 struct sparse_gate {

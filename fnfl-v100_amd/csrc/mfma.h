@@ -208,10 +208,12 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void * base, int32_t bytes) {
 __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, int32_t voff, int32_t soff) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kStreamAux));
 }
-// a wave's 64 x 16 B at base + soff + 16 lane straight into LDS at lds_base + 16 lane
+// a wave's 64 x 16 B at base + soff + 16 lane straight into LDS at lds_base + 16 lane (cache policy AUX: the streaming
+// bit, or 0 where another wave reads the same bytes right after)
+template <int AUX = kStreamAux>
 __device__ __forceinline__ void buf_lds16(rsrc_t r, void * lds_base, int32_t voff, int32_t soff) {
     typedef __attribute__((address_space(3))) void lds_void;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_base, 16, voff, soff, 0, kStreamAux);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_base, 16, voff, soff, 0, AUX);
     keep_issued();
 }
 

@@ -37,13 +37,20 @@
 namespace fnkv {
 
 template <int NT> struct stream_shape {
-    static_assert(NT == 1 || NT == 2, "the accumulators of at most two row tiles fit a wave's registers");
+    static_assert(NT >= 1 && NT <= 3, "G T <= 48 rows");
     static constexpr int WAVES = 8;
+    // NT = 3: the rows split over two waves of a SIMD that walk the same tiles (waves 0-3 row tiles 0 and 1, waves
+    // 4-7 row tile 2: a wave's accumulators for at most two row tiles fit its registers); each loads the tile itself,
+    // the second load served by L2 (cacheable loads). NT <= 2: each wave its own tile stream, every row tile,
+    // streaming loads.
+    static constexpr int GROUPS = NT == 3 ? 2 : 1;
+    static constexpr int STREAMS = WAVES / GROUPS;
+    static constexpr int AUX = NT == 3 ? 0 : kStreamAux;
     static constexpr int SLOT = kTileBytes;          // a tile, in its HBM layout
     static constexpr int RING = WAVES * SLOT;        // 139,264 B
     static constexpr int QOPS = NT * kBlocks * 1024; // the Q operands: [row tile][block][lane] 16 B
     static constexpr int OSTRIDE = kHeadDim + 4;     // floats a row of the fold buffer
-    static constexpr int FOLD = WAVES * 16 * OSTRIDE * 4 + WAVES * NT * 16 * 2 * 4;
+    static constexpr int FOLD = STREAMS * 16 * OSTRIDE * 4 + NT * 16 * STREAMS * 2 * 4;
     static constexpr int LDS = RING + QOPS > FOLD ? RING + QOPS : FOLD;
     static_assert(LDS <= 160 * 1024, "LDS");
     // a half tile is 9 loads: 8 chunks of codes and half of the scales chunk; the wave waits for one half with the
@@ -389,7 +396,7 @@ __device__ void fold_splits(const dec_args & a, int32_t s, int32_t kvh, int32_t 
 template <int NT>
 __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     using SH = stream_shape<NT>;
-    constexpr int WAVES = SH::WAVES;
+    constexpr int WAVES = SH::WAVES, STREAMS = SH::STREAMS;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
     const int32_t wave = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(threadIdx.x) >> 6);
@@ -445,15 +452,16 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
         }
     }
 
-    // this wave's tiles: walk tiles wave, wave + 8, ...
-    const int32_t n_w = __builtin_amdgcn_readfirstlane(n_tiles > wave ? (n_tiles - wave + WAVES - 1) / WAVES : 0);
+    // this wave's tile stream (walk tiles st, st + STREAMS, ...) and row group (its row tiles)
+    const int32_t st = wave % STREAMS, grp = wave / STREAMS;
+    const int32_t n_w = __builtin_amdgcn_readfirstlane(n_tiles > st ? (n_tiles - st + STREAMS - 1) / STREAMS : 0);
     const uint8_t * layer_base = pv.base + int64_t(a.layer) * pv.layer_stride + int64_t(kvh) * kPageBlock;
     uint8_t * const slot = smem + wave * SH::SLOT;
     const int32_t lane16 = lane * 16;
     // iteration i's tile; past the wave's last tile a placeholder (the first tile, every lane reading its first
     // 16 bytes of each chunk), so every iteration issues the same loads and the waits are fixed counts
     auto tile_at = [&](int32_t i) -> const uint8_t * {
-        const int32_t ti = i < n_w ? wave + i * WAVES : 0;
+        const int32_t ti = i < n_w ? st + i * STREAMS : 0;
         return layer_base + src.tile_off(pv, n_tiles > 0 ? ti : 0);
     };
     // half V = 0: the K codes (chunks 0-7) and the K scales (the scales chunk's lanes 0-31); V = 1: the V codes
@@ -463,10 +471,10 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
         const int32_t voff = i < n_w ? lane16 : 0;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            buf_lds16(r, slot + (8 * V + c) * 1024, voff, (8 * V + c) * 1024);
+            buf_lds16<SH::AUX>(r, slot + (8 * V + c) * 1024, voff, (8 * V + c) * 1024);
         }
         if ((lane >> 5) == V) {
-            buf_lds16(r, slot + kKScales, voff, kKScales);
+            buf_lds16<SH::AUX>(r, slot + kKScales, voff, kKScales);
         }
         keep_issued();
     };
@@ -481,209 +489,232 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     }
     barrier_keep_loads(); // the Q operands are in LDS (the tile loads stay in flight)
     FNKV_STAMP(1);
-    // each lane's bias operands (the rows' per-block q sums) and each row's last visible cell
-    half8 sig[NT];
-    int64_t lim[NT];
-#pragma unroll
-    for (int rt = 0; rt < NT; ++rt) {
-        half8 qop[kBlocks];
-#pragma unroll
-        for (int b = 0; b < kBlocks; ++b) {
-            qop[b] = *reinterpret_cast<const half8 *>(qs + (rt * kBlocks + b) * 1024 + lane * 16);
-        }
-        sig[rt] = q_sums(qop, qg);
-        lim[rt] = ctx - a.T + t_of_row(a, rt, j);
-    }
-    floatx4 acc[NT][kBlocks][2];
-    floatx4 lv[NT]; // lane (row j, qg): rows 4 qg + e of sum_t P s_v[t][b] (b < 8) and sum_t P (row 8)
-    float m_run[NT];
-#pragma unroll
-    for (int rt = 0; rt < NT; ++rt) {
-        lv[rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-        m_run[rt] = kNegInf;
-#pragma unroll
-        for (int b = 0; b < kBlocks; ++b) {
-            acc[rt][b][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-            acc[rt][b][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-    }
+    const int32_t n_split = a.split0[s + 1] - a.split0[s];
+    const bool direct = a.fold != nullptr && n_split == 1;
     const half8 zero8 = {};
     const _Float16 one = static_cast<_Float16>(1.0f);
     const half8 ones8 = {one, one, one, one, one, one, one, one};
 
-    // Iteration i: wait for K(i), scores, issue K(i + 1), softmax, wait for V(i), PV, issue V(i + 1).
-    FNKV_PHASE_DECL();
-    for (int32_t i = 0; i < n_w; ++i) {
-        FNKV_PHASE(0 + (i > 0 ? 7 : 0));
-        wait_vmcnt<SH::HALF_LOADS>(); // K(i) has landed (V(i) may be pending)
-        FNKV_PHASE(1);
-        // the scores and the softmax are the longer dependent chain: their wave issues first on a shared SIMD, so
-        // the two waves of a SIMD alternate phases rather than one running ahead
-        __builtin_amdgcn_s_setprio(1);
-        const uint8_t * kb = slot;
-        const uint8_t * sc = kb + kKScales;
-        floatx4 scv[NT][2];
-        stream_scores<NT>(kb, sc, qs, sig, j, qg, lane, scv);
-        issue_half(i + 1, 0); // the scores' reads of K(i) are done (their values are in registers)
-        FNKV_PHASE(2);
-        const int64_t tok0 = src.tok0(wave + i * WAVES);
-        half8 ph[NT], pl[NT];
+    // The walk and the fold for a wave holding row tiles RTB .. RTB + NTW - 1 (every wave passes the same barriers)
+    auto run = [&](auto ntw_c, auto rtb_c) {
+        constexpr int32_t NTW = decltype(ntw_c)::value, RTB = decltype(rtb_c)::value;
+        const uint8_t * const qw = qs + RTB * kBlocks * 1024; // this wave's row tiles' Q operands
+        // each lane's bias operands (the rows' per-block q sums) and each row's last visible cell
+        half8 sig[NTW];
+        int64_t lim[NTW];
 #pragma unroll
-        for (int rt = 0; rt < NT; ++rt) {
-            const int64_t lr = lim[rt] - tok0;
-            const int32_t lim_rel = lr > 64 ? 64 : static_cast<int32_t>(lr < -1 ? -1 : lr);
-            float pf[8];
-            float alpha;
-            stream_softmax(scv[rt], lim_rel, a.c2, qg, m_run[rt], pf, alpha);
-            if (__any(alpha != 1.0f)) {
-#pragma unroll
-                for (int b = 0; b < kBlocks; ++b) {
-                    acc[rt][b][0] *= alpha;
-                    acc[rt][b][1] *= alpha;
-                }
-                lv[rt] *= alpha;
-            }
-            split_hilo(pf, ph[rt], pl[rt]);
-        }
-        FNKV_PHASE(3);
-        __builtin_amdgcn_s_setprio(0);
-        wait_vmcnt<SH::HALF_LOADS>(); // V(i) has landed (K(i + 1) may be pending)
-        FNKV_PHASE(4);
-        // A of the bias MFMAs: lane (block j < 8, qg) holds s_v[token(qg, slot)][j], lanes j = 8 ones (l)
-        const half8 sva = j < 8 ? *reinterpret_cast<const half8 *>(sc + 512 + qg * 128 + j * 16) : j == 8 ? ones8 : zero8;
-#pragma unroll
-        for (int rt = 0; rt < NT; ++rt) {
-            lv[rt] = mfma16(sva, ph[rt], lv[rt]);
-            lv[rt] = mfma16(sva, pl[rt], lv[rt]);
-        }
-#pragma unroll
-        for (int b = 0; b < kBlocks; ++b) {
-            const u32x4 vw = *reinterpret_cast<const u32x4 *>(kb + kVCodes + b * 1024 + lane * 16);
-            const half8 va0 = widen8<false>(vw[0], vw[1]);
-            const half8 va1 = widen8<false>(vw[2], vw[3]);
-            const half8 vs = *reinterpret_cast<const half8 *>(sc + 512 + qg * 128 + b * 16);
-#pragma unroll
-            for (int rt = 0; rt < NT; ++rt) {
-                half8 hi, lo;
-                scale_hilo_pk(ph[rt], pl[rt], vs, hi, lo);
-                acc[rt][b][0] = mfma16(va0, hi, acc[rt][b][0]);
-                acc[rt][b][1] = mfma16(va1, hi, acc[rt][b][1]);
-                acc[rt][b][0] = mfma16(va0, lo, acc[rt][b][0]);
-                acc[rt][b][1] = mfma16(va1, lo, acc[rt][b][1]);
-            }
-            __builtin_amdgcn_sched_barrier(0); // one block's operands live at a time
-        }
-        issue_half(i + 1, 1);
-        FNKV_PHASE(5);
-    }
-    FNKV_PHASE_STORE();
-    wait_vmcnt<0>();
-    FNKV_STAMP_WAVE();
-
-    // the V bias: acc[rt][b] carries 1152 lv[rt][b]; lv[rt][b] of this lane's row sits in lane (j, b / 4), element
-    // b % 4; the row's l in lane (j, 2), element 0
-    float l_row[NT];
-#pragma unroll
-    for (int rt = 0; rt < NT; ++rt) {
-#pragma unroll
-        for (int b = 0; b < kBlocks; ++b) {
-            const float lb = __shfl(lv[rt][b & 3], j + 16 * (b >> 2));
-            acc[rt][b][0] -= 1152.0f * lb;
-            acc[rt][b][1] -= 1152.0f * lb;
-        }
-        l_row[rt] = __shfl(lv[rt][0], j + 32);
-    }
-
-    // ---- fold the eight waves per row in LDS (fixed order), then the workgroup's row: the output itself when the
-    // split is its sequence's only one, else the split's partial (and, with the in-kernel fold, its arrival) ----
-    constexpr int32_t OS = SH::OSTRIDE;
-    const int32_t n_split = a.split0[s + 1] - a.split0[s];
-    const bool direct = a.fold != nullptr && n_split == 1;
-    __syncthreads(); // the slots are no longer read
-    FNKV_STAMP(2);
-    float * ml = reinterpret_cast<float *>(smem);                          // [wave][NT 16 rows][2]
-    float * ob = reinterpret_cast<float *>(smem + WAVES * NT * 16 * 2 * 4); // [wave][16 rows][OS]
-    if (qg == 0) {
-#pragma unroll
-        for (int rt = 0; rt < NT; ++rt) {
-            ml[(wave * NT * 16 + rt * 16 + j) * 2 + 0] = m_run[rt];
-            ml[(wave * NT * 16 + rt * 16 + j) * 2 + 1] = l_row[rt];
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int rt = 0; rt < NT; ++rt) {
-        float M = kNegInf;
-#pragma unroll
-        for (int w = 0; w < WAVES; ++w) {
-            M = fmaxf(M, ml[(w * NT * 16 + rt * 16 + j) * 2]);
-        }
-        const float f = __builtin_amdgcn_exp2f(m_run[rt] - (M == kNegInf ? 0.0f : M));
-        if (rt * 16 + j < a.R) { // padding rows are not folded
+        for (int rt = 0; rt < NTW; ++rt) {
+            half8 qop[kBlocks];
 #pragma unroll
             for (int b = 0; b < kBlocks; ++b) {
+                qop[b] = *reinterpret_cast<const half8 *>(qw + (rt * kBlocks + b) * 1024 + lane * 16);
+            }
+            sig[rt] = q_sums(qop, qg);
+            lim[rt] = ctx - a.T + t_of_row(a, RTB + rt, j);
+        }
+        floatx4 acc[NTW][kBlocks][2];
+        floatx4 lv[NTW]; // lane (row j, qg): rows 4 qg + e of sum_t P s_v[t][b] (b < 8) and sum_t P (row 8)
+        float m_run[NTW];
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    *reinterpret_cast<floatx4 *>(ob + (wave * 16 + j) * OS + 16 * (2 * b + hh) + 4 * qg) =
-                        acc[rt][b][hh] * f;
+        for (int rt = 0; rt < NTW; ++rt) {
+            lv[rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            m_run[rt] = kNegInf;
+#pragma unroll
+            for (int b = 0; b < kBlocks; ++b) {
+                acc[rt][b][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                acc[rt][b][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+
+        // Iteration i: wait for K(i), scores, issue K(i + 1), softmax, wait for V(i), PV, issue V(i + 1).
+        FNKV_PHASE_DECL();
+        for (int32_t i = 0; i < n_w; ++i) {
+            FNKV_PHASE(0 + (i > 0 ? 7 : 0));
+            wait_vmcnt<SH::HALF_LOADS>(); // K(i) has landed (V(i) may be pending)
+            FNKV_PHASE(1);
+            // the scores and the softmax are the longer dependent chain: their wave issues first on a shared SIMD,
+            // so the two waves of a SIMD alternate phases rather than one running ahead
+            __builtin_amdgcn_s_setprio(1);
+            const uint8_t * kb = slot;
+            const uint8_t * sc = kb + kKScales;
+            floatx4 scv[NTW][2];
+            stream_scores<NTW>(kb, sc, qw, sig, j, qg, lane, scv);
+            issue_half(i + 1, 0); // the scores' reads of K(i) are done (their values are in registers)
+            FNKV_PHASE(2);
+            const int64_t tok0 = src.tok0(st + i * STREAMS);
+            half8 ph[NTW], pl[NTW];
+#pragma unroll
+            for (int rt = 0; rt < NTW; ++rt) {
+                const int64_t lr = lim[rt] - tok0;
+                const int32_t lim_rel = lr > 64 ? 64 : static_cast<int32_t>(lr < -1 ? -1 : lr);
+                float pf[8];
+                float alpha;
+                stream_softmax(scv[rt], lim_rel, a.c2, qg, m_run[rt], pf, alpha);
+                if (__any(alpha != 1.0f)) {
+#pragma unroll
+                    for (int b = 0; b < kBlocks; ++b) {
+                        acc[rt][b][0] *= alpha;
+                        acc[rt][b][1] *= alpha;
+                    }
+                    lv[rt] *= alpha;
                 }
+                split_hilo(pf, ph[rt], pl[rt]);
+            }
+            FNKV_PHASE(3);
+            __builtin_amdgcn_s_setprio(0);
+            wait_vmcnt<SH::HALF_LOADS>(); // V(i) has landed (K(i + 1) may be pending)
+            FNKV_PHASE(4);
+            // A of the bias MFMAs: lane (block j < 8, qg) holds s_v[token(qg, slot)][j], lanes j = 8 ones (l)
+            const half8 sva =
+                j < 8 ? *reinterpret_cast<const half8 *>(sc + 512 + qg * 128 + j * 16) : j == 8 ? ones8 : zero8;
+#pragma unroll
+            for (int rt = 0; rt < NTW; ++rt) {
+                lv[rt] = mfma16(sva, ph[rt], lv[rt]);
+                lv[rt] = mfma16(sva, pl[rt], lv[rt]);
+            }
+#pragma unroll
+            for (int b = 0; b < kBlocks; ++b) {
+                const u32x4 vw = *reinterpret_cast<const u32x4 *>(kb + kVCodes + b * 1024 + lane * 16);
+                const half8 va0 = widen8<false>(vw[0], vw[1]);
+                const half8 va1 = widen8<false>(vw[2], vw[3]);
+                const half8 vs = *reinterpret_cast<const half8 *>(sc + 512 + qg * 128 + b * 16);
+#pragma unroll
+                for (int rt = 0; rt < NTW; ++rt) {
+                    half8 hi, lo;
+                    scale_hilo_pk(ph[rt], pl[rt], vs, hi, lo);
+                    acc[rt][b][0] = mfma16(va0, hi, acc[rt][b][0]);
+                    acc[rt][b][1] = mfma16(va1, hi, acc[rt][b][1]);
+                    acc[rt][b][0] = mfma16(va0, lo, acc[rt][b][0]);
+                    acc[rt][b][1] = mfma16(va1, lo, acc[rt][b][1]);
+                }
+                __builtin_amdgcn_sched_barrier(0); // one block's operands live at a time
+            }
+            issue_half(i + 1, 1);
+            FNKV_PHASE(5);
+        }
+        FNKV_PHASE_STORE();
+        wait_vmcnt<0>();
+        FNKV_STAMP_WAVE();
+
+        // the V bias: acc[rt][b] carries 1152 lv[rt][b]; lv[rt][b] of this lane's row sits in lane (j, b / 4),
+        // element b % 4; the row's l in lane (j, 2), element 0
+        float l_row[NTW];
+#pragma unroll
+        for (int rt = 0; rt < NTW; ++rt) {
+#pragma unroll
+            for (int b = 0; b < kBlocks; ++b) {
+                const float lb = __shfl(lv[rt][b & 3], j + 16 * (b >> 2));
+                acc[rt][b][0] -= 1152.0f * lb;
+                acc[rt][b][1] -= 1152.0f * lb;
+            }
+            l_row[rt] = __shfl(lv[rt][0], j + 32);
+        }
+
+        // ---- fold the STREAMS waves holding each row tile in LDS (fixed order), then the workgroup's row: the
+        // output itself when the split is its sequence's only one, else the split's partial ----
+        constexpr int32_t OS = SH::OSTRIDE;
+        const int32_t h = st; // this wave's place among the row tiles' holders
+        __syncthreads();      // the slots are no longer read
+        FNKV_STAMP(2);
+        float * ml = reinterpret_cast<float *>(smem);                              // [NT 16 rows][holder][2]
+        float * ob = reinterpret_cast<float *>(smem + NT * 16 * STREAMS * 2 * 4);  // [holder][16 rows][OS]
+        if (qg == 0) {
+#pragma unroll
+            for (int rt = 0; rt < NTW; ++rt) {
+                ml[(((RTB + rt) * 16 + j) * STREAMS + h) * 2 + 0] = m_run[rt];
+                ml[(((RTB + rt) * 16 + j) * STREAMS + h) * 2 + 1] = l_row[rt];
             }
         }
         __syncthreads();
-        // thread -> (row, values c0 .. c0 + 3 and 128 + c0 .. + 3): 16 rows x 32 groups (a row's 32 threads read
-        // consecutive 16-byte pieces, conflict-free)
-        {
-            const int32_t t = static_cast<int32_t>(threadIdx.x);
-            const int32_t rrow = t >> 5, c0 = (t & 31) * 4;
-            const int32_t r = rt * 16 + rrow;
-            if (r < a.R) {
-                floatx4 sum[2];
 #pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    sum[c] = *reinterpret_cast<const floatx4 *>(ob + rrow * OS + c0 + 128 * c);
+        for (int rt = 0; rt < NT; ++rt) {
+            // this wave holds row tile rt as its rl-th (a constant once the loop is unrolled)
+            const int32_t rl = rt < RTB ? 0 : (rt - RTB >= NTW ? NTW - 1 : rt - RTB);
+            if (rt >= RTB && rt < RTB + NTW) {
+                const float * mlr = ml + ((rt * 16 + j) * STREAMS) * 2;
+                float M = kNegInf;
 #pragma unroll
-                    for (int w = 1; w < WAVES; ++w) {
-                        sum[c] += *reinterpret_cast<const floatx4 *>(ob + (w * 16 + rrow) * OS + c0 + 128 * c);
-                    }
+                for (int w = 0; w < STREAMS; ++w) {
+                    M = fmaxf(M, mlr[2 * w]);
                 }
-                float Mr = kNegInf;
+                const float f = __builtin_amdgcn_exp2f(m_run[rl] - (M == kNegInf ? 0.0f : M));
+                if (rt * 16 + j < a.R) { // padding rows are not folded
 #pragma unroll
-                for (int w = 0; w < WAVES; ++w) {
-                    Mr = fmaxf(Mr, ml[(w * NT * 16 + r) * 2]);
-                }
-                const float Mr_use = Mr == kNegInf ? 0.0f : Mr;
-                float L = 0.0f;
+                    for (int b = 0; b < kBlocks; ++b) {
 #pragma unroll
-                for (int w = 0; w < WAVES; ++w) {
-                    L += ml[(w * NT * 16 + r) * 2 + 1] * __builtin_amdgcn_exp2f(ml[(w * NT * 16 + r) * 2] - Mr_use);
-                }
-                if (unmapped) {
-                    Mr = __builtin_nanf(""); // the merge (or the fold) writes nothing for this row
-                }
-                if (direct && !unmapped) {
-                    store_out4(a, s, kvh, r, c0, sum[0], 1.0f / L);
-                    store_out4(a, s, kvh, r, 128 + c0, sum[1], 1.0f / L);
-                } else if (!direct) {
-                    const int64_t prow = (int64_t(split) * pv.h_kv + kvh) * a.R + r;
-                    float * dst = a.po + prow * kHeadDim + c0;
-                    if (a.fold != nullptr) { // read by other workgroups in this launch: device-scope stores
-                        store_agent(dst, sum[0]);
-                        store_agent(dst + 128, sum[1]);
-                        if ((t & 31) == 0) {
-                            store_agent2(a.pml + prow * 2, Mr, L);
-                        }
-                    } else {
-                        *reinterpret_cast<floatx4 *>(dst) = sum[0];
-                        *reinterpret_cast<floatx4 *>(dst + 128) = sum[1];
-                        if ((t & 31) == 0) {
-                            a.pml[prow * 2 + 0] = Mr;
-                            a.pml[prow * 2 + 1] = L;
+                        for (int hh = 0; hh < 2; ++hh) {
+                            *reinterpret_cast<floatx4 *>(ob + (h * 16 + j) * OS + 16 * (2 * b + hh) + 4 * qg) =
+                                acc[rl][b][hh] * f;
                         }
                     }
                 }
             }
+            __syncthreads();
+            // thread -> (row, values c0 .. c0 + 3 and 128 + c0 .. + 3): 16 rows x 32 groups (a row's 32 threads
+            // read consecutive 16-byte pieces, conflict-free)
+            {
+                const int32_t t = static_cast<int32_t>(threadIdx.x);
+                const int32_t rrow = t >> 5, c0 = (t & 31) * 4;
+                const int32_t r = rt * 16 + rrow;
+                if (r < a.R) {
+                    floatx4 sum[2];
+#pragma unroll
+                    for (int c = 0; c < 2; ++c) {
+                        sum[c] = *reinterpret_cast<const floatx4 *>(ob + rrow * OS + c0 + 128 * c);
+#pragma unroll
+                        for (int w = 1; w < STREAMS; ++w) {
+                            sum[c] += *reinterpret_cast<const floatx4 *>(ob + (w * 16 + rrow) * OS + c0 + 128 * c);
+                        }
+                    }
+                    const float * mlr = ml + (r * STREAMS) * 2;
+                    float Mr = kNegInf;
+#pragma unroll
+                    for (int w = 0; w < STREAMS; ++w) {
+                        Mr = fmaxf(Mr, mlr[2 * w]);
+                    }
+                    const float Mr_use = Mr == kNegInf ? 0.0f : Mr;
+                    float L = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < STREAMS; ++w) {
+                        L += mlr[2 * w + 1] * __builtin_amdgcn_exp2f(mlr[2 * w] - Mr_use);
+                    }
+                    if (unmapped) {
+                        Mr = __builtin_nanf(""); // the merge (or the fold) writes nothing for this row
+                    }
+                    if (direct && !unmapped) {
+                        store_out4(a, s, kvh, r, c0, sum[0], 1.0f / L);
+                        store_out4(a, s, kvh, r, 128 + c0, sum[1], 1.0f / L);
+                    } else if (!direct) {
+                        const int64_t prow = (int64_t(split) * pv.h_kv + kvh) * a.R + r;
+                        float * dst = a.po + prow * kHeadDim + c0;
+                        if (a.fold != nullptr) { // read by other workgroups in this launch: device-scope stores
+                            store_agent(dst, sum[0]);
+                            store_agent(dst + 128, sum[1]);
+                            if ((t & 31) == 0) {
+                                store_agent2(a.pml + prow * 2, Mr, L);
+                            }
+                        } else {
+                            *reinterpret_cast<floatx4 *>(dst) = sum[0];
+                            *reinterpret_cast<floatx4 *>(dst + 128) = sum[1];
+                            if ((t & 31) == 0) {
+                                a.pml[prow * 2 + 0] = Mr;
+                                a.pml[prow * 2 + 1] = L;
+                            }
+                        }
+                    }
+                }
+            }
+            __syncthreads(); // ob is rewritten by the next row tile
         }
-        __syncthreads(); // ob is rewritten by the next row tile
+    };
+    if constexpr (SH::GROUPS == 1) {
+        run(std::integral_constant<int32_t, NT>(), std::integral_constant<int32_t, 0>());
+    } else {
+        if (grp == 0) {
+            run(std::integral_constant<int32_t, 2>(), std::integral_constant<int32_t, 0>());
+        } else {
+            run(std::integral_constant<int32_t, 1>(), std::integral_constant<int32_t, 2>());
+        }
     }
     FNKV_STAMP(3);
     if (a.fold != nullptr && !direct) {
@@ -693,23 +724,24 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
 }
 
 // The split size (cells) for these contexts: the fewest rounds of one workgroup a CU times a workgroup's time, which
-// is its waves' longest walk (an eighth of the split's tiles, rounded up) plus a fixed cost (the ramp, the fold of the
+// is its waves' longest walk (the split's tiles over its tile streams, rounded up) plus a fixed cost (the ramp, the fold of the
 // waves and the partial's write, counted as three tiles); larger splits (fewer partials) win ties.
-int32_t choose_split_stream(int32_t n_seq, const int64_t * ctx, int32_t h_kv, int32_t cus) {
+int32_t choose_split_stream(int32_t n_seq, const int64_t * ctx, int32_t h_kv, int32_t cus, int32_t NT) {
+    const int32_t streams = NT == 3 ? stream_shape<3>::STREAMS : stream_shape<1>::STREAMS;
     int32_t best = kPageTokens;
     int64_t best_cost = INT64_MAX;
-    for (int32_t st = kPageTokens; st <= 8 * kPageTokens; st += kTileTokens) {
+    for (int32_t sz = kPageTokens; sz <= 8 * kPageTokens; sz += kTileTokens) {
         int64_t wgs = 0;
         for (int32_t i = 0; i < n_seq; ++i) {
-            wgs += (ctx[i] + st - 1) / st;
+            wgs += (ctx[i] + sz - 1) / sz;
         }
         wgs *= h_kv;
         const int64_t rounds = (wgs + cus - 1) / cus;
-        const int64_t wave_tiles = (st / kTileTokens + stream_shape<1>::WAVES - 1) / stream_shape<1>::WAVES;
+        const int64_t wave_tiles = (sz / kTileTokens + streams - 1) / streams;
         const int64_t cost = rounds * (wave_tiles + 3);
         if (cost <= best_cost) {
             best_cost = cost;
-            best = st;
+            best = sz;
         }
     }
     return best;
@@ -720,7 +752,7 @@ template <int NT> void set_stream_attr() {
                               hipFuncAttributeMaxDynamicSharedMemorySize, stream_shape<NT>::LDS);
 }
 
-// the dense launch's kernel for NT row tiles (1 or 2), its LDS attribute set once per device
+// the dense launch's kernel for NT row tiles (1 .. 3), its LDS attribute set once per device
 void launch_stream(int32_t device, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
     static std::once_flag attr_once[64];
     if (device >= 0 && device < 64) {
@@ -730,6 +762,7 @@ void launch_stream(int32_t device, int32_t NT, dim3 grid, const dec_args & a, hi
             (void)hipSetDevice(device);
             set_stream_attr<1>();
             set_stream_attr<2>();
+            set_stream_attr<3>();
             (void)hipGetLastError();
             (void)hipSetDevice(cur);
         });
@@ -737,8 +770,10 @@ void launch_stream(int32_t device, int32_t NT, dim3 grid, const dec_args & a, hi
     const dim3 block(64 * stream_shape<1>::WAVES);
     if (NT == 1) {
         hipLaunchKernelGGL(stream_kernel<1>, grid, block, stream_shape<1>::LDS, st, a);
-    } else {
+    } else if (NT == 2) {
         hipLaunchKernelGGL(stream_kernel<2>, grid, block, stream_shape<2>::LDS, st, a);
+    } else {
+        hipLaunchKernelGGL(stream_kernel<3>, grid, block, stream_shape<3>::LDS, st, a);
     }
 }
 
