@@ -85,11 +85,14 @@ def algorithmic_bytes(ctxs, T):
     return kv_read + qo + append
 
 
-def make_pool(torch, fnkv, cases, ctxs, T, layers, seed, h_kv=HKV, fmt=None):
-    n_pages = sum(-(-c // 256) for c in ctxs) + 16
+def make_pool(torch, fnkv, cases, ctxs, T, layers, seed, h_kv=HKV, fmt=None, map_to=None):
+    """A pool holding the sequences' first ctxs cells of every layer (seeded K/V, BASELINE's distribution), their pages
+    scattered; map_to (optional, >= ctxs): the cells each slot has mapped (room for the steps' new cells)."""
+    mapped = list(ctxs) if map_to is None else list(map_to)
+    n_pages = sum(-(-c // 256) for c in mapped) + 16
     pool = fnkv.Pool(len(ctxs) + 1, n_pages, layers, h_kv, **({} if fmt is None else {"fmt": fmt}))
     slots = list(range(len(ctxs)))
-    cases.scatter_ensure(pool, slots, ctxs, seed, churn=0.2)
+    cases.scatter_ensure(pool, slots, mapped, seed, churn=0.2)
     g = torch.Generator(device="cuda")
     for layer in range(layers):
         g.manual_seed(seed * 1000 + layer)
@@ -777,6 +780,13 @@ def run_datc(args, cfg):
 
 
 def run_mixed(args, cfg):
+    line, extra = time_mixed(args, cfg)
+    if not args.no_cpu:
+        line["cpu_baseline"] = mixed_cpu_baseline(args, cfg, extra)
+    print(json.dumps(line), flush=True)
+
+
+def time_mixed(args, cfg):
     """a mixed 8-sequence pool step with page churn. Beforehand three finished sequences take
     interleaved pages and free them (holes in the free list), then the eight sequences grow page by page in a seeded
     random order (a fragmented page table). A step = for each of the 12 layers: two sequences each append a 4,096-token
@@ -958,33 +968,43 @@ def run_mixed(args, cfg):
         },
     }
     pool.close()
-    if not args.no_cpu:
-        import oracle as O
-        info = host_info()
-        threads = info["threads"]
-        # decode half: one layer, the six verify sequences; prefill half: the last 16 rows of one chunk, scaled by
-        # visible pairs to both chunks
-        t_dec = 0.0
-        for i, c in enumerate(vf_ctx):
-            t_dec += _cpu_case(O, cases, args.seed + i, c, T, threads)[2]
-        s0 = pf_slots[0]
-        c0 = ctx_of[s0]
-        kb, vb, _ = _cpu_case(O, cases, args.seed + 50, c0, 1, threads)
-        sample = 16
-        q16 = cases.queries(args.seed + 51, (sample, HQ, D)).view(np.uint16)
-        t_s = _best_of(lambda: O.attn_ggml(q16, kb, vb, c0, q_as_q8=True, threads=threads), reps=3)
-        sample_flops = 4 * D * HQ * sum(c0 - sample + t + 1 for t in range(sample))
-        t_pre = t_s * (flops / layers) / sample_flops
-        cpu_step = layers * (t_dec + t_pre)
-        line["cpu_baseline"] = {
-            "value": round((len(pf_slots) * chunk + nv * T) / cpu_step, 3), "unit": "tokens/s", "cores": threads,
-            "kind": "port",
-            "sample": f"one layer's six verify sequences (T={T}, best of 5) and the last {sample} rows of one chunk "
-                      f"(best of 3, scaled by visible pairs to both chunks), ggml-semantics flash attention (Q as "
-                      f"Q8_0; oracle/fnkv_oracle.c or_attn_ggml), {threads} threads, x {layers} layers",
-            "host": info,
-        }
-    print(json.dumps(line), flush=True)
+    return line, dict(vf_ctx=vf_ctx, pf_slots=pf_slots, ctx_of=ctx_of, flops=flops, nv=nv, chunk=chunk, T=T,
+                      layers=layers)
+
+
+def mixed_cpu_baseline(args, cfg, x):
+    """config 4's CPU baseline (the ggml-semantics port), sampled: see the record's "sample"."""
+    import numpy as np
+
+    import cases
+    import oracle as O
+
+    vf_ctx, pf_slots, ctx_of, flops = x["vf_ctx"], x["pf_slots"], x["ctx_of"], x["flops"]
+    nv, chunk, T, layers = x["nv"], x["chunk"], x["T"], x["layers"]
+    info = host_info()
+    threads = info["threads"]
+    # decode half: one layer, the six verify sequences; prefill half: the last 16 rows of one chunk, scaled by
+    # visible pairs to both chunks
+    t_dec = 0.0
+    for i, c in enumerate(vf_ctx):
+        t_dec += _cpu_case(O, cases, args.seed + i, c, T, threads)[2]
+    s0 = pf_slots[0]
+    c0 = ctx_of[s0]
+    kb, vb, _ = _cpu_case(O, cases, args.seed + 50, c0, 1, threads)
+    sample = 16
+    q16 = cases.queries(args.seed + 51, (sample, HQ, D)).view(np.uint16)
+    t_s = _best_of(lambda: O.attn_ggml(q16, kb, vb, c0, q_as_q8=True, threads=threads), reps=3)
+    sample_flops = 4 * D * HQ * sum(c0 - sample + t + 1 for t in range(sample))
+    t_pre = t_s * (flops / layers) / sample_flops
+    cpu_step = layers * (t_dec + t_pre)
+    return {
+        "value": round((len(pf_slots) * chunk + nv * T) / cpu_step, 3), "unit": "tokens/s", "cores": threads,
+        "kind": "port",
+        "sample": f"one layer's six verify sequences (T={T}, best of 5) and the last {sample} rows of one chunk "
+                  f"(best of 3, scaled by visible pairs to both chunks), ggml-semantics flash attention (Q as "
+                  f"Q8_0; oracle/fnkv_oracle.c or_attn_ggml), {threads} threads, x {layers} layers",
+        "host": info,
+    }
 
 
 def main():
@@ -1068,7 +1088,7 @@ def main():
                    "steps_per_graph": r["copies"], "layers_rotated": layers * r["copies"]},
         "gb_s": r["gb_s"],
         "roofline": {
-            "kernel": "fnkv_attn_decode launch (decode_kernel + merge_kernel), per layer",
+            "kernel": "fnkv_attn_decode launch (stream_kernel + merge_row_kernel), per layer",
             "bound": "hbm",
             "achieved": r["achieved"],
             "peak": PEAK_HBM_GBS,
@@ -1090,6 +1110,24 @@ def main():
             also[name] = {"workload": c2["workload"], "launch_us": x["launch_us"], "achieved_gb_s": x["achieved"],
                           "frac": x["frac"], "tokens_s": x["tokens_s"], "bytes_per_launch": x["bytes_per_launch"],
                           "steps": x["n_steps"]}
+        # the engine's own call: device contexts advancing by T every replay of one captured step
+        xd = time_decode_dev(args, torch, fnkv, cases, ctxs, T, layers, 20, 5)
+        also["cfg1_dev"] = {"workload": "cfg1 through fnkv_attn_decode_dev: one captured graph of the 12 launches "
+                                        "and a context advance, replayed as contexts grow by T",
+                            **xd}
+        c0 = CONFIGS["cfg0"]
+        x0 = time_decode(args, torch, fnkv, cases, c0["ctxs"], c0["T"], c0["layers"], c0["copies"], None, 64, 64)
+        also["cfg0"] = {"workload": c0["workload"], "launch_us": x0["launch_us"], "achieved_gb_s": x0["achieved"],
+                        "frac": x0["frac"], "tokens_s": x0["tokens_s"], "bytes_per_launch": x0["bytes_per_launch"],
+                        "steps": x0["n_steps"], "bound": "latency (4,096 cells: fixed costs dominate)"}
+        c4 = CONFIGS["cfg4"]
+        a4 = argparse.Namespace(**{**vars(args), "steps": 2, "warmup": 1})
+        l4, _ = time_mixed(a4, c4)
+        also["cfg4"] = {"workload": c4["workload"], "step_us": l4["step_us"],
+                        "prefill_tflops": l4["roofline"]["achieved"], "prefill_frac": l4["roofline"]["frac"],
+                        "decode_launch_us": l4["decode_part"]["launch_us"],
+                        "decode_gb_s": l4["decode_part"]["achieved"], "decode_frac": l4["decode_part"]["frac"],
+                        "tokens_s": l4["value"]}
         c3 = CONFIGS["cfg3"]
         _, gpu_s, _, _ = time_prefill(args, c3, 3, 1)
         step_s = gpu_s / 3
@@ -1175,6 +1213,65 @@ def time_decode(args, torch, fnkv, cases, ctxs, T, layers, copies, fmt, steps, w
             "gb_s": round(bytes_layer * layers * n_steps / wall / 1e9, 3), "achieved": round(achieved, 3),
             "frac": round(achieved / PEAK_HBM_GBS, 4), "bytes_per_launch": bytes_layer,
             "launch_us": round(launch_s * 1e6, 3)}
+
+
+def time_decode_dev(args, torch, fnkv, cases, ctxs, T, layers, steps, warmup):
+    """The engine's own call (host/engine_step.cpp's pattern, the reference's TG1 depth, attend.h:108): one captured
+    graph of the step's fnkv_attn_decode_dev launches (one a layer; contexts read from device words by the launch,
+    the grid fixed by a host bound) followed by a device add that advances every sequence's context by T, replayed
+    W times untimed and then K times between HIP events: each replay attends over T more cells than the last and
+    appends its own new cells. Returns the per-launch figures at the timed replays' mean context."""
+    n_adv = warmup + steps + 1  # the eager run advances too
+    bound = [c + T * n_adv for c in ctxs]
+    pool, slots = make_pool(torch, fnkv, cases, ctxs, T, layers, args.seed, map_to=bound)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(args.seed + 7)
+    n = len(ctxs)
+    q = torch.randn((layers, n, T, HQ, D), generator=g, device="cuda").half()
+    kn = torch.randn((layers, n, T, HKV, D), generator=g, device="cuda").half()
+    vn = torch.randn((layers, n, T, HKV, D), generator=g, device="cuda").half()
+    out = torch.empty_like(q)
+    ws = torch.zeros(pool.decode_ws_bytes(bound, T, HQ), dtype=torch.uint8, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ctx_dev = torch.tensor(ctxs, dtype=torch.int64, device="cuda")
+
+    def step():
+        for layer in range(layers):
+            pool.decode_dev(slots, ctx_dev, bound, T, layer, q[layer], out[layer], ws, err, k_new=kn[layer],
+                            v_new=vn[layer])
+        ctx_dev.add_(T)
+
+    step()  # the library's one-time set-up outside the capture (and the first advance)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    first = ctx_dev.cpu().tolist()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    gpu_s = ev0.elapsed_time(ev1) / 1e3
+    assert int(err.item()) == 0, "a launch refused its context"
+    assert torch.isfinite(out.float()).all().item(), "non-finite attention output"
+    del graph
+    pool.close()
+    mean_ctx = [c + T * (steps - 1) / 2.0 for c in first]
+    bytes_layer = algorithmic_bytes([int(round(c)) for c in mean_ctx], T)
+    launch_s = gpu_s / (steps * layers)  # a layer's launch pair (the context add spread over the step's 12)
+    achieved = bytes_layer / launch_s / 1e9
+    return {"launch_us": round(launch_s * 1e6, 3), "achieved_gb_s": round(achieved, 3),
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "tokens_s": round(n * T * steps / gpu_s, 3),
+            "bytes_per_launch": bytes_layer, "steps": steps, "contexts_first": first,
+            "step_us": round(gpu_s / steps * 1e6, 3)}
 
 
 if __name__ == "__main__":

@@ -1,32 +1,33 @@
 // Decode and speculative-verify attention over the Q8_0 page pool (T = 1 .. 6 query tokens a sequence), split-K
-// over pages with a log-sum-exp merge.
+// over pages with a log-sum-exp merge: the dense launches' host side (fnkv_attn_decode, _dev, _noalloc; their kernel
+// is stream.hip's), the kernels of the sparse launches over selection bodies (sparse.hip, qsa.hip, qsp.hip run them),
+// and the split merge of both.
 //
-// What it computes (the reference's decode attention, fn/kernels/qsa/attend.h:8-34, made dense and causal over the
-// whole context, on BASELINE's Q8_0 format): for query row (t, head h) of a sequence holding ctx cells,
-//   o = sum_c softmax_c(q . k_c * scale) v_c over cells c <= ctx - T + t, with k_c, v_c the decoded Q8_0 values
-// (code * fp32(d)); scores, softmax statistics and accumulators in fp32; fp16 out. The split-K partials (m, l, acc)
-// fold in a fixed order as the reference's finish does (attend.cu:621-655): M = max m_j, L = sum l_j e^(m_j - M),
-// A = sum acc_j e^(m_j - M), o = A / L.
+// What it computes (the reference's decode attention, fn/kernels/qsa/attend.h:8-34; dense: causal over the whole
+// context, on BASELINE's Q8_0 format): for query row (t, head h) of a sequence holding ctx cells,
+//   o = sum_c softmax_c(q . k_c * scale) v_c over cells c <= ctx - T + t (sparse: over the row's selected cells),
+// with k_c, v_c the decoded Q8_0 values (code * fp32(d)); scores, softmax statistics and accumulators in fp32; fp16
+// out. The split-K partials (m, l, acc) fold in a fixed order as the reference's finish does (attend.cu:621-655):
+// M = max m_j, L = sum l_j e^(m_j - M), A = sum acc_j e^(m_j - M), o = A / L.
 //
-// How (MI355X): HBM-bound, so every byte is read once and the math rides the matrix cores.
-//   * A workgroup of 8 (6 at three row tiles) waves owns one (sequence, KV head, split of the cells). A tile (32
-//     tokens, 17,408 B: K and V codes, K and V scales) arrives as fully coalesced 1 KiB chunks: the K codes and the
-//     scales straight into LDS (global_load_lds / buffer loads to LDS), the V codes into registers.
+// How the sparse kernels run (MI355X): a workgroup owns one (row, KV head, split of the row's selected tiles).
+//   * A tile (32 tokens, 17,408 B: K and V codes, K and V scales) arrives as fully coalesced 1 KiB chunks: the K
+//     codes and the scales straight into LDS (global_load_lds / buffer loads to LDS), the V codes into registers.
 //   * The tile layout (layout.h) puts each lane's 16 B exactly where v_mfma_f32_16x16x32_f16 wants its operand: one
 //     byte permute makes two codes the fp16 values 1152 + code (exact), and one MFMA a tile half takes the 1152 bias
 //     back out (against the K scales and the rows' q sums for S, against the V scales and P for O).
 //   * S^T = K Q^T one Q8_0 block (32 values) per MFMA; the block's scale folds in with one FMA per score. The G query
-//     heads x T tokens sharing the KV head are the MFMA's 16-wide column side (rows padded to 16 n).
+//     heads sharing the KV head are the MFMA's 16-wide column side (rows padded to 16 n).
 //   * Online softmax in the base-2 domain on the S^T registers (a column's 4 lanes reduce with two lane swaps); P
 //     lands as the B operand of O^T = V^T P^T without moving: each PV MFMA covers 16 values of one block, whose V
 //     scale multiplies P once per block; the product goes to the matrix core as hi + lo fp16 (two MFMAs), which
 //     keeps it to ~2^-22 relative where a single fp16 operand would err by 2^-11.
-//   * Row tiles: decode_kernel<1> (up to 16 rows) runs eight independent tile streams, one a wave;
-//     decode_rows_kernel<2> (up to 32) groups two waves on one stream, each computing S and the softmax of its row
-//     tile and PV of half the value blocks for both, P exchanged in LDS; dense launches with up to 48 rows run
-//     decode_kernel<3> (three waves share a stream's K in LDS, each its row tile's S, softmax and PV), sparse ones
-//     decode_rows_kernel<3>.
+//   * Row tiles: decode_kernel<1> (up to 16 heads) runs eight independent tile streams, one a wave;
+//     decode_rows_kernel<2> / <3> (up to 32 / 48) group two / three waves on one stream, each computing S and the
+//     softmax of its row tile and PV of a share of the value blocks for all, P exchanged in LDS.
 //   * The waves' partials merge in LDS; the workgroup writes (m, l, acc[256]) a row; merge_kernel folds the splits.
+// The kernels are templates over SP (sparse); only their sparse instantiations are built (the dense launches moved
+// to stream.hip), so their SP = false branches are not compiled.
 #include "../../include/fnkv.h"
 #include "common.h"
 #include "layout.h"
@@ -1265,29 +1266,6 @@ int32_t device_cus(int32_t device) {
     return n;
 }
 
-// the split size (tokens, a multiple of the 32-token tile from one page to eight) for these contexts: the fewest
-// rounds of one workgroup a CU times the split, preferring larger splits (fewer partials) on ties. Tile granularity
-// lets the splits just fill the device (cfg1's 120 K cells on 256 CUs: 254 workgroups of 31 tiles, not 240 of 32).
-int32_t choose_split(int32_t n_seq, const int64_t * ctx, int32_t h_kv, int32_t cus) {
-    int32_t best = kPageTokens;
-    double best_cost = 1e300;
-    for (int32_t st = kPageTokens; st <= 8 * kPageTokens; st += kTileTokens) { // a split's tiles fit one wave's lanes
-        int64_t wgs = 0;
-        for (int32_t i = 0; i < n_seq; ++i) {
-            wgs += (ctx[i] + st - 1) / st;
-        }
-        wgs *= h_kv;
-        const int64_t rounds = (wgs + cus - 1) / cus;
-        // a workgroup's fixed cost (ramp, partial write and merge) counted as 96 tokens of streaming
-        const double cost = double(rounds) * (double(st) + 96.0);
-        if (cost <= best_cost) {
-            best_cost = cost;
-            best = st;
-        }
-    }
-    return best;
-}
-
 struct dec_plan {
     int32_t split_tokens = 0, total = 0, strided = 0;
     int32_t split0[FNKV_MAX_SEQS + 1] = {0};
@@ -1297,14 +1275,11 @@ struct dec_plan {
     bool fold = false; // the stream kernel folds the splits itself (no merge launch)
 };
 
-// dense launches run the stream kernel (stream.hip)
-bool uses_stream(int32_t R) { return R <= 48; }
-
 dec_plan plan_decode(const kv_pool & p, int32_t n_seq, const int64_t * ctx, int32_t R) {
     dec_plan pl;
     const int32_t cus = device_cus(p.device());
     pl.split_tokens =
-        uses_stream(R) ? choose_split_stream(n_seq, ctx, p.h_kv(), cus, (R + 15) / 16) : choose_split(n_seq, ctx, p.h_kv(), cus);
+        choose_split_stream(n_seq, ctx, p.h_kv(), cus, (R + 15) / 16);
     // tuning knob for measurement: FNKV_SPLIT_TOKENS (a multiple of 32 from 256 to 2,048), read once per process
     static const int32_t split_knob = env_int_once("FNKV_SPLIT_TOKENS", 0);
     if (split_knob >= kPageTokens && split_knob <= 8 * kPageTokens && split_knob % kTileTokens == 0) {
@@ -1324,7 +1299,7 @@ dec_plan plan_decode(const kv_pool & p, int32_t n_seq, const int64_t * ctx, int3
     pl.pml_bytes = int64_t(pl.total) * p.h_kv() * R * 2 * 4;
     // the fold waits for the other splits of its pair, so every workgroup of the launch must be resident at once:
     // one a CU (the stream kernel's LDS)
-    pl.fold = fold_enabled() && uses_stream(R) && int64_t(pl.total) * p.h_kv() <= cus;
+    pl.fold = fold_enabled() && int64_t(pl.total) * p.h_kv() <= cus;
     return pl;
 }
 
@@ -1445,8 +1420,9 @@ void launch_decode_fmt(int32_t NT, dim3 grid, const dec_args & a, hipStream_t st
     }
 }
 
-// the decode kernel for NT row tiles (sparse or dense) and the pool's format, its LDS attribute set once per device
-template <bool SP> void launch_decode(const kv_pool & p, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
+// the sparse decode kernel for NT row tiles and the pool's format, its LDS attribute set once per device
+void launch_decode_sparse(const kv_pool & p, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
+    constexpr bool SP = true;
     // once per device, before any launch of it returns: a thread arriving while another sets the attributes waits
     static std::once_flag attr_once[64];
     const int32_t dev = p.device();
@@ -1457,33 +1433,25 @@ template <bool SP> void launch_decode(const kv_pool & p, int32_t NT, dim3 grid, 
             (void)hipSetDevice(dev);
             set_decode_attrs<SP, false>();
             set_decode_attrs<SP, true>();
-            if constexpr (SP) {
-                set_decode_attrs<SP, false, true>();
-                set_decode_attrs<SP, true, true>();
-            }
+            set_decode_attrs<SP, false, true>();
+            set_decode_attrs<SP, true, true>();
             (void)hipGetLastError();
             (void)hipSetDevice(cur);
         });
     }
-    if constexpr (SP) {
-        if (a.q_lo != nullptr) {
-            if (a.pv.format == kFormatKV8) {
-                launch_decode_fmt<SP, true, true>(NT, grid, a, st);
-            } else {
-                launch_decode_fmt<SP, false, true>(NT, grid, a, st);
-            }
-            return;
+    if (a.q_lo != nullptr) {
+        if (a.pv.format == kFormatKV8) {
+            launch_decode_fmt<SP, true, true>(NT, grid, a, st);
+        } else {
+            launch_decode_fmt<SP, false, true>(NT, grid, a, st);
         }
+        return;
     }
     if (a.pv.format == kFormatKV8) {
         launch_decode_fmt<SP, true>(NT, grid, a, st);
     } else {
         launch_decode_fmt<SP, false>(NT, grid, a, st);
     }
-}
-
-void launch_decode_sparse(const kv_pool & p, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
-    launch_decode<true>(p, NT, grid, a, st);
 }
 
 } // namespace fnkv
@@ -1585,11 +1553,7 @@ int decode_launch(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, 
     a.ts = g_timing;
 #endif
     const dim3 grid(static_cast<uint32_t>(pl.total), static_cast<uint32_t>(p->h_kv()));
-    if (uses_stream(R)) {
-        launch_stream(p->device(), (R + 15) / 16, grid, a, st);
-    } else {
-        launch_decode<false>(*p, (R + 15) / 16, grid, a, st);
-    }
+    launch_stream(p->device(), (R + 15) / 16, grid, a, st);
     if (pl.fold) {
         if (hipGetLastError() != hipSuccess) {
             set_error(name + ": launch failed");
