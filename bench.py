@@ -223,8 +223,8 @@ def _counter_means(out_dir):
     return {k: sums[k] / counts[k] for k in sums}
 
 
-def measure_traffic(argv, kernels=("decode", "merge_kernel")):
-    """HBM bytes of one fnkv_attn_decode launch (decode + merge kernels) from two rocprofv3 counter passes over a child
+def measure_traffic(argv, kernels=("stream_kernel", "merge_row_kernel", "merge_kernel")):
+    """HBM bytes of one fnkv_attn_decode launch (stream + merge kernels) from two rocprofv3 counter passes over a child
     run of the same workload: FETCH_SIZE, then WRITE_SIZE (KiB a dispatch), each scaled by bytes / reading of the
     same counter for the calibration copy of known size in the same child. Runs before this process touches the GPU.
     Returns (traffic bytes, detail dict) or (None, reason)."""
