@@ -51,12 +51,30 @@ template <bool F32> __device__ __forceinline__ void load4(const void * row, int3
 // and the block's fp16 scale bits (the same in the block's 8 lanes)
 __device__ __forceinline__ void quantize_q8_0(const float (&x)[4], uint32_t & packed, uint16_t & sbits) {
 #pragma clang fp contract(off)
-    float amax = fmaxf(fmaxf(__builtin_fabsf(x[0]), __builtin_fabsf(x[1])),
-                       fmaxf(__builtin_fabsf(x[2]), __builtin_fabsf(x[3])));
-    // the 8 lanes of a block: lanes 8 b .. 8 b + 7
+    // amax as ggml's running MAX(amax, |x_j|) (MAX(a, b) = a > b ? a : b) over the block in order: a NaN makes the
+    // running value NaN and the next value replaces it, so amax is the max |x| after the block's last NaN, and NaN
+    // when that NaN is the block's last value. The 8 lanes of a block are lanes 8 b .. 8 b + 7; this lane's values
+    // are the block's 4 (lane % 8) .. + 3.
+    const int32_t base = (static_cast<int32_t>(__lane_id()) & 7) * 4;
+    int32_t last_nan = -1;
+#pragma unroll
+    for (int32_t e = 0; e < 4; ++e) {
+        last_nan = x[e] != x[e] ? base + e : last_nan;
+    }
+    last_nan = max(last_nan, __shfl_xor(last_nan, 1));
+    last_nan = max(last_nan, __shfl_xor(last_nan, 2));
+    last_nan = max(last_nan, __shfl_xor(last_nan, 4));
+    float amax = 0.0f;
+#pragma unroll
+    for (int32_t e = 0; e < 4; ++e) {
+        amax = base + e > last_nan ? fmaxf(amax, __builtin_fabsf(x[e])) : amax;
+    }
     amax = fmaxf(amax, __shfl_xor(amax, 1));
     amax = fmaxf(amax, __shfl_xor(amax, 2));
     amax = fmaxf(amax, __shfl_xor(amax, 4));
+    if (last_nan == kQK - 1) {
+        amax = __builtin_nanf("");
+    }
     const float d = __fdiv_rn(amax, 127.0f);
     const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
     packed = 0;
@@ -68,7 +86,8 @@ __device__ __forceinline__ void quantize_q8_0(const float (&x)[4], uint32_t & pa
         const int32_t c = __builtin_fabsf(r) < 2147483648.0f ? static_cast<int32_t>(r) : INT32_MIN;
         packed |= uint32_t((c & 0xff) ^ 0x80) << (8 * e); // excess-128 storage
     }
-    sbits = __half_as_ushort(__float2half_rn(d));
+    // ggml's fp32 -> fp16 (ggml-impl.h) gives every NaN as sign | 0x7e00 (here the sign of |x|: +)
+    sbits = d != d ? static_cast<uint16_t>(0x7e00) : __half_as_ushort(__float2half_rn(d));
 }
 
 // The KV8 rule, bit for bit FNFL's kv_q8_quantize_group (fn/quant/kv_q8_ref.cpp:72-87; device kv8::quantize8,

@@ -11,11 +11,13 @@ Fixtures:
                       allf16: every finite fp16 value, in bit order, as fp32 (1,984 blocks: each exponent range)
                       ties:   blocks whose x * id land exactly on k + 0.5 (roundf's ties away from zero)
                       rows:   seeded fp16 K/V rows, N(0, 1) with 4 of 256 channels x8 (BASELINE's distribution)
+                      nonfinite: fp16 rows holding NaN and +-inf among finite values (first, middle, last and
+                              whole-block NaNs, inf alone, both together, seeded placements)
                     each as x (fp32), qs (int8 codes) and d (fp16 bits), plus the dequantized values
                     (dequantize_row_q8_0, ggml-quants.c:551-565)
   f16_golden.npz    ggml_compute_fp32_to_fp16 (ggml-impl.h:414-438) on 40,000 seeded fp32 bit patterns plus edge
                     values; ggml_compute_fp16_to_fp32 (ggml-impl.h:391-412) on all 65,536 halves
-  kv8_golden.npz    FNFL's own KV8 rule kv_q8_quantize (kv_q8_ref.cpp:72-93) on the stress rows and the fp16 rows
+  kv8_golden.npz    FNFL's own KV8 rule kv_q8_quantize (kv_q8_ref.cpp:72-93) on the stress, fp16 and non-finite rows
   act_golden.npz    FNFL's int8 activation format act_quantize_ref (fn/quant/act_ref.cpp:8-29) on seeded rows of the
                     DA-TC output width (3,072), exact ties (x id = k + 0.5), zero, subnormal, huge, NaN and inf runs
 """
@@ -56,6 +58,36 @@ def baseline_rows(seed, n_rows, d=256):
     ch = rng.choice(d, 4, replace=False)
     x[:, ch] *= 8.0
     return x.astype(np.float16).astype(np.float32)
+
+
+def nonfinite_rows():
+    """fp16 rows (whole 256-value rows, 8 blocks) holding NaN and +-inf beside finite values: a NaN first, in the
+    middle (after a larger value), last and everywhere in its block, an inf alone, NaN and inf together, and seeded
+    random placements. ggml's MAX macro (a > b ? a : b) lets a NaN restart the block's running max, and leaves it NaN
+    only from the block's last place; a NaN or inf times id rounds to NaN, whose int8 store keeps the low byte of
+    x86's 0x80000000: code 0."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((24, 256)).astype(np.float32)
+    x[:, rng.choice(256, 4, replace=False)] *= 8.0
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    x[0, 0] = nan                       # first in block 0
+    x[0, 32 + 31] = nan                 # last in block 1: the block's amax NaN
+    x[1, 5], x[1, 3] = nan, 40.0        # a larger value before the NaN: dropped from the max
+    x[1, 64 + 17], x[1, 64 + 30] = nan, nan
+    x[2, 0:32] = nan                    # a whole block
+    x[2, 32 + 7] = inf                  # inf alone: d inf, id 0
+    x[2, 64 + 9] = -inf
+    x[3, 3], x[3, 20] = inf, nan        # inf before the NaN: the max restarts after it
+    x[3, 32 + 3], x[3, 32 + 20] = nan, -inf
+    x[4, 31], x[4, 30] = 0.0, nan       # the NaN's followers all zero
+    x[4, 32:64] = 0.0
+    x[4, 32 + 31] = nan
+    for r in range(5, 24):
+        m = rng.random(256)
+        x[r, m < 0.03] = nan
+        x[r, (m >= 0.03) & (m < 0.05)] = inf
+        x[r, (m >= 0.05) & (m < 0.06)] = -inf
+    return x.astype(np.float16).astype(np.float32).reshape(-1)
 
 
 def tie_blocks():
@@ -106,6 +138,7 @@ def main():
         "allf16": O.f16_to_f32(finite)[: (finite.size // 32) * 32],
         "ties": tie_blocks(),
         "rows": baseline_rows(20261201, 64).reshape(-1),
+        "nonfinite": nonfinite_rows(),
     }
     for name, x in sets.items():
         qs, d, y = ref_q8_0(x)
@@ -128,7 +161,7 @@ def main():
     np.savez_compressed(os.path.join(HERE, "f16_golden.npz"), f32=xf, f16=hf, halves_f32_bits=wf.view(np.uint32))
 
     kv = {}
-    for name in ("stress", "rows"):
+    for name in ("stress", "rows", "nonfinite"):
         x = np.ascontiguousarray(sets[name], np.float32)
         codes = np.empty(x.size, np.int8)
         sc = np.empty(x.size // 64, np.uint16)

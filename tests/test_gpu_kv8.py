@@ -30,7 +30,7 @@ def _export(pool, slot, layer, head, kv, tok0, n):
     return c.cpu().numpy(), s.cpu().numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("name", ["stress", "rows"])
+@pytest.mark.parametrize("name", ["stress", "rows", "nonfinite"])
 def test_kv8_append_matches_reference_golden(golden, name):
     g = golden("kv8_golden.npz")
     x0 = g[f"{name}_x"].reshape(-1, 256)

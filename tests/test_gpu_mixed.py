@@ -129,7 +129,11 @@ def exported_cells(pool, slot, layer, c):
 
 
 def test_config4_full_contexts_properties():
-    seed, layers, T = 41, 1, 5
+    """BASELINE config 4 at its full contexts on a churned pool, two of its layers, K/V in BASELINE's distribution: the
+    two prefill chunks (finite, their last five rows against a T = 5 verify over the same cells, a spread of rows
+    against fp64), and the six-sequence verify launch writing its own new cells, against each sequence launched alone
+    and against fp64 (out_err and the plain max-abs)."""
+    seed, layers, T = 41, 2, 5
     rng = np.random.default_rng([seed, 1])
     pf_slots, vf_slots = [0, 1], [2, 3, 4, 5, 6, 7]
     pf_depth = [int(rng.integers(1024, 196 * 1024)) for _ in pf_slots]
@@ -142,46 +146,64 @@ def test_config4_full_contexts_properties():
     cases.scatter_ensure(pool, order, [ctx_of[s] for s in order], seed)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
-    for s in order:
-        x = torch.randn((2, ctx_of[s], HKV, D), generator=g, device="cuda").half()
-        pool.append(s, 0, 0, x[0].contiguous(), x[1].contiguous())
+    new_cells = {}
+    for layer in range(layers):
+        for s in order:
+            x = torch.randn((2, ctx_of[s], HKV, D), generator=g, device="cuda")
+            for h in range(HKV):  # 4 of a KV head's 256 channels x8 (BASELINE's outliers)
+                for kv in range(2):
+                    ch = torch.randperm(D, generator=g, device="cuda")[:4]
+                    x[kv, :, h, ch] *= 8.0
+            x = x.half()
+            upto = ctx_of[s] - T if s in vf_slots else ctx_of[s]  # a verify launch appends its own T cells
+            pool.append(s, layer, 0, x[0, :upto].contiguous(), x[1, :upto].contiguous())
+            if s in vf_slots:
+                new_cells[(s, layer)] = (x[0, upto:].contiguous(), x[1, upto:].contiguous())
+            del x
     # the prefill chunks: finite; the chunk's last five rows agree with a T = 5 verify over the same cells; a spread
     # of rows against the fp64 attention over the cells as the pool holds them
-    errs = {}
-    for s in pf_slots:
-        c = ctx_of[s]
-        q = torch.randn((CHUNK, HQ, D), generator=g, device="cuda").half()
+    errs, plain = {}, {}
+    for layer in range(layers):
+        for s in pf_slots:
+            c = ctx_of[s]
+            q = torch.randn((CHUNK, HQ, D), generator=g, device="cuda").half()
+            out = torch.empty_like(q)
+            pool.prefill(s, layer, c, q, out)
+            qv = q[None, -5:].contiguous()
+            ov = torch.empty_like(qv)
+            ws = torch.zeros(pool.decode_ws_bytes([c], 5, HQ), dtype=torch.uint8, device="cuda")
+            pool.decode([s], [c], 5, layer, qv, ov, ws)
+            torch.cuda.synchronize()
+            assert torch.isfinite(out.float()).all().item()
+            assert (ov[0].float() - out[-5:].float()).abs().max().item() <= 2 * TOL
+            rows = [0, 1, 511, 2047, 3000, CHUNK - 1]
+            kf, vf = exported_cells(pool, s, layer, c)
+            ref = O.attn_f64(q.cpu().numpy().view(np.uint16), kf, vf, c, rows=rows)
+            errs[("prefill", layer, s)] = cases.out_err(out.cpu().numpy()[rows], ref)
+            plain[("prefill", layer, s)] = cases.plain_err(out.cpu().numpy()[rows], ref)
+        # the six verify steps in one launch, their new cells written by the launch, against each launched alone
+        # (over the same cells, already written) and against fp64
+        q = torch.randn((len(vf_slots), T, HQ, D), generator=g, device="cuda").half()
+        ctxs = [ctx_of[s] for s in vf_slots]
+        kn = torch.stack([new_cells[(s, layer)][0] for s in vf_slots])
+        vn = torch.stack([new_cells[(s, layer)][1] for s in vf_slots])
         out = torch.empty_like(q)
-        pool.prefill(s, 0, c, q, out)
-        qv = q[None, -5:].contiguous()
-        ov = torch.empty_like(qv)
-        ws = torch.zeros(pool.decode_ws_bytes([c], 5, HQ), dtype=torch.uint8, device="cuda")
-        pool.decode([s], [c], 5, 0, qv, ov, ws)
+        ws = torch.zeros(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+        pool.decode(vf_slots, ctxs, T, layer, q, out, ws, k_new=kn, v_new=vn)
         torch.cuda.synchronize()
         assert torch.isfinite(out.float()).all().item()
-        assert (ov[0].float() - out[-5:].float()).abs().max().item() <= 2 * TOL
-        rows = [0, 1, 511, 2047, 3000, CHUNK - 1]
-        kf, vf = exported_cells(pool, s, 0, c)
-        ref = O.attn_f64(q.cpu().numpy().view(np.uint16), kf, vf, c, rows=rows)
-        errs[("prefill", s)] = cases.out_err(out.cpu().numpy()[rows], ref)
-    # the six verify steps in one launch against each launched alone
-    q = torch.randn((len(vf_slots), T, HQ, D), generator=g, device="cuda").half()
-    ctxs = [ctx_of[s] for s in vf_slots]
-    out = torch.empty_like(q)
-    ws = torch.zeros(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
-    pool.decode(vf_slots, ctxs, T, 0, q, out, ws)
-    torch.cuda.synchronize()
-    assert torch.isfinite(out.float()).all().item()
-    got = out.cpu().numpy()
-    q16 = q.cpu().numpy()
-    for i, s in enumerate(vf_slots):
-        one = torch.empty_like(q[i:i + 1])
-        ws1 = torch.zeros(pool.decode_ws_bytes([ctxs[i]], T, HQ), dtype=torch.uint8, device="cuda")
-        pool.decode([s], [ctxs[i]], T, 0, q[i:i + 1].contiguous(), one, ws1)
-        torch.cuda.synchronize()
-        assert (one[0].float() - out[i].float()).abs().max().item() <= 2 * TOL
-        kf, vf = exported_cells(pool, s, 0, ctxs[i])
-        ref = O.attn_f64(q16[i].view(np.uint16), kf, vf, ctxs[i])
-        errs[("verify", s)] = cases.out_err(got[i], ref)
+        got = out.cpu().numpy()
+        q16 = q.cpu().numpy()
+        for i, s in enumerate(vf_slots):
+            one = torch.empty_like(q[i:i + 1])
+            ws1 = torch.zeros(pool.decode_ws_bytes([ctxs[i]], T, HQ), dtype=torch.uint8, device="cuda")
+            pool.decode([s], [ctxs[i]], T, layer, q[i:i + 1].contiguous(), one, ws1)
+            torch.cuda.synchronize()
+            assert (one[0].float() - out[i].float()).abs().max().item() <= 2 * TOL
+            kf, vf = exported_cells(pool, s, layer, ctxs[i])
+            ref = O.attn_f64(q16[i].view(np.uint16), kf, vf, ctxs[i])
+            errs[("verify", layer, s)] = cases.out_err(got[i], ref)
+            plain[("verify", layer, s)] = cases.plain_err(got[i], ref)
     worst = max(errs.values())
     assert np.isfinite(worst) and worst <= TOL, errs
+    assert max(plain.values()) <= TOL, plain

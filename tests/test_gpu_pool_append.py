@@ -106,7 +106,7 @@ def _export_blocks(pool, slot, layer, head, kv, tok0, n):
     return O.from_block_q8_0(out.cpu().numpy().reshape(-1, 34))
 
 
-@pytest.mark.parametrize("name", ["stress", "allf16", "ties", "rows"])
+@pytest.mark.parametrize("name", ["stress", "allf16", "ties", "rows", "nonfinite"])
 def test_append_matches_reference_golden(golden, name):
     g = golden("q8_0_golden.npz")
     x0 = g[f"{name}_x"]
@@ -121,7 +121,7 @@ def test_append_matches_reference_golden(golden, name):
     assert p.ensure(0, rows + 37)[0] == 0
     kt = torch.from_numpy(np.ascontiguousarray(x)).cuda()
     vt = torch.from_numpy(np.ascontiguousarray(x[::-1].copy())).cuda()
-    if name in ("allf16", "rows"):
+    if name in ("allf16", "rows", "nonfinite"):
         kt, vt = kt.half(), vt.half()  # exact: these inputs are fp16 values
     p.append(0, 0, 37, kt, vt)
     got_q = np.empty((2, rows, h_kv, 256), np.int8)

@@ -54,7 +54,7 @@ def test_f16_to_f32_matches_ggml(golden):
     assert np.array_equal(got[ok], w[ok].view(np.uint32))
 
 
-@pytest.mark.parametrize("name", ["stress", "allf16", "ties", "rows"])
+@pytest.mark.parametrize("name", ["stress", "allf16", "ties", "rows", "nonfinite"])
 def test_q8_0_matches_reference(golden, name):
     g = golden("q8_0_golden.npz")
     x = g[f"{name}_x"]
@@ -90,7 +90,7 @@ def test_q8_0_ties_round_away_from_zero(golden):
     assert np.array_equal(O.q8_0_quantize(x)[0], want)
 
 
-@pytest.mark.parametrize("name", ["stress", "rows"])
+@pytest.mark.parametrize("name", ["stress", "rows", "nonfinite"])
 def test_kv8_rule_matches_reference(golden, name):
     g = golden("kv8_golden.npz")
     c, s = O.kv8_quantize(g[f"{name}_x"])
