@@ -1591,40 +1591,98 @@ int decode_launch(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, 
 
 // The no-allocation variant's workspace: the split partials of fnkv_attn_decode_noalloc live in this file-scope
 // device array (each device that runs the library holds its own copy until the process ends). Host code never passes
-// the array's name to a kernel (on the host it is only a stand-in for the symbol): it asks each device once for the
-// array's device address and uses that.
+// the array's name to a kernel (on the host it is only a stand-in for the symbol): it asks each device once, when the
+// first pool on that device is created, for the array's device address and uses that.
+//
+// One device's array serves one (pool, stream) pair at a time: the first fnkv_attn_decode_noalloc call on a device
+// binds it to that call's pool and stream, and calls from another pool or on another stream are refused (they could
+// run while the bound pair's last call is still in flight) until the bound pool is destroyed, which drains the device
+// and releases the binding.
 constexpr int64_t kNoAllocScratchBytes = int64_t(16) << 20;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 namespace {
+constexpr int32_t kScratchDevices = 64;
+struct scratch_binding {
+    void * ptr = nullptr;               // the array's device address on this device
+    const kv_pool * owner = nullptr;    // the pool bound to it, or null
+    hipStream_t stream = nullptr;       // the stream its calls run on (valid while owner is set)
+};
 std::mutex g_scratch_mu;
-void * g_scratch_ptr[64] = {nullptr};
+scratch_binding g_scratch[kScratchDevices];
 } // namespace
 
-// the device address of `scratch` on `device` (the current device while it is looked up), looked up on the first
-// call for that device; null (with the error set) when the lookup fails
-void * scratch_on(int32_t device) {
-    if (device < 0 || device >= 64) {
+bool scratch_init(int32_t device, std::string & err) {
+    if (device < 0 || device >= kScratchDevices) {
+        err = "fnkv_pool_create: device index outside 0 .. 63";
+        return false;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[device].ptr != nullptr) {
+        return true;
+    }
+    int32_t cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess || hipSetDevice(device) != hipSuccess) {
+        err = "fnkv_pool_create: cannot make the pool's device current";
+        return false;
+    }
+    void * ptr = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    (void)hipSetDevice(cur);
+    if (rc != hipSuccess || ptr == nullptr) {
+        err = std::string("fnkv_pool_create: hipGetSymbolAddress of the decode scratch failed: ") +
+              hipGetErrorString(rc);
+        return false;
+    }
+    g_scratch[device].ptr = ptr;
+    return true;
+}
+
+void scratch_release(const kv_pool * pool) {
+    const int32_t device = pool->device();
+    if (device < 0 || device >= kScratchDevices) {
+        return;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[device].owner != pool) {
+        return;
+    }
+    int32_t cur = 0;
+    if (hipGetDevice(&cur) == hipSuccess && hipSetDevice(device) == hipSuccess) {
+        (void)hipDeviceSynchronize();
+        (void)hipSetDevice(cur);
+    }
+    g_scratch[device].owner = nullptr;
+    g_scratch[device].stream = nullptr;
+}
+
+// the device address of the scratch for a call of `pool` on `stream`, binding the pair on the device's first call;
+// null (with the error set) when another pool or stream holds it
+static void * scratch_claim(const kv_pool * pool, hipStream_t stream) {
+    const int32_t device = pool->device();
+    if (device < 0 || device >= kScratchDevices) {
         set_error("fnkv_attn_decode_noalloc: device index outside 0 .. 63");
         return nullptr;
     }
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (g_scratch_ptr[device] == nullptr) {
-        int32_t cur = 0;
-        if (hipGetDevice(&cur) != hipSuccess || hipSetDevice(device) != hipSuccess) {
-            set_error("fnkv_attn_decode_noalloc: cannot make the pool's device current");
-            return nullptr;
-        }
-        void * ptr = nullptr;
-        const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-        (void)hipSetDevice(cur);
-        if (rc != hipSuccess || ptr == nullptr) {
-            set_error(std::string("fnkv_attn_decode_noalloc: hipGetSymbolAddress failed: ") + hipGetErrorString(rc));
-            return nullptr;
-        }
-        g_scratch_ptr[device] = ptr;
+    scratch_binding & b = g_scratch[device];
+    if (b.ptr == nullptr) {
+        set_error("fnkv_attn_decode_noalloc: the decode scratch of the pool's device was never looked up");
+        return nullptr;
     }
-    return g_scratch_ptr[device];
+    if (b.owner == nullptr) {
+        b.owner = pool;
+        b.stream = stream;
+    } else if (b.owner != pool) {
+        set_error("fnkv_attn_decode_noalloc: the device's scratch is bound to another pool (calls could overlap); "
+                  "destroy that pool first or use fnkv_attn_decode_dev");
+        return nullptr;
+    } else if (b.stream != stream) {
+        set_error("fnkv_attn_decode_noalloc: the device's scratch is bound to another stream of this pool (calls "
+                  "could overlap); keep one stream or use fnkv_attn_decode_dev");
+        return nullptr;
+    }
+    return b.ptr;
 }
 
 } // namespace fnkv
@@ -1688,13 +1746,13 @@ int fnkv_attn_decode_noalloc(const fnkv_pool * pool, int32_t n_seq, const int32_
                         std::to_string(fnkv::kNoAllocScratchBytes) + "-byte scratch (use fnkv_attn_decode_dev)");
         return FNKV_ERR_ARG;
     }
-    void * ws = fnkv::scratch_on(p->device());
-    if (ws == nullptr) {
-        return FNKV_ERR_HIP;
-    }
     if (ctx == nullptr || err == nullptr || (reinterpret_cast<uintptr_t>(ctx) & 7) != 0 ||
         (reinterpret_cast<uintptr_t>(err) & 3) != 0) {
         fnkv::set_error("fnkv_attn_decode_noalloc: ctx (8-byte aligned) and err (4-byte aligned) device words required");
+        return FNKV_ERR_ARG;
+    }
+    void * ws = fnkv::scratch_claim(p, static_cast<hipStream_t>(stream));
+    if (ws == nullptr) {
         return FNKV_ERR_ARG;
     }
     return fnkv::decode_launch(pool, n_seq, slots, max_ctx, ctx, err, T, layer, hq, scale, q, k_new, v_new, new_dtype,

@@ -90,4 +90,10 @@ class kv_pool {
     int32_t fail_after_ = -1;
 };
 
+// The no-allocation decode's device scratch (decode.hip). scratch_init looks its address up on `device` (once per
+// device, at pool creation, so that no lookup ever runs under stream capture); scratch_release gives up `pool`'s claim
+// on its device's scratch (after the device has drained), when the pool is destroyed.
+bool scratch_init(int32_t device, std::string & err);
+void scratch_release(const kv_pool * pool);
+
 } // namespace fnkv

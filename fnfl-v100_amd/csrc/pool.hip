@@ -421,11 +421,21 @@ int fnkv_pool_create_fmt(int32_t n_slots, int32_t n_pages, int32_t page_tokens, 
         set_error(err);
         return err.find("HBM") != std::string::npos ? FNKV_ERR_HIP : FNKV_ERR_ARG;
     }
+    if (!fnkv::scratch_init(device, err)) {
+        delete p;
+        set_error(err);
+        return FNKV_ERR_HIP;
+    }
     *out = p;
     return FNKV_OK;
 }
 
-void fnkv_pool_destroy(fnkv_pool * pool) { delete pool; }
+void fnkv_pool_destroy(fnkv_pool * pool) {
+    if (pool != nullptr) {
+        fnkv::scratch_release(&pool->p);
+    }
+    delete pool;
+}
 
 int32_t fnkv_pool_format(const fnkv_pool * pool) { return pool == nullptr ? -1 : pool->p.format(); }
 

@@ -175,8 +175,12 @@ int fnkv_attn_decode_dev(const fnkv_pool * pool, int32_t n_seq, const int32_t * 
  * library (one a GPU, held until the process ends), and the call allocates nothing. A launch whose partials
  * (fnkv_decode_workspace_bytes(pool, n_seq, max_ctx, T, hq)) exceed 16 MiB is refused (FNKV_ERR_ARG, nothing
  * enqueued); cfg-sized launches (4 sequences of 8K-64K at T = 3, or one of 262,144 at T = 5) need 6-11 MiB. Every
- * call on one GPU shares that array (it starts zeroed and every call leaves its fold counters ready for the next): calls that
- * overlap on one GPU (other streams, or other threads) race and must be serialized by the caller. */
+ * call on one GPU shares that array (it starts zeroed and every call leaves its fold counters ready for the next), so
+ * the array is bound to one pool and one stream at a time: the first call on a GPU binds its pool and stream, and a
+ * call from another pool, or on another stream, is refused (FNKV_ERR_ARG, nothing enqueued) until the bound pool is
+ * destroyed (fnkv_pool_destroy drains the GPU and releases the binding). The array's address is looked up when the
+ * first pool on a GPU is created, so the call itself makes no lookup and may be captured into a HIP graph. Calls on the
+ * bound stream from several host threads are not refused and must be serialized by the caller. */
 int fnkv_attn_decode_noalloc(const fnkv_pool * pool, int32_t n_seq, const int32_t * slots, const int64_t * ctx,
                              const int64_t * max_ctx, int32_t T, int32_t layer, int32_t hq, float scale,
                              const void * q, const void * k_new, const void * v_new, int32_t new_dtype, void * out,

@@ -244,10 +244,10 @@ def attn_f64_cells(q16, k, v, cells, scale=1.0 / 16.0):
         c = np.asarray(cells[t], dtype=np.int64)
         kk = k[c].astype(np.float64)  # [n][hkv][d]
         vv = v[c].astype(np.float64)
-        for h in range(hq):
-            s = (kk[:, h // G, :] @ q[t, h]) * scale
-            p = np.exp(s - s.max())
-            out[t, h] = (p @ vv[:, h // G, :]) / p.sum()
+        for g in range(hkv):  # the G query heads of KV head g at once: s [n][G]
+            s = (kk[:, g, :] @ q[t, g * G:(g + 1) * G].T) * scale
+            p = np.exp(s - s.max(axis=0))
+            out[t, g * G:(g + 1) * G] = (p.T @ vv[:, g, :]) / p.sum(axis=0)[:, None]
     return out
 
 

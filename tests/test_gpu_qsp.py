@@ -7,7 +7,9 @@ fn/kernels/qsa/qsa_prompt.h:90-124) on the GPU against the oracle:
   qsp_attend  every (row, head) within 2e-3 max-abs (F32 out) of FP64 attention over the row's selected cells of the
               decoded cache with q = fp16(F32(norm_rope_f64)), times sigmoid(gate); the fp16 out is the F32 out rounded
               to nearest even; bit 0 of err only for an output fp16 cannot hold
-Rows cross slab (128) and launch-chunk (512) boundaries; 12 heads on 1 KV head (the reference's card) and 16 on 2."""
+Rows cross slab (128) and launch-chunk (512) boundaries, up to the 4,096-row limit (eight full chunks) and up to the
+deepest cell the selection layout addresses (a short last chunk there); 12 heads on 1 KV head (the reference's card)
+and 16 on 2. qsp_kv's K and V cells are also bitwise those fnkv_qsa_attend's prepare step writes for the same rows."""
 import numpy as np
 import pytest
 
@@ -126,6 +128,47 @@ def test_qsp_kv_norm_rope_quantize(fmt, h_kv, use_planes):
             assert (np.abs(dec - k64[:, h]) <= step * 0.5 + 1e-6 * np.abs(k64[:, h]).max()).all()
 
 
+@pytest.mark.parametrize("fmt", [fnkv.FMT_Q8_0, fnkv.FMT_KV8])
+def test_qsp_kv_bitwise_the_decode_prepare(fmt):
+    # the same F32 rows, norm and rope positions written once through fnkv_qsa_attend (its prepare step, T rows at a
+    # time) and once through fnkv_qsp_kv (all rows in one launch): the stored cells are identical, byte for byte
+    h_kv, hq, T, depth0, windows = 2, 16, 5, 3001, 12
+    rows = T * windows
+    ctx = depth0 + rows
+    rng = np.random.default_rng([fmt, 41])
+    kv_k = rng.uniform(-2.0, 2.0, (rows, h_kv, 256)).astype(np.float32)
+    kv_v = rng.uniform(-1.5, 1.5, (rows, h_kv, 256)).astype(np.float32)
+    kv_k[7, 0, :32] *= 1e-3  # a near-silent block and an outlier block
+    kv_k[11, 1, 64:96] *= 300.0
+    k_norm = rng.uniform(0.3, 1.8, 256).astype(np.float32)
+    q_norm = rng.uniform(0.3, 1.8, 256).astype(np.float32)
+    planes = planes_of(depth0, rows, True)
+    pools = [fnkv.Pool(2, -(-ctx // 256) + 8, 1, h_kv, fmt=fmt) for _ in range(2)]
+    for p in pools:
+        cases.scatter_ensure(p, [0], [ctx], 8, churn=0.3)
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    kn = dev(k_norm)
+    for w in range(windows):
+        t0, depth = w * T, depth0 + w * T
+        words, offs, _ = O.qsa_body(depth, T, w)
+        out = torch.empty((T, hq, 256), device="cuda")
+        codes = torch.empty((T, hq * 256), dtype=torch.int8, device="cuda")
+        scales = torch.empty((T, hq * 8, 2), device="cuda")
+        pools[0].qsa_attend(0, depth, 0, dev(rng.uniform(-3, 3, (T, hq, 512)).astype(np.float32)),
+                            dev(kv_k[t0:t0 + T]), dev(kv_v[t0:t0 + T]), dev(q_norm), kn,
+                            dev(planes[t0:t0 + T].T), dev(words.view(np.int32)), dev(offs), out, codes, scales)
+    pools[1].qsp_kv(0, 0, depth0, dev(kv_k), dev(kv_v), kn, planes=dev(planes))
+    torch.cuda.synchronize()
+    for h in range(h_kv):
+        for kv in range(2):
+            a = stored(pools[0], fmt, 0, h, kv, depth0, rows)
+            b = stored(pools[1], fmt, 0, h, kv, depth0, rows)
+            assert np.array_equal(a[0], b[0]), (h, kv)
+            assert np.array_equal(a[1].view(np.uint16), b[1].view(np.uint16)), (h, kv)
+    for p in pools:
+        p.close()
+
+
 def run_attend(pos0, rows, hq, h_kv, seed, fmt=fnkv.FMT_Q8_0, use_planes=False, with_f32=True, big_v=False):
     rng = np.random.default_rng([seed, 3])
     ctx = pos0 + rows
@@ -162,6 +205,18 @@ def test_qsp_attend_against_fp64(pos0, rows, hq, h_kv):
     o16, o32, err, ref = run_attend(pos0, rows, hq, h_kv, seed=rows + hq)
     assert err == 0 and np.isfinite(o32).all()
     e = float(np.abs(o32.astype(np.float64) - ref).max())
+    assert e <= TOL, e
+    assert np.array_equal(o16.view(np.uint16), o32.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("pos0,rows", [(100, 4096), (262144 + 32 - 576, 576)])
+def test_qsp_attend_chunks_at_the_limits(pos0, rows):
+    # eight full 512-row chunks (the workspace sized for the deepest one and reused by all); and a full chunk then a
+    # 64-row one whose last row is the deepest cell the selection layout addresses
+    o16, o32, err, ref = run_attend(pos0, rows, 12, 1, seed=rows)
+    assert err == 0 and np.isfinite(o32).all()
+    e = float(np.abs(o32.astype(np.float64) - ref).max())
+    print(f"pos0 {pos0} rows {rows}: max-abs {e:.3g}", flush=True)
     assert e <= TOL, e
     assert np.array_equal(o16.view(np.uint16), o32.astype(np.float16).view(np.uint16))
 

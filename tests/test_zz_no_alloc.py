@@ -1,8 +1,12 @@
 """fnkv_attn_decode_noalloc (the decode entry point that allocates nothing: its split partials live in the library's
 fixed device scratch) against fnkv_attn_decode_dev, the entry point it varies, on the same inputs: bitwise equal
 outputs and appended cells, on two calls in a row, the second with a smaller input (fewer sequences, shorter
-contexts, fewer query tokens), so the second reads none of the first's partials; and a launch too large for the
-scratch is refused with nothing enqueued."""
+contexts, fewer query tokens), so the second reads none of the first's partials; the call captured into a HIP graph
+and replayed (every replay bitwise equal to the eager result, and no device memory taken by the capture beyond what a
+one-kernel graph takes); the scratch bound to one pool and one stream, calls from another refused until that pool is
+destroyed; and a launch too large for the scratch refused with nothing enqueued."""
+import gc
+
 import numpy as np
 import pytest
 
@@ -82,3 +86,91 @@ def test_noalloc_refuses_a_launch_beyond_its_scratch():
     torch.cuda.synchronize()
     assert bool((out == 2.0).all()) and err.item() == 0
     pool.close()
+
+
+def _fresh(ctxs, T, seed):
+    """A pool with `ctxs` cells per sequence, its decode_dev result (reference) and the call's arguments."""
+    pool, slots, kn, vn, q = make(ctxs, T, seed)
+    ctx_dev = torch.tensor(ctxs, dtype=torch.int64, device="cuda")
+    ref = torch.full_like(q, float("nan"))
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws = torch.zeros(pool.decode_ws_bytes(ctxs, T, HQ), dtype=torch.uint8, device="cuda")
+    pool.decode_dev(slots, ctx_dev, ctxs, T, 0, q, ref, ws, err, k_new=kn, v_new=vn)
+    torch.cuda.synchronize()
+    assert err.item() == 0
+    args = dict(slots=slots, ctx_dev=ctx_dev, max_ctx=ctxs, T=T, layer=0, q=q, k_new=kn, v_new=vn)
+    return pool, ref, args
+
+
+def test_noalloc_binds_one_pool_and_one_stream():
+    a, ref_a, args_a = _fresh([5000, 1200], 2, seed=5)
+    b, ref_b, args_b = _fresh([7000], 1, seed=6)
+    try:
+        err = torch.zeros(1, dtype=torch.int32, device="cuda")
+        got_a = torch.full_like(ref_a, float("nan"))
+        a.decode_noalloc(out=got_a, err=err, **args_a)
+        got_b = torch.full_like(ref_b, 2.0)
+        with pytest.raises(fnkv.FnkvError, match="another pool"):
+            b.decode_noalloc(out=got_b, err=err, **args_b)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        again = torch.full_like(ref_a, 2.0)
+        with torch.cuda.stream(side), pytest.raises(fnkv.FnkvError, match="another stream"):
+            a.decode_noalloc(out=again, err=err, **args_a)
+        torch.cuda.synchronize()
+        assert torch.equal(ref_a.view(torch.int16), got_a.view(torch.int16))
+        assert bool((got_b == 2.0).all()) and bool((again == 2.0).all()) and err.item() == 0
+        a.close()  # releases the binding: pool b may now use the scratch
+        b.decode_noalloc(out=got_b, err=err, **args_b)
+        torch.cuda.synchronize()
+        assert torch.equal(ref_b.view(torch.int16), got_b.view(torch.int16)) and err.item() == 0
+    finally:
+        a.close()
+        b.close()
+
+
+def _free_bytes():
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return torch.cuda.mem_get_info()[0]
+
+
+def test_noalloc_captured_in_a_graph_allocates_nothing():
+    pool, ref, args = _fresh([8192, 20000, 3000], 3, seed=21)
+    try:
+        err = torch.zeros(1, dtype=torch.int32, device="cuda")
+        got = torch.full_like(ref, float("nan"))
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            pool.decode_noalloc(out=got, err=err, **args)  # eager, on the stream the graph is captured on
+        torch.cuda.synchronize()
+        assert torch.equal(ref.view(torch.int16), got.view(torch.int16))
+        # a one-kernel graph first, so the runtime's own first-capture memory is not counted against the call
+        ctl = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(ctl, stream=side):
+            got.mul_(1.0)
+        ctl.replay()
+        free0 = _free_bytes()
+        ctl2 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(ctl2, stream=side):
+            got.mul_(1.0)
+        ctl2.replay()
+        free1 = _free_bytes()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            pool.decode_noalloc(out=got, err=err, **args)
+        for i in range(3):
+            got.fill_(float("nan"))
+            err.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(ref.view(torch.int16), got.view(torch.int16)), f"replay {i}"
+            assert err.item() == 0
+        free2 = _free_bytes()
+        print(f"free bytes: one-kernel graph takes {free0 - free1}, the noalloc graph {free1 - free2}", flush=True)
+        assert free1 - free2 <= max(free0 - free1, 0)
+    finally:
+        pool.close()
