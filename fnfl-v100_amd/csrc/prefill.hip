@@ -4,23 +4,24 @@
 // What it computes (the reference's prompt attention, fn/kernels/qsa/qsa_prompt.h:50-58 and qsa_prompt_attn.cu:
 // 229-436, made dense and causal, on the pool's codes): S = Q K^T * scale, online softmax, O = P V, fp16 out. The
 // reference rounds its K/V operand to fp16 once (q4_h4, qsa_prompt_attn.cu:195-207) and P to fp16, within a loose
-// 2e-2 bound; here every product carries ~22 bits, so the result meets 2e-3 against fp64 even when a few cells
-// dominate: K and V go to the matrix cores exactly as hi + lo fp16 (code x scale has 8 x 11 significant bits), P as
-// hi + lo fp16.
+// 2e-2 bound; here every product carries ~19 bits or more, so the result meets 2e-3 against fp64 even when a few
+// cells dominate: the K and V codes go to the matrix cores exactly (an int8 code is an exact fp16 integer), each K
+// block's scale multiplies that block's fp32 scores, and P times each V block's scales enters as hi + lo fp16.
 //
-// How (MI355X): matrix-core bound (4 d flops a visible (query, key) pair and head), so K/V tiles are dequantized once
+// How (MI355X): matrix-core bound (4 d flops a visible (query, key) pair and head), so K/V tiles are converted once
 // a workgroup and shared by all its query rows.
 //   * A workgroup (8 waves, two a SIMD, so one wave's matrix-core work overlaps the other's VALU work) owns 256 query
 //     rows (256 / G query tokens x the G heads of one KV head); each wave owns two 16-row tiles, so each operand
 //     read from LDS feeds two MFMAs. Its waves walk the key tiles (32 tokens) of the workgroup's key split in order;
 //     the splits (blockIdx.z) fill the device when the row blocks alone do not, and a merge kernel folds them.
 //   * Each tile's codes go from HBM straight into the registers of the wave that converts them (wave w: K chunk w
-//     and V chunk w, a tile ahead), its scales chunk into a small LDS ring; every wave converts its two chunks into
-//     the fp16 operand planes of the tile (K hi, K lo, V hi, V lo: code x scale for both, the V scale per token;
-//     double-buffered: tile k + 1's while tile k is computed); then every wave runs S^T = K Q^T (two
-//     v_mfma_f32_16x16x32_f16 a block, half and row tile) and O^T += V^T P^T (three a 16-value tile and row tile:
-//     V hi P hi, V lo P hi, V hi P lo). Scaling V once a workgroup instead of P once a row tile and block keeps the
-//     per-wave VALU work (which the counters showed issuing mostly apart from the matrix cores) to the softmax.
+//     and V chunk w, a tile ahead), its scales chunk into a small LDS ring; every wave writes its two chunks as fp16
+//     operand planes (K codes, V codes; double-buffered: tile k + 1's while tile k is computed), and four waves
+//     write the K scales in the scores' lane order beside them; then every wave runs S^T = K Q^T (one
+//     v_mfma_f32_16x16x32_f16 a block, half and row tile, then one FMA a score for the block's scale) and
+//     O^T += V^T P^T (two a 16-value tile and row tile: the codes against (P x V scale) hi and lo). Against
+//     dequantized hi + lo K and V planes this halves the operand bytes each wave reads from LDS and cuts the MFMAs a
+//     wave and tile from 159 to 96.
 //   * The softmax (base 2, the running max moved lazily) runs on the S^T registers as in the decode kernel; P feeds
 //     the PV MFMA in place.
 #include "../../include/fnkv.h"
@@ -57,7 +58,9 @@ constexpr int32_t kPfWaves = 8;                      // two a SIMD
 constexpr int32_t kPfNT = 2;                         // 16-row tiles a wave (each plane read serves both)
 constexpr int32_t kPfRows = kPfWaves * kPfNT * 16;   // 256 rows a workgroup
 constexpr int32_t kPfPlane = 16 * 1024;             // one fp16 operand plane of a tile
-constexpr int32_t kPfSet = 4 * kPfPlane;             // a tile's planes: K hi, K lo, V hi, V lo
+constexpr int32_t kPfKsc = 512;                      // the K scales in the scores' lane order: [half][block][qg][4]
+constexpr int32_t kPfKscOff = 2 * kPfPlane;
+constexpr int32_t kPfSet = kPfKscOff + kPfKsc;       // a tile's planes: K codes, V codes, K scales
 constexpr int32_t kPfScaleRing = 4;                  // tiles' scale chunks (K then V scales, 1 KiB), a ring
 constexpr int32_t kPfPages = 2048;                   // the split's page table entries held in LDS (a split <= 512 K cells)
 constexpr int32_t kPfLds = 2 * kPfSet + kPfScaleRing * 1024 + kPfPages * 4; // planes double-buffered, ring, pages
@@ -171,40 +174,32 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
         }
     }
 
-    // this wave's chunks of tile ti (in `codes`) -> the fp16 operand planes of set ti & 1, each exactly as hi + lo
-    // (code x scale has 8 x 11 significant bits: hi = fp16(code x scale), lo = the remainder by one fused multiply-add).
-    // K chunk w covers tokens 16 (w / 4) .. + 15 and blocks 2 (w % 4), 2 (w % 4) + 1 (the lane's row is a token: one
-    // scale a block); V chunk w the MFMA tiles 2 w, 2 w + 1 of block w (the lane's 8 slots are 8 tokens: their 8 V
-    // scales of block w, which the ring holds in slot order)
+    // this wave's chunks of tile ti (in `codes`) -> the operand planes of set ti & 1: K and V codes as exact fp16
+    // integers, and (waves 0-3) the K scales in the scores' lane order. K chunk w covers tokens 16 (w / 4) .. + 15 and
+    // blocks 2 (w % 4), 2 (w % 4) + 1; V chunk w the MFMA tiles 2 w, 2 w + 1 of block w (the V scales stay in the
+    // ring, already in the PV operand's slot order)
     auto dequant = [&](int32_t ti) {
         const uint8_t * rg = ring(ti); // K scales [32 tokens][8 blocks], then V scales [4 lane groups][8 blocks][8]
         uint8_t * pl = plane_base + (ti & 1) * kPfSet;
         {
             const int32_t h = wave >> 2, ld = wave & 3;
-            const half2v s2 = *reinterpret_cast<const half2v *>(rg + (16 * h + j) * 16 + ld * 4);
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb) {
                 const int32_t b = 2 * ld + bb;
-                const half8 code = widen8(codes[0][2 * bb], codes[0][2 * bb + 1]);
-                const half8 sv = {s2[bb], s2[bb], s2[bb], s2[bb], s2[bb], s2[bb], s2[bb], s2[bb]};
-                const half8 hi = code * sv;
-                const half8 lo = __builtin_elementwise_fma(code, sv, -hi);
                 const int32_t off = ((h * kBlocks + b) * 64 + lane) * 16;
-                *reinterpret_cast<half8 *>(pl + off) = hi;
-                *reinterpret_cast<half8 *>(pl + kPfPlane + off) = lo;
+                *reinterpret_cast<half8 *>(pl + off) = widen8(codes[0][2 * bb], codes[0][2 * bb + 1]);
             }
         }
-        {
-            const half8 vs = *reinterpret_cast<const half8 *>(rg + 512 + qg * 128 + wave * 16);
+        if (wave < 4) { // entry ((h, b, qg), r) = the scale of token 16 h + 4 qg + r, block b
+            const int32_t e = static_cast<int32_t>(threadIdx.x);
+            const int32_t r = e & 3, g = (e >> 2) & 3, b = (e >> 4) & 7, h = e >> 7;
+            *reinterpret_cast<uint16_t *>(pl + kPfKscOff + e * 2) =
+                *reinterpret_cast<const uint16_t *>(rg + (16 * h + 4 * g + r) * 16 + b * 2);
+        }
 #pragma unroll
-            for (int mm = 0; mm < 2; ++mm) {
-                const half8 code = widen8(codes[1][2 * mm], codes[1][2 * mm + 1]);
-                const half8 hi = code * vs;
-                const half8 lo = __builtin_elementwise_fma(code, vs, -hi);
-                const int32_t off = ((2 * wave + mm) * 64 + lane) * 16;
-                *reinterpret_cast<half8 *>(pl + 2 * kPfPlane + off) = hi;
-                *reinterpret_cast<half8 *>(pl + 3 * kPfPlane + off) = lo;
-            }
+        for (int mm = 0; mm < 2; ++mm) {
+            const int32_t off = ((2 * wave + mm) * 64 + lane) * 16;
+            *reinterpret_cast<half8 *>(pl + kPfPlane + off) = widen8(codes[1][2 * mm], codes[1][2 * mm + 1]);
         }
     };
 
@@ -218,21 +213,29 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
             sc[nt][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
             sc[nt][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         }
+        // S^T block by block: the block's MFMA on the exact codes, then its K scale (the lane's four tokens) by one
+        // FMA a score
 #pragma unroll
-        for (int b = 0; b < kBlocks; ++b) {
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int32_t off = ((h * kBlocks + b) * 64 + lane) * 16;
-                const half8 khi = *reinterpret_cast<const half8 *>(pl + off);
-                const half8 klo = *reinterpret_cast<const half8 *>(pl + kPfPlane + off);
+            for (int b = 0; b < kBlocks; ++b) {
+                const half8 kc = *reinterpret_cast<const half8 *>(pl + ((h * kBlocks + b) * 64 + lane) * 16);
+                const half4v ks =
+                    *reinterpret_cast<const half4v *>(pl + kPfKscOff + ((h * kBlocks + b) * 4 + qg) * 8);
+                floatx4 t[kPfNT];
 #pragma unroll
                 for (int nt = 0; nt < kPfNT; ++nt) {
-                    sc[nt][h] = mfma16(khi, qop[nt][b], sc[nt][h]);
+                    t[nt] = mfma16(kc, qop[nt][b], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
                 }
 #pragma unroll
                 for (int nt = 0; nt < kPfNT; ++nt) {
-                    sc[nt][h] = mfma16(klo, qop[nt][b], sc[nt][h]);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        sc[nt][h][r] = __builtin_fmaf(static_cast<float>(ks[r]), t[nt][r], sc[nt][h][r]);
+                    }
+                    __asm__ volatile("" : "+v"(sc[nt][h]));
                 }
+                __builtin_amdgcn_sched_barrier(0); // one block's products live at a time
             }
         }
 #ifdef FNKV_TIMING
@@ -296,28 +299,22 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
             pf_last = now_;
         }
 #endif
-        // O^T += V^T P^T block by block: V hi P hi, V lo P hi, V hi P lo (the lo x lo term is below 2^-22); one
-        // accumulator's MFMAs are four apart
+        // O^T += V^T P^T block by block: P times the block's V scales (this lane's 8 tokens) as hi + lo fp16 (to
+        // ~2^-19), against the exact codes
+        const uint8_t * rgv = ring(ti) + 512 + qg * 128;
 #pragma unroll
         for (int b = 0; b < kBlocks; ++b) {
-            const half8 vh0 = *reinterpret_cast<const half8 *>(pl + 2 * kPfPlane + ((2 * b) * 64 + lane) * 16);
-            const half8 vh1 = *reinterpret_cast<const half8 *>(pl + 2 * kPfPlane + ((2 * b + 1) * 64 + lane) * 16);
-            const half8 vl0 = *reinterpret_cast<const half8 *>(pl + 3 * kPfPlane + ((2 * b) * 64 + lane) * 16);
-            const half8 vl1 = *reinterpret_cast<const half8 *>(pl + 3 * kPfPlane + ((2 * b + 1) * 64 + lane) * 16);
+            const half8 v0 = *reinterpret_cast<const half8 *>(pl + kPfPlane + ((2 * b) * 64 + lane) * 16);
+            const half8 v1 = *reinterpret_cast<const half8 *>(pl + kPfPlane + ((2 * b + 1) * 64 + lane) * 16);
+            const half8 vsb = *reinterpret_cast<const half8 *>(rgv + b * 16);
 #pragma unroll
             for (int nt = 0; nt < kPfNT; ++nt) {
-                acc[nt][2 * b] = mfma16(vh0, ph[nt], acc[nt][2 * b]);
-                acc[nt][2 * b + 1] = mfma16(vh1, ph[nt], acc[nt][2 * b + 1]);
-            }
-#pragma unroll
-            for (int nt = 0; nt < kPfNT; ++nt) {
-                acc[nt][2 * b] = mfma16(vl0, ph[nt], acc[nt][2 * b]);
-                acc[nt][2 * b + 1] = mfma16(vl1, ph[nt], acc[nt][2 * b + 1]);
-            }
-#pragma unroll
-            for (int nt = 0; nt < kPfNT; ++nt) {
-                acc[nt][2 * b] = mfma16(vh0, plo[nt], acc[nt][2 * b]);
-                acc[nt][2 * b + 1] = mfma16(vh1, plo[nt], acc[nt][2 * b + 1]);
+                half8 hi, lo;
+                scale_hilo_pk(ph[nt], plo[nt], vsb, hi, lo);
+                acc[nt][2 * b] = mfma16(v0, hi, acc[nt][2 * b]);
+                acc[nt][2 * b + 1] = mfma16(v1, hi, acc[nt][2 * b + 1]);
+                acc[nt][2 * b] = mfma16(v0, lo, acc[nt][2 * b]);
+                acc[nt][2 * b + 1] = mfma16(v1, lo, acc[nt][2 * b + 1]);
             }
             if (b & 1) {
                 __builtin_amdgcn_sched_barrier(0); // two blocks' operands live at a time
