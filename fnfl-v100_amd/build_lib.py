@@ -4,6 +4,10 @@ engine_step (host/engine_step.cpp: the reference engine's calling pattern over t
 hipcc compiles each source to an object (in parallel) and links the shared library next to this file. Every HIP
 source is compiled with packed-fp32 instructions disabled (their hand-written forms are avoided on this target) and
 with per-file flags (below).
+
+Measurement builds: FNKV_EXTRA_FLAGS adds flags to every source (e.g. -DFNKV_TIMING, the decode kernels' real-time
+stamps read by decode_timeline.py) and FNKV_LIB_OUT names the library to write instead of the in-tree one (its objects
+go to a build folder beside it; the harness is not built).
 """
 import concurrent.futures
 import os
@@ -12,8 +16,9 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
-BUILD = os.path.join(HERE, "_build")
-LIB = os.path.join(HERE, "libfnkv.so")
+LIB_OUT = os.environ.get("FNKV_LIB_OUT")
+BUILD = os.path.join(os.path.dirname(os.path.abspath(LIB_OUT)), "_build") if LIB_OUT else os.path.join(HERE, "_build")
+LIB = os.path.abspath(LIB_OUT) if LIB_OUT else os.path.join(HERE, "libfnkv.so")
 HARNESS = os.path.join(HERE, "engine_step")
 SOURCES = ["pool.hip", "append.hip", "decode.hip", "stream.hip", "prefill.hip", "sparse.hip", "datc.hip", "qsa.hip", "qsp.hip"]
 ARCH = os.environ.get("FNKV_ARCH", "gfx950")
@@ -53,6 +58,7 @@ def _compile(src):
 
 def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
+    os.makedirs(os.path.dirname(LIB), exist_ok=True)
     srcs = [s for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
@@ -62,6 +68,8 @@ def build(verbose=False):
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    if LIB_OUT:
+        return LIB
     # the host harness: host code only, linked against the library next to it
     tmp = HARNESS + ".tmp"
     cmd = [hipcc(), "-O2", "-std=c++17", "-Wall", "-I", os.path.join(HERE, "..", "include"),
