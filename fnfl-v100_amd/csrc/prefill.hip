@@ -214,28 +214,35 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_kernel(pf_args a) {
             sc[nt][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         }
         // S^T block by block: the block's MFMA on the exact codes, then its K scale (the lane's four tokens) by one
-        // FMA a score
+        // FMA a score; the next block's operands are read from LDS while this block's MFMAs run
+        auto kc_at = [&](int hb) { return *reinterpret_cast<const half8 *>(pl + (hb * 64 + lane) * 16); };
+        auto ks_at = [&](int hb) { return *reinterpret_cast<const half4v *>(pl + kPfKscOff + (hb * 4 + qg) * 8); };
+        half8 kc_next = kc_at(0);
+        half4v ks_next = ks_at(0);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int hb = 0; hb < 2 * kBlocks; ++hb) {
+            const int h = hb / kBlocks, b = hb % kBlocks;
+            const half8 kc = kc_next;
+            const half4v ks = ks_next;
+            if (hb + 1 < 2 * kBlocks) {
+                kc_next = kc_at(hb + 1);
+                ks_next = ks_at(hb + 1);
+            }
+            floatx4 t[kPfNT];
 #pragma unroll
-            for (int b = 0; b < kBlocks; ++b) {
-                const half8 kc = *reinterpret_cast<const half8 *>(pl + ((h * kBlocks + b) * 64 + lane) * 16);
-                const half4v ks =
-                    *reinterpret_cast<const half4v *>(pl + kPfKscOff + ((h * kBlocks + b) * 4 + qg) * 8);
-                floatx4 t[kPfNT];
+            for (int nt = 0; nt < kPfNT; ++nt) {
+                t[nt] = mfma16(kc, qop[nt][b], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+            }
 #pragma unroll
-                for (int nt = 0; nt < kPfNT; ++nt) {
-                    t[nt] = mfma16(kc, qop[nt][b], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+            for (int nt = 0; nt < kPfNT; ++nt) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    sc[nt][h][r] = __builtin_fmaf(static_cast<float>(ks[r]), t[nt][r], sc[nt][h][r]);
                 }
-#pragma unroll
-                for (int nt = 0; nt < kPfNT; ++nt) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        sc[nt][h][r] = __builtin_fmaf(static_cast<float>(ks[r]), t[nt][r], sc[nt][h][r]);
-                    }
-                    __asm__ volatile("" : "+v"(sc[nt][h]));
-                }
-                __builtin_amdgcn_sched_barrier(0); // one block's products live at a time
+                __asm__ volatile("" : "+v"(sc[nt][h]));
+            }
+            if (hb & 1) {
+                __builtin_amdgcn_sched_barrier(0); // two blocks' products live at a time
             }
         }
 #ifdef FNKV_TIMING

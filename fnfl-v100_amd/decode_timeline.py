@@ -74,6 +74,12 @@ def main():
         if v.size:
             r = us(v)
             print(f"  wave {wv} loop end       min {r.min():6.2f} median {np.median(r):6.2f} max {r.max():6.2f} us")
+    # workgroups are dealt to the 8 XCDs round-robin in launch order (x fastest, then y)
+    idx = np.nonzero(used)[0]
+    loop_end = us(s[:, 2])
+    print("loop end + barrier by XCD (workgroup index mod 8): median / max us")
+    print("  " + "  ".join(f"{x}: {np.median(loop_end[idx % 8 == x]):5.2f}/{loop_end[idx % 8 == x].max():5.2f}"
+                           for x in range(8)))
     ph = a[MAX_WG * 16:MAX_WG * 24].reshape(MAX_WG, 8)[used]
     print("wave 0's phase cycles summed over its tiles (median over workgroups):")
     for p, nm in enumerate(PHASES):
