@@ -66,6 +66,17 @@ __device__ __forceinline__ void stream_scores(const uint8_t * kb, const uint8_t 
                                               const half8 (&sig)[NT], int32_t j, int32_t qg, int32_t lane,
                                               floatx4 (&s_out)[NT][2]) {
     const half8 zero8 = {};
+    // a chunk's operands: its 16 K codes a lane and the row tiles' Q operands of its two blocks; each chunk's are read
+    // from LDS one chunk ahead, while the previous chunk's MFMAs run
+    auto kw_at = [&](int c) { return *reinterpret_cast<const u32x4 *>(kb + (c >> 2) * 4096 + (c & 3) * 1024 + lane * 16); };
+    auto qo_at = [&](int rt, int b) { return *reinterpret_cast<const half8 *>(qs + (rt * kBlocks + b) * 1024 + lane * 16); };
+    u32x4 kw_next = kw_at(0);
+    half8 qo_next[NT][2];
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt) {
+        qo_next[rt][0] = qo_at(rt, 0);
+        qo_next[rt][1] = qo_at(rt, 1);
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         half8 ks[4];
@@ -83,16 +94,29 @@ __device__ __forceinline__ void stream_scores(const uint8_t * kb, const uint8_t 
         }
 #pragma unroll
         for (int ld = 0; ld < 4; ++ld) { // one 1 KiB chunk: blocks 2 ld, 2 ld + 1
-            const u32x4 kw = *reinterpret_cast<const u32x4 *>(kb + h * 4096 + ld * 1024 + lane * 16);
+            const int c = 4 * h + ld;
+            const u32x4 kw = kw_next;
+            half8 qo[NT][2];
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt) {
+                qo[rt][0] = qo_next[rt][0];
+                qo[rt][1] = qo_next[rt][1];
+            }
+            if (c + 1 < 8) {
+                kw_next = kw_at(c + 1);
+#pragma unroll
+                for (int rt = 0; rt < NT; ++rt) {
+                    qo_next[rt][0] = qo_at(rt, 2 * ((c + 1) & 3));
+                    qo_next[rt][1] = qo_at(rt, 2 * ((c + 1) & 3) + 1);
+                }
+            }
             floatx4 t[NT][2];
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb) {
-                const int b = 2 * ld + bb;
                 const half8 ka = widen8<false>(kw[2 * bb], kw[2 * bb + 1]);
 #pragma unroll
                 for (int rt = 0; rt < NT; ++rt) {
-                    const half8 qo = *reinterpret_cast<const half8 *>(qs + (rt * kBlocks + b) * 1024 + lane * 16);
-                    t[rt][bb] = mfma16(ka, qo, floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+                    t[rt][bb] = mfma16(ka, qo[rt][bb], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
                 }
             }
 #pragma unroll
@@ -575,12 +599,19 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
                 lv[rt] = mfma16(sva, ph[rt], lv[rt]);
                 lv[rt] = mfma16(sva, pl[rt], lv[rt]);
             }
+            // each block's V codes and scales are read from LDS one block ahead
+            u32x4 vw_next = *reinterpret_cast<const u32x4 *>(kb + kVCodes + lane * 16);
+            half8 vs_next = *reinterpret_cast<const half8 *>(sc + 512 + qg * 128);
 #pragma unroll
             for (int b = 0; b < kBlocks; ++b) {
-                const u32x4 vw = *reinterpret_cast<const u32x4 *>(kb + kVCodes + b * 1024 + lane * 16);
+                const u32x4 vw = vw_next;
+                const half8 vs = vs_next;
+                if (b + 1 < kBlocks) {
+                    vw_next = *reinterpret_cast<const u32x4 *>(kb + kVCodes + (b + 1) * 1024 + lane * 16);
+                    vs_next = *reinterpret_cast<const half8 *>(sc + 512 + qg * 128 + (b + 1) * 16);
+                }
                 const half8 va0 = widen8<false>(vw[0], vw[1]);
                 const half8 va1 = widen8<false>(vw[2], vw[3]);
-                const half8 vs = *reinterpret_cast<const half8 *>(sc + 512 + qg * 128 + b * 16);
 #pragma unroll
                 for (int rt = 0; rt < NTW; ++rt) {
                     half8 hi, lo;
