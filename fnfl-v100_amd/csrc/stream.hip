@@ -422,9 +422,6 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     using SH = stream_shape<NT>;
     constexpr int WAVES = SH::WAVES, STREAMS = SH::STREAMS;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-#if FNKV_EXP == 1
-    return;
-#endif
     const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
     const int32_t wave = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(threadIdx.x) >> 6);
     const int32_t j = lane & 15, qg = lane >> 4;
@@ -728,27 +725,12 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
                                 store_agent2(a.pml + prow * 2, Mr, L);
                             }
                         } else {
-#if FNKV_EXP == 2
-                            if (L == 12345.0f) {
-#endif
-#if FNKV_EXP == 3
-                            __builtin_nontemporal_store(sum[0], reinterpret_cast<floatx4 *>(dst));
-                            __builtin_nontemporal_store(sum[1], reinterpret_cast<floatx4 *>(dst + 128));
-                            if ((t & 31) == 0) {
-                                __builtin_nontemporal_store(Mr, a.pml + prow * 2);
-                                __builtin_nontemporal_store(L, a.pml + prow * 2 + 1);
-                            }
-#else
                             *reinterpret_cast<floatx4 *>(dst) = sum[0];
                             *reinterpret_cast<floatx4 *>(dst + 128) = sum[1];
                             if ((t & 31) == 0) {
                                 a.pml[prow * 2 + 0] = Mr;
                                 a.pml[prow * 2 + 1] = L;
                             }
-#endif
-#if FNKV_EXP == 2
-                            }
-#endif
                         }
                     }
                 }
