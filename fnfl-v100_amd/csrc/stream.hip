@@ -50,8 +50,7 @@ template <int NT> struct stream_shape {
     static constexpr int RING = WAVES * SLOT;        // 139,264 B
     static constexpr int QOPS = NT * kBlocks * 1024; // the Q operands: [row tile][block][lane] 16 B
     static constexpr int OSTRIDE = kHeadDim + 4;     // floats a row of the fold buffer
-    static constexpr int FOLD = STREAMS * 16 * OSTRIDE * 4 + NT * 16 * STREAMS * 2 * 4;
-    static constexpr int LDS = RING + QOPS > FOLD ? RING + QOPS : FOLD;
+    static constexpr int LDS = RING + QOPS; // the 8-wave fold reuses the tile slots
     static_assert(LDS <= 160 * 1024, "LDS");
     // a half tile is 9 loads: 8 chunks of codes and half of the scales chunk; the wave waits for one half with the
     // other half's 9 issued after it
@@ -641,101 +640,105 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
             l_row[rt] = __shfl(lv[rt][0], j + 32);
         }
 
-        // ---- fold the STREAMS waves holding each row tile in LDS (fixed order), then the workgroup's row: the
-        // output itself when the split is its sequence's only one, else the split's partial ----
+        // ---- fold the STREAMS waves holding each row tile (fixed order), then the workgroup's row: the output itself
+        // when the split is its sequence's only one, else the split's partial. A wave writes a row tile's unscaled
+        // accumulators and its rows' (m, l) into its own tile slot as soon as its walk has ended (no other wave
+        // reads that slot), so the first waves' writes run beside the last waves' walks; the reads scale each
+        // holder's values by 2^(m - M). Pass k folds each group's k-th row tile. ----
         constexpr int32_t OS = SH::OSTRIDE;
-        const int32_t h = st; // this wave's place among the row tiles' holders
-        __syncthreads();      // the slots are no longer read
-        FNKV_STAMP(2);
-        float * ml = reinterpret_cast<float *>(smem);                              // [NT 16 rows][holder][2]
-        float * ob = reinterpret_cast<float *>(smem + NT * 16 * STREAMS * 2 * 4);  // [holder][16 rows][OS]
-        if (qg == 0) {
+        constexpr int32_t ML = 16 * OS;                 // floats: (m, l) of the slot's 16 rows, after its values
+        static_assert((ML + 16 * 2) * 4 <= SH::SLOT, "a row tile's fold buffer fits a tile slot");
+        constexpr int32_t PASSES = SH::GROUPS == 1 ? NT : 2;
+        float * const mine = reinterpret_cast<float *>(slot);
 #pragma unroll
-            for (int rt = 0; rt < NTW; ++rt) {
-                ml[(((RTB + rt) * 16 + j) * STREAMS + h) * 2 + 0] = m_run[rt];
-                ml[(((RTB + rt) * 16 + j) * STREAMS + h) * 2 + 1] = l_row[rt];
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int rt = 0; rt < NT; ++rt) {
-            // this wave holds row tile rt as its rl-th (a constant once the loop is unrolled)
-            const int32_t rl = rt < RTB ? 0 : (rt - RTB >= NTW ? NTW - 1 : rt - RTB);
-            if (rt >= RTB && rt < RTB + NTW) {
-                const float * mlr = ml + ((rt * 16 + j) * STREAMS) * 2;
-                float M = kNegInf;
-#pragma unroll
-                for (int w = 0; w < STREAMS; ++w) {
-                    M = fmaxf(M, mlr[2 * w]);
-                }
-                const float f = __builtin_amdgcn_exp2f(m_run[rl] - (M == kNegInf ? 0.0f : M));
-                if (rt * 16 + j < a.R) { // padding rows are not folded
+        for (int32_t k = 0; k < PASSES; ++k) {
+            if (k < NTW) {
+                if ((RTB + k) * 16 + j < a.R) { // padding rows are not folded
 #pragma unroll
                     for (int b = 0; b < kBlocks; ++b) {
 #pragma unroll
                         for (int hh = 0; hh < 2; ++hh) {
-                            *reinterpret_cast<floatx4 *>(ob + (h * 16 + j) * OS + 16 * (2 * b + hh) + 4 * qg) =
-                                acc[rl][b][hh] * f;
+                            *reinterpret_cast<floatx4 *>(mine + j * OS + 16 * (2 * b + hh) + 4 * qg) = acc[k][b][hh];
                         }
                     }
+                }
+                if (qg == 0) {
+                    *reinterpret_cast<float2 *>(mine + ML + 2 * j) = float2{m_run[k], l_row[k]};
                 }
             }
             __syncthreads();
-            // thread -> (row, values c0 .. c0 + 3 and 128 + c0 .. + 3): 16 rows x 32 groups (a row's 32 threads
-            // read consecutive 16-byte pieces, conflict-free)
-            {
+            if (k == 0) {
+                FNKV_STAMP(2);
+            }
+            // thread -> (row, values c0 .. c0 + 3 and 128 + c0 .. + 3) of each of the pass's row tiles: 16 rows x 32
+            // groups (a row's 32 threads read consecutive 16-byte pieces of each holder's slot, conflict-free)
+#pragma unroll
+            for (int32_t g = 0; g < SH::GROUPS; ++g) {
+                const int32_t ntw_g = SH::GROUPS == 1 ? NT : (g == 0 ? 2 : 1);
+                const int32_t rtb_g = g == 0 ? 0 : 2;
+                if (k >= ntw_g) {
+                    continue;
+                }
+                const int32_t rt = rtb_g + k;
                 const int32_t t = static_cast<int32_t>(threadIdx.x);
                 const int32_t rrow = t >> 5, c0 = (t & 31) * 4;
                 const int32_t r = rt * 16 + rrow;
-                if (r < a.R) {
-                    floatx4 sum[2];
+                if (r >= a.R) {
+                    continue;
+                }
+                const float * const hold = reinterpret_cast<const float *>(smem + g * STREAMS * SH::SLOT);
+                float2 mlw[STREAMS];
+                float Mr = kNegInf;
+#pragma unroll
+                for (int w = 0; w < STREAMS; ++w) {
+                    mlw[w] = *reinterpret_cast<const float2 *>(hold + w * (SH::SLOT / 4) + ML + 2 * rrow);
+                    Mr = fmaxf(Mr, mlw[w].x);
+                }
+                const float Mr_use = Mr == kNegInf ? 0.0f : Mr;
+                float L = 0.0f;
+                floatx4 sum[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+                for (int w = 0; w < STREAMS; ++w) {
+                    const float f = __builtin_amdgcn_exp2f(mlw[w].x - Mr_use);
+                    L = __builtin_fmaf(mlw[w].y, f, L);
 #pragma unroll
                     for (int c = 0; c < 2; ++c) {
-                        sum[c] = *reinterpret_cast<const floatx4 *>(ob + rrow * OS + c0 + 128 * c);
+                        const floatx4 v =
+                            *reinterpret_cast<const floatx4 *>(hold + w * (SH::SLOT / 4) + rrow * OS + c0 + 128 * c);
 #pragma unroll
-                        for (int w = 1; w < STREAMS; ++w) {
-                            sum[c] += *reinterpret_cast<const floatx4 *>(ob + (w * 16 + rrow) * OS + c0 + 128 * c);
+                        for (int e = 0; e < 4; ++e) {
+                            sum[c][e] = __builtin_fmaf(v[e], f, sum[c][e]);
                         }
                     }
-                    const float * mlr = ml + (r * STREAMS) * 2;
-                    float Mr = kNegInf;
-#pragma unroll
-                    for (int w = 0; w < STREAMS; ++w) {
-                        Mr = fmaxf(Mr, mlr[2 * w]);
-                    }
-                    const float Mr_use = Mr == kNegInf ? 0.0f : Mr;
-                    float L = 0.0f;
-#pragma unroll
-                    for (int w = 0; w < STREAMS; ++w) {
-                        L += mlr[2 * w + 1] * __builtin_amdgcn_exp2f(mlr[2 * w] - Mr_use);
-                    }
-                    if (unmapped) {
-                        Mr = __builtin_nanf(""); // the merge (or the fold) writes nothing for this row
-                    }
-                    if (direct && !unmapped) {
-                        store_out4(a, s, kvh, r, c0, sum[0], 1.0f / L);
-                        store_out4(a, s, kvh, r, 128 + c0, sum[1], 1.0f / L);
-                    } else if (!direct) {
-                        const int64_t prow = (int64_t(split) * pv.h_kv + kvh) * a.R + r;
-                        float * dst = a.po + prow * kHeadDim + c0;
-                        if (a.fold != nullptr) { // read by other workgroups in this launch: device-scope stores
-                            store_agent(dst, sum[0]);
-                            store_agent(dst + 128, sum[1]);
-                            if ((t & 31) == 0) {
-                                store_agent2(a.pml + prow * 2, Mr, L);
-                            }
-                        } else {
-                            *reinterpret_cast<floatx4 *>(dst) = sum[0];
-                            *reinterpret_cast<floatx4 *>(dst + 128) = sum[1];
-                            if ((t & 31) == 0) {
-                                a.pml[prow * 2 + 0] = Mr;
-                                a.pml[prow * 2 + 1] = L;
-                            }
+                }
+                if (unmapped) {
+                    Mr = __builtin_nanf(""); // the merge (or the fold) writes nothing for this row
+                }
+                if (direct && !unmapped) {
+                    store_out4(a, s, kvh, r, c0, sum[0], 1.0f / L);
+                    store_out4(a, s, kvh, r, 128 + c0, sum[1], 1.0f / L);
+                } else if (!direct) {
+                    const int64_t prow = (int64_t(split) * pv.h_kv + kvh) * a.R + r;
+                    float * dst = a.po + prow * kHeadDim + c0;
+                    if (a.fold != nullptr) { // read by other workgroups in this launch: device-scope stores
+                        store_agent(dst, sum[0]);
+                        store_agent(dst + 128, sum[1]);
+                        if ((t & 31) == 0) {
+                            store_agent2(a.pml + prow * 2, Mr, L);
+                        }
+                    } else {
+                        *reinterpret_cast<floatx4 *>(dst) = sum[0];
+                        *reinterpret_cast<floatx4 *>(dst + 128) = sum[1];
+                        if ((t & 31) == 0) {
+                            a.pml[prow * 2 + 0] = Mr;
+                            a.pml[prow * 2 + 1] = L;
                         }
                     }
                 }
             }
-            __syncthreads(); // ob is rewritten by the next row tile
+            if (k + 1 < PASSES) {
+                __syncthreads(); // the slots are rewritten by the next pass
+            }
         }
     };
     if constexpr (SH::GROUPS == 1) {
