@@ -163,6 +163,39 @@ def test_decode_refused_context_writes_nothing(bad):
     assert cases.out_err(out[1].cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_replay_after_trim_reads_no_unmapped_page(T):
+    # Outside the contract (a slot must stay mapped up to the bound while a captured launch can run): the slot of
+    # sequence 1 is trimmed below the context its captured launch reads, so the tail of its page-table row is
+    # unmapped (-1). The replay reads nothing through those entries (the walk takes page 0 instead), writes nothing
+    # for that sequence (no outputs, no new cells) and sets the refused-depth bit; sequence 0 is computed as before.
+    # T = 1 walks strided splits, T = 3 contiguous ones.
+    ctx = [3000, 5000]
+    L = DecodeLoop(ctx, T, 0, seed=21 + T)
+    ctx_dev = torch.tensor(ctx, dtype=torch.int64, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    q = torch.from_numpy(cases.queries(5, (2, T, HQ, D))).cuda()
+    kn = torch.from_numpy(np.stack([L.kv[i][0][c - T:c] for i, c in enumerate(ctx)])).cuda()
+    vn = torch.from_numpy(np.stack([L.kv[i][1][c - T:c] for i, c in enumerate(ctx)])).cuda()
+    out = torch.full_like(q, 7.0)
+    ws = torch.zeros(L.pool.decode_ws_bytes(ctx, T, HQ), dtype=torch.uint8, device="cuda")
+    g = capture(lambda: L.pool.decode_dev(L.slots, ctx_dev, ctx, T, 0, q, out, ws, err, k_new=kn, v_new=vn))
+    g.replay()
+    torch.cuda.synchronize()
+    assert err.item() == 0
+    ref = out.clone()
+    assert L.pool.trim(1, 1024) == 0  # the engine would drain and re-capture first; this replay runs regardless
+    assert L.pool.mapped_cells(1) == 1024
+    out.fill_(7.0)
+    for _ in range(2):
+        g.replay()
+        torch.cuda.synchronize()
+        assert err.item() == fnkv.DEV_ERR_DEPTH
+        assert bool((out[1] == 7.0).all())  # nothing written for the trimmed sequence
+        assert torch.equal(out[0].view(torch.int16), ref[0].view(torch.int16))  # the other one as before
+        err.zero_()
+
+
 def test_decode_dev_host_refusals_enqueue_nothing():
     L = DecodeLoop([600], 1, 1, seed=2)
     q = torch.zeros((1, 1, HQ, D), dtype=torch.float16, device="cuda")
