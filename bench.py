@@ -1129,8 +1129,8 @@ def main():
                         "decode_gb_s": l4["decode_part"]["achieved"], "decode_frac": l4["decode_part"]["frac"],
                         "tokens_s": l4["value"]}
         c3 = CONFIGS["cfg3"]
-        _, gpu_s, _, _ = time_prefill(args, c3, 3, 1)
-        step_s = gpu_s / 3
+        _, gpu_s, _, _ = time_prefill(args, c3, 10, 2)
+        step_s = gpu_s / 10
         tf = prefill_flops(c3["ctxs"][0], c3["T"]) / step_s / 1e12
         also["cfg3"] = {"workload": c3["workload"], "step_us": round(step_s * 1e6, 3), "achieved_tflops": round(tf, 3),
                         "frac": round(tf / PEAK_MFMA_F16_TFLOPS, 4), "bound": "mfma"}
