@@ -421,6 +421,7 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     using SH = stream_shape<NT>;
     constexpr int WAVES = SH::WAVES, STREAMS = SH::STREAMS;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    FNKV_STAMP(5);
     const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
     const int32_t wave = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(threadIdx.x) >> 6);
     const int32_t j = lane & 15, qg = lane >> 4;
@@ -453,6 +454,7 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     }
     split_src<false> src;
     src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, nullptr, ctx);
+    FNKV_STAMP(6);
     if (refused<false>(a, s, ctx, sp, kvh)) {
         return;
     }

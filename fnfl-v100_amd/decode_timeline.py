@@ -5,7 +5,9 @@ end, and wave 0 sums its shader-clock cycles per loop phase).
     FNKV_EXTRA_FLAGS=-DFNKV_TIMING FNKV_LIB_OUT=/tmp/fnkv_timing/libfnkv.so python3 fnfl-v100_amd/build_lib.py
     FNKV_LIB_PATH=/tmp/fnkv_timing/libfnkv.so python3 fnfl-v100_amd/decode_timeline.py --ctxs 8192,16384,32768,65536 --T 3
 
-Times are microseconds after the first workgroup's first stamp (taken after its kernel-argument and page-table reads).
+Times are microseconds after the first workgroup's "entry" stamp (its first instruction once its kernel arguments
+are in); "page table in" is the landing of its walk's page-table entries and Q rows, "start" its first stamp after
+them.
 A product build has no stamps: this tool refuses to run on one."""
 import argparse
 import ctypes
@@ -19,7 +21,7 @@ for p in (os.path.join(ROOT, "fnfl-v100_amd"), os.path.join(ROOT, "tests"), ROOT
     if p not in sys.path:
         sys.path.insert(0, p)
 
-STAMPS = ["start", "q + first tile in", "loop end + barrier", "LDS fold done", "end"]
+STAMPS = ["start", "q + first tile in", "loop end + barrier", "LDS fold done", "end", "entry", "page table in"]
 PHASES = ["wait K", "scores + issue K", "softmax", "wait V", "PV + issue V", "-", "loop back"]
 MAX_WG = 4096
 
@@ -59,7 +61,7 @@ def main():
     s = st[used]
     if not used.any():
         sys.exit("decode_timeline: no stamps were written")
-    t0 = s[:, 0].min()
+    t0 = s[:, 5].min() if (s[:, 5] != 0).all() else s[:, 0].min()  # the first workgroup's entry
     us = lambda v: (v - t0) * 10 / 1000.0  # noqa: E731 (real-time ticks of 10 ns)
     print(f"contexts {ctxs}, T = {args.T}: {int(used.sum())} workgroups")
     for k, nm in enumerate(STAMPS):
