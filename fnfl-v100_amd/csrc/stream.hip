@@ -59,8 +59,9 @@ template <int NT> struct stream_shape {
 
 // S^T = K Q^T of one tile for NT row tiles from the K codes (kb) and the scales chunk (sc) in LDS: sc_out[rt][h][r]
 // is the score (q . k, unscaled) of token 16 h + 4 qg + r against row 16 rt + j. Each 1 KiB chunk of K codes is
-// widened once and feeds the MFMAs of every row tile.
-template <int NT>
+// widened once and feeds the MFMAs of every row tile. KV8: a chunk's two blocks are one 64-value group with one
+// scale, so their two MFMAs chain and the group takes one FMA a score.
+template <int NT, bool KV8>
 __device__ __forceinline__ void stream_scores(const uint8_t * kb, const uint8_t * sc, const uint8_t * qs,
                                               const half8 (&sig)[NT], int32_t j, int32_t qg, int32_t lane,
                                               floatx4 (&s_out)[NT][2]) {
@@ -115,11 +116,15 @@ __device__ __forceinline__ void stream_scores(const uint8_t * kb, const uint8_t 
                 const half8 ka = widen8<false>(kw[2 * bb], kw[2 * bb + 1]);
 #pragma unroll
                 for (int rt = 0; rt < NT; ++rt) {
-                    t[rt][bb] = mfma16(ka, qo[rt][bb], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+                    if constexpr (KV8) { // the group's second block adds to its first
+                        t[rt][0] = mfma16(ka, qo[rt][bb], bb == 0 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : t[rt][0]);
+                    } else {
+                        t[rt][bb] = mfma16(ka, qo[rt][bb], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+                    }
                 }
             }
 #pragma unroll
-            for (int bb = 0; bb < 2; ++bb) {
+            for (int bb = 0; bb < (KV8 ? 1 : 2); ++bb) {
 #pragma unroll
                 for (int rt = 0; rt < NT; ++rt) {
 #pragma unroll
@@ -416,7 +421,7 @@ __device__ void fold_splits(const dec_args & a, int32_t s, int32_t kvh, int32_t 
     }
 }
 
-template <int NT>
+template <int NT, bool KV8>
 __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     using SH = stream_shape<NT>;
     constexpr int WAVES = SH::WAVES, STREAMS = SH::STREAMS;
@@ -563,7 +568,7 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
             const uint8_t * kb = slot;
             const uint8_t * sc = kb + kKScales;
             floatx4 scv[NTW][2];
-            stream_scores<NTW>(kb, sc, qw, sig, j, qg, lane, scv);
+            stream_scores<NTW, KV8>(kb, sc, qw, sig, j, qg, lane, scv);
             issue_half(i + 1, 0); // the scores' reads of K(i) are done (their values are in registers)
             FNKV_PHASE(2);
             const int64_t tok0 = src.tok0(st + i * STREAMS);
@@ -600,20 +605,26 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
             // each block's V codes and scales are read from LDS one block ahead
             u32x4 vw_next = *reinterpret_cast<const u32x4 *>(kb + kVCodes + lane * 16);
             half8 vs_next = *reinterpret_cast<const half8 *>(sc + 512 + qg * 128);
+            // KV8: a group's two blocks share their scales, so its P x V-scale products serve both
+            half8 phs[NTW], pls[NTW];
 #pragma unroll
             for (int b = 0; b < kBlocks; ++b) {
                 const u32x4 vw = vw_next;
                 const half8 vs = vs_next;
                 if (b + 1 < kBlocks) {
                     vw_next = *reinterpret_cast<const u32x4 *>(kb + kVCodes + (b + 1) * 1024 + lane * 16);
-                    vs_next = *reinterpret_cast<const half8 *>(sc + 512 + qg * 128 + (b + 1) * 16);
+                    if (!KV8 || (b & 1) == 1) {
+                        vs_next = *reinterpret_cast<const half8 *>(sc + 512 + qg * 128 + (b + 1) * 16);
+                    }
                 }
                 const half8 va0 = widen8<false>(vw[0], vw[1]);
                 const half8 va1 = widen8<false>(vw[2], vw[3]);
 #pragma unroll
                 for (int rt = 0; rt < NTW; ++rt) {
-                    half8 hi, lo;
-                    scale_hilo_pk(ph[rt], pl[rt], vs, hi, lo);
+                    if (!KV8 || (b & 1) == 0) {
+                        scale_hilo_pk(ph[rt], pl[rt], vs, phs[rt], pls[rt]);
+                    }
+                    const half8 hi = phs[rt], lo = pls[rt];
                     acc[rt][b][0] = mfma16(va0, hi, acc[rt][b][0]);
                     acc[rt][b][1] = mfma16(va1, hi, acc[rt][b][1]);
                     acc[rt][b][0] = mfma16(va0, lo, acc[rt][b][0]);
@@ -784,11 +795,13 @@ int32_t choose_split_stream(int32_t n_seq, const int64_t * ctx, int32_t h_kv, in
 }
 
 template <int NT> void set_stream_attr() {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(stream_kernel<NT>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(stream_kernel<NT, false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, stream_shape<NT>::LDS);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(stream_kernel<NT, true>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, stream_shape<NT>::LDS);
 }
 
-// the dense launch's kernel for NT row tiles (1 .. 3), its LDS attribute set once per device
+// the dense launch's kernel for NT row tiles (1 .. 3) and the pool's format, its LDS attribute set once per device
 void launch_stream(int32_t device, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
     static std::once_flag attr_once[64];
     if (device >= 0 && device < 64) {
@@ -804,12 +817,25 @@ void launch_stream(int32_t device, int32_t NT, dim3 grid, const dec_args & a, hi
         });
     }
     const dim3 block(64 * stream_shape<1>::WAVES);
+    const bool kv8 = a.pv.format == kFormatKV8;
     if (NT == 1) {
-        hipLaunchKernelGGL(stream_kernel<1>, grid, block, stream_shape<1>::LDS, st, a);
+        if (kv8) {
+            hipLaunchKernelGGL((stream_kernel<1, true>), grid, block, stream_shape<1>::LDS, st, a);
+        } else {
+            hipLaunchKernelGGL((stream_kernel<1, false>), grid, block, stream_shape<1>::LDS, st, a);
+        }
     } else if (NT == 2) {
-        hipLaunchKernelGGL(stream_kernel<2>, grid, block, stream_shape<2>::LDS, st, a);
+        if (kv8) {
+            hipLaunchKernelGGL((stream_kernel<2, true>), grid, block, stream_shape<2>::LDS, st, a);
+        } else {
+            hipLaunchKernelGGL((stream_kernel<2, false>), grid, block, stream_shape<2>::LDS, st, a);
+        }
     } else {
-        hipLaunchKernelGGL(stream_kernel<3>, grid, block, stream_shape<3>::LDS, st, a);
+        if (kv8) {
+            hipLaunchKernelGGL((stream_kernel<3, true>), grid, block, stream_shape<3>::LDS, st, a);
+        } else {
+            hipLaunchKernelGGL((stream_kernel<3, false>), grid, block, stream_shape<3>::LDS, st, a);
+        }
     }
 }
 
