@@ -71,3 +71,14 @@ def test_rope_theta_scale_is_the_f32_power():
     got = np.float32(fnkv.rope_theta_scale())
     want = np.float32(10000000.0 ** (-2.0 / 64.0))
     assert abs(float(got) - float(want)) <= float(np.spacing(want))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    # the bench contract: N > 1 exits with a message (one GPU only), before touching a device
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)
