@@ -15,8 +15,9 @@
  *                                   code = clamp(nearbyint(x / s), -127, 127)).
  *   or_pages_*                      fn/model/kv_pool.cpp:85-144 kv_pages (pages_for, take, give, physical).
  *   or_reclaim_victim               fn/model/kv_pool.cpp:146-158 kv_reclaim_victim.
- *   or_attn_f64                     fn/kernels/qsa/qa2_test.cpp:532-583, the FP64 attention form (scores q.k / 16,
- *                                   max-subtracted exp, sum, normalise) over the DECODED cache, made dense and causal.
+ *   or_attn_f64, or_attn_f64_mt     fn/kernels/qsa/qa2_test.cpp:532-583, the FP64 attention form (scores q.k / 16,
+ *                                   max-subtracted exp, sum, normalise) over the DECODED cache, made dense and causal;
+ *                                   _mt spreads the (row, KV head) pairs over threads, the same bits.
  *   or_attn_ggml                    ggml-cpu's flash attention over Q8_0 K/V as the pinned llama.cpp runs it (source
  *                                   not in the checkout; restated from its published algorithm): F32 online softmax
  *                                   per query row over keys in order, K rows dequantized (or Q quantized to Q8_0 and
@@ -242,40 +243,128 @@ int32_t or_reclaim_victim(const uint8_t * active, const int32_t * pages, const u
  *   rows  query tokens to evaluate (n_rows of them; NULL: all T)
  *   out   f64 [n_rows][hq][d]
  */
-void or_attn_f64(const uint16_t * q, const float * k, const float * v, int32_t n_ctx, int32_t T, int32_t hq,
-                 int32_t hkv, int32_t d, double scale, const int32_t * rows, int32_t n_rows, double * out) {
+/* One (row, KV head) of or_attn_f64: the group's query heads side by side (each head's dot products, maxima, sums and
+ * accumulators in the same order as one head alone, so the result is the same bits), s: [n_ctx][grp] scratch. */
+static void attn_f64_row_group(const uint16_t * q, const float * k, const float * v, int32_t n_ctx, int32_t T,
+                               int32_t hq, int32_t hkv, int32_t d, double scale, int32_t t, int32_t kh, double * s,
+                               double * qd, double * out_row) {
     const int32_t grp = hq / hkv;
-    double * s = (double *)malloc(sizeof(double) * (size_t)(n_ctx > 0 ? n_ctx : 1));
-    double * qd = (double *)malloc(sizeof(double) * (size_t)d);
-    const int32_t nr = rows ? n_rows : T;
-    for (int32_t ri = 0; ri < nr; ++ri) {
-        const int32_t t = rows ? rows[ri] : ri;
-        const int32_t last = n_ctx - T + t;
-        for (int32_t h = 0; h < hq; ++h) {
-            const int32_t kh = h / grp;
-            for (int32_t e = 0; e < d; ++e) qd[e] = (double)or_f16_to_f32(q[((int64_t)t * hq + h) * d + e]);
-            double m = -INFINITY;
-            for (int32_t c = 0; c <= last; ++c) {
-                const float * kr = k + ((int64_t)c * hkv + kh) * d;
-                double acc = 0.0;
-                for (int32_t e = 0; e < d; ++e) acc += qd[e] * (double)kr[e];
-                s[c] = acc * scale;
-                if (s[c] > m) m = s[c];
-            }
-            double * o = out + ((int64_t)ri * hq + h) * d;
-            for (int32_t e = 0; e < d; ++e) o[e] = 0.0;
-            double l = 0.0;
-            for (int32_t c = 0; c <= last; ++c) {
-                const double p = exp(s[c] - m);
-                l += p;
-                const float * vr = v + ((int64_t)c * hkv + kh) * d;
-                for (int32_t e = 0; e < d; ++e) o[e] += p * (double)vr[e];
-            }
-            for (int32_t e = 0; e < d; ++e) o[e] /= l;
+    const int32_t last = n_ctx - T + t;
+    for (int32_t g = 0; g < grp; ++g) {
+        const int32_t h = kh * grp + g;
+        for (int32_t e = 0; e < d; ++e) qd[(int64_t)e * grp + g] = (double)or_f16_to_f32(q[((int64_t)t * hq + h) * d + e]);
+    }
+    double m[64], l[64];
+    for (int32_t g = 0; g < grp; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0;
+    }
+    for (int32_t c = 0; c <= last; ++c) {
+        const float * kr = k + ((int64_t)c * hkv + kh) * d;
+        double acc[64];
+        for (int32_t g = 0; g < grp; ++g) acc[g] = 0.0;
+        for (int32_t e = 0; e < d; ++e) { /* each head's sum in the order e = 0, 1, ...; the heads side by side */
+            const double ke = (double)kr[e];
+            for (int32_t g = 0; g < grp; ++g) acc[g] += qd[(int64_t)e * grp + g] * ke;
         }
+        for (int32_t g = 0; g < grp; ++g) {
+            const double sc = acc[g] * scale;
+            s[(int64_t)c * grp + g] = sc;
+            if (sc > m[g]) m[g] = sc;
+        }
+    }
+    for (int32_t g = 0; g < grp; ++g) {
+        double * o = out_row + (int64_t)(kh * grp + g) * d;
+        for (int32_t e = 0; e < d; ++e) o[e] = 0.0;
+    }
+    for (int32_t c = 0; c <= last; ++c) {
+        const float * vr = v + ((int64_t)c * hkv + kh) * d;
+        for (int32_t g = 0; g < grp; ++g) {
+            const double p = exp(s[(int64_t)c * grp + g] - m[g]);
+            l[g] += p;
+            double * o = out_row + (int64_t)(kh * grp + g) * d;
+            for (int32_t e = 0; e < d; ++e) o[e] += p * (double)vr[e];
+        }
+    }
+    for (int32_t g = 0; g < grp; ++g) {
+        double * o = out_row + (int64_t)(kh * grp + g) * d;
+        for (int32_t e = 0; e < d; ++e) o[e] /= l[g];
+    }
+}
+
+typedef struct {
+    const uint16_t * q;
+    const float * k;
+    const float * v;
+    int32_t n_ctx, T, hq, hkv, d;
+    double scale;
+    const int32_t * rows;
+    int32_t n_rows;
+    double * out;
+    int32_t next; /* the next (row, KV head) job */
+    pthread_mutex_t mu;
+} attn_f64_job;
+
+static void * attn_f64_worker(void * arg) {
+    attn_f64_job * j = (attn_f64_job *)arg;
+    const int32_t grp = j->hq / j->hkv;
+    double * s = (double *)malloc(sizeof(double) * (size_t)(j->n_ctx > 0 ? j->n_ctx : 1) * (size_t)grp);
+    double * qd = (double *)malloc(sizeof(double) * (size_t)j->d * (size_t)grp);
+    const int32_t jobs = j->n_rows * j->hkv;
+    for (;;) {
+        pthread_mutex_lock(&j->mu);
+        const int32_t i = j->next++;
+        pthread_mutex_unlock(&j->mu);
+        if (i >= jobs) break;
+        const int32_t ri = i / j->hkv, kh = i % j->hkv;
+        const int32_t t = j->rows ? j->rows[ri] : ri;
+        attn_f64_row_group(j->q, j->k, j->v, j->n_ctx, j->T, j->hq, j->hkv, j->d, j->scale, t, kh, s, qd,
+                           j->out + (int64_t)ri * j->hq * j->d);
     }
     free(s);
     free(qd);
+    return NULL;
+}
+
+/* or_attn_f64 over `threads` threads, one (row, KV head) a job: the same bits as one thread */
+void or_attn_f64_mt(const uint16_t * q, const float * k, const float * v, int32_t n_ctx, int32_t T, int32_t hq,
+                    int32_t hkv, int32_t d, double scale, const int32_t * rows, int32_t n_rows, double * out,
+                    int32_t threads) {
+    if (hkv <= 0 || hq % hkv != 0 || hq / hkv > 64) { /* the group's statistics are held in arrays of 64 */
+        const int32_t nr = rows ? n_rows : T;
+        for (int64_t i = 0; i < (int64_t)nr * hq * d; ++i) out[i] = NAN;
+        return;
+    }
+    attn_f64_job j;
+    j.q = q;
+    j.k = k;
+    j.v = v;
+    j.n_ctx = n_ctx;
+    j.T = T;
+    j.hq = hq;
+    j.hkv = hkv;
+    j.d = d;
+    j.scale = scale;
+    j.rows = rows;
+    j.n_rows = rows ? n_rows : T;
+    j.out = out;
+    j.next = 0;
+    pthread_mutex_init(&j.mu, NULL);
+    if (threads < 1) threads = 1;
+    if (threads == 1) {
+        attn_f64_worker(&j);
+    } else {
+        pthread_t * th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
+        for (int32_t i = 0; i < threads; ++i) pthread_create(&th[i], NULL, attn_f64_worker, &j);
+        for (int32_t i = 0; i < threads; ++i) pthread_join(th[i], NULL);
+        free(th);
+    }
+    pthread_mutex_destroy(&j.mu);
+}
+
+void or_attn_f64(const uint16_t * q, const float * k, const float * v, int32_t n_ctx, int32_t T, int32_t hq,
+                 int32_t hkv, int32_t d, double scale, const int32_t * rows, int32_t n_rows, double * out) {
+    or_attn_f64_mt(q, k, v, n_ctx, T, hq, hkv, d, scale, rows, n_rows, out, 1);
 }
 
 /* ggml block_q8_0 as it lies in memory: fp16 d, then 32 int8 codes (34 bytes, no padding) */

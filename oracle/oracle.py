@@ -57,6 +57,7 @@ def lib():
         L.or_reclaim_victim.restype = I32
         L.or_reclaim_victim.argtypes = [P, P, P, I32, I32]
         L.or_attn_f64.argtypes = [P, P, P, I32, I32, I32, I32, I32, ctypes.c_double, P, I32, P]
+        L.or_attn_f64_mt.argtypes = [P, P, P, I32, I32, I32, I32, I32, ctypes.c_double, P, I32, P, I32]
         L.or_attn_ggml.argtypes = [P, P, P, I32, I32, I32, I32, I32, ctypes.c_float, I32, I32, P]
         L.or_block_q8_0_size.restype = I32
         _lib = L
@@ -206,9 +207,10 @@ def reclaim_victim(views, for_slot):
 
 # ---- attention ----
 
-def attn_f64(q16, k, v, n_ctx, scale=1.0 / 16.0, rows=None):
+def attn_f64(q16, k, v, n_ctx, scale=1.0 / 16.0, rows=None, threads=1):
     """FP64 dense causal attention over the decoded cache (qa2_test.cpp:532-583 form).
-    q16: uint16 [T][hq][d]; k, v: float32 [n_ctx][hkv][d]; -> float64 [len(rows)][hq][d]."""
+    q16: uint16 [T][hq][d]; k, v: float32 [n_ctx][hkv][d]; -> float64 [len(rows)][hq][d]. threads > 1 spreads the
+    (row, KV head) pairs over threads (the same bits)."""
     q16 = np.ascontiguousarray(q16, dtype=np.uint16)
     k = np.ascontiguousarray(k, dtype=np.float32)
     v = np.ascontiguousarray(v, dtype=np.float32)
@@ -222,8 +224,8 @@ def attn_f64(q16, k, v, n_ctx, scale=1.0 / 16.0, rows=None):
         rows_a = np.ascontiguousarray(rows, dtype=np.int32)
         nr = rows_a.size
     out = np.empty((nr, hq, d), np.float64)
-    lib().or_attn_f64(_ptr(q16), _ptr(k), _ptr(v), n_ctx, T, hq, hkv, d, scale,
-                      _ptr(rows_a) if rows_a is not None else None, nr, _ptr(out))
+    lib().or_attn_f64_mt(_ptr(q16), _ptr(k), _ptr(v), n_ctx, T, hq, hkv, d, scale,
+                         _ptr(rows_a) if rows_a is not None else None, nr, _ptr(out), max(1, int(threads)))
     return out
 
 
