@@ -24,7 +24,7 @@ def gpu():
         pytest.skip("no GPU")
 
 
-def prefill_case(depth, rows, seed, check_rows, hq=HQ, hkv=HKV, threads=1):
+def prefill_case(depth, rows, seed, check_rows, hq=HQ, hkv=HKV, threads=1, plain=False):
     ctx = depth + rows
     pool = fnkv.Pool(2, -(-ctx // 256) + 4, 1, hkv)
     cases.scatter_ensure(pool, [0], [ctx], seed, churn=0.3)
@@ -41,7 +41,7 @@ def prefill_case(depth, rows, seed, check_rows, hq=HQ, hkv=HKV, threads=1):
     got = out.cpu().numpy()
     (_, _, kf), (_, _, vf) = cases.decoded(O, k16, v16)
     ref = O.attn_f64(q16.view(np.uint16), kf, vf, ctx, rows=check_rows, threads=threads)
-    err = cases.out_err(got[check_rows], ref)
+    err = (cases.plain_err if plain else cases.out_err)(got[check_rows], ref)
     return pool, got, err, (q16, kf, vf, ctx)
 
 
@@ -84,9 +84,9 @@ def test_config3_chunk_at_depth_131072():
     check = list(range(rows))
     print("config 3: the oracle's fp64 attention over 2,048 rows x 133,120 cells", flush=True)
     pool, got, err, (q16, kf, vf, ctx) = prefill_case(131072, rows, seed=3, check_rows=check,
-                                                      threads=min(16, os.cpu_count() or 1))
+                                                      threads=min(16, os.cpu_count() or 1), plain=True)
     assert np.isfinite(got).all()
-    assert err <= TOL
+    assert err <= TOL  # the north star's plain max-abs (BASELINE's outputs sit far below 4)
     # every one of the 2,048 rows against the decode kernel: rows t - 5 .. t are the last six positions of context
     # depth + t + 1, a T = 6 verify over the same cells (a different kernel, the same causal rule); both are within
     # the tolerance of the fp64 attention, so they agree within twice it
