@@ -20,7 +20,10 @@
 //     block's V scale enters the matrix core as fp16 hi + lo (~2^-20 relative); the accumulators O^T (NT x 64
 //     registers) stay in VGPRs (NT <= 2 within a wave's 256);
 //   * one MFMA pair a tile against the V scales (and a row of ones) gives each row's V bias sums and its l;
-//   * after the loop the eight waves fold their (m, l, acc) per row in LDS and the workgroup writes the partial.
+//   * a KV8 pool (group-64 scales, stored at both blocks of a group) takes the KV8 instantiation: a group's two score
+//     MFMAs chain before its one scale FMA, and its P x V-scale products serve both of its blocks;
+//   * after the loop each wave writes its unscaled (m, l, acc) into its own tile slot, and the workgroup folds the
+//     eight waves' rows from there (each scaled by 2^(m - M) as it is read) and writes the split's partial.
 #include "../../include/fnkv.h"
 #include "common.h"
 #include "decode_common.h"
