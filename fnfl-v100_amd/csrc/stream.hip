@@ -12,7 +12,8 @@
 // one's VALU work with the other's MFMAs:
 //   * a tile goes straight from HBM into the wave's LDS slot (its layout is the tile's): the K half (K codes and K
 //     scales) as soon as the scores have read the previous tile's, the V half (V codes and V scales) as soon as PV
-//     has, so each half's latency hides under the other half's work;
+//     has, so each half's latency hides under the other half's work (the first tile's V half only once its K half is
+//     in: the launch's first requests are the waves' K halves alone);
 //   * the K codes are widened once a tile (one byte permute makes two codes the fp16 values 1152 + code) and feed the
 //     S^T = K Q^T MFMA of every row tile (the Q operands sit once in LDS for the workgroup); each block's K scale is
 //     one FMA a score; one MFMA a half takes the 1152 bias back out against the rows' q sums;
@@ -512,9 +513,10 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
         keep_issued();
     };
 
+    // the first tile's K half alone: the launch's first requests are every wave's K codes, so the scores start
+    // before the V halves are in (V(0) is issued once K(0) has landed)
     if (n_w > 0) {
         issue_half(0, 0);
-        issue_half(0, 1);
     }
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
@@ -559,11 +561,17 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
             }
         }
 
-        // Iteration i: wait for K(i), scores, issue K(i + 1), softmax, wait for V(i), PV, issue V(i + 1).
+        // Iteration i: wait for K(i) (i = 0: then issue V(0)), scores, issue K(i + 1), softmax, wait for V(i), PV,
+        // issue V(i + 1).
         FNKV_PHASE_DECL();
         for (int32_t i = 0; i < n_w; ++i) {
             FNKV_PHASE(0 + (i > 0 ? 7 : 0));
-            wait_vmcnt<SH::HALF_LOADS>(); // K(i) has landed (V(i) may be pending)
+            if (i == 0) {
+                wait_vmcnt<0>(); // K(0) has landed; V(0) now loads under its scores
+                issue_half(0, 1);
+            } else {
+                wait_vmcnt<SH::HALF_LOADS>(); // K(i) has landed (V(i) may be pending)
+            }
             FNKV_PHASE(1);
             // the scores and the softmax are the longer dependent chain: their wave issues first on a shared SIMD,
             // so the two waves of a SIMD alternate phases rather than one running ahead
