@@ -110,7 +110,10 @@ constexpr uint32_t kFoldEpoch = 1024;
         }                                                                                                            \
         __builtin_amdgcn_s_waitcnt(0);                                                                               \
     } while (0)
-// phase clocks of wave 0 (20-bit shader cycle counter, no memory counters touched), summed over the loop
+#endif
+#if defined(FNKV_TIMING) && defined(FNKV_TIMING_PHASES)
+// phase clocks of wave 0 (20-bit shader cycle counter, no memory counters touched), summed over the loop: a build of
+// their own, since the clock reads constrain the loop's schedule (and its registers) more than the stamps do
 #define FNKV_PHASE_DECL() uint32_t ph_last = 0, ph_sum[8] = {0, 0, 0, 0, 0, 0, 0, 0}
 #define FNKV_PHASE(p)                                                                                                \
     do {                                                                                                             \
@@ -138,6 +141,8 @@ constexpr uint32_t kFoldEpoch = 1024;
 #define FNKV_PHASE_STORE()                                                                                           \
     do {                                                                                                             \
     } while (0)
+#endif
+#ifndef FNKV_TIMING
 #define FNKV_STAMP_WAVE()                                                                                            \
     do {                                                                                                             \
     } while (0)

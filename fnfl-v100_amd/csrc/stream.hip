@@ -561,17 +561,16 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
             }
         }
 
-        // Iteration i: wait for K(i) (i = 0: then issue V(0)), scores, issue K(i + 1), softmax, wait for V(i), PV,
-        // issue V(i + 1).
+        // Iteration i: wait for K(i), scores, issue K(i + 1), softmax, wait for V(i), PV, issue V(i + 1). V(0) is
+        // issued once K(0) has landed, so it loads under tile 0's scores.
+        if (n_w > 0) {
+            wait_vmcnt<0>();
+            issue_half(0, 1);
+        }
         FNKV_PHASE_DECL();
         for (int32_t i = 0; i < n_w; ++i) {
             FNKV_PHASE(0 + (i > 0 ? 7 : 0));
-            if (i == 0) {
-                wait_vmcnt<0>(); // K(0) has landed; V(0) now loads under its scores
-                issue_half(0, 1);
-            } else {
-                wait_vmcnt<SH::HALF_LOADS>(); // K(i) has landed (V(i) may be pending)
-            }
+            wait_vmcnt<SH::HALF_LOADS>(); // K(i) has landed (V(i) may be pending)
             FNKV_PHASE(1);
             // the scores and the softmax are the longer dependent chain: their wave issues first on a shared SIMD,
             // so the two waves of a SIMD alternate phases rather than one running ahead

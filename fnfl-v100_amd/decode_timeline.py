@@ -1,6 +1,7 @@
 """Per-workgroup timeline and wave-0 phase clocks of one dense decode launch (stream_kernel), from an instrumented
-build of the library (-DFNKV_TIMING: every workgroup stamps the real-time counter at five points, every wave its loop's
-end, and wave 0 sums its shader-clock cycles per loop phase).
+build of the library (-DFNKV_TIMING: every workgroup stamps the real-time counter at five points and every wave its
+loop's end; with -DFNKV_TIMING_PHASES as well, wave 0 also sums its shader-clock cycles per loop phase, in a build of
+its own because the clock reads reshape the loop's schedule).
 
     FNKV_EXTRA_FLAGS=-DFNKV_TIMING FNKV_LIB_OUT=/tmp/fnkv_timing/libfnkv.so python3 fnfl-v100_amd/build_lib.py
     FNKV_LIB_PATH=/tmp/fnkv_timing/libfnkv.so python3 fnfl-v100_amd/decode_timeline.py --ctxs 8192,16384,32768,65536 --T 3
@@ -83,6 +84,10 @@ def main():
     print("  " + "  ".join(f"{x}: {np.median(loop_end[idx % 8 == x]):5.2f}/{loop_end[idx % 8 == x].max():5.2f}"
                            for x in range(8)))
     ph = a[MAX_WG * 16:MAX_WG * 24].reshape(MAX_WG, 8)[used]
+    if not ph.any():
+        print("(no phase clocks: a build without -DFNKV_TIMING_PHASES)")
+        pool.close()
+        return
     print("wave 0's phase cycles summed over its tiles (median over workgroups):")
     for p, nm in enumerate(PHASES):
         if nm != "-":
