@@ -366,6 +366,13 @@ __device__ __forceinline__ dec_args sparse_row_view(const dec_args & in) {
     return a;
 }
 
+// A lane's page-table entry, loaded by every lane (a lane past the walk reads entry 0; guard_unmapped replaces its
+// value), so the load is not under a branch: there the compiler would first wait for every load issued before it
+// (the launch's Q rows)
+__device__ __forceinline__ int32_t page_of(const int32_t * table, bool active, int32_t idx) {
+    return table[active ? idx : 0];
+}
+
 template <bool SP, bool LANES = true> struct split_src {
     int32_t n_tiles = 0;
     int32_t page_lane = 0;
@@ -408,7 +415,7 @@ template <bool SP, bool LANES = true> struct split_src {
                 const int32_t j = split - a.split0[s], n = a.split0[s + 1] - a.split0[s];
                 const int32_t tiles_cap = static_cast<int32_t>((a.ctx[s] + kTileTokens - 1) / kTileTokens);
                 const int32_t cap_n = tiles_cap > j ? (tiles_cap - j + n - 1) / n : 0;
-                page_lane = lane < cap_n ? table[(j + n * lane) >> 3] : 0;
+                page_lane = page_of(table, lane < cap_n, (j + n * lane) >> 3);
                 const int32_t tiles = static_cast<int32_t>((ctx + kTileTokens - 1) / kTileTokens);
                 g0 = j;
                 stride = n;
@@ -419,15 +426,22 @@ template <bool SP, bool LANES = true> struct split_src {
                 stride = 1;
                 n_tiles = static_cast<int32_t>((e - b + kTileTokens - 1) / kTileTokens);
             }
-            page_lane = lane < n_tiles ? table[(g0 + stride * lane) >> 3] : 0;
+            page_lane = page_of(table, lane < n_tiles, (g0 + stride * lane) >> 3);
         }
+    }
+    // A strided walk sized by the host's bound: its tile count for the sequence's actual context (read from the
+    // device after the page lookups were issued)
+    __device__ __forceinline__ void recount(int64_t ctx) {
+        const int32_t tiles = static_cast<int32_t>((ctx + kTileTokens - 1) / kTileTokens);
+        n_tiles = tiles > g0 ? (tiles - g0 + stride - 1) / stride : 0;
     }
     // A walk tile whose page is not mapped (page-table entry -1: the slot was trimmed under a captured launch, outside
     // the contract): its lanes read page 0 instead, so nothing faults, and the workgroup is told (uniform) so that it
     // writes no output for its sequence (its partials carry a NaN max: the merge writes nothing for such a row).
+    // Lanes past the walk take page 0 too. Every dense walk calls this once its tile count is final.
     __device__ __forceinline__ bool guard_unmapped(int32_t lane) {
         const bool neg = lane < n_tiles && page_lane < 0;
-        if (neg) {
+        if (neg || lane >= n_tiles) {
             page_lane = 0;
         }
         return __any(neg);
@@ -477,7 +491,8 @@ template <bool SP, bool LANES = true> struct split_src {
 template <bool SP> __device__ __forceinline__ int64_t seq_ctx(const dec_args & a, int32_t s) {
     if constexpr (!SP) {
         if (a.ctx_dev != nullptr) {
-            return a.ctx_dev[s];
+            // a vector load: a scalar one would hold up every later kernel-argument read until it returned
+            return *(const volatile __attribute__((address_space(1))) int64_t *)(a.ctx_dev + s);
         }
     }
     return a.ctx[s];

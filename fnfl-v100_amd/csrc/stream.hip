@@ -438,9 +438,10 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     const int32_t kvh = static_cast<int32_t>(blockIdx.y);
     const int32_t s = seq_of(a, split);
     const int32_t sp = split - a.split0[s];
-    const int64_t ctx = seq_ctx<false>(a, s);
+    // the context (host contexts), or the host's bound on it (device contexts: the walk is strided and its page
+    // lookups are sized by the bound, so the device word is read after they are issued)
+    int64_t ctx = a.ctx[s];
     const int64_t begin = int64_t(sp) * a.split_tokens;
-    const int64_t end = ctx < begin + a.split_tokens ? ctx : begin + a.split_tokens;
     const pool_view & pv = a.pv;
     const int32_t * table = pv.table + int64_t(a.slot[s]) * pv.table_stride;
 
@@ -448,21 +449,25 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     // w + 8, ...); their loads are issued first, beside the page-table read
     uint8_t * const qs = smem + SH::RING;
     constexpr int PER = NT * kBlocks / WAVES;
+    // (a padding row loads the last real row, unconditionally, and is zeroed when the operands are stored: a load
+    // under a branch would make the compiler wait for it before the page-table read)
     u32x4 qv[PER];
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
         const int32_t c = wave + e * WAVES, rt = c / kBlocks, b = c % kBlocks;
-        const int32_t row = rt * 16 + j;
-        qv[e] = u32x4{0, 0, 0, 0};
-        if (row < a.R) {
-            const int32_t t_row = row / a.G;
-            qv[e] = *reinterpret_cast<const u32x4 *>(
-                a.q + ((int64_t(s) * a.T + t_row) * a.hq + int64_t(kvh) * a.G + row % a.G) * kHeadDim + b * kQK +
-                8 * qg);
-        }
+        const int32_t row = rt * 16 + j < a.R ? rt * 16 + j : a.R - 1;
+        const int32_t t_row = row / a.G;
+        qv[e] = *reinterpret_cast<const u32x4 *>(
+            a.q + ((int64_t(s) * a.T + t_row) * a.hq + int64_t(kvh) * a.G + row % a.G) * kHeadDim + b * kQK + 8 * qg);
     }
     split_src<false> src;
-    src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, nullptr, ctx);
+    src.template init<64 * WAVES>(a, table, split, begin, ctx < begin + a.split_tokens ? ctx : begin + a.split_tokens,
+                                  lane, smem, nullptr, ctx);
+    if (a.ctx_dev != nullptr) {
+        ctx = seq_ctx<false>(a, s);
+        src.recount(ctx);
+    }
+    const int64_t end = ctx < begin + a.split_tokens ? ctx : begin + a.split_tokens;
     FNKV_STAMP(6);
     if (refused<false>(a, s, ctx, sp, kvh)) {
         return;
@@ -520,7 +525,9 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     }
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
-        *reinterpret_cast<u32x4 *>(qs + (wave + e * WAVES) * 1024 + lane * 16) = qv[e];
+        const int32_t c = wave + e * WAVES;
+        const bool real = (c / kBlocks) * 16 + j < a.R;
+        *reinterpret_cast<u32x4 *>(qs + c * 1024 + lane * 16) = real ? qv[e] : u32x4{0, 0, 0, 0};
     }
     barrier_keep_loads(); // the Q operands are in LDS (the tile loads stay in flight)
     FNKV_STAMP(1);

@@ -32,6 +32,9 @@ def main():
     ap.add_argument("--ctxs", default="8192,16384,32768,65536")
     ap.add_argument("--T", type=int, default=3)
     ap.add_argument("--reps", type=int, default=6)
+    ap.add_argument("--dev", type=int, default=0, metavar="SLACK",
+                    help="launch through fnkv_attn_decode_dev: contexts in a device word, the host bound SLACK cells "
+                         "above them (0: fnkv_attn_decode with host contexts)")
     args = ap.parse_args()
     import torch
 
@@ -43,18 +46,26 @@ def main():
         sys.exit("decode_timeline: the loaded library has no timing stamps (build it with -DFNKV_TIMING)")
     L.fnkv_debug_timing.argtypes = [ctypes.c_void_p]
     ctxs = [int(x) for x in args.ctxs.split(",")]
-    pool, slots = bench.make_pool(torch, fnkv, cases, ctxs, args.T, 1, 1234)
+    bound = [c + args.dev for c in ctxs]
+    pool, slots = bench.make_pool(torch, fnkv, cases, ctxs, args.T, 1, 1234, map_to=bound)
     g = torch.Generator(device="cuda")
     g.manual_seed(3)
     q = torch.randn((len(ctxs), args.T, 16, 256), generator=g, device="cuda").half()
     out = torch.empty_like(q)
-    ws = torch.zeros(pool.decode_ws_bytes(ctxs, args.T, 16), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(pool.decode_ws_bytes(bound, args.T, 16), dtype=torch.uint8, device="cuda")
+    ctx_dev = torch.tensor(ctxs, dtype=torch.int64, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
     ts = torch.zeros(MAX_WG * 24, dtype=torch.int64, device="cuda")
     for _ in range(args.reps):  # the last launch's stamps are kept
         ts.zero_()
         L.fnkv_debug_timing(ctypes.c_void_p(ts.data_ptr()))
-        pool.decode(slots, ctxs, args.T, 0, q, out, ws)
+        if args.dev > 0:
+            pool.decode_dev(slots, ctx_dev, bound, args.T, 0, q, out, ws, err)
+        else:
+            pool.decode(slots, ctxs, args.T, 0, q, out, ws)
         torch.cuda.synchronize()
+    if int(err.item()) != 0:
+        sys.exit("decode_timeline: the launch refused a context")
     L.fnkv_debug_timing(ctypes.c_void_p(0))
     a = ts.cpu().numpy()
     st = a[:MAX_WG * 16].reshape(MAX_WG, 16)
@@ -64,7 +75,8 @@ def main():
         sys.exit("decode_timeline: no stamps were written")
     t0 = s[:, 5].min() if (s[:, 5] != 0).all() else s[:, 0].min()  # the first workgroup's entry
     us = lambda v: (v - t0) * 10 / 1000.0  # noqa: E731 (real-time ticks of 10 ns)
-    print(f"contexts {ctxs}, T = {args.T}: {int(used.sum())} workgroups")
+    how = f", device contexts (host bound + {args.dev})" if args.dev > 0 else ""
+    print(f"contexts {ctxs}, T = {args.T}{how}: {int(used.sum())} workgroups")
     for k, nm in enumerate(STAMPS):
         v = s[:, k]
         v = v[v != 0]
