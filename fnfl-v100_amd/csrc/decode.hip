@@ -175,6 +175,41 @@ template <int NT> __device__ __forceinline__ void group_sync() {
 template <int NT, bool SP, bool KV8 = false, bool QLO = false>
 __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(dec_args a_in) {
     static_assert(!QLO || (SP && NT == 1 && dec_shape<NT>::WAVES == kBlocks), "QLO: one row tile, a wave a block");
+    constexpr int GR = dec_shape<NT>::GR;
+    constexpr int WAVES = dec_shape<NT>::WAVES;
+    const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
+    // the wave index is uniform in a wave; readfirstlane tells the compiler so (scalar registers, no waterfall loops)
+    const int32_t wave = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(threadIdx.x) >> 6);
+    const int32_t kvh = static_cast<int32_t>(blockIdx.y);
+    // A launch that prepares its row: the row's inputs are loaded first, before the row view's dependent reads of the
+    // depth word and the selection offsets, so their latencies overlap. Wave w takes the KV head's query heads w and
+    // w + 8 (a head past G loads head G - 1 and is not used); the row's own cell's inputs are loaded by every wave
+    // (the K row or, for the wave of its V job, the V row) and used by the two waves whose jobs they are.
+    // (unset without a prepare: an arbitrary value, never read, so no zeroing waits on the loads of the other path)
+    float4 xq[2], gq, own_x, own_g;
+    int32_t pq;
+    {
+        const float u = __builtin_nondeterministic_value(0.0f);
+        xq[0] = xq[1] = gq = own_x = own_g = make_float4(u, u, u, u);
+        pq = __builtin_nondeterministic_value(0);
+    }
+    if constexpr (SP) {
+        if (a_in.fp.qfull != nullptr) {
+            const int32_t zc = static_cast<int32_t>(blockIdx.z);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int32_t h = wave + 8 * i < a_in.G ? wave + 8 * i : a_in.G - 1;
+                xq[i] = reinterpret_cast<const float4 *>(
+                    a_in.fp.qfull + (int64_t(zc) * a_in.hq + kvh * a_in.G + h) * 512)[lane];
+            }
+            gq = reinterpret_cast<const float4 *>(a_in.fp.q_norm)[lane];
+            pq = rope_pos(a_in.fp.pos, a_in.fp.rows, zc, lane);
+            const int64_t crow = (int64_t(zc) * a_in.pv.h_kv + kvh) * kHeadDim;
+            own_x = reinterpret_cast<const float4 *>((wave == (2 * zc + 1) % WAVES ? a_in.fp.kv_v : a_in.fp.kv_k) +
+                                                     crow)[lane];
+            own_g = reinterpret_cast<const float4 *>(a_in.fp.k_norm)[lane];
+        }
+    }
     const dec_args a = SP ? sparse_row_view(a_in) : a_in;
     if constexpr (SP) {
         if (sparse_refused(a)) {
@@ -182,16 +217,10 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
         }
         FNKV_STAMP(8); // the wave stamps (8..) are not taken in sparse launches
     }
-    constexpr int GR = dec_shape<NT>::GR;
-    constexpr int WAVES = dec_shape<NT>::WAVES;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int32_t lane = static_cast<int32_t>(threadIdx.x) & 63;
-    // the wave index is uniform in a wave; readfirstlane tells the compiler so (scalar registers, no waterfall loops)
-    const int32_t wave = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(threadIdx.x) >> 6);
     const int32_t grp = wave / NT, rt = wave % NT; // tile group and row tile
     const int32_t j = lane & 15, qg = lane >> 4;
     const int32_t split = static_cast<int32_t>(blockIdx.x);
-    const int32_t kvh = static_cast<int32_t>(blockIdx.y);
     const int32_t s = SP ? 0 : seq_of(a, split); // a sparse launch is one sequence (constant: no scratch copy of a)
     const int32_t sp = split - a.split0[s];
     const int64_t ctx = seq_ctx<SP>(a, s);
@@ -204,31 +233,8 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     // latency each but overlapped, not three in a row.
     half8 qop[kBlocks];
     int64_t lim;
-    float4 xq[2], gq;
-    float4 own_x = {0.0f, 0.0f, 0.0f, 0.0f}, own_g = {0.0f, 0.0f, 0.0f, 0.0f}; // a prepared row's own cell
-    int32_t pq = 0;
     if constexpr (SP) { // the Q rows' latency hidden behind the selection's build
-        if (a.fp.qfull != nullptr) {
-            // forming the rows: wave w takes the KV head's query heads w and w + 8; their inputs load now
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int32_t h = wave + 8 * i;
-                xq[i] = h < a.G ? reinterpret_cast<const float4 *>(
-                                      a.fp.qfull + (int64_t(blockIdx.z) * a.hq + kvh * a.G + h) * 512)[lane]
-                                : float4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
-            gq = reinterpret_cast<const float4 *>(a.fp.q_norm)[lane];
-            pq = rope_pos(a.fp.pos, a.fp.rows, static_cast<int32_t>(blockIdx.z), lane);
-            // the row's own cell's inputs, for the waves that write its K (and the k norm) and its V
-            const int32_t zc = static_cast<int32_t>(blockIdx.z);
-            const int64_t crow = (int64_t(zc) * pv.h_kv + kvh) * kHeadDim;
-            if (wave == (2 * zc) % WAVES) {
-                own_x = reinterpret_cast<const float4 *>(a.fp.kv_k + crow)[lane];
-                own_g = reinterpret_cast<const float4 *>(a.fp.k_norm)[lane];
-            } else if (wave == (2 * zc + 1) % WAVES) {
-                own_x = reinterpret_cast<const float4 *>(a.fp.kv_v + crow)[lane];
-            }
-        } else {
+        if (a.fp.qfull == nullptr) {
             load_q_operands(a, s, ctx, kvh, rt, j, qg, qop, lim);
         }
     }
@@ -251,7 +257,9 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
     float sn = 0.0f, cs = 0.0f;
     src.template init<64 * WAVES>(a, table, split, begin, end, lane, smem, smem + GR * kGroupLds, ctx, [&] {
         if (SP && a.fp.qfull != nullptr) {
-            rope_angle(sn, cs, pq, a.fp.theta_scale, lane);
+            int32_t p = pq;
+            __asm__ volatile("" : "+v"(p)); // the position's load is waited for here, not where it was issued
+            rope_angle(sn, cs, p, a.fp.theta_scale, lane);
         }
     });
     if (refused<SP>(a, s, ctx, sp, kvh)) {
