@@ -449,8 +449,9 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     // w + 8, ...); their loads are issued first, beside the page-table read
     uint8_t * const qs = smem + SH::RING;
     constexpr int PER = NT * kBlocks / WAVES;
-    // (a padding row loads the last real row, unconditionally, and is zeroed when the operands are stored: a load
-    // under a branch would make the compiler wait for it before the page-table read)
+    // (a padding row takes the last real row's q, loaded unconditionally: a load under a branch would make the
+    // compiler wait for it before the page-table read; padding rows are computed like the others and never folded or
+    // written)
     u32x4 qv[PER];
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
@@ -525,9 +526,7 @@ __global__ __launch_bounds__(512, 1) void stream_kernel(dec_args a) {
     }
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
-        const int32_t c = wave + e * WAVES;
-        const bool real = (c / kBlocks) * 16 + j < a.R;
-        *reinterpret_cast<u32x4 *>(qs + c * 1024 + lane * 16) = real ? qv[e] : u32x4{0, 0, 0, 0};
+        *reinterpret_cast<u32x4 *>(qs + (wave + e * WAVES) * 1024 + lane * 16) = qv[e];
     }
     barrier_keep_loads(); // the Q operands are in LDS (the tile loads stay in flight)
     FNKV_STAMP(1);
