@@ -120,6 +120,31 @@ def test_decode_one_graph_advancing_context(T, ctx0):
         assert np.array_equal(qs.reshape(kq.shape), kq) and np.array_equal(dd.reshape(kd.shape), kd)
 
 
+@pytest.mark.parametrize("T", [1, 3, 5])
+def test_decode_dev_context_far_below_bound(T):
+    # the grid and the strided splits come from the host bound (~9,000 cells above each context here), the walks'
+    # tile counts from the device word: most splits hold no tile of their sequence and the merge skips them
+    steps = 3000
+    L = DecodeLoop([T + 40, 2000, 5003], T, steps, seed=70 + T)
+    n = len(L.ctx0)
+    ctx_dev = torch.tensor(L.ctx0, dtype=torch.int64, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    q16 = cases.queries(90 + T, (n, T, HQ, D))
+    q = torch.from_numpy(q16).cuda()
+    kn = torch.from_numpy(np.stack([L.kv[s][0][c - T:c] for s, c in enumerate(L.ctx0)])).cuda()
+    vn = torch.from_numpy(np.stack([L.kv[s][1][c - T:c] for s, c in enumerate(L.ctx0)])).cuda()
+    out = torch.empty_like(q)
+    ws = torch.zeros(L.pool.decode_ws_bytes(L.cap, T, HQ), dtype=torch.uint8, device="cuda")
+    L.pool.decode_dev(L.slots, ctx_dev, L.cap, T, 0, q, out, ws, err, k_new=kn, v_new=vn)
+    torch.cuda.synchronize()
+    assert err.item() == 0
+    got = out.cpu().numpy()
+    for s, c in enumerate(L.ctx0):
+        kf, vf = L.dec[s]
+        ref = O.attn_f64(q16[s].view(np.uint16), kf, vf, c)
+        assert cases.out_err(got[s], ref) <= TOL, (s, c)
+
+
 def test_decode_dev_matches_host_context_launch():
     # T = 1 (16 query rows a KV head): the host-value launch splits the same way, so the outputs are bitwise equal
     L = DecodeLoop([4100, 777], 1, 0, seed=3)
