@@ -145,6 +145,35 @@ def test_decode_dev_context_far_below_bound(T):
         assert cases.out_err(got[s], ref) <= TOL, (s, c)
 
 
+@pytest.mark.parametrize("case", range(6))
+def test_seeded_random_device_context_launches(case):
+    # seeded shapes through fnkv_attn_decode_dev: 1-8 sequences, T 1-6, contexts log-uniform in [T + 1, 40,000], each
+    # sequence's host bound 0-3,000 steps of T above its context (so the grid's strided splits hold from all to few
+    # of its tiles), the step's new cells written by the launch
+    rng = np.random.default_rng([case, 5151])
+    n = int(rng.integers(1, 9))
+    T = int(rng.integers(1, 7))
+    ctx0 = [int(max(T + 1, round(np.exp(rng.uniform(np.log(T + 2), np.log(40000)))))) for _ in range(n)]
+    steps = int(rng.integers(0, 3001))
+    print(f"case {case}: n {n} T {T} ctxs {ctx0} slack {T * steps}", flush=True)
+    L = DecodeLoop(ctx0, T, steps, seed=500 + case)
+    ctx_dev = torch.tensor(ctx0, dtype=torch.int64, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    q16 = cases.queries(600 + case, (n, T, HQ, D))
+    q = torch.from_numpy(q16).cuda()
+    kn = torch.from_numpy(np.stack([L.kv[s][0][c - T:c] for s, c in enumerate(ctx0)])).cuda()
+    vn = torch.from_numpy(np.stack([L.kv[s][1][c - T:c] for s, c in enumerate(ctx0)])).cuda()
+    out = torch.empty_like(q)
+    ws = torch.zeros(L.pool.decode_ws_bytes(L.cap, T, HQ), dtype=torch.uint8, device="cuda")
+    L.pool.decode_dev(L.slots, ctx_dev, L.cap, T, 0, q, out, ws, err, k_new=kn, v_new=vn)
+    torch.cuda.synchronize()
+    assert err.item() == 0
+    got = out.cpu().numpy()
+    for s, c in enumerate(ctx0):
+        kf, vf = L.dec[s]
+        assert cases.out_err(got[s], O.attn_f64(q16[s].view(np.uint16), kf, vf, c)) <= TOL, (case, s, c)
+
+
 def test_decode_dev_matches_host_context_launch():
     # T = 1 (16 query rows a KV head): the host-value launch splits the same way, so the outputs are bitwise equal
     L = DecodeLoop([4100, 777], 1, 0, seed=3)
