@@ -581,9 +581,7 @@ __global__ __launch_bounds__(64 * dec_shape<NT>::WAVES, 1) void decode_kernel(de
 // the buffers are fixed registers. The Q operands stay in registers at NT = 2 and sit once in LDS at NT = 3. The
 // groups of the second half run half an iteration behind the first (see the loop), so the two waves sharing a SIMD
 // are in different phases.
-// (two groups a workgroup at NT = 2, two workgroups a CU, measured slower on cfg1: 47.4 against 42.7 us a layer)
-// Dense launches at NT = 3 run decode_kernel<3> instead (each wave its own row tile over all value blocks, V loaded by
-// each wave: cfg2v T = 5 111 against 118 us a layer); sparse ones keep this kernel.
+// (two groups a workgroup at NT = 2, two workgroups a CU, measured slower when this kernel served dense launches)
 #ifndef FNKV_QK_PRIO
 #define FNKV_QK_PRIO 1
 #endif
@@ -1219,19 +1217,16 @@ template <int NT, bool SP, bool QLO = false> int32_t rows_lds() {
     const int32_t merge = SH::GR * NT * 16 * 2 * 4 + SH::GR * NT * 16 * (kHeadDim + 4) * 4;
     return SP ? std::max(std::max(ring + kSelSlice, merge), kSelLds) : std::max(ring, merge);
 }
-int32_t decode_lds(int32_t nt, bool sp, bool qlo = false) {
+// the sparse kernels' dynamic LDS for nt row tiles (qlo: q's low parts after the selection slice)
+int32_t decode_lds(int32_t nt, bool qlo = false) {
     if (nt == 1) {
         constexpr int32_t waves = dec_shape<1>::WAVES;
         const int32_t tiles = dec_shape<1>::GR * kGroupLds;
         const int32_t merge = waves * 16 * 2 * 4 + waves * 16 * (kHeadDim + 4) * 4;
-        return sp ? std::max(std::max(tiles + kSelSlice + kFusedQLds, merge), kSelLds) : std::max(tiles, merge);
+        return std::max(std::max(tiles + kSelSlice + kFusedQLds, merge), kSelLds);
     }
     if (nt == 2) {
-        return sp ? (qlo ? rows_lds<2, true, true>() : rows_lds<2, true>()) : rows_lds<2, false>();
-    }
-    if (!sp) { // decode_kernel<3>: the groups' tile buffers, or the merge's (m, l) and partial rows
-        constexpr int32_t waves = dec_shape<3>::WAVES;
-        return std::max(dec_shape<3>::GR * kGroupLds, waves * 16 * 2 * 4 + waves * 16 * (kHeadDim + 4) * 4);
+        return qlo ? rows_lds<2, true, true>() : rows_lds<2, true>();
     }
     return qlo ? rows_lds<3, true, true>() : rows_lds<3, true>();
 }
@@ -1395,42 +1390,33 @@ void launch_merge(const merge_args & m, hipStream_t st) {
     hipLaunchKernelGGL(merge_kernel, dim3(static_cast<uint32_t>(m.n_seq * m.h_kv * m.R * 8)), dim3(256), 0, st, m);
 }
 
-template <bool SP, bool KV8, bool QLO = false> void set_decode_attrs() {
+// the sparse kernels' instantiations for the pool's format (KV8) and the q form (QLO)
+template <bool KV8, bool QLO = false> void set_decode_attrs() {
+    constexpr bool SP = true;
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<1, SP, KV8, QLO>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(1, SP, QLO));
+                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(1, QLO));
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<2, SP, KV8, QLO>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(2, SP, QLO));
-    if constexpr (SP) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<3, SP, KV8, QLO>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3, SP, QLO));
-    } else {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<3, SP, KV8>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3, SP));
-    }
+                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(2, QLO));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(decode_rows_kernel<3, SP, KV8, QLO>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, decode_lds(3, QLO));
 }
 
-template <bool SP, bool KV8, bool QLO = false>
-void launch_decode_fmt(int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
+template <bool KV8, bool QLO = false> void launch_decode_fmt(int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
+    constexpr bool SP = true;
     if (NT == 1) {
         hipLaunchKernelGGL((decode_kernel<1, SP, KV8, QLO>), grid, dim3(64 * dec_shape<1>::WAVES),
-                           decode_lds(1, SP, QLO), st, a);
+                           decode_lds(1, QLO), st, a);
     } else if (NT == 2) {
         hipLaunchKernelGGL((decode_rows_kernel<2, SP, KV8, QLO>), grid, dim3(64 * rows_shape<2, SP, QLO>::WAVES),
-                           decode_lds(2, SP, QLO), st, a);
+                           decode_lds(2, QLO), st, a);
     } else {
-        if constexpr (!SP) { // dense: each wave of a 3-wave group runs its row tile's scores and PV
-            hipLaunchKernelGGL((decode_kernel<3, SP, KV8>), grid, dim3(64 * dec_shape<3>::WAVES), decode_lds(3, SP),
-                               st, a);
-        } else {
-            hipLaunchKernelGGL((decode_rows_kernel<3, SP, KV8, QLO>), grid, dim3(64 * rows_shape<3, SP, QLO>::WAVES),
-                               decode_lds(3, SP, QLO), st, a);
-        }
+        hipLaunchKernelGGL((decode_rows_kernel<3, SP, KV8, QLO>), grid, dim3(64 * rows_shape<3, SP, QLO>::WAVES),
+                           decode_lds(3, QLO), st, a);
     }
 }
 
 // the sparse decode kernel for NT row tiles and the pool's format, its LDS attribute set once per device
 void launch_decode_sparse(const kv_pool & p, int32_t NT, dim3 grid, const dec_args & a, hipStream_t st) {
-    constexpr bool SP = true;
     // once per device, before any launch of it returns: a thread arriving while another sets the attributes waits
     static std::once_flag attr_once[64];
     const int32_t dev = p.device();
@@ -1439,26 +1425,26 @@ void launch_decode_sparse(const kv_pool & p, int32_t NT, dim3 grid, const dec_ar
             int32_t cur = 0;
             (void)hipGetDevice(&cur);
             (void)hipSetDevice(dev);
-            set_decode_attrs<SP, false>();
-            set_decode_attrs<SP, true>();
-            set_decode_attrs<SP, false, true>();
-            set_decode_attrs<SP, true, true>();
+            set_decode_attrs<false>();
+            set_decode_attrs<true>();
+            set_decode_attrs<false, true>();
+            set_decode_attrs<true, true>();
             (void)hipGetLastError();
             (void)hipSetDevice(cur);
         });
     }
     if (a.q_lo != nullptr) {
         if (a.pv.format == kFormatKV8) {
-            launch_decode_fmt<SP, true, true>(NT, grid, a, st);
+            launch_decode_fmt<true, true>(NT, grid, a, st);
         } else {
-            launch_decode_fmt<SP, false, true>(NT, grid, a, st);
+            launch_decode_fmt<false, true>(NT, grid, a, st);
         }
         return;
     }
     if (a.pv.format == kFormatKV8) {
-        launch_decode_fmt<SP, true>(NT, grid, a, st);
+        launch_decode_fmt<true>(NT, grid, a, st);
     } else {
-        launch_decode_fmt<SP, false>(NT, grid, a, st);
+        launch_decode_fmt<false>(NT, grid, a, st);
     }
 }
 
